@@ -1,0 +1,126 @@
+/*
+ * mlk_hip.h -- C ABI of the MI355X (gfx950) RDT4quant fused-forward kernels.
+ *
+ * This library replaces, for device-resident tensors, the CPU operators that
+ * the reference exposes through its PyTorch extension module montlok._C
+ * (rdt4quant_cpu/montlok.cpp, op table at montlok.cpp:1457-1499). Each entry
+ * point below names the reference operator it stands in for (file:line).
+ *
+ * Conventions
+ *   - Plain device pointers, element counts and element strides; no torch
+ *     types. fp32 tensors unless stated; the last dimension of every tensor
+ *     is dense, leading dimensions may be strided where a stride is given.
+ *   - Outputs are written into caller-provided device buffers (the Python
+ *     layer allocates them with the caching allocator, as montlok.cpp
+ *     allocates with torch::empty). No entry point allocates device memory.
+ *   - Work is enqueued on `stream` (a hipStream_t) and is stream-ordered; no
+ *     entry point synchronises the device.
+ *   - Every entry point returns an mlk_status; on failure mlk_last_error()
+ *     returns a thread-local message (the reference raises RuntimeError with
+ *     the TORCH_CHECK text; the Python layer raises the same text). This
+ *     mirrors montlok_status + montlok_last_error of the reference's product
+ *     C ABI (include/montlok/montlok.h:16-17,43-52).
+ *   - Scalar parameters that the reference reads from 0-d tensors (the mHC
+ *     alphas) are passed as device pointers so no call reads device memory
+ *     from the host.
+ */
+#ifndef MLK_HIP_H
+#define MLK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* mlk_stream_t; /* identical to hipStream_t */
+
+typedef enum mlk_status {
+    MLK_OK = 0,
+    MLK_ERR_INVALID_ARGUMENT = 1,
+    MLK_ERR_RUNTIME = 2,
+    MLK_ERR_UNSUPPORTED = 3
+} mlk_status;
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* mlk_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int mlk_abi_version(void);
+
+/* JSON object describing the build and the current device: gfx arch, CU
+ * count, kernel variant. Replaces build_info() (montlok.cpp:1417-1455).
+ * Writes at most `capacity` bytes including the terminating NUL. */
+mlk_status mlk_build_info(char* buffer, size_t capacity);
+
+/* ---------------------------------------------------------------- norms -- */
+
+/* rms_norm(x, weight, eps, groups) -- montlok.cpp:915-938, kernel
+ * montlok_layers.h:20-65. x: rows of `dim` floats, `row_stride` apart;
+ * out: [rows, dim] contiguous. eps is the Python float (cast through float32
+ * as the reference does). groups must divide dim. */
+mlk_status mlk_rms_norm(const float* x, int64_t rows, int64_t dim, int64_t row_stride, const float* weight,
+                        double eps, int64_t groups, float* out, mlk_stream_t stream);
+
+/* add_rms_norm(left, right, weight, eps, groups) -- montlok.cpp:978-1007,
+ * kernel montlok_layers.h:71-90. left/right/residual/normalized: [rows, dim]
+ * contiguous. */
+mlk_status mlk_add_rms_norm(const float* left, const float* right, int64_t rows, int64_t dim, const float* weight,
+                            double eps, int64_t groups, float* residual, float* normalized, mlk_stream_t stream);
+
+/* layer_norm(x, weight, bias, eps) -- montlok.cpp:1057-1082, kernel
+ * montlok_layers.h:117-184. bias may be NULL. */
+mlk_status mlk_layer_norm(const float* x, int64_t rows, int64_t dim, int64_t row_stride, const float* weight,
+                          const float* bias, double eps, float* out, mlk_stream_t stream);
+
+/* swiglu(x) -- montlok.cpp:942-963, kernel montlok_layers.h:95-112. x rows
+ * hold [gate | up] (2*hidden floats, row_stride apart); out: [rows, hidden]. */
+mlk_status mlk_swiglu(const float* x, int64_t rows, int64_t hidden, int64_t row_stride, float* out,
+                      mlk_stream_t stream);
+
+/* ----------------------------------------------------------------- mHC -- */
+
+/* mhc_prepare(streams, norm_w, eps, proj_w, pre_bias, post_bias, res_bias,
+ *             pre_alpha, post_alpha, res_alpha, iters, n_streams,
+ *             agg_norm_w, agg_norm_eps) -- montlok.cpp:659-691, kernel
+ * montlok_mhc.h:198-322.
+ *   streams: `tokens` tokens `token_stride` floats apart, each holding n rows
+ *            of d floats `stream_stride` apart (0 = the broadcast backbone).
+ *   proj_w:  float64 [2n + n*n, d] = cat(pre, post, res projection weights).
+ *   alphas:  device pointers to the three fp32 scalars.
+ *   agg_norm_w: optional [d] (NULL = no in-place RMSNorm of agg).
+ *   outputs: agg [tokens, d], pre [tokens, n], post [tokens, n],
+ *            res [tokens, n, n], all contiguous. */
+mlk_status mlk_mhc_prepare(const float* streams, int64_t tokens, int64_t n, int64_t d, int64_t stream_stride,
+                           int64_t token_stride, const float* norm_w, double eps, const double* proj_w,
+                           const float* pre_bias, const float* post_bias, const float* res_bias,
+                           const float* pre_alpha, const float* post_alpha, const float* res_alpha,
+                           int64_t sinkhorn_iters, const float* agg_norm_w, double agg_norm_eps, float* agg,
+                           float* pre, float* post, float* res, mlk_stream_t stream);
+
+/* mhc_combine(streams, res, post, out) -- montlok.cpp:726-739, and
+ * mhc_combine_collapse -- montlok.cpp:743-758 (kernel montlok_mhc.h:336-438).
+ * new_streams: [tokens, n, d] contiguous or NULL; collapsed: [tokens, d] or
+ * NULL (mean over the rounded new streams). At least one must be given. */
+mlk_status mlk_mhc_combine(const float* streams, int64_t tokens, int64_t n, int64_t d, int64_t stream_stride,
+                           int64_t token_stride, const float* res, const float* post, const float* out,
+                           float* new_streams, float* collapsed, mlk_stream_t stream);
+
+/* mhc_combine_prepare(streams, res, post, out, <next hc args>) --
+ * montlok.cpp:763-802, kernel montlok_mhc.h:511-522. Writes new_streams
+ * [tokens, n, d] and the next residual's agg/pre/post/res. */
+mlk_status mlk_mhc_combine_prepare(const float* streams, int64_t tokens, int64_t n, int64_t d,
+                                   int64_t stream_stride, int64_t token_stride, const float* res, const float* post,
+                                   const float* out, const float* norm_w, double eps, const double* proj_w,
+                                   const float* pre_bias, const float* post_bias, const float* res_bias,
+                                   const float* pre_alpha, const float* post_alpha, const float* res_alpha,
+                                   int64_t sinkhorn_iters, const float* agg_norm_w, double agg_norm_eps,
+                                   float* new_streams, float* agg_out, float* pre_out, float* post_out,
+                                   float* res_out, mlk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLK_HIP_H */

@@ -1,0 +1,600 @@
+// Manifold-constrained hyper-connection (mHC) residual mix on gfx950.
+//
+// Read side (mhc_prepare, reference rdt4quant_cpu/montlok_mhc.h:198-322), per
+// token of n streams x d:
+//   ref    = RMSNorm_d(mean_i streams_i) * norm_w          (double)
+//   logits = tanh(W64 . ref), W64 = cat(pre, post, res projections) [2n+n^2, d]
+//   pre    = sigmoid(pre_b + a_pre * logit)                 -> fp32
+//   post   = 2 * sigmoid(post_b + a_post * logit)           -> fp32
+//   res    = Sinkhorn(exp(res_b + a_res * logit)), max(iters, 1) rounds of row
+//            then column normalisation in double            -> fp32
+//   agg    = sum_i double(pre_i) * streams_i (one rounding), optionally
+//            RMSNorm'd in place with agg_norm_w.
+// Write side (mhc_combine, montlok_mhc.h:336-438):
+//   new_i = double(post_i) * out + sum_j double(res_ij) * streams_j (one
+//   rounding), collapsed = mean_i of the rounded new_i (double, one rounding).
+//
+// Kernels
+//   prepare_n4<D> (n = 4, d = D in {64, 128, 256, 512}): one 256-thread block
+//     per 16 tokens. Lane l of every wave is (token t = l % 16, k-lane
+//     q = l / 16). The 24 dot products of each token run on the fp64 matrix
+//     cores, v_mfma_f64_16x16x4_f64: A = 16 projection rows x 4 k, B = 4 k x
+//     16 tokens, two row tiles (tile 0 = the 16 res rows, tile 1 = 4 pre + 4
+//     post rows + 8 zero rows). The k range is split over the block's four
+//     waves (wave w owns steps [w*S/4, (w+1)*S/4), S = D/4, step s covering
+//     k = 4s + q); partial tiles are summed through LDS by wave 0 in wave
+//     order. norm_w and the RMS scale are applied on the B side and after the
+//     sum: logit = scale * sum_k W[r,k] * (w_k * m_k). The accumulator of the
+//     16x16x4 f64 MFMA holds tile rows q, q+4, q+8, q+12 of token t in lane
+//     (t, q); the projection rows are permuted on the A side so that after the
+//     tanh every lane holds one full row of its token's 4x4 Sinkhorn matrix
+//     (and lanes q = 0 / 1 the pre / post logits): row sums are lane-local,
+//     column sums gather the four
+//     lanes of the token with the reference's sequential order, and the
+//     reciprocals are IEEE divisions like the reference's 1 / s.
+//     Traffic per token: n*d*4 bytes read twice (the second read, for agg,
+//     hits L2) + d*4 written + 36 floats of coefficients.
+//   prepare_generic: one wave per token, every sum in the reference's own
+//     order (bit-exact with it); used for other n or d. Slow, small shapes.
+//   combine<N>: one thread per (token, float4 of d), HBM-bound.
+#include "mlk_common.h"
+
+namespace mlk {
+namespace {
+
+typedef double double4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ double sigmoid_d(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+// ---------------------------------------------------------------------------
+// prepare, n = 4 fast path
+// ---------------------------------------------------------------------------
+
+struct PrepareArgs {
+    const float* streams;
+    int64_t tokens;
+    int64_t sd;  // stream stride (0: broadcast backbone)
+    int64_t ts;  // token stride
+    const float* norm_w;
+    double eps;
+    const double* proj_w;  // [24, D]: pre rows 0-3, post rows 4-7, res rows 8-23
+    const float* pre_bias;
+    const float* post_bias;
+    const float* res_bias;
+    const float* pre_alpha;
+    const float* post_alpha;
+    const float* res_alpha;
+    int iters;
+    const float* agg_norm_w;
+    double agg_norm_eps;
+    float* agg;
+    float* pre;
+    float* post;
+    float* res;
+};
+
+template <int D>
+__global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
+    constexpr int S = D / 4;       // MFMA k-steps over d
+    constexpr int SW = S / 4;      // steps per wave
+    constexpr int n = 4;
+    __shared__ double part[3][2][4][64];  // partial tiles of waves 1..3
+    __shared__ double part_sq[3][64];
+    __shared__ float pre_lds[16][4];
+    __shared__ double agg_sq[4][64];
+
+    const int wave = threadIdx.x / kWave;
+    const int l = threadIdx.x % kWave;
+    const int t = l % 16;
+    const int q = l / 16;
+    const int64_t token = static_cast<int64_t>(blockIdx.x) * 16 + t;
+    const bool valid = token < a.tokens;
+    const float* base = a.streams + (valid ? token : 0) * a.ts;
+    const double inv_n = 1.0 / n;
+
+    // Stream values of this lane's k set, kept for the agg pass.
+    float sv[SW][n];
+    double sq = 0.0;
+    double4_t acc0 = {0.0, 0.0, 0.0, 0.0};
+    double4_t acc1 = {0.0, 0.0, 0.0, 0.0};
+    // Projection row fed by this lane as A-operand row i = l % 16 of each tile.
+    // The 16x16x4 f64 accumulator gives lane (t, q) register v = tile row
+    // q + 4v, so A row i = q' + 4v' is chosen to land where it is used: tile 0
+    // row i carries res entry (row i % 4, column i / 4), which puts res row q
+    // in lane q; tile 1 row i carries pre[i / 4] when i % 4 == 0 and
+    // post[i / 4] when i % 4 == 1 (zero rows otherwise).
+    const double* w_res = a.proj_w + static_cast<int64_t>(2 * n + 4 * (t % 4) + t / 4) * D;
+    const bool pp_row = t % 4 < 2;
+    const double* w_pp = a.proj_w + static_cast<int64_t>((t % 4 == 0 ? 0 : n) + t / 4) * D;
+#pragma unroll
+    for (int j = 0; j < SW; ++j) {
+        const int s = wave * SW + j;
+        const int k = 4 * s + q;
+#pragma unroll
+        for (int i = 0; i < n; ++i) sv[j][i] = valid ? base[i * a.sd + k] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < SW; ++j) {
+        const int s = wave * SW + j;
+        const int k = 4 * s + q;
+        double m = static_cast<double>(sv[j][0]);
+#pragma unroll
+        for (int i = 1; i < n; ++i) m += static_cast<double>(sv[j][i]);
+        m *= inv_n;
+        sq = fma(m, m, sq);
+        const double b = m * static_cast<double>(a.norm_w[k]);
+        const double a0 = w_res[k];
+        const double a1 = pp_row ? w_pp[k] : 0.0;
+        acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b, acc1, 0, 0, 0);
+    }
+    // Sum of squares over the token's four k-lanes, then over the waves.
+    sq += shfl_xor_d(sq, 16);
+    sq += shfl_xor_d(sq, 32);
+    if (wave > 0) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            part[wave - 1][0][v][l] = acc0[v];
+            part[wave - 1][1][v][l] = acc1[v];
+        }
+        part_sq[wave - 1][l] = sq;
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < 3; ++w) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                acc0[v] += part[w][0][v][l];
+                acc1[v] += part[w][1][v][l];
+            }
+            sq += part_sq[w][l];
+        }
+        const double scale = 1.0 / sqrt(sq / static_cast<double>(D) + a.eps);
+        const double pre_alpha = static_cast<double>(*a.pre_alpha);
+        const double post_alpha = static_cast<double>(*a.post_alpha);
+        const double res_alpha = static_cast<double>(*a.res_alpha);
+        // Tile 1: lane q = 0 holds the 4 pre logits, q = 1 the 4 post logits.
+        if (q < 2) {
+            float outv[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const double th = tanh(acc1[v] * scale);
+                if (q == 0) {
+                    outv[v] = static_cast<float>(sigmoid_d(fma(pre_alpha, th, static_cast<double>(a.pre_bias[v]))));
+                } else {
+                    outv[v] =
+                        static_cast<float>(2.0 * sigmoid_d(fma(post_alpha, th, static_cast<double>(a.post_bias[v]))));
+                }
+            }
+            if (q == 0) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) pre_lds[t][v] = outv[v];
+            }
+            if (valid) {
+                float* dst = (q == 0 ? a.pre : a.post) + token * n;
+                *reinterpret_cast<float4*>(dst) = make_float4(outv[0], outv[1], outv[2], outv[3]);
+            }
+        }
+        // Tile 0: lane q holds row q of the res matrix.
+        double m[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const double th = tanh(acc0[v] * scale);
+            m[v] = exp(fma(res_alpha, th, static_cast<double>(a.res_bias[4 * q + v])));
+        }
+        const int rounds = a.iters > 1 ? a.iters : 1;
+        for (int it = 0; it < rounds; ++it) {
+            const double inv = 1.0 / (((m[0] + m[1]) + m[2]) + m[3]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) m[v] *= inv;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const double x0 = shfl_d(m[v], t);
+                const double x1 = shfl_d(m[v], t + 16);
+                const double x2 = shfl_d(m[v], t + 32);
+                const double x3 = shfl_d(m[v], t + 48);
+                const double r = 1.0 / (((x0 + x1) + x2) + x3);
+                m[v] *= r;
+            }
+        }
+        if (valid) {
+            *reinterpret_cast<float4*>(a.res + token * 16 + 4 * q) =
+                make_float4(static_cast<float>(m[0]), static_cast<float>(m[1]), static_cast<float>(m[2]),
+                            static_cast<float>(m[3]));
+        }
+    }
+    __syncthreads();
+    // agg over this wave's k set: sum_i pre_i * s_i, exact products, one rounding.
+    double p[n];
+#pragma unroll
+    for (int i = 0; i < n; ++i) p[i] = static_cast<double>(pre_lds[t][i]);
+    float aggv[SW];
+    double asq = 0.0;
+#pragma unroll
+    for (int j = 0; j < SW; ++j) {
+        double acc = p[0] * static_cast<double>(sv[j][0]);
+#pragma unroll
+        for (int i = 1; i < n; ++i) acc = fma(p[i], static_cast<double>(sv[j][i]), acc);
+        aggv[j] = static_cast<float>(acc);
+        const double av = static_cast<double>(aggv[j]);
+        asq = fma(av, av, asq);
+    }
+    float* agg_row = a.agg + (valid ? token : 0) * D;
+    if (a.agg_norm_w == nullptr) {
+        if (valid) {
+#pragma unroll
+            for (int j = 0; j < SW; ++j) agg_row[4 * (wave * SW + j) + q] = aggv[j];
+        }
+        return;
+    }
+    asq += shfl_xor_d(asq, 16);
+    asq += shfl_xor_d(asq, 32);
+    agg_sq[wave][l] = asq;
+    __syncthreads();
+    // Every wave forms the same total in the same (wave) order.
+    const double total = ((agg_sq[0][l] + agg_sq[1][l]) + agg_sq[2][l]) + agg_sq[3][l];
+    const double ascale = 1.0 / sqrt(total / static_cast<double>(D) + a.agg_norm_eps);
+    if (valid) {
+#pragma unroll
+        for (int j = 0; j < SW; ++j) {
+            const int k = 4 * (wave * SW + j) + q;
+            agg_row[k] = static_cast<float>((static_cast<double>(aggv[j]) * ascale) *
+                                            static_cast<double>(a.agg_norm_w[k]));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// prepare, generic path: one wave per token, reference association
+// ---------------------------------------------------------------------------
+
+struct GenericArgs {
+    PrepareArgs p;
+    int n;
+    int64_t d;
+};
+
+__global__ __launch_bounds__(kWave) void mhc_prepare_generic_kernel(GenericArgs g) {
+    extern __shared__ double smem[];
+    const PrepareArgs& a = g.p;
+    const int n = g.n;
+    const int64_t d = g.d;
+    const int rows = 2 * n + n * n;
+    double* ref = smem;                 // [d]
+    double* logit = ref + d;            // [rows]
+    double* mat = logit + rows;         // [n*n]
+    double* sums = mat + n * n;         // [n]
+    float* pref = reinterpret_cast<float*>(sums + n);  // [n]
+    float* aggf = pref + n;                             // [d]
+    const int lane = threadIdx.x;
+    const int64_t token = blockIdx.x;
+    const float* s = a.streams + token * a.ts;
+    const double inv_n = 1.0 / static_cast<double>(n);
+
+    for (int64_t k = lane; k < d; k += kWave) {
+        double m = static_cast<double>(s[k]);
+        for (int i = 1; i < n; ++i) m += static_cast<double>(s[i * a.sd + k]);
+        ref[k] = m * inv_n;
+    }
+    __syncthreads();
+    __shared__ double scale_s;
+    if (lane == 0) {
+        // Four double lanes over the 4-aligned part, hsum, scalar tail.
+        double sq[4] = {0.0, 0.0, 0.0, 0.0};
+        int64_t k = 0;
+        for (; k + 4 <= d; k += 4) {
+            for (int v = 0; v < 4; ++v) sq[v] = fma(ref[k + v], ref[k + v], sq[v]);
+        }
+        double sumsq = (sq[0] + sq[1]) + (sq[2] + sq[3]);
+        for (; k < d; ++k) sumsq = fma(ref[k], ref[k], sumsq);
+        scale_s = 1.0 / sqrt(sumsq / static_cast<double>(d) + a.eps);
+    }
+    __syncthreads();
+    const double scale = scale_s;
+    for (int64_t k = lane; k < d; k += kWave) ref[k] = (ref[k] * scale) * static_cast<double>(a.norm_w[k]);
+    __syncthreads();
+    for (int r = lane; r < rows; r += kWave) {
+        const double* w = a.proj_w + static_cast<int64_t>(r) * d;
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};
+        int64_t k = 0;
+        for (; k + 4 <= d; k += 4) {
+            for (int v = 0; v < 4; ++v) acc[v] = fma(w[k + v], ref[k + v], acc[v]);
+        }
+        double out = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        for (; k < d; ++k) out = fma(w[k], ref[k], out);
+        logit[r] = tanh(out);
+    }
+    __syncthreads();
+    const double pre_alpha = static_cast<double>(*a.pre_alpha);
+    const double post_alpha = static_cast<double>(*a.post_alpha);
+    const double res_alpha = static_cast<double>(*a.res_alpha);
+    for (int i = lane; i < n; i += kWave) {
+        pref[i] = static_cast<float>(sigmoid_d(fma(pre_alpha, logit[i], static_cast<double>(a.pre_bias[i]))));
+        a.pre[token * n + i] = pref[i];
+        a.post[token * n + i] =
+            static_cast<float>(2.0 * sigmoid_d(fma(post_alpha, logit[n + i], static_cast<double>(a.post_bias[i]))));
+    }
+    for (int e = lane; e < n * n; e += kWave) {
+        mat[e] = fma(res_alpha, logit[2 * n + e], static_cast<double>(a.res_bias[e]));
+    }
+    __syncthreads();
+    for (int64_t k = lane; k < d; k += kWave) {
+        double acc = static_cast<double>(pref[0]) * static_cast<double>(s[k]);
+        for (int i = 1; i < n; ++i) {
+            acc = fma(static_cast<double>(pref[i]), static_cast<double>(s[i * a.sd + k]), acc);
+        }
+        aggf[k] = static_cast<float>(acc);
+    }
+    __syncthreads();
+    if (lane == 0) {
+        if (a.agg_norm_w != nullptr) {
+            double acc0[4] = {0, 0, 0, 0}, acc1[4] = {0, 0, 0, 0};
+            int64_t k = 0;
+            for (; k + 8 <= d; k += 8) {
+                for (int v = 0; v < 4; ++v) {
+                    const double x0 = aggf[k + v], x1 = aggf[k + 4 + v];
+                    acc0[v] = fma(x0, x0, acc0[v]);
+                    acc1[v] = fma(x1, x1, acc1[v]);
+                }
+            }
+            double tv[4];
+            for (int v = 0; v < 4; ++v) tv[v] = acc0[v] + acc1[v];
+            double sumsq = (tv[0] + tv[1]) + (tv[2] + tv[3]);
+            for (; k < d; ++k) sumsq = fma(static_cast<double>(aggf[k]), static_cast<double>(aggf[k]), sumsq);
+            scale_s = 1.0 / sqrt(sumsq / static_cast<double>(d) + a.agg_norm_eps);
+        }
+        // Sinkhorn in the reference's order.
+        for (int e = 0; e < n * n; ++e) mat[e] = exp(mat[e]);
+        const int rounds = a.iters > 1 ? a.iters : 1;
+        for (int it = 0; it < rounds; ++it) {
+            for (int i = 0; i < n; ++i) {
+                double sum = mat[i * n];
+                for (int j = 1; j < n; ++j) sum += mat[i * n + j];
+                const double inv = 1.0 / sum;
+                for (int j = 0; j < n; ++j) mat[i * n + j] *= inv;
+            }
+            for (int j = 0; j < n; ++j) {
+                double sum = mat[j];
+                for (int i = 1; i < n; ++i) sum += mat[i * n + j];
+                sums[j] = 1.0 / sum;
+            }
+            for (int i = 0; i < n; ++i) {
+                for (int j = 0; j < n; ++j) mat[i * n + j] *= sums[j];
+            }
+        }
+    }
+    __syncthreads();
+    for (int e = lane; e < n * n; e += kWave) a.res[token * n * n + e] = static_cast<float>(mat[e]);
+    const double ascale = scale_s;
+    for (int64_t k = lane; k < d; k += kWave) {
+        float v = aggf[k];
+        if (a.agg_norm_w != nullptr) {
+            v = static_cast<float>((static_cast<double>(v) * ascale) * static_cast<double>(a.agg_norm_w[k]));
+        }
+        a.agg[token * d + k] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// combine
+// ---------------------------------------------------------------------------
+
+template <int N>
+__global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __restrict__ streams, int64_t tokens,
+                                                                 int64_t d, int64_t sd, int64_t ts,
+                                                                 const float* __restrict__ res,
+                                                                 const float* __restrict__ post,
+                                                                 const float* __restrict__ out,
+                                                                 float* __restrict__ new_streams,
+                                                                 float* __restrict__ collapsed) {
+    const int64_t chunks = d / 4;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (idx >= tokens * chunks) return;
+    const int64_t token = idx / chunks;
+    const int64_t k = (idx % chunks) * 4;
+    const float4 o = *reinterpret_cast<const float4*>(out + token * d + k);
+    float4 s[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) s[j] = *reinterpret_cast<const float4*>(streams + token * ts + j * sd + k);
+    const float* r = res + token * N * N;
+    const float* p = post + token * N;
+    double mean[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const double pi = static_cast<double>(p[i]);
+        double acc[4] = {pi * o.x, pi * o.y, pi * o.z, pi * o.w};
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const double rij = static_cast<double>(r[i * N + j]);
+            acc[0] = fma(rij, static_cast<double>(s[j].x), acc[0]);
+            acc[1] = fma(rij, static_cast<double>(s[j].y), acc[1]);
+            acc[2] = fma(rij, static_cast<double>(s[j].z), acc[2]);
+            acc[3] = fma(rij, static_cast<double>(s[j].w), acc[3]);
+        }
+        const float4 nv = make_float4(static_cast<float>(acc[0]), static_cast<float>(acc[1]),
+                                      static_cast<float>(acc[2]), static_cast<float>(acc[3]));
+        if (new_streams != nullptr) *reinterpret_cast<float4*>(new_streams + (token * N + i) * d + k) = nv;
+        mean[0] += static_cast<double>(nv.x);
+        mean[1] += static_cast<double>(nv.y);
+        mean[2] += static_cast<double>(nv.z);
+        mean[3] += static_cast<double>(nv.w);
+    }
+    if (collapsed != nullptr) {
+        const double inv_n = 1.0 / static_cast<double>(N);
+        *reinterpret_cast<float4*>(collapsed + token * d + k) =
+            make_float4(static_cast<float>(mean[0] * inv_n), static_cast<float>(mean[1] * inv_n),
+                        static_cast<float>(mean[2] * inv_n), static_cast<float>(mean[3] * inv_n));
+    }
+}
+
+// Any n, d, stride and alignment: one thread per (token, k).
+__global__ __launch_bounds__(kBlock) void mhc_combine_scalar_kernel(const float* __restrict__ streams,
+                                                                    int64_t tokens, int n, int64_t d, int64_t sd,
+                                                                    int64_t ts, const float* __restrict__ res,
+                                                                    const float* __restrict__ post,
+                                                                    const float* __restrict__ out,
+                                                                    float* __restrict__ new_streams,
+                                                                    float* __restrict__ collapsed) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (idx >= tokens * d) return;
+    const int64_t token = idx / d;
+    const int64_t k = idx % d;
+    const double o = static_cast<double>(out[token * d + k]);
+    const float* s = streams + token * ts + k;
+    double mean = 0.0;
+    for (int i = 0; i < n; ++i) {
+        double acc = static_cast<double>(post[token * n + i]) * o;
+        for (int j = 0; j < n; ++j) {
+            acc = fma(static_cast<double>(res[(token * n + i) * n + j]), static_cast<double>(s[j * sd]), acc);
+        }
+        const float nv = static_cast<float>(acc);
+        if (new_streams != nullptr) new_streams[(token * n + i) * d + k] = nv;
+        mean += static_cast<double>(nv);
+    }
+    if (collapsed != nullptr) collapsed[token * d + k] = static_cast<float>(mean * (1.0 / static_cast<double>(n)));
+}
+
+mlk_status launch_combine(const float* streams, int64_t tokens, int64_t n, int64_t d, int64_t sd, int64_t ts,
+                          const float* res, const float* post, const float* out, float* new_streams,
+                          float* collapsed, hipStream_t stream) {
+    if (tokens == 0) return MLK_OK;
+    auto al16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool vec = d % 4 == 0 && sd % 4 == 0 && ts % 4 == 0 && al16(streams) && al16(out) && al16(new_streams) &&
+                     al16(collapsed) && n >= 1 && n <= 8;
+    if (vec) {
+        const int64_t blocks = ceil_div(tokens * (d / 4), kBlock);
+#define MLK_COMBINE(NN)                                                                                        \
+    case NN:                                                                                                   \
+        hipLaunchKernelGGL(mhc_combine_vec_kernel<NN>, dim3(blocks), dim3(kBlock), 0, stream, streams, tokens, d, \
+                           sd, ts, res, post, out, new_streams, collapsed);                                    \
+        break;
+        switch (n) {
+            MLK_COMBINE(1)
+            MLK_COMBINE(2)
+            MLK_COMBINE(3)
+            MLK_COMBINE(4)
+            MLK_COMBINE(5)
+            MLK_COMBINE(6)
+            MLK_COMBINE(7)
+            MLK_COMBINE(8)
+            default: break;
+        }
+#undef MLK_COMBINE
+        return launch_status("mhc_combine");
+    }
+    const int64_t blocks = ceil_div(tokens * d, kBlock);
+    hipLaunchKernelGGL(mhc_combine_scalar_kernel, dim3(blocks), dim3(kBlock), 0, stream, streams, tokens,
+                       static_cast<int>(n), d, sd, ts, res, post, out, new_streams, collapsed);
+    return launch_status("mhc_combine");
+}
+
+mlk_status launch_prepare(const PrepareArgs& a, int64_t n, int64_t d, hipStream_t stream) {
+    if (a.tokens == 0) return MLK_OK;
+    const bool fast = n == 4 && (d == 64 || d == 128 || d == 256 || d == 512);
+    if (fast) {
+        const int64_t blocks = ceil_div(a.tokens, 16);
+        switch (d) {
+            case 64:
+                hipLaunchKernelGGL(mhc_prepare_n4_kernel<64>, dim3(blocks), dim3(kBlock), 0, stream, a);
+                break;
+            case 128:
+                hipLaunchKernelGGL(mhc_prepare_n4_kernel<128>, dim3(blocks), dim3(kBlock), 0, stream, a);
+                break;
+            case 256:
+                hipLaunchKernelGGL(mhc_prepare_n4_kernel<256>, dim3(blocks), dim3(kBlock), 0, stream, a);
+                break;
+            default:
+                hipLaunchKernelGGL(mhc_prepare_n4_kernel<512>, dim3(blocks), dim3(kBlock), 0, stream, a);
+                break;
+        }
+        return launch_status("mhc_prepare");
+    }
+    GenericArgs g{a, static_cast<int>(n), d};
+    const size_t shmem = sizeof(double) * static_cast<size_t>(d + 2 * n + 2 * n * n + n) + sizeof(float) * (d + n);
+    if (shmem > 64 * 1024) {
+        set_error("mhc_prepare: d too large for the generic path");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL(mhc_prepare_generic_kernel, dim3(a.tokens), dim3(kWave), shmem, stream, g);
+    return launch_status("mhc_prepare");
+}
+
+mlk_status check_prepare(int64_t tokens, int64_t n, int64_t d, const double* proj_w, int64_t iters) {
+    MLK_CHECK(n > 0 && d > 0, "streams must be non-empty");
+    MLK_CHECK(iters >= 0, "sinkhorn_iters must be non-negative");
+    MLK_CHECK(tokens >= 0, "streams must be [B,L,n,d] or a broadcast [B,L,d]");
+    MLK_CHECK(tokens == 0 || proj_w != nullptr, "proj_w must be [2n + n*n, d]");
+    return MLK_OK;
+}
+
+}  // namespace
+}  // namespace mlk
+
+using namespace mlk;
+
+extern "C" {
+
+mlk_status mlk_mhc_prepare(const float* streams, int64_t tokens, int64_t n, int64_t d, int64_t stream_stride,
+                           int64_t token_stride, const float* norm_w, double eps, const double* proj_w,
+                           const float* pre_bias, const float* post_bias, const float* res_bias,
+                           const float* pre_alpha, const float* post_alpha, const float* res_alpha,
+                           int64_t sinkhorn_iters, const float* agg_norm_w, double agg_norm_eps, float* agg,
+                           float* pre, float* post, float* res, mlk_stream_t stream) {
+    const mlk_status st = check_prepare(tokens, n, d, proj_w, sinkhorn_iters);
+    if (st != MLK_OK) return st;
+    PrepareArgs a{};
+    a.streams = streams;
+    a.tokens = tokens;
+    a.sd = stream_stride;
+    a.ts = token_stride;
+    a.norm_w = norm_w;
+    a.eps = static_cast<double>(static_cast<float>(eps));
+    a.proj_w = proj_w;
+    a.pre_bias = pre_bias;
+    a.post_bias = post_bias;
+    a.res_bias = res_bias;
+    a.pre_alpha = pre_alpha;
+    a.post_alpha = post_alpha;
+    a.res_alpha = res_alpha;
+    a.iters = static_cast<int>(sinkhorn_iters < (1 << 20) ? sinkhorn_iters : (1 << 20));
+    a.agg_norm_w = agg_norm_w;
+    a.agg_norm_eps = static_cast<double>(static_cast<float>(agg_norm_eps));
+    a.agg = agg;
+    a.pre = pre;
+    a.post = post;
+    a.res = res;
+    return launch_prepare(a, n, d, stream);
+}
+
+mlk_status mlk_mhc_combine(const float* streams, int64_t tokens, int64_t n, int64_t d, int64_t stream_stride,
+                           int64_t token_stride, const float* res, const float* post, const float* out,
+                           float* new_streams, float* collapsed, mlk_stream_t stream) {
+    MLK_CHECK(n > 0 && d > 0, "streams must be non-empty");
+    MLK_CHECK(new_streams != nullptr || collapsed != nullptr, "mhc_combine needs an output");
+    return launch_combine(streams, tokens, n, d, stream_stride, token_stride, res, post, out, new_streams, collapsed,
+                          stream);
+}
+
+mlk_status mlk_mhc_combine_prepare(const float* streams, int64_t tokens, int64_t n, int64_t d,
+                                   int64_t stream_stride, int64_t token_stride, const float* res, const float* post,
+                                   const float* out, const float* norm_w, double eps, const double* proj_w,
+                                   const float* pre_bias, const float* post_bias, const float* res_bias,
+                                   const float* pre_alpha, const float* post_alpha, const float* res_alpha,
+                                   int64_t sinkhorn_iters, const float* agg_norm_w, double agg_norm_eps,
+                                   float* new_streams, float* agg_out, float* pre_out, float* post_out,
+                                   float* res_out, mlk_stream_t stream) {
+    MLK_CHECK(new_streams != nullptr || tokens == 0, "new_streams must be given");
+    mlk_status st = check_prepare(tokens, n, d, proj_w, sinkhorn_iters);
+    if (st != MLK_OK) return st;
+    st = launch_combine(streams, tokens, n, d, stream_stride, token_stride, res, post, out, new_streams, nullptr,
+                        stream);
+    if (st != MLK_OK) return st;
+    return mlk_mhc_prepare(new_streams, tokens, n, d, d, n * d, norm_w, eps, proj_w, pre_bias, post_bias, res_bias,
+                           pre_alpha, post_alpha, res_alpha, sinkhorn_iters, agg_norm_w, agg_norm_eps, agg_out,
+                           pre_out, post_out, res_out, stream);
+}
+
+}  // extern "C"

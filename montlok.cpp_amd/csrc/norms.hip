@@ -1,0 +1,320 @@
+// Row-wise layers of the RDT4quant path on gfx950: RMSNorm / GroupedRMSNorm,
+// add + RMSNorm, LayerNorm and the SwiGLU gate.
+//
+// Semantics (reference rdt4quant_cpu/montlok_layers.h): every intermediate is
+// evaluated in double and the output rounded to float32 once; eps is the
+// Python float cast through float32 (montlok.cpp:932, :1000, :1076).
+//   RMSNorm   out = (x * (1 / sqrt(sum(x^2) / gs + eps))) * w   per group of gs
+//   LayerNorm out = ((x - mean) * (1 / sqrt(var + eps))) * w + b (biased var)
+//   SwiGLU    out = (g / (1 + exp(-g))) * u
+// The squares of fp32 inputs are exact in double, so the RMSNorm result does
+// not depend on the summation order except through the final rounding of the
+// double sum.
+//
+// Mapping: a group of `gs` floats is held by LPG lanes (a power of two up to
+// 64), each lane owning CPL float4 chunks; the group sum is a butterfly over
+// the LPG lanes. One 256-thread block covers 256 / LPG groups. Rows whose
+// group size, stride or alignment do not allow float4 access fall back to a
+// one-wave-per-group kernel with scalar loads. All kernels are HBM-bound:
+// algorithmic traffic is one read of x (and w, from cache) and one write.
+#include "mlk_common.h"
+
+namespace mlk {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int LPG, int CPL, bool ADD>
+__global__ __launch_bounds__(kBlock) void rms_norm_vec_kernel(const float* __restrict__ x,
+                                                              const float* __restrict__ right,
+                                                              const float* __restrict__ w, int64_t total_groups,
+                                                              int64_t groups, int64_t gs, int64_t dim,
+                                                              int64_t row_stride, double eps,
+                                                              float* __restrict__ residual, float* __restrict__ out) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * (kBlock / LPG) + threadIdx.x / LPG;
+    const int li = threadIdx.x % LPG;
+    const bool active = gid < total_groups;
+    const int64_t row = active ? gid / groups : 0;
+    const int64_t g = active ? gid % groups : 0;
+    const float* xg = x + row * row_stride + g * gs;
+    float4 v[CPL];
+    double sumsq = 0.0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int64_t off = static_cast<int64_t>(c * LPG + li) * 4;
+        if (active) {
+            v[c] = *reinterpret_cast<const float4*>(xg + off);
+            if constexpr (ADD) {
+                const float4 r = *reinterpret_cast<const float4*>(right + row * row_stride + g * gs + off);
+                v[c].x += r.x;
+                v[c].y += r.y;
+                v[c].z += r.z;
+                v[c].w += r.w;
+                *reinterpret_cast<float4*>(residual + row * dim + g * gs + off) = v[c];
+            }
+        } else {
+            v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const double a = v[c].x, b = v[c].y, cc = v[c].z, d = v[c].w;
+        sumsq += (a * a + b * b) + (cc * cc + d * d);
+    }
+    sumsq = group_sum_d<LPG>(sumsq);
+    if (!active) return;
+    const double scale = 1.0 / sqrt(sumsq / static_cast<double>(gs) + eps);
+    const float* wg = w + g * gs;
+    float* og = out + row * dim + g * gs;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int64_t off = static_cast<int64_t>(c * LPG + li) * 4;
+        const float4 wv = *reinterpret_cast<const float4*>(wg + off);
+        float4 o;
+        o.x = static_cast<float>((static_cast<double>(v[c].x) * scale) * static_cast<double>(wv.x));
+        o.y = static_cast<float>((static_cast<double>(v[c].y) * scale) * static_cast<double>(wv.y));
+        o.z = static_cast<float>((static_cast<double>(v[c].z) * scale) * static_cast<double>(wv.z));
+        o.w = static_cast<float>((static_cast<double>(v[c].w) * scale) * static_cast<double>(wv.w));
+        *reinterpret_cast<float4*>(og + off) = o;
+    }
+}
+
+// One wave per group, scalar loads: any group size, stride and alignment.
+template <bool ADD>
+__global__ __launch_bounds__(kBlock) void rms_norm_scalar_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ right,
+                                                                 const float* __restrict__ w, int64_t total_groups,
+                                                                 int64_t groups, int64_t gs, int64_t dim,
+                                                                 int64_t row_stride, double eps,
+                                                                 float* __restrict__ residual,
+                                                                 float* __restrict__ out) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (gid >= total_groups) return;  // whole waves exit together
+    const int64_t row = gid / groups;
+    const int64_t g = gid % groups;
+    const float* xg = x + row * row_stride + g * gs;
+    double sumsq = 0.0;
+    for (int64_t k = lane; k < gs; k += kWave) {
+        float v = xg[k];
+        if constexpr (ADD) {
+            v += right[row * row_stride + g * gs + k];
+            residual[row * dim + g * gs + k] = v;
+        }
+        sumsq += static_cast<double>(v) * static_cast<double>(v);
+    }
+    sumsq = group_sum_d<kWave>(sumsq);
+    const double scale = 1.0 / sqrt(sumsq / static_cast<double>(gs) + eps);
+    for (int64_t k = lane; k < gs; k += kWave) {
+        float v = xg[k];
+        if constexpr (ADD) v += right[row * row_stride + g * gs + k];
+        out[row * dim + g * gs + k] =
+            static_cast<float>((static_cast<double>(v) * scale) * static_cast<double>(w[g * gs + k]));
+    }
+}
+
+template <bool ADD>
+mlk_status launch_rms(const float* x, const float* right, const float* w, int64_t rows, int64_t dim,
+                      int64_t row_stride, double eps, int64_t groups, float* residual, float* out,
+                      hipStream_t stream) {
+    const int64_t gs = dim / groups;
+    const int64_t total = rows * groups;
+    if (total == 0) return MLK_OK;
+    const double eps_f = static_cast<double>(static_cast<float>(eps));
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(out) % 16 == 0) && row_stride % 4 == 0 && gs % 4 == 0 &&
+                         (!ADD || (reinterpret_cast<uintptr_t>(right) % 16 == 0 &&
+                                   reinterpret_cast<uintptr_t>(residual) % 16 == 0));
+    const int64_t chunks = gs / 4;
+#define MLK_RMS_VEC(LPG, CPL)                                                                                \
+    do {                                                                                                     \
+        const int64_t blocks = ceil_div(total, kBlock / (LPG));                                              \
+        hipLaunchKernelGGL((rms_norm_vec_kernel<LPG, CPL, ADD>), dim3(blocks), dim3(kBlock), 0, stream, x,   \
+                           right, w, total, groups, gs, dim, row_stride, eps_f, residual, out);              \
+        return launch_status("rms_norm");                                                                    \
+    } while (0)
+    if (aligned) {
+        switch (chunks) {
+            case 1: MLK_RMS_VEC(1, 1);
+            case 2: MLK_RMS_VEC(2, 1);
+            case 4: MLK_RMS_VEC(4, 1);
+            case 8: MLK_RMS_VEC(8, 1);
+            case 16: MLK_RMS_VEC(16, 1);
+            case 32: MLK_RMS_VEC(32, 1);
+            case 64: MLK_RMS_VEC(64, 1);
+            case 128: MLK_RMS_VEC(64, 2);
+            case 256: MLK_RMS_VEC(64, 4);
+            default: break;
+        }
+    }
+#undef MLK_RMS_VEC
+    const int64_t blocks = ceil_div(total, kBlock / kWave);
+    hipLaunchKernelGGL((rms_norm_scalar_kernel<ADD>), dim3(blocks), dim3(kBlock), 0, stream, x, right, w, total,
+                       groups, gs, dim, row_stride, eps_f, residual, out);
+    return launch_status("rms_norm");
+}
+
+// LayerNorm: one wave per row, the row held in registers as float4 chunks
+// when possible (two passes over registers: mean, then centred squares).
+template <int CPL>
+__global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ bias, int64_t rows,
+                                                                int64_t dim, int64_t row_stride, double eps,
+                                                                float* __restrict__ out) {
+    // LPG lanes per row: dim = 4 * CPL * LPG with LPG = 64 / rows-per-wave.
+    const int lpg = static_cast<int>(dim / (4 * CPL));
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / lpg) + threadIdx.x / lpg;
+    const int li = threadIdx.x % lpg;
+    const bool active = row < rows;
+    const float* xr = x + (active ? row : 0) * row_stride;
+    float4 v[CPL];
+    double sum = 0.0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        v[c] = active ? *reinterpret_cast<const float4*>(xr + (c * lpg + li) * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        sum += (static_cast<double>(v[c].x) + static_cast<double>(v[c].y)) +
+               (static_cast<double>(v[c].z) + static_cast<double>(v[c].w));
+    }
+    for (int mask = lpg / 2; mask > 0; mask >>= 1) sum += shfl_xor_d(sum, mask);
+    const double inv_dim = 1.0 / static_cast<double>(dim);
+    const double mean = sum * inv_dim;
+    double sumsq = 0.0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const double a = static_cast<double>(v[c].x) - mean, b = static_cast<double>(v[c].y) - mean;
+        const double cc = static_cast<double>(v[c].z) - mean, d = static_cast<double>(v[c].w) - mean;
+        sumsq += (a * a + b * b) + (cc * cc + d * d);
+    }
+    for (int mask = lpg / 2; mask > 0; mask >>= 1) sumsq += shfl_xor_d(sumsq, mask);
+    if (!active) return;
+    const double rstd = 1.0 / sqrt(fma(sumsq, inv_dim, eps));
+    float* outr = out + row * dim;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int off = (c * lpg + li) * 4;
+        const float4 wv = *reinterpret_cast<const float4*>(w + off);
+        float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (bias != nullptr) bv = *reinterpret_cast<const float4*>(bias + off);
+        float4 o;
+        o.x = static_cast<float>(((static_cast<double>(v[c].x) - mean) * rstd) * wv.x + static_cast<double>(bv.x));
+        o.y = static_cast<float>(((static_cast<double>(v[c].y) - mean) * rstd) * wv.y + static_cast<double>(bv.y));
+        o.z = static_cast<float>(((static_cast<double>(v[c].z) - mean) * rstd) * wv.z + static_cast<double>(bv.z));
+        o.w = static_cast<float>(((static_cast<double>(v[c].w) - mean) * rstd) * wv.w + static_cast<double>(bv.w));
+        *reinterpret_cast<float4*>(outr + off) = o;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void layer_norm_scalar_kernel(const float* __restrict__ x,
+                                                                   const float* __restrict__ w,
+                                                                   const float* __restrict__ bias, int64_t rows,
+                                                                   int64_t dim, int64_t row_stride, double eps,
+                                                                   float* __restrict__ out) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (row >= rows) return;
+    const float* xr = x + row * row_stride;
+    double sum = 0.0;
+    for (int64_t k = lane; k < dim; k += kWave) sum += static_cast<double>(xr[k]);
+    sum = group_sum_d<kWave>(sum);
+    const double inv_dim = 1.0 / static_cast<double>(dim);
+    const double mean = sum * inv_dim;
+    double sumsq = 0.0;
+    for (int64_t k = lane; k < dim; k += kWave) {
+        const double a = static_cast<double>(xr[k]) - mean;
+        sumsq += a * a;
+    }
+    sumsq = group_sum_d<kWave>(sumsq);
+    const double rstd = 1.0 / sqrt(fma(sumsq, inv_dim, eps));
+    for (int64_t k = lane; k < dim; k += kWave) {
+        double y = ((static_cast<double>(xr[k]) - mean) * rstd) * static_cast<double>(w[k]);
+        if (bias != nullptr) y += static_cast<double>(bias[k]);
+        out[row * dim + k] = static_cast<float>(y);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void swiglu_kernel(const float* __restrict__ x, int64_t rows, int64_t hidden,
+                                                        int64_t row_stride, float* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= rows * hidden) return;
+    const int64_t row = i / hidden;
+    const int64_t k = i % hidden;
+    const double z = static_cast<double>(x[row * row_stride + k]);
+    const double u = static_cast<double>(x[row * row_stride + hidden + k]);
+    out[i] = static_cast<float>((z / (1.0 + exp(-z))) * u);
+}
+
+}  // namespace
+}  // namespace mlk
+
+using namespace mlk;
+
+extern "C" {
+
+mlk_status mlk_rms_norm(const float* x, int64_t rows, int64_t dim, int64_t row_stride, const float* weight,
+                        double eps, int64_t groups, float* out, mlk_stream_t stream) {
+    MLK_CHECK(rows >= 0 && dim >= 1, "x must have at least one dimension");
+    MLK_CHECK(groups > 0 && dim % groups == 0, "groups must divide the normalised dimension");
+    MLK_CHECK(rows == 0 || (x != nullptr && weight != nullptr && out != nullptr), "null tensor pointer");
+    MLK_CHECK(row_stride >= dim || rows <= 1, "x rows overlap");
+    return launch_rms<false>(x, nullptr, weight, rows, dim, row_stride, eps, groups, nullptr, out, stream);
+}
+
+mlk_status mlk_add_rms_norm(const float* left, const float* right, int64_t rows, int64_t dim, const float* weight,
+                            double eps, int64_t groups, float* residual, float* normalized, mlk_stream_t stream) {
+    MLK_CHECK(rows >= 0 && dim >= 1, "residual operands must have the same shape");
+    MLK_CHECK(groups > 0 && dim % groups == 0, "groups must divide the normalized dimension");
+    MLK_CHECK(rows == 0 || (left && right && weight && residual && normalized), "null tensor pointer");
+    return launch_rms<true>(left, right, weight, rows, dim, dim, eps, groups, residual, normalized, stream);
+}
+
+mlk_status mlk_layer_norm(const float* x, int64_t rows, int64_t dim, int64_t row_stride, const float* weight,
+                          const float* bias, double eps, float* out, mlk_stream_t stream) {
+    MLK_CHECK(rows >= 0 && dim >= 1, "x must have at least one dimension");
+    MLK_CHECK(rows == 0 || (x != nullptr && weight != nullptr && out != nullptr), "null tensor pointer");
+    if (rows == 0) return MLK_OK;
+    const double eps_f = static_cast<double>(static_cast<float>(eps));
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                         (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0) && row_stride % 4 == 0;
+    // dim = 4 * CPL * lpg with lpg a power of two <= 64.
+    int cpl = 0;
+    if (aligned && dim % 4 == 0) {
+        const int64_t chunks = dim / 4;
+        if (chunks <= 64 && (chunks & (chunks - 1)) == 0) cpl = 1;
+        else if (chunks == 128) cpl = 2;
+        else if (chunks == 256) cpl = 4;
+    }
+    if (cpl > 0) {
+        const int lpg = static_cast<int>(dim / (4 * cpl));
+        const int64_t blocks = ceil_div(rows, kBlock / lpg);
+        switch (cpl) {
+            case 1:
+                hipLaunchKernelGGL(layer_norm_vec_kernel<1>, dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias,
+                                   rows, dim, row_stride, eps_f, out);
+                break;
+            case 2:
+                hipLaunchKernelGGL(layer_norm_vec_kernel<2>, dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias,
+                                   rows, dim, row_stride, eps_f, out);
+                break;
+            default:
+                hipLaunchKernelGGL(layer_norm_vec_kernel<4>, dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias,
+                                   rows, dim, row_stride, eps_f, out);
+                break;
+        }
+        return launch_status("layer_norm");
+    }
+    const int64_t blocks = ceil_div(rows, kBlock / kWave);
+    hipLaunchKernelGGL(layer_norm_scalar_kernel, dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias, rows, dim,
+                       row_stride, eps_f, out);
+    return launch_status("layer_norm");
+}
+
+mlk_status mlk_swiglu(const float* x, int64_t rows, int64_t hidden, int64_t row_stride, float* out,
+                      mlk_stream_t stream) {
+    MLK_CHECK(rows >= 0 && hidden >= 1, "x must end in an even dimension [gate | up]");
+    MLK_CHECK(rows == 0 || (x != nullptr && out != nullptr), "null tensor pointer");
+    if (rows == 0) return MLK_OK;
+    const int64_t blocks = ceil_div(rows * hidden, kBlock);
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(kBlock), 0, stream, x, rows, hidden, row_stride, out);
+    return launch_status("swiglu");
+}
+
+}  // extern "C"

@@ -1,0 +1,313 @@
+"""GPU operators of the RDT4quant fused forward, under the names of ``montlok._C``.
+
+The reference exposes these operators from a pybind11 CPU extension
+(rdt4quant_cpu/montlok.cpp, op table at montlok.cpp:1457-1499). This module
+keeps their names, positional/keyword order, return tuples and error texts,
+and runs them on the ROCm device through the C ABI of ``libmlk_hip.so``
+(``include/mlk_hip.h``). Inputs must be float32 tensors on the GPU; outputs
+are allocated here with the caching allocator and filled on the current
+stream. There is no CPU fallback: a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import json
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "rdt" / "lib" / "libmlk_hip.so"
+
+_vp = C.c_void_p
+_i64 = C.c_int64
+_dbl = C.c_double
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("MLK_HIP_LIB", LIB_PATH))
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built: run __graft_entry__.build() (make -C montlok.cpp_amd)")
+    lib = C.CDLL(str(path))
+    lib.mlk_last_error.restype = C.c_char_p
+    lib.mlk_abi_version.restype = C.c_int
+    lib.mlk_build_info.argtypes = [C.c_char_p, C.c_size_t]
+    sigs = {
+        "mlk_rms_norm": [_vp, _i64, _i64, _i64, _vp, _dbl, _i64, _vp, _vp],
+        "mlk_add_rms_norm": [_vp, _vp, _i64, _i64, _vp, _dbl, _i64, _vp, _vp, _vp],
+        "mlk_layer_norm": [_vp, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp],
+        "mlk_swiglu": [_vp, _i64, _i64, _i64, _vp, _vp],
+        "mlk_mhc_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                            _vp, _dbl, _vp, _vp, _vp, _vp, _vp],
+        "mlk_mhc_combine": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp],
+        "mlk_mhc_combine_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _dbl, _vp, _vp, _vp, _vp,
+                                    _vp, _vp, _vp, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp],
+    }
+    for name, args in sigs.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = C.c_int
+    _lib = lib
+    return lib
+
+
+def library():
+    """The loaded ``libmlk_hip.so`` (ctypes.CDLL)."""
+    return _load()
+
+
+def _call(name: str, *args) -> None:
+    lib = _load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        raise RuntimeError(lib.mlk_last_error().decode())
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+# Validation mirrors montlok.cpp:43-65 with "on the GPU" in place of "on CPU".
+def _require_f32_gpu(t: torch.Tensor | None, name: str) -> None:
+    _check(t is not None, f"{name} must be defined")
+    _check(t.device.type == "cuda", f"{name} must be on the GPU")
+    _check(t.dtype == torch.float32, f"{name} must be float32")
+
+
+def _dense_parameter(t: torch.Tensor, numel: int, name: str) -> torch.Tensor:
+    _require_f32_gpu(t, name)
+    _check(t.numel() == numel, f"{name} must have {numel} elements, got {t.numel()}")
+    return t.contiguous()
+
+
+def _rows(x: torch.Tensor, dim: int) -> tuple[torch.Tensor, int, int]:
+    """[..., dim] -> (2-D view, rows, row stride), like x.reshape(-1, dim) (montlok.cpp:921-924)."""
+    rows = x.reshape(-1, dim)
+    if rows.stride(1) != 1 and dim != 1:
+        rows = rows.contiguous()
+    stride = rows.stride(0) if rows.size(0) > 1 else dim
+    return rows, rows.size(0), stride
+
+
+# ------------------------------------------------------------------ norms
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, groups: int) -> torch.Tensor:
+    """montlok.cpp:915-938."""
+    _require_f32_gpu(x, "x")
+    _check(x.dim() >= 1, "x must have at least one dimension")
+    dim = x.size(-1)
+    _check(groups > 0 and dim % groups == 0, "groups must divide the normalised dimension")
+    w = _dense_parameter(weight, dim, "weight")
+    rows, count, stride = _rows(x, dim)
+    out = torch.empty((count, dim), dtype=torch.float32, device=x.device)
+    _call("mlk_rms_norm", _ptr(rows), count, dim, stride, _ptr(w), float(eps), int(groups), _ptr(out), _stream())
+    return out.view(x.shape)
+
+
+def add_rms_norm(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor, eps: float,
+                 groups: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """montlok.cpp:978-1007: (left + right, rms_norm(left + right))."""
+    _require_f32_gpu(left, "left")
+    _require_f32_gpu(right, "right")
+    _check(left.shape == right.shape and left.dim() >= 1, "residual operands must have the same shape")
+    dim = left.size(-1)
+    _check(groups > 0 and dim % groups == 0, "groups must divide the normalized dimension")
+    lr = left.reshape(-1, dim).contiguous()
+    rr = right.reshape(-1, dim).contiguous()
+    w = _dense_parameter(weight, dim, "weight")
+    residual = torch.empty_like(lr)
+    normalized = torch.empty_like(lr)
+    _call("mlk_add_rms_norm", _ptr(lr), _ptr(rr), lr.size(0), dim, _ptr(w), float(eps), int(groups), _ptr(residual),
+          _ptr(normalized), _stream())
+    return residual.view(left.shape), normalized.view(left.shape)
+
+
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """montlok.cpp:1057-1082 (bias may be None or empty)."""
+    _require_f32_gpu(x, "x")
+    _check(x.dim() >= 1, "x must have at least one dimension")
+    dim = x.size(-1)
+    w = _dense_parameter(weight, dim, "weight")
+    b = None
+    if bias is not None and bias.numel() > 0:
+        b = _dense_parameter(bias, dim, "bias")
+    rows, count, stride = _rows(x, dim)
+    out = torch.empty((count, dim), dtype=torch.float32, device=x.device)
+    _call("mlk_layer_norm", _ptr(rows), count, dim, stride, _ptr(w), _ptr(b), float(eps), _ptr(out), _stream())
+    return out.view(x.shape)
+
+
+def swiglu(x: torch.Tensor) -> torch.Tensor:
+    """montlok.cpp:942-963: x [..., 2*hidden] = [gate | up] -> silu(gate) * up."""
+    _require_f32_gpu(x, "x")
+    _check(x.dim() >= 1 and x.size(-1) % 2 == 0, "x must end in an even dimension [gate | up]")
+    width = x.size(-1)
+    hidden = width // 2
+    rows, count, stride = _rows(x, width)
+    out = torch.empty((count, hidden), dtype=torch.float32, device=x.device)
+    _call("mlk_swiglu", _ptr(rows), count, hidden, stride, _ptr(out), _stream())
+    return out.view(*x.shape[:-1], hidden)
+
+
+# ------------------------------------------------------------------ mHC
+
+
+def _streams_view(streams: torch.Tensor, n_streams: int, name: str):
+    """montlok.cpp:535-557 (StreamsView): [B,L,n,d] or the broadcast [B,L,d] backbone."""
+    _require_f32_gpu(streams, name)
+    _check(streams.is_contiguous(), f"{name} must be contiguous")
+    if streams.dim() == 4:
+        n, d = streams.size(2), streams.size(3)
+        sd = d
+        _check(n_streams <= 0 or n_streams == n, f"{name} has {n} streams, expected {n_streams}")
+    else:
+        _check(streams.dim() == 3, f"{name} must be [B,L,n,d] or a broadcast [B,L,d]")
+        _check(n_streams > 0, f"n_streams is required for a broadcast [B,L,d] {name}")
+        n, d = n_streams, streams.size(2)
+        sd = 0
+    B, L = streams.size(0), streams.size(1)
+    ts = d if sd == 0 else n * d
+    _check(n > 0 and d > 0, f"{name} must be non-empty")
+    return B, L, n, d, sd, ts
+
+
+def _scalar(t: torch.Tensor, name: str) -> torch.Tensor:
+    _require_f32_gpu(t, name)
+    _check(t.numel() == 1, f"{name} must be a scalar")
+    return t.reshape(1).contiguous()
+
+
+def _prepare_params(n, d, norm_w, proj_w, pre_bias, post_bias, res_bias, pre_alpha, post_alpha, res_alpha,
+                    sinkhorn_iters, agg_norm_w):
+    """montlok.cpp:568-649 (mhc_prepare_plan)."""
+    _check(sinkhorn_iters >= 0, "sinkhorn_iters must be non-negative")
+    params = [
+        _dense_parameter(norm_w, d, "dyn_norm.weight"),
+        _dense_parameter(pre_bias, n, "pre_bias"),
+        _dense_parameter(post_bias, n, "post_bias"),
+        _dense_parameter(res_bias, n * n, "res_bias"),
+    ]
+    _check(proj_w.device.type == "cuda" and proj_w.dtype == torch.float64 and proj_w.is_contiguous(),
+           "proj_w must be a contiguous float64 GPU tensor")
+    _check(proj_w.dim() == 2 and proj_w.size(0) == 2 * n + n * n and proj_w.size(1) == d,
+           "proj_w must be [2n + n*n, d]")
+    alphas = [_scalar(pre_alpha, "pre_alpha"), _scalar(post_alpha, "post_alpha"), _scalar(res_alpha, "res_alpha")]
+    anw = None
+    if agg_norm_w is not None and agg_norm_w.numel() > 0:
+        anw = _dense_parameter(agg_norm_w, d, "agg_norm_w")
+    return params, alphas, anw
+
+
+def mhc_prepare(streams, norm_w, eps, proj_w, pre_bias, post_bias, res_bias, pre_alpha, post_alpha, res_alpha,
+                sinkhorn_iters, n_streams=0, agg_norm_w=None, agg_norm_eps=0.0):
+    """montlok.cpp:659-691 -> (agg [B,L,d], pre [B,L,n], post [B,L,n], res [B,L,n,n])."""
+    B, L, n, d, sd, ts = _streams_view(streams, n_streams, "streams")
+    (nw, pb, qb, rb), (pa, qa, ra), anw = _prepare_params(n, d, norm_w, proj_w, pre_bias, post_bias, res_bias,
+                                                          pre_alpha, post_alpha, res_alpha, sinkhorn_iters,
+                                                          agg_norm_w)
+    dev = streams.device
+    agg = torch.empty((B, L, d), dtype=torch.float32, device=dev)
+    pre = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+    post = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+    res = torch.empty((B, L, n, n), dtype=torch.float32, device=dev)
+    _call("mlk_mhc_prepare", _ptr(streams), B * L, n, d, sd, ts, _ptr(nw), float(eps), _ptr(proj_w), _ptr(pb),
+          _ptr(qb), _ptr(rb), _ptr(pa), _ptr(qa), _ptr(ra), int(sinkhorn_iters), _ptr(anw), float(agg_norm_eps),
+          _ptr(agg), _ptr(pre), _ptr(post), _ptr(res), _stream())
+    return agg, pre, post, res
+
+
+def _combine_inputs(streams, res, post, out):
+    B, L, n, d, sd, ts = _streams_view(streams, res.size(-1) if res.dim() == 4 else 0, "streams")
+    _require_f32_gpu(res, "res")
+    _require_f32_gpu(post, "post")
+    _require_f32_gpu(out, "out")
+    _check(tuple(res.shape) == (B, L, n, n) and res.is_contiguous(), "res must be contiguous [B,L,n,n]")
+    _check(tuple(post.shape) == (B, L, n) and post.is_contiguous(), "post must be contiguous [B,L,n]")
+    _check(tuple(out.shape) == (B, L, d) and out.is_contiguous(), "out must be contiguous [B,L,d]")
+    return B, L, n, d, sd, ts
+
+
+def mhc_combine(streams, res, post, out):
+    """montlok.cpp:726-739 -> new streams [B,L,n,d]."""
+    B, L, n, d, sd, ts = _combine_inputs(streams, res, post, out)
+    new = torch.empty((B, L, n, d), dtype=torch.float32, device=streams.device)
+    _call("mlk_mhc_combine", _ptr(streams), B * L, n, d, sd, ts, _ptr(res), _ptr(post), _ptr(out), _ptr(new), None,
+          _stream())
+    return new
+
+
+def mhc_combine_collapse(streams, res, post, out):
+    """montlok.cpp:743-758 -> mean over the new streams [B,L,d]; streams never materialised."""
+    B, L, n, d, sd, ts = _combine_inputs(streams, res, post, out)
+    hidden = torch.empty((B, L, d), dtype=torch.float32, device=streams.device)
+    _call("mlk_mhc_combine", _ptr(streams), B * L, n, d, sd, ts, _ptr(res), _ptr(post), _ptr(out), None,
+          _ptr(hidden), _stream())
+    return hidden
+
+
+def mhc_combine_prepare(streams, res, post, out, norm_w, eps, proj_w, pre_bias, post_bias, res_bias, pre_alpha,
+                        post_alpha, res_alpha, sinkhorn_iters, agg_norm_w=None, agg_norm_eps=0.0):
+    """montlok.cpp:763-802 -> (new_streams, agg, pre, post, res) of the next residual."""
+    B, L, n, d, sd, ts = _combine_inputs(streams, res, post, out)
+    (nw, pb, qb, rb), (pa, qa, ra), anw = _prepare_params(n, d, norm_w, proj_w, pre_bias, post_bias, res_bias,
+                                                          pre_alpha, post_alpha, res_alpha, sinkhorn_iters,
+                                                          agg_norm_w)
+    dev = streams.device
+    new = torch.empty((B, L, n, d), dtype=torch.float32, device=dev)
+    agg = torch.empty((B, L, d), dtype=torch.float32, device=dev)
+    pre_o = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+    post_o = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+    res_o = torch.empty((B, L, n, n), dtype=torch.float32, device=dev)
+    _call("mlk_mhc_combine_prepare", _ptr(streams), B * L, n, d, sd, ts, _ptr(res), _ptr(post), _ptr(out), _ptr(nw),
+          float(eps), _ptr(proj_w), _ptr(pb), _ptr(qb), _ptr(rb), _ptr(pa), _ptr(qa), _ptr(ra), int(sinkhorn_iters),
+          _ptr(anw), float(agg_norm_eps), _ptr(new), _ptr(agg), _ptr(pre_o), _ptr(post_o), _ptr(res_o), _stream())
+    return new, agg, pre_o, post_o, res_o
+
+
+# ------------------------------------------------------------------ introspection
+
+
+def build_info() -> dict:
+    """Kernel variant and device of this build (replaces montlok.cpp:1417-1455)."""
+    lib = _load()
+    buf = C.create_string_buffer(1024)
+    _call("mlk_build_info", buf, len(buf))
+    info = json.loads(buf.value.decode())
+    info["library"] = str(LIB_PATH)
+    return info
+
+
+def isa_variants() -> list[dict]:
+    """One kernel variant (gfx950); the reference lists its x86 ISA variants here."""
+    return [{"name": "gfx950", "supported": True, "fma": True}]
+
+
+def active_isa() -> str:
+    return "gfx950"
+
+
+def set_isa(name: str, force: bool = False) -> str:
+    if name not in ("gfx950", "auto"):
+        raise RuntimeError(f"unknown kernel variant {name!r}: this build has gfx950 only")
+    return "gfx950"
+
+
+def exported_symbols() -> list[str]:
+    """Names of the C ABI entry points this module binds."""
+    return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
+            "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare"]

@@ -187,7 +187,7 @@ class Oracle(_Lib):
                                _f32p, _dbl, _dbl, _f32p, _dbl, _f32p, _f32p, _f32p, _f32p, _f32p]
         L.orc_mamba3_siso_forward.argtypes = [_i64, _i64, _f32p, _i64, _i64] + [_i64] * 5 + [_f32p] * 4 + [
             _dbl, _dbl, _f32p, _f32p, _dbl, _f32p]
-        L.orc_mamba3_step.argtypes = [_i64, _f32p, _i64] + [_i64] * 4 + [_f32p] * 4 + [_dbl, _dbl, _f32p, _f32p,
+        L.orc_mamba3_step.argtypes = [_i64, _f32p, _i64] + [_i64] * 5 + [_f32p] * 4 + [_dbl, _dbl, _f32p, _f32p,
                                                                                       _dbl, _f32p, _f32p, _f32p,
                                                                                       _f64p, C.c_int, _f32p]
         L.orc_mhc_combine.argtypes = [_f32p, _i64, _i64, _f32p, _f32p, _f32p, _i64, _i64, _i64, _f32p, _f32p]

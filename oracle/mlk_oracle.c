@@ -304,12 +304,14 @@ void orc_siso(int64_t B, int64_t L, int64_t H, int64_t N, int64_t D, const float
 /* ------------------------------------------------------------------------ */
 
 /* BCNorm, fp32 throughout (montlok_kernel.h:464-474). The sum of squares is
- * sequential. In the compiled reference GCC vectorises the squares of the
- * first 8*floor(n/8) elements (8-float vectors, each square rounded before
- * the in-order add) and contracts the scalar remainder into fma. */
+ * sequential. In the compiled reference (AVX2 variant) GCC vectorises the
+ * squares of the first 4*floor(n/4) elements (8- then 4-float vectors, each
+ * square rounded before the in-order add) and contracts the scalar remainder
+ * into fma. (The reference's AVX-512 variant vectorises 8*floor(n/8); the two
+ * differ by an ulp when n mod 8 >= 4. n = 16 and 64 agree.) */
 static void bc_norm(const float* x, const float* w, float eps, int64_t n, float* out) {
     float ss = 0.0f;
-    const int64_t body = n - n % 8;
+    const int64_t body = n - n % 4;
     for (int64_t i = 0; i < body; ++i) ss = ss + x[i] * x[i];
     for (int64_t i = body; i < n; ++i) ss = fmaf(x[i], x[i], ss);
     const float scale = 1.0f / sqrtf(ss / (float)n + eps);
