@@ -87,12 +87,45 @@ def cpu_baseline_mhc(cfg: dict, budget_s: float = 12.0) -> dict:
         step()
         reps += 1
         elapsed = time.perf_counter() - t0
-        if elapsed >= budget_s or reps >= 2000:
+        if elapsed >= budget_s or reps >= 100000:
             break
     windows_per_s = reps * cfg["windows"] / elapsed
     return {"value": windows_per_s, "unit": "windows/s", "cores": threads, "kind": kind,
             "sample": f"{reps} full steps (prepare + combine, {T} tokens each) in {elapsed:.1f} s, "
                       f"{variant} build, {threads} OpenMP threads of {cores} host cores"}
+
+
+def _graph(fn_list):
+    """Capture the given launch closures, in order, into one HIP graph."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for fn in fn_list:
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in fn_list:
+            fn()
+    return g
+
+
+def _time_graph(g, replays: int) -> float:
+    """Milliseconds per replay, HIP events on the replay stream."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(replays):
+        g.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / replays
 
 
 def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
@@ -119,62 +152,54 @@ def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
     post = [torch.empty(W, L, n, device=dev) for _ in range(sets)]
     res = [torch.empty(W, L, n, n, device=dev) for _ in range(sets)]
     lib = _C.library()
-    stream = torch.cuda.current_stream()
-    sh = stream.cuda_stream
     ptr = lambda t: t.data_ptr()  # noqa: E731
-    args_prep = [(ptr(streams[i]), T, n, d, d, n * d, ptr(norm_w), 1e-5, ptr(proj_w), ptr(pre_b), ptr(post_b),
-                  ptr(res_b), ptr(alphas[0]), ptr(alphas[1]), ptr(alphas[2]), iters, None, 0.0, ptr(agg[i]),
-                  ptr(pre[i]), ptr(post[i]), ptr(res[i]), sh) for i in range(sets)]
-    args_comb = [(ptr(streams[i]), T, n, d, d, n * d, ptr(res[i]), ptr(post[i]), ptr(agg[i]), ptr(outs[i]), None, sh)
-                 for i in range(sets)]
-    prep_fn, comb_fn = lib.mlk_mhc_prepare, lib.mlk_mhc_combine
 
-    def step(i, ev=None):
-        a = i % sets
-        if ev is not None:
-            ev[0].record(stream)
-        if prep_fn(*args_prep[a]) != 0:
-            raise RuntimeError(lib.mlk_last_error().decode())
-        if ev is not None:
-            ev[1].record(stream)
-        if comb_fn(*args_comb[a]) != 0:
-            raise RuntimeError(lib.mlk_last_error().decode())
-        if ev is not None:
-            ev[2].record(stream)
+    def prepare(i):
+        def run():
+            st = lib.mlk_mhc_prepare(ptr(streams[i]), T, n, d, d, n * d, ptr(norm_w), 1e-5, ptr(proj_w), ptr(pre_b),
+                                     ptr(post_b), ptr(res_b), ptr(alphas[0]), ptr(alphas[1]), ptr(alphas[2]), iters,
+                                     None, 0.0, ptr(agg[i]), ptr(pre[i]), ptr(post[i]), ptr(res[i]),
+                                     torch.cuda.current_stream().cuda_stream)
+            if st != 0:
+                raise RuntimeError(lib.mlk_last_error().decode())
+        return run
 
-    # Correctness guard on the timed configuration (first set) before timing.
-    step(0)
-    torch.cuda.synchronize()
-    assert torch.isfinite(outs[0]).all().item()
+    def combine(i):
+        def run():
+            st = lib.mlk_mhc_combine(ptr(streams[i]), T, n, d, d, n * d, ptr(res[i]), ptr(post[i]), ptr(agg[i]),
+                                     ptr(outs[i]), None, torch.cuda.current_stream().cuda_stream)
+            if st != 0:
+                raise RuntimeError(lib.mlk_last_error().decode())
+        return run
 
-    for i in range(warmup):
-        step(i)
+    # Correctness guard on the timed configuration before timing: eager run,
+    # then the captured graph, bit-identical.
+    prepare(0)()
+    combine(0)()
     torch.cuda.synchronize()
-    # Whole-job throughput: K steps between two synchronisations, no events inside.
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        step(i)
-    stop.record(stream)
+    eager = outs[0].clone()
+    assert torch.isfinite(eager).all().item()
+    step_graph = _graph([f for i in range(sets) for f in (prepare(i), combine(i))])
+    prep_graph = _graph([prepare(i) for i in range(sets)])
+    comb_graph = _graph([combine(i) for i in range(sets)])
+    step_graph.replay()
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(stop)
-    # Per-kernel launch durations, HIP events on the kernels' stream.
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    for i in range(steps):
-        step(i, evs[i])
-    torch.cuda.synchronize()
-    prep_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
-    comb_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
-    # Warm-cache rate (one input set, Infinity-Cache resident) for reference.
-    start.record(stream)
-    for i in range(steps):
-        step(0)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    warm_ms = start.elapsed_time(stop) / steps
+    assert torch.equal(outs[0], eager), "graph replay differs from the eager step"
+
+    replays = max(1, steps // sets)
+    steps = replays * sets
+    for _ in range(max(1, warmup // sets)):
+        step_graph.replay()
+    # Timed region: `steps` steps (graph replays of 16 steps each) between two
+    # synchronisations.
+    ms_per_step = _time_graph(step_graph, replays) / sets
+    prep_ms = _time_graph(prep_graph, replays) / sets
+    comb_ms = _time_graph(comb_graph, replays) / sets
+    # Warm-cache rate: one input set over and over (Infinity-Cache resident).
+    warm_graph = _graph([f for _ in range(sets) for f in (prepare(0), combine(0))])
+    warm_ms = _time_graph(warm_graph, replays) / sets
 
     prep_bytes, comb_bytes = mhc_bytes(n, d, T)
-    ms_per_step = total_ms / steps
     windows_per_s = W / (ms_per_step * 1e-3)
     kernels = {"mhc_prepare": (prep_ms, prep_bytes), "mhc_combine": (comb_ms, comb_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0])
@@ -199,6 +224,7 @@ def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
         "data": "synthetic (seeded N(0,1) streams, random-init mHC weights)",
         "config": {"workload": "mhc_residual_mix", "n_streams": n, "d_model": d, "tokens": T, "windows": W,
                    "seq_len": L, "sinkhorn_iters": iters, "step": "mhc_prepare + identity fn + mhc_combine",
+                   "launch": "HIP graph of 16 steps over 16 independent input sets, replayed",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "algorithmic_bytes": dom_bytes,

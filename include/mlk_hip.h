@@ -119,6 +119,15 @@ mlk_status mlk_mhc_combine_prepare(const float* streams, int64_t tokens, int64_t
                                    float* new_streams, float* agg_out, float* pre_out, float* post_out,
                                    float* res_out, mlk_stream_t stream);
 
+/* --------------------------------------------------------- diagnostics -- */
+
+/* Evaluates the kernels' device math helpers on x[count] (float64):
+ * out[0:count] = exp, out[count:2count] = tanh, out[2count:3count] =
+ * sigmoid, out[3count:4count] = 1/x (for positive x). No reference operator;
+ * it plays the role of the reference self-test of its own polynomial exp
+ * (rdt4quant_cpu/montlok_selftest.cpp:770-790). */
+mlk_status mlk_math_check(const double* x, int64_t count, double* out, mlk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

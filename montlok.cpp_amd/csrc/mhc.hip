@@ -48,6 +48,31 @@ constexpr int kBlock = 256;
 
 __device__ __forceinline__ double sigmoid_d(double x) { return 1.0 / (1.0 + exp(-x)); }
 
+// DPP moves of a double (two 32-bit halves). Control words (GFX9 DPP):
+// quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_ror:4 = 0x124,
+// row_ror:8 = 0x128.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+
+// Sum over the 4 lanes of a quad (a row of a 4x4 matrix held one entry per
+// lane, entry e = 4i + j at lane e of a 16-lane group): (x0 + x1) + (x2 + x3)
+// by commutativity bit-identical in all four lanes.
+__device__ __forceinline__ double quad_sum(double v) {
+    const double s = v + dpp_d<0xB1>(v);
+    return s + dpp_d<0x4E>(s);
+}
+
+// Sum over lanes j, j+4, j+8, j+12 of a 16-lane group (a column of the
+// matrix): (m[i] + m[i+2]) + (m[i+1] + m[i+3]), identical in all four rows.
+__device__ __forceinline__ double column_sum(double v) {
+    const double s = v + dpp_d<0x128>(v);
+    return s + dpp_d<0x124>(s);
+}
+
 // ---------------------------------------------------------------------------
 // prepare, n = 4 fast path
 // ---------------------------------------------------------------------------
@@ -75,15 +100,41 @@ struct PrepareArgs {
     float* res;
 };
 
+// Values held by lanes (t, 0..3) of a wave, gathered into every lane of
+// token t with the gfx950 cross-row swaps: permlane16_swap pairs rows
+// (0,1) and (2,3), permlane32_swap then pairs the halves. Three VALU
+// operations per dword, no LDS traffic.
+__device__ __forceinline__ void gather_rows(double v, double x[4]) {
+    const int lo = __double2loint(v);
+    const int hi = __double2hiint(v);
+    const auto p_lo = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);  // {r0 r0 r2 r2}, {r1 r1 r3 r3}
+    const auto p_hi = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const auto e_lo = __builtin_amdgcn_permlane32_swap(p_lo[0], p_lo[0], false, false);  // {r0}, {r2}
+    const auto e_hi = __builtin_amdgcn_permlane32_swap(p_hi[0], p_hi[0], false, false);
+    const auto o_lo = __builtin_amdgcn_permlane32_swap(p_lo[1], p_lo[1], false, false);  // {r1}, {r3}
+    const auto o_hi = __builtin_amdgcn_permlane32_swap(p_hi[1], p_hi[1], false, false);
+    x[0] = __hiloint2double(e_hi[0], e_lo[0]);
+    x[1] = __hiloint2double(o_hi[0], o_lo[0]);
+    x[2] = __hiloint2double(e_hi[1], e_lo[1]);
+    x[3] = __hiloint2double(o_hi[1], o_lo[1]);
+}
+
+// The value of lane (t, 0) in every lane (t, q).
+__device__ __forceinline__ float bcast_row0(float v) {
+    const int bits = __float_as_int(v);
+    const auto p = __builtin_amdgcn_permlane16_swap(bits, bits, false, false);
+    const auto e = __builtin_amdgcn_permlane32_swap(p[0], p[0], false, false);
+    return __int_as_float(e[0]);
+}
+
 template <int D>
 __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
-    constexpr int S = D / 4;       // MFMA k-steps over d
-    constexpr int SW = S / 4;      // steps per wave
     constexpr int n = 4;
-    __shared__ double part[3][2][4][64];  // partial tiles of waves 1..3
-    __shared__ double part_sq[3][64];
-    __shared__ float pre_lds[16][4];
+    constexpr int GW = D / 64;  // groups of 16 k per wave; group g covers k in [16g, 16g + 16)
+    __shared__ double part[4][2][4][64];
+    __shared__ double part_sq[4][64];
     __shared__ double agg_sq[4][64];
+    __shared__ float pre_lds[16][4];
 
     const int wave = threadIdx.x / kWave;
     const int l = threadIdx.x % kWave;
@@ -94,157 +145,158 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     const float* base = a.streams + (valid ? token : 0) * a.ts;
     const double inv_n = 1.0 / n;
 
-    // Stream values of this lane's k set, kept for the agg pass.
-    float sv[SW][n];
-    double sq = 0.0;
-    double4_t acc0 = {0.0, 0.0, 0.0, 0.0};
-    double4_t acc1 = {0.0, 0.0, 0.0, 0.0};
-    // Projection row fed by this lane as A-operand row i = l % 16 of each tile.
-    // The 16x16x4 f64 accumulator gives lane (t, q) register v = tile row
-    // q + 4v, so A row i = q' + 4v' is chosen to land where it is used: tile 0
-    // row i carries res entry (row i % 4, column i / 4), which puts res row q
-    // in lane q; tile 1 row i carries pre[i / 4] when i % 4 == 0 and
-    // post[i / 4] when i % 4 == 1 (zero rows otherwise).
+    // MFMA step s = 4g + r multiplies k = 16g + 4q + r: lane (t, q) owns the
+    // float4 at 16g + 4q of every group g of its wave.
+    float4 sv[GW][n];
+#pragma unroll
+    for (int j = 0; j < GW; ++j) {
+        const int k0 = 16 * (wave * GW + j) + 4 * q;
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+            sv[j][i] = valid ? *reinterpret_cast<const float4*>(base + i * a.sd + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    // A operand: projection row for tile row i = l % 16. The accumulator of
+    // the 16x16x4 f64 MFMA puts tile rows q, q+4, q+8, q+12 of token t in
+    // lane (t, q), so tile 0 row i carries res entry (i % 4, i / 4) and lane q
+    // ends with res row q; tile 1 row i carries pre[i / 4] (i % 4 == 0) or
+    // post[i / 4] (i % 4 == 1), zero rows otherwise.
     const double* w_res = a.proj_w + static_cast<int64_t>(2 * n + 4 * (t % 4) + t / 4) * D;
     const bool pp_row = t % 4 < 2;
     const double* w_pp = a.proj_w + static_cast<int64_t>((t % 4 == 0 ? 0 : n) + t / 4) * D;
+    double sq = 0.0;
+    double4_t acc0 = {0.0, 0.0, 0.0, 0.0};
+    double4_t acc1 = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-    for (int j = 0; j < SW; ++j) {
-        const int s = wave * SW + j;
-        const int k = 4 * s + q;
+    for (int j = 0; j < GW; ++j) {
+        const int k0 = 16 * (wave * GW + j) + 4 * q;
+        const float4 w4 = *reinterpret_cast<const float4*>(a.norm_w + k0);
+        const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
+        const float s0[4] = {sv[j][0].x, sv[j][0].y, sv[j][0].z, sv[j][0].w};
+        const float s1[4] = {sv[j][1].x, sv[j][1].y, sv[j][1].z, sv[j][1].w};
+        const float s2[4] = {sv[j][2].x, sv[j][2].y, sv[j][2].z, sv[j][2].w};
+        const float s3[4] = {sv[j][3].x, sv[j][3].y, sv[j][3].z, sv[j][3].w};
 #pragma unroll
-        for (int i = 0; i < n; ++i) sv[j][i] = valid ? base[i * a.sd + k] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < SW; ++j) {
-        const int s = wave * SW + j;
-        const int k = 4 * s + q;
-        double m = static_cast<double>(sv[j][0]);
-#pragma unroll
-        for (int i = 1; i < n; ++i) m += static_cast<double>(sv[j][i]);
-        m *= inv_n;
-        sq = fma(m, m, sq);
-        const double b = m * static_cast<double>(a.norm_w[k]);
-        const double a0 = w_res[k];
-        const double a1 = pp_row ? w_pp[k] : 0.0;
-        acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b, acc1, 0, 0, 0);
-    }
-    // Sum of squares over the token's four k-lanes, then over the waves.
-    sq += shfl_xor_d(sq, 16);
-    sq += shfl_xor_d(sq, 32);
-    if (wave > 0) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            part[wave - 1][0][v][l] = acc0[v];
-            part[wave - 1][1][v][l] = acc1[v];
+        for (int r = 0; r < 4; ++r) {
+            // m = ((s0 + s1) + s2) + s3, then * (1/n): the reference's order.
+            double m = static_cast<double>(s0[r]);
+            m += static_cast<double>(s1[r]);
+            m += static_cast<double>(s2[r]);
+            m += static_cast<double>(s3[r]);
+            m *= inv_n;
+            sq = fma(m, m, sq);
+            const double b = m * static_cast<double>(wk[r]);
+            const double a0 = w_res[k0 + r];
+            const double a1 = pp_row ? w_pp[k0 + r] : 0.0;
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b, acc1, 0, 0, 0);
         }
-        part_sq[wave - 1][l] = sq;
+    }
+    {
+        double x[4];
+        gather_rows(sq, x);
+        sq = ((x[0] + x[1]) + x[2]) + x[3];
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        part[wave][0][v][l] = acc0[v];
+        part[wave][1][v][l] = acc1[v];
+    }
+    part_sq[wave][l] = sq;
+    __syncthreads();
+
+    // Coefficients, one matrix entry per lane: wave w maps tokens
+    // 4w .. 4w+3, lane l -> token tt = 4w + l / 16, entry e = l % 16 (res row
+    // e / 4, column e % 4); lanes e < 8 also map pre[e] (e < 4) or
+    // post[e - 4]. Partial tiles are summed in wave order, as the same value
+    // in every wave.
+    const int tt = 4 * wave + l / 16;
+    const int e = l % 16;
+    const int64_t token_e = static_cast<int64_t>(blockIdx.x) * 16 + tt;
+    const bool valid_e = token_e < a.tokens;
+    const double sq_tt = ((part_sq[0][tt] + part_sq[1][tt]) + part_sq[2][tt]) + part_sq[3][tt];
+    const double scale = 1.0 / sqrt(sq_tt / static_cast<double>(D) + a.eps);
+    const int src_res = tt + 16 * (e / 4);            // accumulator lane of res entry e (tile 0, v = e % 4)
+    const int src_pp = tt + 16 * (e < 4 ? 0 : 1);     // pre in lane q = 0, post in q = 1 (tile 1, v = e % 4)
+    const int v = e % 4;
+    const double logit_res =
+        ((part[0][0][v][src_res] + part[1][0][v][src_res]) + part[2][0][v][src_res]) + part[3][0][v][src_res];
+    const double logit_pp =
+        ((part[0][1][v][src_pp] + part[1][1][v][src_pp]) + part[2][1][v][src_pp]) + part[3][1][v][src_pp];
+    const double th_res = tanh_d(logit_res * scale);
+    const double th_pp = tanh_d(logit_pp * scale);
+    double m = exp_d(fma(static_cast<double>(*a.res_alpha), th_res, static_cast<double>(a.res_bias[e])));
+    if (e < 8) {
+        const bool is_pre = e < 4;
+        const double alpha = static_cast<double>(is_pre ? *a.pre_alpha : *a.post_alpha);
+        const double bias = static_cast<double>(is_pre ? a.pre_bias[v] : a.post_bias[v]);
+        const float c = static_cast<float>((is_pre ? 1.0 : 2.0) * sigmoid_fast(fma(alpha, th_pp, bias)));
+        if (is_pre) pre_lds[tt][v] = c;
+        if (valid_e) (is_pre ? a.pre : a.post)[token_e * n + v] = c;
     }
     __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-        for (int w = 0; w < 3; ++w) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                acc0[v] += part[w][0][v][l];
-                acc1[v] += part[w][1][v][l];
-            }
-            sq += part_sq[w][l];
-        }
-        const double scale = 1.0 / sqrt(sq / static_cast<double>(D) + a.eps);
-        const double pre_alpha = static_cast<double>(*a.pre_alpha);
-        const double post_alpha = static_cast<double>(*a.post_alpha);
-        const double res_alpha = static_cast<double>(*a.res_alpha);
-        // Tile 1: lane q = 0 holds the 4 pre logits, q = 1 the 4 post logits.
-        if (q < 2) {
-            float outv[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const double th = tanh(acc1[v] * scale);
-                if (q == 0) {
-                    outv[v] = static_cast<float>(sigmoid_d(fma(pre_alpha, th, static_cast<double>(a.pre_bias[v]))));
-                } else {
-                    outv[v] =
-                        static_cast<float>(2.0 * sigmoid_d(fma(post_alpha, th, static_cast<double>(a.post_bias[v]))));
-                }
-            }
-            if (q == 0) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) pre_lds[t][v] = outv[v];
-            }
-            if (valid) {
-                float* dst = (q == 0 ? a.pre : a.post) + token * n;
-                *reinterpret_cast<float4*>(dst) = make_float4(outv[0], outv[1], outv[2], outv[3]);
-            }
-        }
-        // Tile 0: lane q holds row q of the res matrix.
-        double m[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const double th = tanh(acc0[v] * scale);
-            m[v] = exp(fma(res_alpha, th, static_cast<double>(a.res_bias[4 * q + v])));
-        }
-        const int rounds = a.iters > 1 ? a.iters : 1;
-        for (int it = 0; it < rounds; ++it) {
-            const double inv = 1.0 / (((m[0] + m[1]) + m[2]) + m[3]);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) m[v] *= inv;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const double x0 = shfl_d(m[v], t);
-                const double x1 = shfl_d(m[v], t + 16);
-                const double x2 = shfl_d(m[v], t + 32);
-                const double x3 = shfl_d(m[v], t + 48);
-                const double r = 1.0 / (((x0 + x1) + x2) + x3);
-                m[v] *= r;
-            }
-        }
-        if (valid) {
-            *reinterpret_cast<float4*>(a.res + token * 16 + 4 * q) =
-                make_float4(static_cast<float>(m[0]), static_cast<float>(m[1]), static_cast<float>(m[2]),
-                            static_cast<float>(m[3]));
-        }
-    }
-    __syncthreads();
-    // agg over this wave's k set: sum_i pre_i * s_i, exact products, one rounding.
+
+    // agg = sum_i pre_i * s_i over this wave's k set for its 16 tokens
+    // (lane (t, q) layout of the loads): exact products, one rounding.
     double p[n];
 #pragma unroll
     for (int i = 0; i < n; ++i) p[i] = static_cast<double>(pre_lds[t][i]);
-    float aggv[SW];
+    float4 aggv[GW];
     double asq = 0.0;
 #pragma unroll
-    for (int j = 0; j < SW; ++j) {
-        double acc = p[0] * static_cast<double>(sv[j][0]);
+    for (int j = 0; j < GW; ++j) {
+        float o[4];
+        const float s0[4] = {sv[j][0].x, sv[j][0].y, sv[j][0].z, sv[j][0].w};
+        const float s1[4] = {sv[j][1].x, sv[j][1].y, sv[j][1].z, sv[j][1].w};
+        const float s2[4] = {sv[j][2].x, sv[j][2].y, sv[j][2].z, sv[j][2].w};
+        const float s3[4] = {sv[j][3].x, sv[j][3].y, sv[j][3].z, sv[j][3].w};
 #pragma unroll
-        for (int i = 1; i < n; ++i) acc = fma(p[i], static_cast<double>(sv[j][i]), acc);
-        aggv[j] = static_cast<float>(acc);
-        const double av = static_cast<double>(aggv[j]);
-        asq = fma(av, av, asq);
+        for (int r = 0; r < 4; ++r) {
+            double acc = p[0] * static_cast<double>(s0[r]);
+            acc = fma(p[1], static_cast<double>(s1[r]), acc);
+            acc = fma(p[2], static_cast<double>(s2[r]), acc);
+            acc = fma(p[3], static_cast<double>(s3[r]), acc);
+            o[r] = static_cast<float>(acc);
+            asq = fma(static_cast<double>(o[r]), static_cast<double>(o[r]), asq);
+        }
+        aggv[j] = make_float4(o[0], o[1], o[2], o[3]);
     }
     float* agg_row = a.agg + (valid ? token : 0) * D;
-    if (a.agg_norm_w == nullptr) {
-        if (valid) {
+    if (a.agg_norm_w != nullptr) {
+        double x[4];
+        gather_rows(asq, x);
+        asq = ((x[0] + x[1]) + x[2]) + x[3];
+        agg_sq[wave][l] = asq;
+        __syncthreads();
+        const double total = ((agg_sq[0][l] + agg_sq[1][l]) + agg_sq[2][l]) + agg_sq[3][l];
+        const double ascale = 1.0 / sqrt(total / static_cast<double>(D) + a.agg_norm_eps);
 #pragma unroll
-            for (int j = 0; j < SW; ++j) agg_row[4 * (wave * SW + j) + q] = aggv[j];
+        for (int j = 0; j < GW; ++j) {
+            const int k0 = 16 * (wave * GW + j) + 4 * q;
+            const float4 w4 = *reinterpret_cast<const float4*>(a.agg_norm_w + k0);
+            float4& o = aggv[j];
+            o.x = static_cast<float>((static_cast<double>(o.x) * ascale) * static_cast<double>(w4.x));
+            o.y = static_cast<float>((static_cast<double>(o.y) * ascale) * static_cast<double>(w4.y));
+            o.z = static_cast<float>((static_cast<double>(o.z) * ascale) * static_cast<double>(w4.z));
+            o.w = static_cast<float>((static_cast<double>(o.w) * ascale) * static_cast<double>(w4.w));
         }
-        return;
     }
-    asq += shfl_xor_d(asq, 16);
-    asq += shfl_xor_d(asq, 32);
-    agg_sq[wave][l] = asq;
-    __syncthreads();
-    // Every wave forms the same total in the same (wave) order.
-    const double total = ((agg_sq[0][l] + agg_sq[1][l]) + agg_sq[2][l]) + agg_sq[3][l];
-    const double ascale = 1.0 / sqrt(total / static_cast<double>(D) + a.agg_norm_eps);
     if (valid) {
 #pragma unroll
-        for (int j = 0; j < SW; ++j) {
-            const int k = 4 * (wave * SW + j) + q;
-            agg_row[k] = static_cast<float>((static_cast<double>(aggv[j]) * ascale) *
-                                            static_cast<double>(a.agg_norm_w[k]));
+        for (int j = 0; j < GW; ++j) {
+            *reinterpret_cast<float4*>(agg_row + 16 * (wave * GW + j) + 4 * q) = aggv[j];
         }
     }
+
+    // Sinkhorn, one entry per lane (token tt, entry e): row sums over the quad,
+    // column sums over the 16-lane group, reciprocals then products as in the
+    // reference (1 / s, then m * (1 / s)).
+    const int rounds = a.iters > 1 ? a.iters : 1;
+    for (int it = 0; it < rounds; ++it) {
+        m *= recip_pos(quad_sum(m));
+        m *= recip_pos(column_sum(m));
+    }
+    if (valid_e) a.res[token_e * 16 + e] = static_cast<float>(m);
 }
 
 // ---------------------------------------------------------------------------
@@ -493,7 +545,10 @@ mlk_status launch_combine(const float* streams, int64_t tokens, int64_t n, int64
 
 mlk_status launch_prepare(const PrepareArgs& a, int64_t n, int64_t d, hipStream_t stream) {
     if (a.tokens == 0) return MLK_OK;
-    const bool fast = n == 4 && (d == 64 || d == 128 || d == 256 || d == 512);
+    auto al16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool fast = n == 4 && (d == 64 || d == 128 || d == 256 || d == 512) && a.sd % 4 == 0 && a.ts % 4 == 0 &&
+                      al16(a.streams) && al16(a.norm_w) && al16(a.agg_norm_w) && al16(a.agg) && al16(a.pre) &&
+                      al16(a.post) && al16(a.res);
     if (fast) {
         const int64_t blocks = ceil_div(a.tokens, 16);
         switch (d) {

@@ -45,6 +45,7 @@ def _load():
         "mlk_mhc_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                             _vp, _dbl, _vp, _vp, _vp, _vp, _vp],
         "mlk_mhc_combine": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp],
+        "mlk_math_check": [_vp, _i64, _vp, _vp],
         "mlk_mhc_combine_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _dbl, _vp, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp],
     }
@@ -310,4 +311,15 @@ def set_isa(name: str, force: bool = False) -> str:
 def exported_symbols() -> list[str]:
     """Names of the C ABI entry points this module binds."""
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
-            "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare"]
+            "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
+            "mlk_math_check"]
+
+
+def math_check(x: torch.Tensor) -> dict:
+    """Device exp / tanh / sigmoid / reciprocal (float64) of x, for error bounds."""
+    _check(x.device.type == "cuda" and x.dtype == torch.float64, "x must be a float64 GPU tensor")
+    x = x.contiguous().reshape(-1)
+    out = torch.empty(4 * x.numel(), dtype=torch.float64, device=x.device)
+    _call("mlk_math_check", _ptr(x), x.numel(), _ptr(out), _stream())
+    e, t, s, r = out.view(4, -1)
+    return {"exp": e, "tanh": t, "sigmoid": s, "recip": r}
