@@ -119,6 +119,62 @@ mlk_status mlk_mhc_combine_prepare(const float* streams, int64_t tokens, int64_t
                                    float* new_streams, float* agg_out, float* pre_out, float* post_out,
                                    float* res_out, mlk_stream_t stream);
 
+/* ------------------------------------------------------------- Mamba-3 -- */
+
+/* Bytes of device workspace mamba3_siso_forward needs: q, k [B,L,H,N],
+ * (alpha, beta, gamma) [3,B,L,H] and the rotary angle terms [B,L,H,max(R,1)]
+ * (the slab of montlok.cpp:396-420). */
+size_t mlk_mamba3_workspace_bytes(int64_t batch, int64_t length, int64_t nheads, int64_t d_state,
+                                  int64_t num_rope_angles);
+
+/* mamba3_siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip) --
+ * montlok.cpp:245-325, kernel montlok_kernel.h:251-457. q, k: [B,L,H,N];
+ * v, gate: [B,L,H,D] (gate = z * sigmoid(z)); adt, dt, trap_logit: [B,L,H];
+ * each with element strides {b, t, h} (3 int64 on the host) and a dense last
+ * dimension. skip: [H]. out: [B,L,H,D] contiguous. workspace: 3*B*L*H floats. */
+mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, const float* k,
+                                     const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                                     const float* gate, const int64_t* gate_strides, const float* adt,
+                                     const int64_t* adt_strides, const float* dt, const int64_t* dt_strides,
+                                     const float* trap_logit, const int64_t* trap_strides, const float* skip,
+                                     int64_t batch, int64_t length, int64_t heads, int64_t d_state,
+                                     int64_t headdim, float* out, void* workspace, size_t workspace_bytes,
+                                     mlk_stream_t stream);
+
+/* mamba3_siso_forward(projected, gate, B_bias, C_bias, B_norm_w, C_norm_w,
+ * dt_bias, D, d_state, ngroups, nheads, headdim, num_rope_angles, b_eps,
+ * c_eps, a_floor) -- montlok.cpp:333-492, kernels montlok_kernel.h:463-597
+ * and :251-457. projected: [B,L,W] in_proj output with batch/token strides
+ * (W = 2*d_inner + 2*G*N + 3*H + R, dense last dim); gate: NULL (silu of the
+ * z lanes in the kernel, double, rounded once) or [B,L,d_inner] with strides.
+ * out: [B,L,d_inner] contiguous. */
+mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_t length, int64_t width,
+                                   int64_t proj_batch_stride, int64_t proj_token_stride, const float* gate,
+                                   int64_t gate_batch_stride, int64_t gate_token_stride, const float* b_bias,
+                                   const float* c_bias, const float* b_norm_w, const float* c_norm_w,
+                                   const float* dt_bias, const float* skip, int64_t d_state, int64_t ngroups,
+                                   int64_t nheads, int64_t headdim, int64_t num_rope_angles, double b_eps,
+                                   double c_eps, double a_floor, float* out, void* workspace,
+                                   size_t workspace_bytes, mlk_stream_t stream);
+
+/* One token of the same layer for `streams` independent sequences with
+ * carried state. No reference operator exists (the reference kernel keeps the
+ * state inside one call, montlok_kernel.h:257-259); this is the state the
+ * sequence kernel carries, made explicit, in the shape of the upstream step
+ * API (u, angle_state, ssm_state, k_state, v_state) of
+ * reference/Model/layers/mamba3_layer.py:567-580. projected: [S, W] rows
+ * `proj_stride` apart. State, updated in place: ssm [S,H,N,D], k [S,H,N],
+ * v [S,H,D] (fp32), angle [S,H,max(R,1)] (fp64 running phase sum).
+ * started = 0 for the first token of a zero state. out: [S, H*D].
+ * Stepping T tokens from a zero state reproduces mamba3_siso_forward over the
+ * T tokens. headdim <= 64, d_state <= 128. */
+mlk_status mlk_mamba3_siso_step(const float* projected, int64_t streams, int64_t proj_stride, const float* b_bias,
+                                const float* c_bias, const float* b_norm_w, const float* c_norm_w,
+                                const float* dt_bias, const float* skip, int64_t d_state, int64_t ngroups,
+                                int64_t nheads, int64_t headdim, int64_t num_rope_angles, double b_eps, double c_eps,
+                                double a_floor, float* ssm_state, float* k_state, float* v_state,
+                                double* angle_state, int started, float* out, mlk_stream_t stream);
+
 /* --------------------------------------------------------- diagnostics -- */
 
 /* Evaluates the kernels' device math helpers on x[count] (float64):

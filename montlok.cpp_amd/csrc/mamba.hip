@@ -1,0 +1,646 @@
+// Mamba-3 SISO mixer on gfx950: the in_proj post-processing (phases A, B, C)
+// and the trapezoidal recurrence, plus the one-token step with carried state.
+//
+// Reference semantics: rdt4quant_cpu/montlok_kernel.h (prep :463-597,
+// recurrence :251-457), rdt4quant_cpu/montlok_types.h (softplus, sigmoid,
+// heavy_tail, step_coefficients :57-93), op glue rdt4quant_cpu/montlok.cpp
+// (:245-492).
+//
+// in_proj row layout [z | x | B | C | dt | A | trap | angles], widths
+// [d_inner, d_inner, G*N, G*N, H, H, H, R].
+//
+// Kernels
+//   prep_kernel     one thread per (token, head): BCNorm of the head's B and C
+//                   group (fp32, sequential sum), biases -> unrotated k, q;
+//                   dt/A/trap -> (alpha, beta, gamma); tanh(angle)*pi*dt.
+//   rotate_kernel   one thread per (window, head, angle r): the running angle
+//                   sum over time in double, rounded to fp32 per step, wrapped
+//                   to [0, 2pi) with a separately rounded 2pi*floor product,
+//                   sin/cos in double, rotation of pair (2r, 2r+1) of q and k.
+//   rec_kernel<NM>  one wave per (window, head, 64 headdim columns): lane d
+//                   owns state column S[:, d] (N <= NM floats in VGPRs); q_t,
+//                   k_t, k_{t-1} and the coefficients are wave-uniform (scalar
+//                   loads). Per step and state row n:
+//                     s = fma(k_t[n], gamma*v_t[d], fma(s, alpha, k_{t-1}[n] * beta*v_{t-1}[d]))
+//                     acc_{n%2} = fma(s, q_t[n], acc)
+//                   (even/odd accumulators when headdim % 8 == 0, one
+//                   otherwise, as the reference's vector and scalar paths),
+//                   y = fma(D, v_t[d], acc0 + acc1), out = y * silu(z) in double
+//                   rounded once (or y * gate).
+//   The recurrence is FP32-VALU bound: ~4N flops... 7 flop per state element
+//   per token; q/k/coefficients come through the scalar cache.
+#include "mlk_common.h"
+
+namespace mlk {
+namespace {
+
+constexpr float kPiF = 3.14159265358979323846f;
+constexpr float kTwoPiF = 6.28318530717958647692f;
+
+// fp32 exp / log1p / tanh evaluated in double and rounded once: the
+// correctly rounded value except in rare double-rounding cases, which is what
+// the host libm the reference links (glibc) returns for these functions.
+__device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(exp_d(static_cast<double>(x))); }
+__device__ __forceinline__ float log1pf_cr(float x) { return static_cast<float>(log1p(static_cast<double>(x))); }
+__device__ __forceinline__ float tanhf_cr(float x) { return static_cast<float>(tanh_d(static_cast<double>(x))); }
+
+// torch softplus (beta 1, threshold 20) as montlok_types.h:58-60 evaluates it.
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf_cr(expf_cr(x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf_cr(-x)); }
+__device__ __forceinline__ float heavy_tail_f(float x) {
+    const float negative = fminf(x, 0.0f);
+    const float positive = fmaxf(x, 0.0f);
+    return positive + 1.0f / (1.0f - negative);
+}
+
+// (alpha, beta, gamma) = (exp(adt), (1 - sig(trap)) * dt * alpha, sig(trap) * dt).
+__device__ __forceinline__ void step_coefficients(float adt, float dt, float trap_logit, float* alpha, float* beta,
+                                                  float* gamma) {
+    const float a = expf_cr(adt);
+    const float trap = sigmoid_f(trap_logit);
+    *alpha = a;
+    *beta = ((1.0f - trap) * dt) * a;
+    *gamma = trap * dt;
+}
+
+// BCNorm scale of one group (montlok_kernel.h:464-474): sequential fp32 sum of
+// squares, each square of the first 4*floor(n/4) elements rounded before the
+// add and the remainder fused, as the compiled reference evaluates it.
+__device__ __forceinline__ float bc_norm_scale(const float* x, int64_t n, float eps) {
+    float ss = 0.0f;
+    const int64_t body = n - n % 4;
+    for (int64_t i = 0; i < body; ++i) ss = ss + x[i] * x[i];
+    for (int64_t i = body; i < n; ++i) ss = fmaf(x[i], x[i], ss);
+    return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+}
+
+struct PrepArgs {
+    const float* proj;
+    int64_t sb, st;
+    int64_t B, L, N, G, H, D, R;
+    const float* b_bias;
+    const float* c_bias;
+    const float* b_norm_w;
+    const float* c_norm_w;
+    float b_eps, c_eps;
+    const float* dt_bias;
+    float a_floor;
+    float* q;      // [B, L, H, N]
+    float* k;      // [B, L, H, N]
+    float* alpha;  // [B, L, H]
+    float* beta;
+    float* gamma;
+    float* term;   // [B, L, H, max(R, 1)]
+};
+
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= p.B * p.L * p.H) return;
+    const int64_t h = idx % p.H;
+    const int64_t tok = idx / p.H;
+    const int64_t b = tok / p.L;
+    const int64_t t = tok % p.L;
+    const int64_t N = p.N;
+    const int64_t GN = p.G * N;
+    const int64_t d_inner = p.H * p.D;
+    const float* row = p.proj + b * p.sb + t * p.st;
+    const int64_t g = h / (p.H / p.G);
+    const float* b_raw = row + 2 * d_inner + g * N;
+    const float* c_raw = row + 2 * d_inner + GN + g * N;
+    const float* raw_dt = row + 2 * d_inner + 2 * GN;
+    const float* raw_a = raw_dt + p.H;
+    const float* raw_trap = raw_a + p.H;
+    const float* raw_ang = raw_trap + p.H;
+
+    const float bs = bc_norm_scale(b_raw, N, p.b_eps);
+    const float cs = bc_norm_scale(c_raw, N, p.c_eps);
+    float* k_out = p.k + idx * N;
+    float* q_out = p.q + idx * N;
+    for (int64_t n = 0; n < N; ++n) {
+        k_out[n] = (b_raw[n] * bs) * p.b_norm_w[n] + p.b_bias[h * N + n];
+        q_out[n] = (c_raw[n] * cs) * p.c_norm_w[n] + p.c_bias[h * N + n];
+    }
+    const float dt = softplus_f(raw_dt[h] + p.dt_bias[h]);
+    const float a = -fmaxf(heavy_tail_f(raw_a[h]), p.a_floor);
+    float al, be, ga;
+    step_coefficients(a * dt, dt, raw_trap[h], &al, &be, &ga);
+    p.alpha[idx] = al;
+    p.beta[idx] = be;
+    p.gamma[idx] = ga;
+    for (int64_t r = 0; r < p.R; ++r) p.term[idx * p.R + r] = (tanhf_cr(raw_ang[r]) * kPiF) * dt;
+}
+
+// Phase B + C: chain (b, h, r).
+__global__ __launch_bounds__(256) void rotate_kernel(int64_t B, int64_t L, int64_t H, int64_t N, int64_t R,
+                                                     const float* __restrict__ term, float* __restrict__ q,
+                                                     float* __restrict__ k) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= B * H * R) return;
+    const int64_t r = idx % R;
+    const int64_t h = (idx / R) % H;
+    const int64_t b = idx / (R * H);
+    double running = 0.0;
+    for (int64_t t = 0; t < L; ++t) {
+        const int64_t th = (b * L + t) * H + h;
+        running += static_cast<double>(term[th * R + r]);
+        const float cumulative = static_cast<float>(running);
+        const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
+        const float angle = cumulative - wraps;
+        double sd, cd;
+        sincos_d(static_cast<double>(angle), &sd, &cd);
+        const float sine = static_cast<float>(sd);
+        const float cosine = static_cast<float>(cd);
+        float* qp = q + th * N + 2 * r;
+        float* kp = k + th * N + 2 * r;
+        const float ql = qp[0], qr = qp[1], kl = kp[0], kr = kp[1];
+        qp[0] = fmaf(ql, cosine, -(qr * sine));
+        qp[1] = fmaf(ql, sine, qr * cosine);
+        kp[0] = fmaf(kl, cosine, -(kr * sine));
+        kp[1] = fmaf(kl, sine, kr * cosine);
+    }
+}
+
+struct Strides3 {
+    int64_t b, t, h;
+};
+
+// Per-token coefficients for mamba3_siso_recurrent (montlok.cpp:279-299).
+__global__ __launch_bounds__(256) void coef_kernel(int64_t B, int64_t L, int64_t H, const float* adt, Strides3 as,
+                                                   const float* dt, Strides3 ds, const float* trap, Strides3 ts_,
+                                                   float* alpha, float* beta, float* gamma) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= B * L * H) return;
+    const int64_t h = idx % H;
+    const int64_t t = (idx / H) % L;
+    const int64_t b = idx / (H * L);
+    step_coefficients(adt[b * as.b + t * as.t + h * as.h], dt[b * ds.b + t * ds.t + h * ds.h],
+                      trap[b * ts_.b + t * ts_.t + h * ts_.h], alpha + idx, beta + idx, gamma + idx);
+}
+
+struct RecArgs {
+    int64_t B, L, H, N, D;
+    const float* q;
+    Strides3 qs;
+    const float* k;
+    Strides3 ks;
+    const float* v;
+    Strides3 vs;
+    const float* gate;
+    Strides3 gs;
+    int gate_logits;
+    const float* alpha;  // [B, L, H] contiguous
+    const float* beta;
+    const float* gamma;
+    const float* skip;   // [H]
+    float* out;
+    Strides3 os;
+};
+
+// The recurrence proper. Kernel parameters (not a struct) with __restrict__
+// so that the wave-uniform q/k/coefficient reads become scalar loads. NM is
+// the register capacity of the state column; EXACT means N == NM (no guards).
+template <int NM, bool EXACT, bool VEC>
+__global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D, int N,
+                                                 const float* __restrict__ q, Strides3 qs,
+                                                 const float* __restrict__ k, Strides3 ks,
+                                                 const float* __restrict__ v, Strides3 vs,
+                                                 const float* __restrict__ gate, Strides3 gs, int gate_logits,
+                                                 const float* __restrict__ alpha, const float* __restrict__ beta,
+                                                 const float* __restrict__ gamma, const float* __restrict__ skip_p,
+                                                 float* __restrict__ out, Strides3 os) {
+    const int64_t blocks_per_head = (D + 63) / 64;
+    const int64_t item = blockIdx.x;
+    const int64_t dblk = item % blocks_per_head;
+    const int64_t bh = item / blocks_per_head;
+    const int64_t h = bh % H;
+    const int64_t b = bh / H;
+    const int lane = threadIdx.x;
+    const int64_t d = dblk * 64 + lane;
+    const bool active = d < D;
+    if (EXACT) N = NM;
+
+    float s[NM];
+#pragma unroll
+    for (int n = 0; n < NM; ++n) s[n] = 0.0f;
+    const float skip = skip_p[h];
+    const float* qrow = q + b * qs.b + h * qs.h;
+    const float* krow = k + b * ks.b + h * ks.h;
+    const float* vrow = v + b * vs.b + h * vs.h + (active ? d : 0);
+    const float* grow = gate + b * gs.b + h * gs.h + (active ? d : 0);
+    float* orow = out + b * os.b + h * os.h + (active ? d : 0);
+    const int64_t cbase = b * L * H + h;
+    float v_prev = 0.0f;
+    float v_cur = active ? vrow[0] : 0.0f;
+    float g_cur = active ? grow[0] : 0.0f;
+    for (int64_t t = 0; t < L; ++t) {
+        const float al = alpha[cbase + t * H];
+        const float be = beta[cbase + t * H];
+        const float ga = gamma[cbase + t * H];
+        float v_next = 0.0f, g_next = 0.0f;
+        if (active && t + 1 < L) {
+            v_next = vrow[(t + 1) * vs.t];
+            g_next = grow[(t + 1) * gs.t];
+        }
+        const float* qt = qrow + t * qs.t;
+        const float* kt = krow + t * ks.t;
+        const float* kp = t > 0 ? kt - ks.t : kt;
+        const float pv = t > 0 ? be * v_prev : 0.0f;
+        const float cv = ga * v_cur;
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            if (EXACT || n < N) {
+                float upd;
+                if (VEC || t > 0) {
+                    upd = fmaf(kt[n], cv, fmaf(s[n], al, kp[n] * pv));
+                } else {
+                    upd = fmaf(kt[n], cv, s[n] * al);
+                }
+                s[n] = upd;
+                if (VEC && (n & 1)) {
+                    acc1 = fmaf(upd, qt[n], acc1);
+                } else {
+                    acc0 = fmaf(upd, qt[n], acc0);
+                }
+            }
+        }
+        const float y = fmaf(skip, v_cur, VEC ? acc0 + acc1 : acc0);
+        float o;
+        if (gate_logits) {
+            const double z = static_cast<double>(g_cur);
+            o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
+        } else {
+            o = y * g_cur;
+        }
+        if (active) orow[t * os.t] = o;
+        v_prev = v_cur;
+        v_cur = v_next;
+        g_cur = g_next;
+    }
+}
+
+mlk_status launch_rec(const RecArgs& a, hipStream_t stream) {
+    if (a.B * a.L * a.H == 0 || a.D == 0) return MLK_OK;
+    const bool vec = a.D % 8 == 0;
+    const int64_t grid = a.B * a.H * ((a.D + 63) / 64);
+    const int N = static_cast<int>(a.N);
+#define MLK_REC(NM, EXACT)                                                                                         \
+    do {                                                                                                           \
+        if (vec) {                                                                                                 \
+            hipLaunchKernelGGL((rec_kernel<NM, EXACT, true>), dim3(grid), dim3(64), 0, stream, a.L, a.H, a.D, N,   \
+                               a.q, a.qs, a.k, a.ks, a.v, a.vs, a.gate, a.gs, a.gate_logits, a.alpha, a.beta,      \
+                               a.gamma, a.skip, a.out, a.os);                                                      \
+        } else {                                                                                                   \
+            hipLaunchKernelGGL((rec_kernel<NM, EXACT, false>), dim3(grid), dim3(64), 0, stream, a.L, a.H, a.D, N,  \
+                               a.q, a.qs, a.k, a.ks, a.v, a.vs, a.gate, a.gs, a.gate_logits, a.alpha, a.beta,      \
+                               a.gamma, a.skip, a.out, a.os);                                                      \
+        }                                                                                                          \
+        return launch_status("mamba3 recurrence");                                                                 \
+    } while (0)
+    switch (N) {
+        case 16: MLK_REC(16, true);
+        case 32: MLK_REC(32, true);
+        case 64: MLK_REC(64, true);
+        case 128: MLK_REC(128, true);
+        default: break;
+    }
+    if (N <= 16) MLK_REC(16, false);
+    if (N <= 64) MLK_REC(64, false);
+    if (N <= 128) MLK_REC(128, false);
+#undef MLK_REC
+    set_error("d_state above 128 is not supported by the GPU recurrence");
+    return MLK_ERR_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// One-token step with carried state (no reference op; see mlk_hip.h)
+// ---------------------------------------------------------------------------
+
+struct StepArgs {
+    int64_t S, N, G, H, D, R;
+    const float* proj;  // [S, W] rows proj_ss apart
+    int64_t proj_ss;
+    const float* b_bias;
+    const float* c_bias;
+    const float* b_norm_w;
+    const float* c_norm_w;
+    float b_eps, c_eps;
+    const float* dt_bias;
+    const float* skip;
+    float a_floor;
+    float* ssm;     // [S, H, N, D]
+    float* k_prev;  // [S, H, N]
+    float* v_prev;  // [S, H, D]
+    double* angle;  // [S, H, max(R, 1)]
+    int started;    // 0 for the first token of a zero state: the beta term is dropped
+    float* out;     // [S, H * D]
+};
+
+// One wave per (stream, head); lanes = headdim columns (D <= 64). The q/k
+// preparation of the head is done by the wave cooperatively in LDS.
+template <int NM, bool VEC>
+__global__ __launch_bounds__(64) void step_kernel(StepArgs p) {
+    __shared__ float qk[2][NM];
+    __shared__ float coef[3];
+    const int64_t s_idx = blockIdx.x / p.H;
+    const int64_t h = blockIdx.x % p.H;
+    const int lane = threadIdx.x;
+    const int N = static_cast<int>(p.N);
+    const int64_t d_inner = p.H * p.D;
+    const int64_t GN = p.G * p.N;
+    const float* row = p.proj + s_idx * p.proj_ss;
+    const int64_t g = h / (p.H / p.G);
+    const float* b_raw = row + 2 * d_inner + g * p.N;
+    const float* c_raw = row + 2 * d_inner + GN + g * p.N;
+    const float* raw_dt = row + 2 * d_inner + 2 * GN;
+    const float* raw_a = raw_dt + p.H;
+    const float* raw_trap = raw_a + p.H;
+    const float* raw_ang = raw_trap + p.H;
+    const int started = p.started;
+
+    // Lanes 0 / 1: BCNorm scales (sequential sums); lane 2: dt and coefficients.
+    __shared__ float scales[2];
+    __shared__ float dt_s;
+    if (lane == 0) scales[0] = bc_norm_scale(b_raw, p.N, p.b_eps);
+    if (lane == 1) scales[1] = bc_norm_scale(c_raw, p.N, p.c_eps);
+    if (lane == 2) {
+        const float dt = softplus_f(raw_dt[h] + p.dt_bias[h]);
+        const float a = -fmaxf(heavy_tail_f(raw_a[h]), p.a_floor);
+        step_coefficients(a * dt, dt, raw_trap[h], &coef[0], &coef[1], &coef[2]);
+        dt_s = dt;
+    }
+    __syncthreads();
+    for (int n = lane; n < N; n += 64) {
+        qk[1][n] = (b_raw[n] * scales[0]) * p.b_norm_w[n] + p.b_bias[h * p.N + n];  // k
+        qk[0][n] = (c_raw[n] * scales[1]) * p.c_norm_w[n] + p.c_bias[h * p.N + n];  // q
+    }
+    __syncthreads();
+    // Rotary pairs: lane r < R advances the running angle and rotates pair r.
+    const int64_t Rw = p.R > 0 ? p.R : 1;
+    for (int64_t r = lane; r < p.R; r += 64) {
+        double* run = p.angle + (s_idx * p.H + h) * Rw + r;
+        const double next = *run + static_cast<double>((tanhf_cr(raw_ang[r]) * kPiF) * dt_s);
+        *run = next;
+        const float cumulative = static_cast<float>(next);
+        const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
+        double sd, cd;
+        sincos_d(static_cast<double>(cumulative - wraps), &sd, &cd);
+        const float sine = static_cast<float>(sd), cosine = static_cast<float>(cd);
+        for (int w = 0; w < 2; ++w) {
+            const float l = qk[w][2 * r], rr = qk[w][2 * r + 1];
+            qk[w][2 * r] = fmaf(l, cosine, -(rr * sine));
+            qk[w][2 * r + 1] = fmaf(l, sine, rr * cosine);
+        }
+    }
+    __syncthreads();
+    const int d = lane;
+    if (d >= p.D) return;
+    const float al = coef[0], be = coef[1], ga = coef[2];
+    const float* x = row + d_inner + h * p.D;
+    const float* z = row + h * p.D;
+    float* st = p.ssm + ((s_idx * p.H + h) * p.N) * p.D + d;
+    float* kps = p.k_prev + (s_idx * p.H + h) * p.N;
+    float* vps = p.v_prev + (s_idx * p.H + h) * p.D;
+    const float v_cur = x[d];
+    const float pv = started ? be * vps[d] : 0.0f;
+    const float cv = ga * v_cur;
+    float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NM; ++n) {
+        if (n < N) {
+            const float kc = qk[1][n];
+            const float kp = started ? kps[n] : kc;
+            const float sv = st[static_cast<int64_t>(n) * p.D];
+            const float upd = (VEC || started) ? fmaf(kc, cv, fmaf(sv, al, kp * pv)) : fmaf(kc, cv, sv * al);
+            st[static_cast<int64_t>(n) * p.D] = upd;
+            if (VEC && (n & 1)) {
+                acc1 = fmaf(upd, qk[0][n], acc1);
+            } else {
+                acc0 = fmaf(upd, qk[0][n], acc0);
+            }
+        }
+    }
+    const float y = fmaf(p.skip[h], v_cur, VEC ? acc0 + acc1 : acc0);
+    const double zz = static_cast<double>(z[d]);
+    p.out[s_idx * d_inner + h * p.D + d] = static_cast<float>(static_cast<double>(y) * (zz / (1.0 + exp_d(-zz))));
+    // k_prev is read above by every lane before any lane replaces it: the
+    // wave executes the loop in lockstep, and the write below is after it.
+    vps[d] = v_cur;
+    for (int n = d; n < N; n += static_cast<int>(p.D)) kps[n] = qk[1][n];
+}
+
+}  // namespace
+}  // namespace mlk
+
+using namespace mlk;
+
+extern "C" {
+
+size_t mlk_mamba3_workspace_bytes(int64_t batch, int64_t length, int64_t nheads, int64_t d_state,
+                                  int64_t num_rope_angles) {
+    const int64_t blh = batch * length * nheads;
+    const int64_t rw = num_rope_angles > 0 ? num_rope_angles : 1;
+    return sizeof(float) * static_cast<size_t>(2 * blh * d_state + 3 * blh + blh * rw);
+}
+
+mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, const float* k,
+                                     const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                                     const float* gate, const int64_t* gate_strides, const float* adt,
+                                     const int64_t* adt_strides, const float* dt, const int64_t* dt_strides,
+                                     const float* trap_logit, const int64_t* trap_strides, const float* skip,
+                                     int64_t batch, int64_t length, int64_t heads, int64_t d_state,
+                                     int64_t headdim, float* out, void* workspace, size_t workspace_bytes,
+                                     mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 0 && heads >= 0 && d_state >= 0 && headdim >= 0, "q/k must be [B,L,H,N]");
+    const int64_t blh = batch * length * heads;
+    MLK_CHECK(workspace_bytes >= sizeof(float) * static_cast<size_t>(3 * blh), "workspace too small");
+    if (blh == 0 || headdim == 0) return MLK_OK;
+    MLK_CHECK(q && k && v && gate && adt && dt && trap_logit && skip && out && workspace, "null tensor pointer");
+    MLK_CHECK(q_strides && k_strides && v_strides && gate_strides && adt_strides && dt_strides && trap_strides,
+              "null stride array");
+    float* alpha = static_cast<float*>(workspace);
+    float* beta = alpha + blh;
+    float* gamma = beta + blh;
+    auto s3 = [](const int64_t* x) { return Strides3{x[0], x[1], x[2]}; };
+    hipLaunchKernelGGL(coef_kernel, dim3(ceil_div(blh, 256)), dim3(256), 0, stream, batch, length, heads, adt,
+                       s3(adt_strides), dt, s3(dt_strides), trap_logit, s3(trap_strides), alpha, beta, gamma);
+    const mlk_status st = launch_status("mamba3 coefficients");
+    if (st != MLK_OK) return st;
+    RecArgs a{};
+    a.B = batch;
+    a.L = length;
+    a.H = heads;
+    a.N = d_state;
+    a.D = headdim;
+    a.q = q;
+    a.qs = s3(q_strides);
+    a.k = k;
+    a.ks = s3(k_strides);
+    a.v = v;
+    a.vs = s3(v_strides);
+    a.gate = gate;
+    a.gs = s3(gate_strides);
+    a.gate_logits = 0;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.gamma = gamma;
+    a.skip = skip;
+    a.out = out;
+    a.os = {length * heads * headdim, heads * headdim, headdim};
+    return launch_rec(a, stream);
+}
+
+mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_t length, int64_t width,
+                                   int64_t proj_batch_stride, int64_t proj_token_stride, const float* gate,
+                                   int64_t gate_batch_stride, int64_t gate_token_stride, const float* b_bias,
+                                   const float* c_bias, const float* b_norm_w, const float* c_norm_w,
+                                   const float* dt_bias, const float* skip, int64_t d_state, int64_t ngroups,
+                                   int64_t nheads, int64_t headdim, int64_t num_rope_angles, double b_eps,
+                                   double c_eps, double a_floor, float* out, void* workspace,
+                                   size_t workspace_bytes, mlk_stream_t stream) {
+    MLK_CHECK(d_state > 0 && ngroups > 0 && nheads > 0 && headdim > 0, "invalid Mamba-3 geometry");
+    MLK_CHECK(nheads % ngroups == 0, "nheads must be divisible by ngroups");
+    MLK_CHECK(num_rope_angles >= 0 && 2 * num_rope_angles <= d_state, "num_rope_angles must fit in d_state");
+    const int64_t d_inner = nheads * headdim;
+    const int64_t expected = 2 * d_inner + 2 * ngroups * d_state + 3 * nheads + num_rope_angles;
+    if (width != expected) {
+        set_error("projected width " + std::to_string(width) + " does not match the Mamba-3 layout width " +
+                  std::to_string(expected));
+        return MLK_ERR_INVALID_ARGUMENT;
+    }
+    MLK_CHECK(workspace_bytes >= mlk_mamba3_workspace_bytes(batch, length, nheads, d_state, num_rope_angles),
+              "workspace too small");
+    const int64_t blh = batch * length * nheads;
+    if (blh == 0) return MLK_OK;
+    MLK_CHECK(projected && b_bias && c_bias && b_norm_w && c_norm_w && dt_bias && skip && out && workspace,
+              "null tensor pointer");
+    const int64_t rw = num_rope_angles > 0 ? num_rope_angles : 1;
+    float* q = static_cast<float*>(workspace);
+    float* k = q + blh * d_state;
+    float* alpha = k + blh * d_state;
+    float* beta = alpha + blh;
+    float* gamma = beta + blh;
+    float* term = gamma + blh;
+    (void)rw;
+    PrepArgs pa{};
+    pa.proj = projected;
+    pa.sb = proj_batch_stride;
+    pa.st = proj_token_stride;
+    pa.B = batch;
+    pa.L = length;
+    pa.N = d_state;
+    pa.G = ngroups;
+    pa.H = nheads;
+    pa.D = headdim;
+    pa.R = num_rope_angles;
+    pa.b_bias = b_bias;
+    pa.c_bias = c_bias;
+    pa.b_norm_w = b_norm_w;
+    pa.c_norm_w = c_norm_w;
+    pa.b_eps = static_cast<float>(b_eps);
+    pa.c_eps = static_cast<float>(c_eps);
+    pa.dt_bias = dt_bias;
+    pa.a_floor = static_cast<float>(a_floor);
+    pa.q = q;
+    pa.k = k;
+    pa.alpha = alpha;
+    pa.beta = beta;
+    pa.gamma = gamma;
+    pa.term = term;
+    hipLaunchKernelGGL(prep_kernel, dim3(ceil_div(blh, 256)), dim3(256), 0, stream, pa);
+    mlk_status st = launch_status("mamba3 prep");
+    if (st != MLK_OK) return st;
+    if (num_rope_angles > 0) {
+        const int64_t chains = batch * nheads * num_rope_angles;
+        hipLaunchKernelGGL(rotate_kernel, dim3(ceil_div(chains, 256)), dim3(256), 0, stream, batch, length, nheads,
+                           d_state, num_rope_angles, term, q, k);
+        st = launch_status("mamba3 rotate");
+        if (st != MLK_OK) return st;
+    }
+    RecArgs a{};
+    a.B = batch;
+    a.L = length;
+    a.H = nheads;
+    a.N = d_state;
+    a.D = headdim;
+    a.q = q;
+    a.qs = {length * nheads * d_state, nheads * d_state, d_state};
+    a.k = k;
+    a.ks = a.qs;
+    a.v = projected + d_inner;
+    a.vs = {proj_batch_stride, proj_token_stride, headdim};
+    if (gate == nullptr) {
+        a.gate = projected;
+        a.gs = {proj_batch_stride, proj_token_stride, headdim};
+        a.gate_logits = 1;
+    } else {
+        a.gate = gate;
+        a.gs = {gate_batch_stride, gate_token_stride, headdim};
+        a.gate_logits = 0;
+    }
+    a.alpha = alpha;
+    a.beta = beta;
+    a.gamma = gamma;
+    a.skip = skip;
+    a.out = out;
+    a.os = {length * d_inner, d_inner, headdim};
+    return launch_rec(a, stream);
+}
+
+mlk_status mlk_mamba3_siso_step(const float* projected, int64_t streams, int64_t proj_stride, const float* b_bias,
+                                const float* c_bias, const float* b_norm_w, const float* c_norm_w,
+                                const float* dt_bias, const float* skip, int64_t d_state, int64_t ngroups,
+                                int64_t nheads, int64_t headdim, int64_t num_rope_angles, double b_eps, double c_eps,
+                                double a_floor, float* ssm_state, float* k_state, float* v_state,
+                                double* angle_state, int started, float* out, mlk_stream_t stream) {
+    MLK_CHECK(d_state > 0 && ngroups > 0 && nheads > 0 && headdim > 0, "invalid Mamba-3 geometry");
+    MLK_CHECK(nheads % ngroups == 0, "nheads must be divisible by ngroups");
+    MLK_CHECK(num_rope_angles >= 0 && 2 * num_rope_angles <= d_state, "num_rope_angles must fit in d_state");
+    MLK_CHECK(headdim <= 64, "the GPU step handles headdim <= 64");
+    MLK_CHECK(d_state <= 128, "d_state above 128 is not supported by the GPU step");
+    if (streams == 0) return MLK_OK;
+    MLK_CHECK(projected && b_bias && c_bias && b_norm_w && c_norm_w && dt_bias && skip && ssm_state && k_state &&
+                  v_state && angle_state && out,
+              "null tensor pointer");
+    StepArgs p{};
+    p.S = streams;
+    p.N = d_state;
+    p.G = ngroups;
+    p.H = nheads;
+    p.D = headdim;
+    p.R = num_rope_angles;
+    p.proj = projected;
+    p.proj_ss = proj_stride;
+    p.b_bias = b_bias;
+    p.c_bias = c_bias;
+    p.b_norm_w = b_norm_w;
+    p.c_norm_w = c_norm_w;
+    p.b_eps = static_cast<float>(b_eps);
+    p.c_eps = static_cast<float>(c_eps);
+    p.dt_bias = dt_bias;
+    p.skip = skip;
+    p.a_floor = static_cast<float>(a_floor);
+    p.ssm = ssm_state;
+    p.k_prev = k_state;
+    p.v_prev = v_state;
+    p.angle = angle_state;
+    p.started = started;
+    p.out = out;
+    const bool vec = headdim % 8 == 0;
+    const dim3 grid(static_cast<unsigned>(streams * nheads));
+#define MLK_STEP(NM)                                                                                         \
+    do {                                                                                                     \
+        if (vec) {                                                                                           \
+            hipLaunchKernelGGL((step_kernel<NM, true>), grid, dim3(64), 0, stream, p);                       \
+        } else {                                                                                             \
+            hipLaunchKernelGGL((step_kernel<NM, false>), grid, dim3(64), 0, stream, p);                      \
+        }                                                                                                    \
+        return launch_status("mamba3 step");                                                                 \
+    } while (0)
+    if (d_state <= 16) MLK_STEP(16);
+    if (d_state <= 64) MLK_STEP(64);
+    MLK_STEP(128);
+#undef MLK_STEP
+}
+
+}  // extern "C"

@@ -107,6 +107,45 @@ __device__ __forceinline__ double tanh_d(double x) {
 // 1 / (1 + exp(-x)).
 __device__ __forceinline__ double sigmoid_fast(double x) { return recip_pos(1.0 + exp_d(-x)); }
 
+// sin and cos of x in double for |x| below a few multiples of pi (the Mamba
+// rotary phases are wrapped to [0, 2pi) before this call). Cody-Waite
+// reduction by pi/2 with fdlibm's two-part constant (pio2_1 carries 33
+// significant bits, so k * pio2_1 is exact for the small quadrant counts k
+// here) to r in [-pi/4, pi/4], then the Taylor series of sin to r^15 and of
+// cos to r^16 (truncation below 1e-16 relative at |r| = pi/4), evaluated in
+// r^2 with Estrin's scheme, and the quadrant swap/negation. Results agree
+// with a correctly rounded sin/cos to a couple of double ulp.
+__device__ __forceinline__ void sincos_d(double x, double* sine, double* cosine) {
+    const double kf = __builtin_rint(x * 0.63661977236758134308);
+    const double r = fma(-kf, 6.07710050650619224932e-11, fma(-kf, 1.57079632673412561417e+00, x));
+    const double z = r * r;
+    const double z2 = z * z;
+    const double z4 = z2 * z2;
+    // sin(r) = r * P(z), P(z) = sum_i (-1)^i z^i / (2i+1)!, i = 0..7
+    const double s01 = fma(z, -1.0 / 6.0, 1.0);
+    const double s23 = fma(z, -1.0 / 5040.0, 1.0 / 120.0);
+    const double s45 = fma(z, -1.0 / 39916800.0, 1.0 / 362880.0);
+    const double s67 = fma(z, -1.0 / 1307674368000.0, 1.0 / 6227020800.0);
+    const double sp = fma(fma(s67, z2, s45), z4, fma(s23, z2, s01));
+    // cos(r) = Q(z), Q(z) = sum_i (-1)^i z^i / (2i)!, i = 0..8
+    const double c01 = fma(z, -0.5, 1.0);
+    const double c23 = fma(z, -1.0 / 720.0, 1.0 / 24.0);
+    const double c45 = fma(z, -1.0 / 3628800.0, 1.0 / 40320.0);
+    const double c67 = fma(z, -1.0 / 87178291200.0, 1.0 / 479001600.0);
+    const double c8 = 1.0 / 20922789888000.0;
+    const double cq = fma(fma(fma(c8, z2, c67), z2, c45), z4, fma(c23, z2, c01));
+    const double sr = r * sp;
+    const int quadrant = static_cast<int>(kf) & 3;
+    double so = (quadrant & 1) ? cq : sr;
+    double co = (quadrant & 1) ? -sr : cq;
+    if (quadrant & 2) {
+        so = -so;
+        co = -co;
+    }
+    *sine = so;
+    *cosine = co;
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64);
 // every lane of a group receives the group total.
 template <int width>

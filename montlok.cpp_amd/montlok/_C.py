@@ -46,6 +46,11 @@ def _load():
                             _vp, _dbl, _vp, _vp, _vp, _vp, _vp],
         "mlk_mhc_combine": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp],
         "mlk_math_check": [_vp, _i64, _vp, _vp],
+        "mlk_mamba3_siso_recurrent": [_vp, _vp] * 7 + [_vp] + [_i64] * 5 + [_vp, _vp, C.c_size_t, _vp],
+        "mlk_mamba3_siso_forward": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64] + [_vp] * 6 + [_i64] * 5 +
+                                   [_dbl, _dbl, _dbl, _vp, _vp, C.c_size_t, _vp],
+        "mlk_mamba3_siso_step": [_vp, _i64, _i64] + [_vp] * 6 + [_i64] * 5 + [_dbl, _dbl, _dbl] + [_vp] * 4 +
+                                [C.c_int, _vp, _vp],
         "mlk_mhc_combine_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _dbl, _vp, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp],
     }
@@ -53,6 +58,8 @@ def _load():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = C.c_int
+    lib.mlk_mamba3_workspace_bytes.argtypes = [_i64] * 5
+    lib.mlk_mamba3_workspace_bytes.restype = C.c_size_t
     _lib = lib
     return lib
 
@@ -280,6 +287,127 @@ def mhc_combine_prepare(streams, res, post, out, norm_w, eps, proj_w, pre_bias, 
     return new, agg, pre_o, post_o, res_o
 
 
+# ------------------------------------------------------------------ Mamba-3
+
+
+def _strides3(t: torch.Tensor):
+    arr = (C.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+    return arr
+
+
+def _require_inner_dense(t: torch.Tensor, name: str) -> None:
+    """montlok.cpp:52-55."""
+    _check(t.dim() >= 1 and (t.stride(-1) == 1 or t.size(-1) == 1),
+           f"{name} must be contiguous along its last dimension")
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 4), dtype=torch.uint8, device=device)
+
+
+def mamba3_siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip):
+    """montlok.cpp:245-325: gated SSM output [B, L, H, D] (gate = z * sigmoid(z))."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (gate, "gate"), (adt, "adt"), (dt, "dt"),
+                    (trap_logit, "trap_logit")):
+        _require_f32_gpu(t, name)
+    _check(q.dim() == 4 and k.shape == q.shape, "q/k must be [B,L,H,N]")
+    _check(v.dim() == 4 and gate.shape == v.shape, "v/gate must be [B,L,H,D]")
+    B, L, H, N = q.shape
+    D = v.size(3)
+    _check(v.size(0) == B and v.size(1) == L and v.size(2) == H, "v shape mismatch")
+    _check(tuple(adt.shape) == (B, L, H), "adt must be [B,L,H]")
+    _check(dt.shape == adt.shape and trap_logit.shape == adt.shape, "dt/trap_logit shape mismatch")
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (gate, "gate")):
+        _require_inner_dense(t, name)
+    sk = _dense_parameter(skip, H, "skip")
+    out = torch.empty((B, L, H, D), dtype=torch.float32, device=q.device)
+    ws = _workspace(4 * 3 * B * L * H, q.device)
+    _call("mlk_mamba3_siso_recurrent", _ptr(q), _strides3(q), _ptr(k), _strides3(k), _ptr(v), _strides3(v),
+          _ptr(gate), _strides3(gate), _ptr(adt), _strides3(adt), _ptr(dt), _strides3(dt), _ptr(trap_logit),
+          _strides3(trap_logit), _ptr(sk), B, L, H, N, D, _ptr(out), _ptr(ws), ws.numel(), _stream())
+    return out
+
+
+def _mamba_params(b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, nheads):
+    return (_dense_parameter(b_bias, nheads * d_state, "B_bias"), _dense_parameter(c_bias, nheads * d_state, "C_bias"),
+            _dense_parameter(b_norm_w, d_state, "B_norm.weight"), _dense_parameter(c_norm_w, d_state, "C_norm.weight"),
+            _dense_parameter(dt_bias, nheads, "dt_bias"), _dense_parameter(skip, nheads, "D"))
+
+
+def mamba3_siso_forward(projected, gate, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups,
+                        nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor):
+    """montlok.cpp:333-492: in_proj output [B, L, W] -> out_proj input [B, L, d_inner].
+
+    An empty ``gate`` evaluates silu of the z lanes of ``projected`` in the kernel."""
+    _require_f32_gpu(projected, "projected")
+    gate_logits = gate is None or gate.numel() == 0
+    if not gate_logits:
+        _require_f32_gpu(gate, "gate")
+    _check(projected.dim() == 3, "projected must be [B,L,W]")
+    _check(d_state > 0 and ngroups > 0 and nheads > 0 and headdim > 0, "invalid Mamba-3 geometry")
+    _check(nheads % ngroups == 0, "nheads must be divisible by ngroups")
+    _check(num_rope_angles >= 0 and 2 * num_rope_angles <= d_state, "num_rope_angles must fit in d_state")
+    _require_inner_dense(projected, "projected")
+    B, L, W = projected.shape
+    d_inner = nheads * headdim
+    if not gate_logits:
+        _require_inner_dense(gate, "gate")
+        _check(gate.dim() == 3 and tuple(gate.shape) == (B, L, d_inner), "gate must be [B,L,d_inner]")
+    expected = 2 * d_inner + 2 * ngroups * d_state + 3 * nheads + num_rope_angles
+    _check(W == expected, f"projected width {W} does not match the Mamba-3 layout width {expected}")
+    params = _mamba_params(b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, nheads)
+    out = torch.empty((B, L, d_inner), dtype=torch.float32, device=projected.device)
+    lib = _load()
+    ws = _workspace(lib.mlk_mamba3_workspace_bytes(B, L, nheads, d_state, num_rope_angles), projected.device)
+    gsb, gst = (0, 0) if gate_logits else (gate.stride(0), gate.stride(1))
+    _call("mlk_mamba3_siso_forward", _ptr(projected), B, L, W, projected.stride(0), projected.stride(1),
+          None if gate_logits else _ptr(gate), gsb, gst, *(_ptr(t) for t in params), d_state, ngroups, nheads, headdim,
+          num_rope_angles, float(b_eps), float(c_eps), float(a_floor), _ptr(out), _ptr(ws), ws.numel(), _stream())
+    return out
+
+
+def mamba3_siso_step(projected, state, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups,
+                     nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor):
+    """One token for S streams with carried state (no reference operator).
+
+    projected: [S, W]; state: dict with ssm [S,H,N,D], k [S,H,N], v [S,H,D]
+    (float32), angle [S,H,max(R,1)] (float64) updated in place, and
+    ``started`` (False before the first token of a zero state; set True here).
+    Returns [S, H*D]."""
+    _require_f32_gpu(projected, "projected")
+    _check(projected.dim() == 2, "projected must be [S,W]")
+    _require_inner_dense(projected, "projected")
+    S, W = projected.shape
+    d_inner = nheads * headdim
+    expected = 2 * d_inner + 2 * ngroups * d_state + 3 * nheads + num_rope_angles
+    _check(W == expected, f"projected width {W} does not match the Mamba-3 layout width {expected}")
+    rw = max(num_rope_angles, 1)
+    shapes = {"ssm": (S, nheads, d_state, headdim), "k": (S, nheads, d_state), "v": (S, nheads, headdim),
+              "angle": (S, nheads, rw)}
+    for key, shape in shapes.items():
+        t = state[key]
+        _check(tuple(t.shape) == shape and t.is_contiguous() and t.device.type == "cuda",
+               f"state['{key}'] must be a contiguous GPU tensor of shape {shape}")
+        _check(t.dtype == (torch.float64 if key == "angle" else torch.float32), f"state['{key}'] has the wrong dtype")
+    params = _mamba_params(b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, nheads)
+    out = torch.empty((S, d_inner), dtype=torch.float32, device=projected.device)
+    _call("mlk_mamba3_siso_step", _ptr(projected), S, projected.stride(0), *(_ptr(t) for t in params), d_state,
+          ngroups, nheads, headdim, num_rope_angles, float(b_eps), float(c_eps), float(a_floor), _ptr(state["ssm"]),
+          _ptr(state["k"]), _ptr(state["v"]), _ptr(state["angle"]), int(bool(state.get("started", False))), _ptr(out),
+          _stream())
+    state["started"] = True
+    return out
+
+
+def new_mamba3_state(streams: int, nheads: int, d_state: int, headdim: int, num_rope_angles: int, device) -> dict:
+    """Zero carried state for mamba3_siso_step."""
+    return {"ssm": torch.zeros(streams, nheads, d_state, headdim, device=device),
+            "k": torch.zeros(streams, nheads, d_state, device=device),
+            "v": torch.zeros(streams, nheads, headdim, device=device),
+            "angle": torch.zeros(streams, nheads, max(num_rope_angles, 1), dtype=torch.float64, device=device),
+            "started": False}
+
+
 # ------------------------------------------------------------------ introspection
 
 
@@ -312,7 +440,8 @@ def exported_symbols() -> list[str]:
     """Names of the C ABI entry points this module binds."""
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
-            "mlk_math_check"]
+            "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent", "mlk_mamba3_siso_forward",
+            "mlk_mamba3_siso_step"]
 
 
 def math_check(x: torch.Tensor) -> dict:

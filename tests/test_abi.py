@@ -16,7 +16,7 @@ LIB = ROOT / "montlok.cpp_amd" / "montlok" / "rdt" / "lib" / "libmlk_hip.so"
 
 def declared_symbols() -> list[str]:
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const char\*|int|mlk_status)\s+(mlk_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int|size_t|mlk_status)\s+(mlk_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
