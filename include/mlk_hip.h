@@ -36,6 +36,12 @@ extern "C" {
 
 typedef struct ihipStream_t* mlk_stream_t; /* identical to hipStream_t */
 
+/* Element type of a weight operand. */
+typedef enum mlk_dtype {
+    MLK_DTYPE_F32 = 0,
+    MLK_DTYPE_BF16 = 1
+} mlk_dtype;
+
 typedef enum mlk_status {
     MLK_OK = 0,
     MLK_ERR_INVALID_ARGUMENT = 1,
@@ -78,6 +84,18 @@ mlk_status mlk_layer_norm(const float* x, int64_t rows, int64_t dim, int64_t row
  * hold [gate | up] (2*hidden floats, row_stride apart); out: [rows, hidden]. */
 mlk_status mlk_swiglu(const float* x, int64_t rows, int64_t hidden, int64_t row_stride, float* out,
                       mlk_stream_t stream);
+
+/* -------------------------------------------------------------- linear -- */
+
+/* linear(input, weight, bias=None) -- linear_dispatch, montlok.cpp:67-91
+ * (op table :1458). y[rows, N] = x[rows, K] W[N, K]^T + bias[N].
+ * x: fp32 rows `x_stride` floats apart; W: contiguous, fp32 or bf16
+ * (weight_dtype, an mlk_dtype); bias: fp32 [N] or NULL; out: fp32 rows
+ * `out_stride` floats apart. bf16 weights run on bf16 matrix cores with x
+ * rounded to bf16 and fp32 accumulation; fp32 weights stay fp32 throughout. */
+mlk_status mlk_linear(const float* x, int64_t rows, int64_t in_features, int64_t x_stride, const void* weight,
+                      int32_t weight_dtype, const float* bias, int64_t out_features, float* out,
+                      int64_t out_stride, mlk_stream_t stream);
 
 /* ----------------------------------------------------------------- mHC -- */
 

@@ -42,6 +42,7 @@ def _load():
         "mlk_add_rms_norm": [_vp, _vp, _i64, _i64, _vp, _dbl, _i64, _vp, _vp, _vp],
         "mlk_layer_norm": [_vp, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp],
         "mlk_swiglu": [_vp, _i64, _i64, _i64, _vp, _vp],
+        "mlk_linear": [_vp, _i64, _i64, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp],
         "mlk_mhc_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                             _vp, _dbl, _vp, _vp, _vp, _vp, _vp],
         "mlk_mhc_combine": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp],
@@ -170,6 +171,48 @@ def swiglu(x: torch.Tensor) -> torch.Tensor:
     out = torch.empty((count, hidden), dtype=torch.float32, device=x.device)
     _call("mlk_swiglu", _ptr(rows), count, hidden, stride, _ptr(out), _stream())
     return out.view(*x.shape[:-1], hidden)
+
+
+# ------------------------------------------------------------------ linear
+
+_WEIGHT_DTYPES = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def _weight(weight: torch.Tensor, name: str = "weight") -> torch.Tensor:
+    _check(weight is not None, f"{name} must be defined")
+    _check(weight.device.type == "cuda", f"{name} must be on the GPU")
+    _check(weight.dtype in _WEIGHT_DTYPES, f"{name} must be float32 or bfloat16")
+    _check(weight.dim() == 2, f"{name} must be [out_features, in_features]")
+    return weight.contiguous()
+
+
+def _linear_into(rows: torch.Tensor, count: int, stride: int, weight: torch.Tensor, bias, out: torch.Tensor,
+                 out_stride: int) -> None:
+    n, k = weight.shape
+    _call("mlk_linear", _ptr(rows), count, k, stride, _ptr(weight), _WEIGHT_DTYPES[weight.dtype], _ptr(bias), n,
+          _ptr(out), out_stride, _stream())
+
+
+def linear(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """linear_dispatch (montlok.cpp:67-91): input [..., K] @ weight[N, K]^T + bias -> [..., N].
+
+    weight may be float32 or bfloat16 (bf16 matrix cores, fp32 accumulate)."""
+    _require_f32_gpu(input, "input")
+    w = _weight(weight)
+    n, k = w.shape
+    _check(input.dim() >= 1 and input.size(-1) == k, f"input must end in in_features={k}")
+    b = None
+    if bias is not None and bias.numel() > 0:
+        b = _dense_parameter(bias, n, "bias")
+    rows, count, stride = _rows(input, k)
+    out = torch.empty((count, n), dtype=torch.float32, device=input.device)
+    _linear_into(rows, count, stride, w, b, out, n)
+    return out.view(*input.shape[:-1], n)
+
+
+def swiglu_mlp(input, in_weight, in_bias=None, out_weight=None, out_bias=None):
+    """montlok.cpp:967-976: linear -> swiglu -> linear."""
+    return linear(swiglu(linear(input, in_weight, in_bias)), out_weight, out_bias)
 
 
 # ------------------------------------------------------------------ mHC
@@ -399,6 +442,39 @@ def mamba3_siso_step(projected, state, b_bias, c_bias, b_norm_w, c_norm_w, dt_bi
     return out
 
 
+def mamba3_siso_layer(inputs, in_weight, out_weight, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state,
+                      ngroups, nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor):
+    """montlok.cpp:496-519: in_proj -> mamba3_siso_forward (in-kernel gate) -> out_proj."""
+    projected = linear(inputs, in_weight)
+    output = mamba3_siso_forward(projected, None, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups,
+                                 nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor)
+    return linear(output, out_weight)
+
+
+def stage1_forward(inputs, layers, mamba_norm_eps, mamba_norm_groups, ffn_norm_eps, d_state, ngroups, nheads, headdim,
+                   num_rope_angles, b_eps, c_eps, a_floor):
+    """montlok.cpp:1011-1053. Each layer pack holds 14 tensors: outer norm, Mamba in/out, B/C bias and norm,
+    dt bias, D, FFN norm, FFN in weight/bias, FFN out weight/bias (empty tensor = no bias)."""
+    _check(len(layers) > 0, "stage1 layers must not be empty")
+    for layer in layers:
+        _check(len(layer) == 14, "each stage1 tensor pack must contain 14 tensors")
+    hidden = inputs
+    mamba_input = rms_norm(hidden, layers[0][0], mamba_norm_eps, mamba_norm_groups)
+    for index, layer in enumerate(layers):
+        mamba_output = mamba3_siso_layer(mamba_input, *layer[1:9], d_state, ngroups, nheads, headdim,
+                                         num_rope_angles, b_eps, c_eps, a_floor)
+        hidden, normalized = add_rms_norm(hidden, mamba_output, layer[9], ffn_norm_eps, 1)
+        in_bias = layer[11] if layer[11].numel() else None
+        out_bias = layer[13] if layer[13].numel() else None
+        ffn_output = swiglu_mlp(normalized, layer[10], in_bias, layer[12], out_bias)
+        if index + 1 == len(layers):
+            hidden = hidden + ffn_output
+        else:
+            hidden, mamba_input = add_rms_norm(hidden, ffn_output, layers[index + 1][0], mamba_norm_eps,
+                                               mamba_norm_groups)
+    return hidden
+
+
 def new_mamba3_state(streams: int, nheads: int, d_state: int, headdim: int, num_rope_angles: int, device) -> dict:
     """Zero carried state for mamba3_siso_step."""
     return {"ssm": torch.zeros(streams, nheads, d_state, headdim, device=device),
@@ -441,7 +517,7 @@ def exported_symbols() -> list[str]:
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent", "mlk_mamba3_siso_forward",
-            "mlk_mamba3_siso_step"]
+            "mlk_mamba3_siso_step", "mlk_linear"]
 
 
 def math_check(x: torch.Tensor) -> dict:

@@ -1,0 +1,172 @@
+"""GPU parity of the matrix-core linear and the ops built on it (linear,
+swiglu_mlp, mamba3_siso_layer, stage1_forward).
+
+The reference runs these GEMMs in oneDNN fp32 (montlok.cpp:67-91); the oracle
+is an fp64 dot product rounded once. Gates (normwise relative error): fp32
+weights 1e-5; bf16 weights 2e-2 against the fp32 product with the weights
+upcast (the contract for bf16-weight configs), and 1e-6 against the exact
+product of bf16-rounded inputs and weights, which pins what the kernel
+computes: x rounded to bf16 (nearest even), fp32 accumulation.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16_TOL, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _bf16_round(a: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).bfloat16().float().numpy()
+
+
+SHAPES = [(2048, 64, 304, False),    # RMSNorm->Mamba-3 block in_proj
+          (2048, 128, 64, False),    # ... and out_proj
+          (1000, 40, 256, True),     # raw-feature projection with bias
+          (37, 7, 5, True),          # ragged everything
+          (333, 300, 70, False),     # K beyond one 256-wide chunk
+          (4100, 520, 1, True),      # one output column, two K chunks
+          (1, 256, 336, False),      # a single row
+          (64, 512, 1192, False)]    # full-stack Mamba in_proj width
+
+
+@pytest.mark.parametrize("M,K,N,with_bias", SHAPES)
+def test_linear_fp32_weights(dev, oracle, M, K, N, with_bias):
+    from montlok import _C
+
+    rng = np.random.default_rng(M + K + N)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if with_bias else None
+    out = _C.linear(_t(x, dev), _t(w, dev), None if b is None else _t(b, dev))
+    assert out.shape == (M, N)
+    assert_close(out, oracle.linear(x, w, b), name=f"linear fp32 {M}x{K}->{N}")
+
+
+@pytest.mark.parametrize("M,K,N,with_bias", SHAPES)
+def test_linear_bf16_weights(dev, oracle, M, K, N, with_bias):
+    from montlok import _C
+
+    rng = np.random.default_rng(M * 3 + K + N)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = _bf16_round(rng.standard_normal((N, K)) * 0.02)
+    b = rng.standard_normal(N).astype(np.float32) if with_bias else None
+    out = _C.linear(_t(x, dev), _t(w, dev).bfloat16(), None if b is None else _t(b, dev))
+    assert_close(out, oracle.linear(x, w, b), tol=BF16_TOL, name="bf16 weights vs fp32 product")
+    assert_close(out, oracle.linear(_bf16_round(x), w, b), tol=1e-6, name="bf16 weights vs bf16-input product")
+
+
+def test_linear_strided_input_and_leading_dims(dev, oracle):
+    """A column slice of a wider buffer (montlok.cpp:52-55 accepts leading strides) and [B, L, K] inputs."""
+    from montlok import _C
+
+    rng = np.random.default_rng(5)
+    wide = _t(rng.standard_normal((3, 50, 100)).astype(np.float32), dev)
+    x = wide[:, :, 12:76]
+    w = rng.standard_normal((48, 64)).astype(np.float32)
+    out = _C.linear(x, _t(w, dev))
+    assert out.shape == (3, 50, 48)
+    assert_close(out, oracle.linear(x.cpu().numpy(), w), name="strided linear")
+
+
+def test_linear_errors(dev):
+    from montlok import _C
+
+    x = torch.zeros(4, 8, device=dev)
+    with pytest.raises(RuntimeError, match="input must end in in_features=16"):
+        _C.linear(x, torch.zeros(3, 16, device=dev))
+    with pytest.raises(RuntimeError, match="weight must be float32 or bfloat16"):
+        _C.linear(x, torch.zeros(3, 8, device=dev, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="bias must have 3 elements"):
+        _C.linear(x, torch.zeros(3, 8, device=dev), torch.zeros(4, device=dev))
+    with pytest.raises(RuntimeError, match="input must be on the GPU"):
+        _C.linear(torch.zeros(4, 8), torch.zeros(3, 8, device=dev))
+
+
+def test_swiglu_mlp(dev, oracle):
+    from montlok import _C
+
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((300, 64)).astype(np.float32)
+    w_in = (rng.standard_normal((256, 64)) / 8).astype(np.float32)
+    b_in = rng.standard_normal(256).astype(np.float32)
+    w_out = (rng.standard_normal((64, 128)) / 11).astype(np.float32)
+    out = _C.swiglu_mlp(_t(x, dev), _t(w_in, dev), _t(b_in, dev), _t(w_out, dev), None)
+    expect = oracle.linear(oracle.swiglu(oracle.linear(x, w_in, b_in)), w_out)
+    assert_close(out, expect, name="swiglu_mlp")
+
+
+def _mamba_layer_params(rng, d_model, N, H, D, R, G=1):
+    d_inner = H * D
+    W = 2 * d_inner + 2 * G * N + 3 * H + R
+    bound_in, bound_out = 1 / np.sqrt(d_model), 1 / np.sqrt(d_inner)
+    return dict(in_w=rng.uniform(-bound_in, bound_in, (W, d_model)).astype(np.float32),
+                out_w=rng.uniform(-bound_out, bound_out, (d_model, d_inner)).astype(np.float32),
+                b_bias=np.ones((H, N), np.float32), c_bias=np.ones((H, N), np.float32),
+                b_norm_w=np.ones(N, np.float32), c_norm_w=np.ones(N, np.float32),
+                dt_bias=np.log(np.expm1(np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), H)))).astype(np.float32),
+                skip=np.ones(H, np.float32))
+
+
+_MAMBA_KEYS = ("in_w", "out_w", "b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")
+
+
+def _oracle_mamba_layer(oracle, x, p, N, G, H, D, R):
+    projected = oracle.linear(x, p["in_w"])
+    y = oracle.mamba3_siso_forward(projected, N, G, H, D, R, p["b_bias"], p["c_bias"], p["b_norm_w"], p["c_norm_w"],
+                                   1e-5, 1e-5, p["dt_bias"], p["skip"], 1e-4)
+    return oracle.linear(y, p["out_w"])
+
+
+def test_mamba3_siso_layer_block_geometry(dev, oracle):
+    """RMSNorm->Mamba-3 block: 64 windows x 32 tokens, d_model 64, 4 heads, d_state 16, expand 2."""
+    from montlok import _C
+
+    rng = np.random.default_rng(0)
+    B, L, d, N, H, D, R = 64, 32, 64, 16, 4, 32, 4
+    x = rng.standard_normal((B, L, d)).astype(np.float32)
+    p = _mamba_layer_params(rng, d, N, H, D, R)
+    out = _C.mamba3_siso_layer(_t(x, dev), *(_t(p[k], dev) for k in _MAMBA_KEYS), N, 1, H, D, R, 1e-5, 1e-5, 1e-4)
+    assert_close(out, _oracle_mamba_layer(oracle, x, p, N, 1, H, D, R), name="mamba3_siso_layer")
+
+
+def test_stage1_forward_two_layers(dev, oracle):
+    """montlok.cpp:1011-1053 chained over two layers, against the same chain of oracle ops."""
+    from montlok import _C
+
+    rng = np.random.default_rng(3)
+    B, L, d, N, H, D, R, groups = 4, 24, 64, 16, 4, 32, 4, 8
+    x = rng.standard_normal((B, L, d)).astype(np.float32)
+    packs_np = []
+    for _ in range(2):
+        p = _mamba_layer_params(rng, d, N, H, D, R)
+        norm_w = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+        ffn_norm_w = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+        ffn_in = (rng.standard_normal((4 * d, d)) / 8).astype(np.float32)
+        ffn_in_b = (0.1 * rng.standard_normal(4 * d)).astype(np.float32)
+        ffn_out = (rng.standard_normal((d, 2 * d)) / 11).astype(np.float32)
+        packs_np.append([norm_w] + [p[k] for k in _MAMBA_KEYS] + [ffn_norm_w, ffn_in, ffn_in_b, ffn_out,
+                                                                   np.zeros(0, np.float32)])
+    packs = [[_t(a, dev) for a in pack] for pack in packs_np]
+    out = _C.stage1_forward(_t(x, dev), packs, 1e-5, groups, 1e-5, N, 1, H, D, R, 1e-5, 1e-5, 1e-4)
+
+    hidden = x
+    mamba_in = oracle.rms_norm(hidden, packs_np[0][0], 1e-5, groups)
+    for i, pk in enumerate(packs_np):
+        p = dict(zip(_MAMBA_KEYS, pk[1:9]))
+        m = _oracle_mamba_layer(oracle, mamba_in, p, N, 1, H, D, R)
+        hidden, normed = oracle.add_rms_norm(hidden, m, pk[9], 1e-5, 1)
+        ffn = oracle.linear(oracle.swiglu(oracle.linear(normed, pk[10], pk[11])), pk[12])
+        if i + 1 == len(packs_np):
+            hidden = hidden + ffn
+        else:
+            hidden, mamba_in = oracle.add_rms_norm(hidden, ffn, packs_np[i + 1][0], 1e-5, groups)
+    assert_close(out, hidden, name="stage1_forward")
