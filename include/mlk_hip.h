@@ -42,6 +42,14 @@ typedef enum mlk_dtype {
     MLK_DTYPE_BF16 = 1
 } mlk_dtype;
 
+/* Attention mask (which keys j a query i sees; queries sit at the trailing
+ * q_length of kv_length positions). */
+typedef enum mlk_mask {
+    MLK_MASK_NONE = 0,                /* every key */
+    MLK_MASK_CAUSAL_TOP_LEFT = 1,     /* j <= i (SDPA is_causal) */
+    MLK_MASK_CAUSAL_BOTTOM_RIGHT = 2  /* j <= kv_length - q_length + i */
+} mlk_mask;
+
 typedef enum mlk_status {
     MLK_OK = 0,
     MLK_ERR_INVALID_ARGUMENT = 1,
@@ -96,6 +104,35 @@ mlk_status mlk_swiglu(const float* x, int64_t rows, int64_t hidden, int64_t row_
 mlk_status mlk_linear(const float* x, int64_t rows, int64_t in_features, int64_t x_stride, const void* weight,
                       int32_t weight_dtype, const float* bias, int64_t out_features, float* out,
                       int64_t out_stride, mlk_stream_t stream);
+
+/* ----------------------------------------------------------------- MLA -- */
+
+/* mla_rope_qk(q, kv, k_rope, cos, sin, nope_dim) -- montlok.cpp:1093-1154,
+ * kernel montlok_layers.h:190-234. q: [B, q_length, H, head_dim] tokens
+ * `q_token_stride` floats apart, rotated IN PLACE on the last rope_dim =
+ * head_dim - nope_dim lanes of every head (rotate_half convention, fp64
+ * arithmetic, one rounding); the rows hold the trailing q_length positions.
+ * kv: [B, L, H, nope_dim + head_dim] contiguous; k_rope: [B, L, rope_dim]
+ * tokens `k_rope_token_stride` apart; cos/sin: [L, rope_dim] contiguous.
+ * k: [B, L, H, head_dim] = cat(kv[..., :nope_dim], rope(k_rope)). */
+mlk_status mlk_mla_rope_qk(float* q, int64_t q_token_stride, int64_t q_length, const float* kv,
+                           const float* k_rope, int64_t k_rope_token_stride, const float* cosine,
+                           const float* sine, int64_t batch, int64_t length, int64_t heads, int64_t head_dim,
+                           int64_t nope_dim, float* k, mlk_stream_t stream);
+
+/* Scaled dot-product attention, softmax(q k^T * scale) v, per window and
+ * head -- the at::scaled_dot_product_attention call of mla_forward
+ * (montlok.cpp:1205-1208) and of MLACPU._attend (python/montlok/rdt/mla.py
+ * :191-213). q: [B, q_length, H, head_dim], k/v: [B, kv_length, H,
+ * head_dim], each with its own token and head strides (dense head_dim);
+ * out: [B, q_length, H, head_dim] contiguous. mask: an mlk_mask. precision:
+ * MLK_DTYPE_BF16 (bf16 matrix cores, fp32 softmax and accumulation) or
+ * MLK_DTYPE_F32 (fp32 throughout). head_dim <= 128. */
+mlk_status mlk_attention(const float* q, int64_t q_token_stride, int64_t q_head_stride, const float* k,
+                         int64_t k_token_stride, int64_t k_head_stride, const float* v, int64_t v_token_stride,
+                         int64_t v_head_stride, int64_t batch, int64_t heads, int64_t q_length, int64_t kv_length,
+                         int64_t head_dim, int32_t mask, double scale, int32_t precision, float* out,
+                         mlk_stream_t stream);
 
 /* ----------------------------------------------------------------- mHC -- */
 

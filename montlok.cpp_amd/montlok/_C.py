@@ -43,6 +43,9 @@ def _load():
         "mlk_layer_norm": [_vp, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp],
         "mlk_swiglu": [_vp, _i64, _i64, _i64, _vp, _vp],
         "mlk_linear": [_vp, _i64, _i64, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp],
+        "mlk_mla_rope_qk": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
+        "mlk_attention": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, C.c_int32,
+                          _dbl, C.c_int32, _vp, _vp],
         "mlk_mhc_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                             _vp, _dbl, _vp, _vp, _vp, _vp, _vp],
         "mlk_mhc_combine": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp],
@@ -484,6 +487,102 @@ def new_mamba3_state(streams: int, nheads: int, d_state: int, headdim: int, num_
             "started": False}
 
 
+# ------------------------------------------------------------------ MLA
+
+MASK_NONE, MASK_CAUSAL_TOP_LEFT, MASK_CAUSAL_BOTTOM_RIGHT = 0, 1, 2
+
+
+def mla_rope_qk(q: torch.Tensor, kv: torch.Tensor, k_rope: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                nope_dim: int) -> torch.Tensor:
+    """montlok.cpp:1093-1154: rotates q's rope lanes IN PLACE and returns k = cat(k_nope, rope(k_rope))."""
+    for t, name in ((q, "q"), (kv, "kv"), (k_rope, "k_rope"), (cos, "cos"), (sin, "sin")):
+        _require_f32_gpu(t, name)
+    _check(q.dim() == 4, "q must be [B,Lq,H,head_dim]")
+    _check(kv.dim() == 4 and kv.is_contiguous(), "kv must be contiguous [B,L,H,nope_dim+head_dim]")
+    batch, q_length, heads, head_dim = q.shape
+    length = kv.size(1)
+    rope_dim = head_dim - nope_dim
+    _check(nope_dim >= 0 and rope_dim > 0 and rope_dim % 2 == 0, "head_dim - nope_dim must be a positive even rope_dim")
+    _check(1 <= q_length <= length, "q must cover between 1 and L trailing positions")
+    _check((q.stride(3) == 1 or head_dim == 1) and (q.stride(2) == head_dim or heads == 1) and
+           (q.stride(0) == q_length * q.stride(1) or batch == 1),
+           "q must be dense within a token with a uniform token stride")
+    _check(tuple(kv.shape) == (batch, length, heads, nope_dim + head_dim), "kv must be [B,L,H,nope_dim+head_dim]")
+    _check(tuple(k_rope.shape) == (batch, length, rope_dim), "k_rope must be [B,L,rope_dim]")
+    _check((k_rope.stride(2) == 1 or rope_dim == 1) and (k_rope.stride(0) == length * k_rope.stride(1) or batch == 1),
+           "k_rope must be dense within a token with a uniform token stride")
+    _check(tuple(cos.shape) == (length, rope_dim) and cos.is_contiguous(), "cos must be contiguous [L,rope_dim]")
+    _check(sin.shape == cos.shape and sin.is_contiguous(), "sin must be contiguous [L,rope_dim]")
+    k = torch.empty((batch, length, heads, head_dim), dtype=torch.float32, device=q.device)
+    q_ts = q.stride(1) if q_length > 1 or batch == 1 else q.stride(0)
+    kr_ts = k_rope.stride(1) if length > 1 else k_rope.stride(0)
+    _call("mlk_mla_rope_qk", _ptr(q), max(q_ts, heads * head_dim), q_length, _ptr(kv), _ptr(k_rope),
+          max(kr_ts, rope_dim), _ptr(cos), _ptr(sin), batch, length, heads, head_dim, nope_dim, _ptr(k), _stream())
+    return k
+
+
+def _token_strides(t: torch.Tensor, name: str) -> tuple[int, int]:
+    """(token stride, head stride) of a [B, L, H, hd] view whose sequences are L tokens apart."""
+    B, L, H, hd = t.shape
+    _check(t.stride(3) == 1 or hd == 1, f"{name} must be dense in head_dim")
+    ts = t.stride(1) if L > 1 else (t.stride(0) if B > 1 else H * t.stride(2))
+    _check(B == 1 or t.stride(0) == L * ts, f"{name} must have a uniform token stride")
+    return ts, (t.stride(2) if H > 1 else hd)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: int, scale: float,
+              precision: torch.dtype = torch.float32) -> torch.Tensor:
+    """softmax(q k^T * scale) v over [B, L, H, hd] views -> [B, Lq, H, hd] (montlok.cpp:1205-1208).
+
+    mask: MASK_NONE, MASK_CAUSAL_TOP_LEFT (is_causal) or MASK_CAUSAL_BOTTOM_RIGHT (trailing queries).
+    precision: torch.bfloat16 runs QK^T and PV on bf16 matrix cores, torch.float32 stays fp32."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _require_f32_gpu(t, name)
+        _check(t.dim() == 4, f"{name} must be [B,L,H,head_dim]")
+    B, Lq, H, hd = q.shape
+    Lk = k.size(1)
+    _check(tuple(k.shape) == (B, Lk, H, hd) and tuple(v.shape) == (B, Lk, H, hd), "k and v must be [B,L,H,head_dim]")
+    _check(precision in (torch.float32, torch.bfloat16), "precision must be float32 or bfloat16")
+    qs, ks, vs = _token_strides(q, "q"), _token_strides(k, "k"), _token_strides(v, "v")
+    out = torch.empty((B, Lq, H, hd), dtype=torch.float32, device=q.device)
+    _call("mlk_attention", _ptr(q), *qs, _ptr(k), *ks, _ptr(v), *vs, B, H, Lq, Lk, hd, int(mask), float(scale),
+          _WEIGHT_DTYPES[precision], _ptr(out), _stream())
+    return out
+
+
+def mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight,
+                cosine, sine, n_heads, head_dim, nope_dim, kv_lora_rank, n_last, causal, scale):
+    """montlok.cpp:1159-1211: projection, latent LayerNorm, kv_up, RoPE, attention and output projection.
+
+    Weights may be float32 or bfloat16; with bf16 weights the attention contractions run on bf16 matrix
+    cores as well (fp32 softmax and accumulation)."""
+    _require_f32_gpu(x, "x")
+    _check(x.dim() == 3, "x must be [B,L,d_model]")
+    batch, length, d_model = x.shape
+    _check(n_heads > 0 and head_dim > 0 and d_model == n_heads * head_dim, "invalid MLA head geometry")
+    _check(0 <= nope_dim < head_dim and kv_lora_rank > 0, "invalid MLA latent geometry")
+    _check(n_last == 1 or n_last == length, "native MLA supports the final query or the full sequence")
+    precision = torch.bfloat16 if _weight(in_proj_weight, "in_proj_weight").dtype == torch.bfloat16 else torch.float32
+    full = n_last == length
+    projected = linear(x, in_proj_weight)
+    q_width = d_model if full else 0
+    if full:
+        q = projected[..., :q_width]
+    else:
+        _check(q_weight.numel() == d_model * d_model, "q_weight must be [d_model,d_model] for a tail query")
+        q = linear(x[:, length - 1:], q_weight)
+    q = q.view(batch, n_last, n_heads, head_dim) if q.is_contiguous() else q.unflatten(-1, (n_heads, head_dim))
+    kv_latent = projected[..., q_width:q_width + kv_lora_rank]
+    k_rope = projected[..., q_width + kv_lora_rank:]
+    kv_normalized = layer_norm(kv_latent, kv_norm_weight, kv_norm_bias, kv_norm_eps)
+    kv = linear(kv_normalized, kv_up_weight).view(batch, length, n_heads, nope_dim + head_dim)
+    k = mla_rope_qk(q, kv, k_rope, cosine, sine, nope_dim)
+    v = kv[..., nope_dim:]
+    mask = MASK_CAUSAL_TOP_LEFT if (full and causal) else MASK_NONE
+    attended = attention(q, k, v, mask, scale, precision)
+    return linear(attended.view(batch, n_last, d_model), out_weight)
+
+
 # ------------------------------------------------------------------ introspection
 
 
@@ -517,7 +616,7 @@ def exported_symbols() -> list[str]:
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent", "mlk_mamba3_siso_forward",
-            "mlk_mamba3_siso_step", "mlk_linear"]
+            "mlk_mamba3_siso_step", "mlk_linear", "mlk_mla_rope_qk", "mlk_attention"]
 
 
 def math_check(x: torch.Tensor) -> dict:

@@ -1,0 +1,201 @@
+"""GPU parity of MLA: the rotary key assembly (mla_rope_qk), the attention
+contraction, and the whole mla_forward block.
+
+mla_rope_qk is fp64 arithmetic rounded once, the same operations as the
+reference kernel, so it is compared bit for bit with the reference's golden
+vectors and the oracle. Attention and mla_forward are compared with the
+oracle's float64 softmax attention (which itself is pinned against torch in
+float64): fp32 precision and fp32 weights within 1e-5, bf16 precision and
+bf16 weights within 2e-2 (normwise relative).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16_TOL, assert_bitwise, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def rope_tables(length: int, rope_dim: int, theta: float = 10000.0):
+    """Token-index RoPE tables as the reference builds them with torch on the CPU
+    (reference/Model/layers/rope.py:9-16, 138-166): cat(angles, angles)."""
+    idx = torch.arange(0, rope_dim, 2, dtype=torch.float32)
+    freqs = 1.0 / (theta ** (idx / rope_dim))
+    pos = torch.arange(0, length, dtype=torch.float32)
+    angles = pos.unsqueeze(-1) * freqs.unsqueeze(0)
+    emb = torch.cat([angles, angles], dim=-1)
+    return emb.cos().numpy(), emb.sin().numpy()
+
+
+def test_rope_golden(dev, golden):
+    from montlok import _C
+
+    g = golden("rope")
+    cases = sorted({k.split("_")[0] for k in g})
+    for c in cases:
+        case = {k[len(c) + 1:]: v for k, v in g.items() if k.startswith(c + "_")}
+        nope = int(case["nope"][0])
+        q = _t(case["q"], dev)
+        k = _C.mla_rope_qk(q, _t(case["kv"], dev), _t(case["k_rope"], dev), _t(case["cos"], dev),
+                           _t(case["sin"], dev), nope)
+        assert_bitwise(q, case["q_out"], f"{c} q")
+        assert_bitwise(k, case["k_out"], f"{c} k")
+
+
+@pytest.mark.parametrize("B,L,Lq,H,hd,nope", [(4, 128, 128, 8, 32, 16), (2, 256, 256, 4, 64, 32),
+                                              (3, 19, 5, 3, 12, 4), (2, 33, 1, 2, 64, 0)])
+def test_rope_vs_oracle_column_slices(dev, oracle, B, L, Lq, H, hd, nope):
+    """q and k_rope as column slices of one fused projection output (montlok.cpp:1109-1118)."""
+    from montlok import _C
+
+    rng = np.random.default_rng(B * L + hd)
+    rope = hd - nope
+    kv_rank = 16
+    W = H * hd + kv_rank + rope
+    proj = rng.standard_normal((B, L, W)).astype(np.float32)
+    kv = rng.standard_normal((B, L, H, nope + hd)).astype(np.float32)
+    cos, sin = rope_tables(L, rope)
+    tproj = _t(proj, dev)
+    q_full = tproj[:, L - Lq:, :H * hd]
+    q = torch.empty((B, Lq, H * hd), device=dev)
+    q.copy_(q_full)
+    q = q.view(B, Lq, H, hd) if Lq != L else q_full.unflatten(-1, (H, hd))
+    k_rope = tproj[..., H * hd + kv_rank:]
+    k = _C.mla_rope_qk(q, _t(kv, dev), k_rope, _t(cos, dev), _t(sin, dev), nope)
+    q_exp, k_exp = oracle.mla_rope(proj[:, L - Lq:, :H * hd].reshape(B, Lq, H, hd), kv, proj[..., H * hd + kv_rank:],
+                                   cos, sin, nope)
+    assert_bitwise(k, k_exp, "k")
+    assert_bitwise(q, q_exp, "q rotated in place")
+
+
+ATTN_CASES = [  # B, Lq, Lk, H, hd, mask
+    (3, 128, 128, 8, 32, 1),   # MLA block geometry, causal
+    (2, 256, 256, 4, 64, 1),   # full-stack MLA geometry
+    (2, 200, 200, 2, 48, 1),   # ragged length, hd padded inside the kernel
+    (2, 1, 77, 3, 32, 0),      # one trailing query sees every key
+    (2, 5, 77, 3, 16, 2),      # several trailing queries, bottom-right mask
+    (1, 130, 130, 1, 128, 0),  # widest head, no mask
+    (2, 480, 480, 2, 64, 1),   # the deployed sequence length
+]
+
+
+@pytest.mark.parametrize("B,Lq,Lk,H,hd,mask", ATTN_CASES)
+@pytest.mark.parametrize("precision", [torch.float32, torch.bfloat16])
+def test_attention_vs_oracle(dev, oracle, B, Lq, Lk, H, hd, mask, precision):
+    from montlok import _C
+
+    rng = np.random.default_rng(B + Lq + Lk + hd + mask)
+    q = rng.standard_normal((B, Lq, H, hd)).astype(np.float32)
+    k = rng.standard_normal((B, Lk, H, hd)).astype(np.float32)
+    v = rng.standard_normal((B, Lk, H, hd)).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    out = _C.attention(_t(q, dev), _t(k, dev), _t(v, dev), mask, scale, precision)
+    expect = oracle.sdpa(q, k, v, mask, scale)
+    tol = 1e-5 if precision == torch.float32 else BF16_TOL
+    assert_close(out, expect, tol=tol, name=f"attention {precision}")
+
+
+def test_attention_strided_views(dev, oracle):
+    """q as a column slice of a projection, v as the tail of each kv head (mla_forward's views)."""
+    from montlok import _C
+
+    rng = np.random.default_rng(17)
+    B, L, H, hd, nope = 3, 70, 4, 32, 16
+    proj = _t(rng.standard_normal((B, L, H * hd + 40)).astype(np.float32), dev)
+    q = proj[..., :H * hd].unflatten(-1, (H, hd))
+    kv = _t(rng.standard_normal((B, L, H, nope + hd)).astype(np.float32), dev)
+    v = kv[..., nope:]
+    k = _t(rng.standard_normal((B, L, H, hd)).astype(np.float32), dev)
+    out = _C.attention(q, k, v, _C.MASK_CAUSAL_TOP_LEFT, 0.2)
+    expect = oracle.sdpa(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), 1, 0.2)
+    assert_close(out, expect, name="strided attention")
+
+
+def _mla_params(rng, d, H, hd, nope, kv_rank, bf16):
+    rope = hd - nope
+    std = 0.02 if bf16 else 1 / math.sqrt(d)
+    p = dict(q=rng.standard_normal((H * hd, d)) * std, kv_down=rng.standard_normal((kv_rank, d)) * std,
+             k_rope=rng.standard_normal((rope, d)) * std,
+             kv_up=rng.standard_normal((H * (nope + hd), kv_rank)) * (0.02 if bf16 else 1 / math.sqrt(kv_rank)),
+             o=rng.standard_normal((d, H * hd)) * (0.02 if bf16 else 1 / math.sqrt(H * hd)))
+    p = {k: v.astype(np.float32) for k, v in p.items()}
+    if bf16:
+        p = {k: torch.from_numpy(v).bfloat16().float().numpy() for k, v in p.items()}
+    p["ln_w"] = (1 + 0.1 * rng.standard_normal(kv_rank)).astype(np.float32)
+    p["ln_b"] = (0.1 * rng.standard_normal(kv_rank)).astype(np.float32)
+    return p
+
+
+def _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, n_last, causal, scale, cos, sin):
+    B, L, d = x.shape
+    in_w = np.concatenate([p["q"], p["kv_down"], p["k_rope"]]) if n_last == L else np.concatenate(
+        [p["kv_down"], p["k_rope"]])
+    projected = oracle.linear(x, in_w)
+    qw = d if n_last == L else 0
+    q = projected[..., :qw] if n_last == L else oracle.linear(x[:, L - 1:], p["q"])
+    q = q.reshape(B, n_last, H, hd)
+    kv_lat = projected[..., qw:qw + kv_rank]
+    k_rope = projected[..., qw + kv_rank:]
+    kv = oracle.linear(oracle.layer_norm(kv_lat, p["ln_w"], p["ln_b"], 1e-5), p["kv_up"]).reshape(B, L, H, nope + hd)
+    q, k = oracle.mla_rope(q, kv, k_rope, cos, sin, nope)
+    att = oracle.sdpa(q, k, np.ascontiguousarray(kv[..., nope:]), 1 if (n_last == L and causal) else 0, scale)
+    return oracle.linear(att.reshape(B, n_last, d), p["o"])
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("n_last", ["full", 1])
+def test_mla_forward_block_geometry(dev, oracle, bf16, n_last):
+    """d_model 256, 8 heads of 32 (rope 16, nope 16), kv rank 64, 128 tokens; 16 windows."""
+    from montlok import _C
+
+    rng = np.random.default_rng(1 + bf16)
+    B, L, d, H, hd, nope, kv_rank = 16, 128, 256, 8, 32, 16, 64
+    n_last = L if n_last == "full" else n_last
+    x = rng.standard_normal((B, L, d)).astype(np.float32)
+    p = _mla_params(rng, d, H, hd, nope, kv_rank, bf16)
+    cos, sin = rope_tables(L, hd - nope)
+    scale = 1.0 / math.sqrt(hd)
+    wdt = torch.bfloat16 if bf16 else torch.float32
+
+    def w(a):
+        return _t(a, dev).to(wdt)
+
+    in_w = np.concatenate([p["q"], p["kv_down"], p["k_rope"]]) if n_last == L else np.concatenate(
+        [p["kv_down"], p["k_rope"]])
+    q_w = w(p["q"]) if n_last == 1 else torch.empty(0, device=dev)
+    out = _C.mla_forward(_t(x, dev), w(in_w), q_w, _t(p["ln_w"], dev), _t(p["ln_b"], dev), 1e-5, w(p["kv_up"]),
+                         w(p["o"]), _t(cos, dev), _t(sin, dev), H, hd, nope, kv_rank, n_last, True, scale)
+    assert out.shape == (B, n_last, d)
+    expect = _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, n_last, True, scale, cos, sin)
+    assert_close(out, expect, tol=BF16_TOL if bf16 else 1e-5, name=f"mla_forward bf16={bf16} n_last={n_last}")
+
+
+def test_mla_errors(dev):
+    from montlok import _C
+
+    x = torch.zeros(2, 8, 64, device=dev)
+    w = torch.zeros(64 + 16 + 8, 64, device=dev)
+    with pytest.raises(RuntimeError, match="invalid MLA head geometry"):
+        _C.mla_forward(x, w, x.new_empty(0), torch.ones(16, device=dev), None, 1e-5, w, w, w, w, 3, 16, 8, 16, 8,
+                       True, 0.25)
+    with pytest.raises(RuntimeError, match="native MLA supports the final query or the full sequence"):
+        _C.mla_forward(x, w, x.new_empty(0), torch.ones(16, device=dev), None, 1e-5, w, w, w, w, 4, 16, 8, 16, 3,
+                       True, 0.25)
+    q = torch.zeros(1, 4, 2, 16, device=dev)
+    kv = torch.zeros(1, 4, 2, 24, device=dev)
+    with pytest.raises(RuntimeError, match="positive even rope_dim"):
+        _C.mla_rope_qk(q, kv, torch.zeros(1, 4, 7, device=dev), torch.zeros(4, 7, device=dev),
+                       torch.zeros(4, 7, device=dev), 9)
+    with pytest.raises(RuntimeError, match="k_rope must be \\[B,L,rope_dim\\]"):
+        _C.mla_rope_qk(q, kv, torch.zeros(1, 4, 6, device=dev), torch.zeros(4, 8, device=dev),
+                       torch.zeros(4, 8, device=dev), 8)
