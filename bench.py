@@ -128,6 +128,85 @@ def _time_graph(g, replays: int) -> float:
     return start.elapsed_time(stop) / replays
 
 
+MFMA_PEAK_TFS = {"bf16": 2500.0, "f32": 157.3}
+RIDGE = {k: v * 1e3 / HBM_PEAK_GBS for k, v in MFMA_PEAK_TFS.items()}  # flop per byte
+
+
+def _op_times(ops: dict, replays: int, reps: int = 8) -> dict:
+    """Per-op milliseconds per launch: each op captured `reps` times in its own graph and replayed."""
+    times = {}
+    for name, op in ops.items():
+        g = _graph([op["fn"]] * reps)
+        for _ in range(2):
+            g.replay()
+        times[name] = _time_graph(g, replays) / reps
+    return times
+
+
+def _kernel_table(ops: dict, times: dict, precision: str) -> dict:
+    table = {}
+    for name, op in ops.items():
+        ms = times[name]
+        entry = {"launch_ms": ms, "algorithmic_bytes": op["bytes"], "achieved_GBs": op["bytes"] / (ms * 1e-3) / 1e9}
+        if op.get("flops"):
+            entry["flops"] = op["flops"]
+            entry["achieved_TFs"] = op["flops"] / (ms * 1e-3) / 1e12
+            entry["mfma_frac"] = entry["achieved_TFs"] / MFMA_PEAK_TFS[op.get("precision", precision)]
+        entry["hbm_frac"] = entry["achieved_GBs"] / HBM_PEAK_GBS
+        table[name] = entry
+    return table
+
+
+def _roofline(name: str, entry: dict, op: dict, precision: str, traffic=None) -> dict:
+    """HBM or MFMA roofline of one kernel, whichever its arithmetic intensity makes binding."""
+    prec = op.get("precision", precision)
+    flops = op.get("flops") or 0
+    if flops and flops / op["bytes"] > RIDGE[prec]:
+        return {"bound": "mfma", "kernel": name, "achieved": entry["achieved_TFs"], "peak": MFMA_PEAK_TFS[prec],
+                "unit": "TFLOP/s", "frac": entry["mfma_frac"], "traffic": traffic, "algorithmic_flops": flops,
+                "launch_ms": entry["launch_ms"]}
+    return {"bound": "hbm", "kernel": name, "achieved": entry["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": entry["hbm_frac"], "traffic": traffic, "algorithmic_bytes": op["bytes"],
+            "launch_ms": entry["launch_ms"]}
+
+
+def _base_line(value, unit, steps, warmup, ms, dtype, data, config) -> dict:
+    return {"metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+            "data": data, "config": config}
+
+
+def _time_steps(step_fns, steps: int, warmup: int, per_graph: int):
+    """Captures `per_graph` steps in one graph; returns (steps actually timed, ms per step)."""
+    g = _graph(step_fns * per_graph if len(step_fns) == 1 else step_fns)
+    replays = max(1, steps // per_graph)
+    for _ in range(max(1, warmup // per_graph)):
+        g.replay()
+    return replays * per_graph, _time_graph(g, replays) / per_graph
+
+
+def _torch_cpu_threads() -> int:
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def _timed_loop(fn, budget_s: float, cap: int = 100000) -> tuple[int, float]:
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s or reps >= cap:
+            return reps, elapsed
+
+
+# ---------------------------------------------------------------- workloads
+
+
 def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
     import torch
 
@@ -242,7 +321,429 @@ def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
     return line
 
 
-WORKLOADS = {"mhc": bench_mhc}
+# ------------------------------------------------------------ Mamba-3 block
+
+# RMSNorm -> Mamba-3 block, fp32: 64 windows x 32 tokens, d_model 64, 4 heads, d_state 16, expand 2.
+BLOCK = dict(windows=64, seq=32, d_model=64, d_state=16, headdim=32, expand=2, norm_groups=8)
+
+
+def _mamba_geometry(d_model: int, d_state: int, headdim: int, expand: int) -> dict:
+    """Mamba-3 geometry: d_inner = expand d_model, H = d_inner / headdim, R = d_state / 4 rotary angles
+    (rope fraction 0.5, mamba3.py:121-124), in_proj width 2 d_inner + 2 N + 3 H + R (one B/C group)."""
+    d_inner = expand * d_model
+    H = d_inner // headdim
+    R = ((d_state // 2) // 2 * 2) // 2
+    return dict(d_inner=d_inner, H=H, N=d_state, D=headdim, R=R, G=1, W=2 * d_inner + 2 * d_state + 3 * H + R)
+
+
+def _mamba_weights(g, d_model: int, geo: dict, dev, dtype=None):
+    """nn.Linear default (Kaiming-uniform) projections; dt_bias so softplus(dt_bias) is log-uniform in
+    [1e-3, 1e-1] (mamba3.py:128-130); B/C biases, B/C norm weights and D at their init (ones)."""
+    import math
+
+    import torch
+
+    W, d_inner, H, N = geo["W"], geo["d_inner"], geo["H"], geo["N"]
+    b_in, b_out = 1 / math.sqrt(d_model), 1 / math.sqrt(d_inner)
+    in_w = (torch.rand(W, d_model, generator=g) * 2 - 1) * b_in
+    out_w = (torch.rand(d_model, d_inner, generator=g) * 2 - 1) * b_out
+    dt = torch.exp(torch.rand(H, generator=g) * (math.log(1e-1) - math.log(1e-3)) + math.log(1e-3))
+    dt_bias = dt + torch.log(-torch.expm1(-dt))
+    params = dict(in_w=in_w, out_w=out_w, b_bias=torch.ones(H, N), c_bias=torch.ones(H, N), b_norm_w=torch.ones(N),
+                  c_norm_w=torch.ones(N), dt_bias=dt_bias, skip=torch.ones(H))
+    return {k: v.to(dev) if dtype is None or k not in ("in_w", "out_w") else v.to(dev, dtype)
+            for k, v in params.items()}
+
+
+MAMBA_PARAM_KEYS = ("b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")
+
+
+def cpu_baseline_block(cfg: dict, x_cpu, norm_w, weights: dict, geo: dict, budget_s: float = 10.0) -> dict:
+    """Reference CPU kernels (oracle/_ref) for the norm and the mixer, torch CPU for the two GEMMs and the
+    residual add, as the reference itself calls oneDNN / at::linear (montlok.cpp:67-91)."""
+    import torch
+
+    from oracle import Oracle, Reference, reference_available
+
+    cores = _torch_cpu_threads()
+    lib = Reference() if reference_available() else Oracle()
+    kind = "reference" if isinstance(lib, Reference) else "port"
+    if kind == "reference":
+        lib.set_threads(cores)
+    w = {k: v.cpu() for k, v in weights.items()}
+    x = x_cpu.numpy()
+    nw = norm_w.cpu().numpy()
+    p = [w[k].numpy() for k in MAMBA_PARAM_KEYS]
+    N, G, H, D, R = geo["N"], geo["G"], geo["H"], geo["D"], geo["R"]
+
+    def step():
+        h = torch.from_numpy(lib.rms_norm(x, nw, 1e-5, cfg["norm_groups"]))
+        proj = torch.nn.functional.linear(h, w["in_w"]).numpy()
+        y = lib.mamba3_siso_forward(proj, N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4)
+        return x_cpu + torch.nn.functional.linear(torch.from_numpy(y), w["out_w"])
+
+    reps, elapsed = _timed_loop(step, budget_s)
+    return {"value": reps * cfg["windows"] / elapsed, "unit": "windows/s", "cores": cores, "kind": kind,
+            "sample": f"{reps} full steps ({cfg['windows']} windows x {cfg['seq']} tokens) in {elapsed:.1f} s; "
+                      f"norm + mixer in the {'reference ' + lib.variant if kind == 'reference' else 'oracle'} "
+                      f"build, GEMMs in torch CPU, {cores} threads"}
+
+
+def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
+    import torch
+
+    from montlok import _C
+
+    cfg = BLOCK
+    geo = _mamba_geometry(cfg["d_model"], cfg["d_state"], cfg["headdim"], cfg["expand"])
+    B, L, d = cfg["windows"], cfg["seq"], cfg["d_model"]
+    T = B * L
+    N, G, H, D, R, W, d_inner = (geo[k] for k in ("N", "G", "H", "D", "R", "W", "d_inner"))
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    x_cpu = torch.randn(B, L, d, generator=g)
+    x = x_cpu.to(dev)
+    norm_w = torch.ones(d, device=dev)
+    wts = _mamba_weights(g, d, geo, dev)
+    mp = [wts[k] for k in MAMBA_PARAM_KEYS]
+    out = torch.empty_like(x)
+    consts = (N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+
+    def step():
+        h = _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"])
+        y = _C.mamba3_siso_layer(h, wts["in_w"], wts["out_w"], *mp, *consts)
+        torch.add(x, y, out=out)
+
+    step()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    steps, ms = _time_steps([step], steps, warmup, per_graph=16)
+    assert torch.equal(out, eager), "graph replay differs from the eager step"
+
+    h = _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"])
+    proj = _C.linear(h, wts["in_w"])
+    y = _C.mamba3_siso_forward(proj, None, *mp, *consts)
+    o = _C.linear(y, wts["out_w"])
+    f = 4
+    ops = {
+        "rms_norm": dict(fn=lambda: _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"]), bytes=2 * T * d * f + d * f),
+        "in_proj": dict(fn=lambda: _C.linear(h, wts["in_w"]), bytes=(T * d + W * d + T * W) * f,
+                        flops=2 * T * d * W),
+        "mamba3_siso_forward": dict(fn=lambda: _C.mamba3_siso_forward(proj, None, *mp, *consts),
+                                    bytes=(T * W + T * d_inner) * f, flops=7 * T * H * N * D),
+        "out_proj": dict(fn=lambda: _C.linear(y, wts["out_w"]), bytes=(T * d_inner + d * d_inner + T * d) * f,
+                         flops=2 * T * d_inner * d),
+        "residual_add": dict(fn=lambda: torch.add(x, o, out=out), bytes=3 * T * d * f),
+    }
+    table = _kernel_table(ops, _op_times(ops, max(4, steps // 16)), "f32")
+    dom = max(table, key=lambda k: table[k]["launch_ms"])
+    total_bytes = (2 * T * d + W * d + d * d_inner) * f + d * f
+    total_flops = 2 * T * d * W + 7 * T * H * N * D + 2 * T * d_inner * d
+    line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms, "f32",
+                      "synthetic (seeded N(0,1) inputs, Kaiming-uniform weights, dt bias per mamba3.py:128-130)",
+                      {"workload": "rmsnorm_mamba3_block", "windows": B, "seq_len": L, "d_model": d, "heads": H,
+                       "d_state": N, "headdim": D, "rope_angles": R, "expand": cfg["expand"],
+                       "norm_groups": cfg["norm_groups"], "step": "x + out_proj(mamba3(in_proj(GroupedRMSNorm(x))))",
+                       "launch": "HIP graph of 16 steps, replayed", "parallelism": "single GPU"})
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32")
+    line["kernels"] = table
+    line["step_algorithmic_bytes"] = total_bytes
+    line["step_algorithmic_flops"] = total_flops
+    line["step_hbm_frac"] = total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+    line["tokens_per_s"] = T / (ms * 1e-3)
+    if cpu:
+        line["cpu_baseline"] = cpu_baseline_block(cfg, x_cpu, norm_w, wts, geo)
+        line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
+    return line
+
+
+# --------------------------------------------------------------------- MLA
+
+# MLA causal self-attention fwd: 256 windows x 128 tokens, d_model 256, 8 heads of 32 (RoPE slice 16,
+# base 10000), KV latent rank 64, bf16 weights N(0, 0.02), fp32 inputs and accumulation.
+MLA = dict(windows=256, seq=128, d_model=256, heads=8, head_dim=32, rope=16, kv_rank=64, theta=10000.0)
+
+
+def rope_tables(length: int, rope_dim: int, theta: float):
+    """Token-index RoPE tables, built with torch on the CPU as the reference does
+    (reference/Model/layers/rope.py:9-16, 138-166)."""
+    import torch
+
+    idx = torch.arange(0, rope_dim, 2, dtype=torch.float32)
+    freqs = 1.0 / (theta ** (idx / rope_dim))
+    angles = torch.arange(0, length, dtype=torch.float32).unsqueeze(-1) * freqs.unsqueeze(0)
+    emb = torch.cat([angles, angles], dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def cpu_baseline_mla(cfg: dict, x_cpu, w: dict, cos, sin, budget_s: float = 10.0, windows: int = 16) -> dict:
+    """torch CPU for the GEMMs and SDPA (the reference calls oneDNN and at::scaled_dot_product_attention,
+    montlok.cpp:1187-1210), reference CPU kernels for the latent LayerNorm and the rotary step."""
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import Oracle, Reference, reference_available
+
+    cores = _torch_cpu_threads()
+    lib = Reference() if reference_available() else Oracle()
+    kind = "reference" if isinstance(lib, Reference) else "port"
+    if kind == "reference":
+        lib.set_threads(cores)
+    H, hd, r, kvr = cfg["heads"], cfg["head_dim"], cfg["rope"], cfg["kv_rank"]
+    nope = hd - r
+    x = x_cpu[:windows].contiguous()
+    B, L, d = x.shape
+    wf = {k: v.float().cpu() for k, v in w.items()}
+    cosn, sinn = cos.numpy(), sin.numpy()
+    scale = 1.0 / hd ** 0.5
+
+    def step():
+        projected = F.linear(x, wf["in_w"])
+        q = projected[..., :d].reshape(B, L, H, hd).numpy()
+        kv_lat = projected[..., d:d + kvr].contiguous().numpy()
+        k_rope = projected[..., d + kvr:].contiguous().numpy()
+        kvn = torch.from_numpy(lib.layer_norm(kv_lat, wf["ln_w"].numpy(), wf["ln_b"].numpy(), 1e-5))
+        kv = F.linear(kvn, wf["kv_up"]).reshape(B, L, H, nope + hd)
+        q, k = lib.mla_rope(q, kv.numpy(), k_rope, cosn, sinn, nope)
+        att = F.scaled_dot_product_attention(torch.from_numpy(q).transpose(1, 2), torch.from_numpy(k).transpose(1, 2),
+                                             kv[..., nope:].transpose(1, 2), is_causal=True, scale=scale)
+        return F.linear(att.transpose(1, 2).reshape(B, L, d), wf["o"])
+
+    reps, elapsed = _timed_loop(step, budget_s)
+    return {"value": reps * windows / elapsed, "unit": "windows/s", "cores": cores, "kind": kind,
+            "sample": f"{reps} steps over {windows} of the {cfg['windows']} windows in {elapsed:.1f} s (rate scales "
+                      f"per window); LayerNorm + RoPE in the {'reference ' + lib.variant if kind == 'reference' else 'oracle'} "
+                      f"build, GEMMs and SDPA in torch CPU (fp32, bf16 weights upcast), {cores} threads"}
+
+
+def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
+    import torch
+
+    from montlok import _C
+
+    cfg = MLA
+    B, L, d, H, hd, r, kvr = (cfg[k] for k in ("windows", "seq", "d_model", "heads", "head_dim", "rope", "kv_rank"))
+    nope = hd - r
+    T = B * L
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    sets = 8  # 8 x 32 MiB inputs plus the intermediates exceed the 256 MB Infinity Cache
+    x_cpu = torch.randn(B, L, d, generator=g)
+    xs = [x_cpu.to(dev)] + [torch.randn(B, L, d, generator=g).to(dev) for _ in range(sets - 1)]
+    bf = torch.bfloat16
+    w_cpu = dict(in_w=(torch.randn(d + kvr + r, d, generator=g) * 0.02).to(bf),
+                 kv_up=(torch.randn(H * (nope + hd), kvr, generator=g) * 0.02).to(bf),
+                 o=(torch.randn(d, H * hd, generator=g) * 0.02).to(bf), ln_w=torch.ones(kvr), ln_b=torch.zeros(kvr))
+    w = {k: v.to(dev) for k, v in w_cpu.items()}
+    cos_cpu, sin_cpu = rope_tables(L, r, cfg["theta"])
+    cos, sin = cos_cpu.to(dev), sin_cpu.to(dev)
+    empty = torch.empty(0, device=dev)
+    scale = 1.0 / hd ** 0.5
+    outs = [None] * sets
+
+    def step(i):
+        def run():
+            outs[i] = _C.mla_forward(xs[i], w["in_w"], empty, w["ln_w"], w["ln_b"], 1e-5, w["kv_up"], w["o"], cos, sin,
+                                     H, hd, nope, kvr, L, True, scale)
+        return run
+
+    step(0)()
+    torch.cuda.synchronize()
+    eager = outs[0].clone()
+    assert torch.isfinite(eager).all().item()
+    steps, ms = _time_steps([step(i) for i in range(sets)], steps, warmup, per_graph=sets)
+    assert torch.equal(outs[0], eager), "graph replay differs from the eager step"
+
+    x = xs[0]
+    projected = _C.linear(x, w["in_w"])
+    q = projected[..., :d].unflatten(-1, (H, hd))
+    kv_lat = projected[..., d:d + kvr]
+    k_rope = projected[..., d + kvr:]
+    kvn = _C.layer_norm(kv_lat, w["ln_w"], w["ln_b"], 1e-5)
+    kv = _C.linear(kvn, w["kv_up"]).view(B, L, H, nope + hd)
+    k = _C.mla_rope_qk(q, kv, k_rope, cos, sin, nope)
+    v = kv[..., nope:]
+    att = _C.attention(q, k, v, _C.MASK_CAUSAL_TOP_LEFT, scale, torch.bfloat16).view(B, L, d)
+    f, h2 = 4, 2
+    pairs = B * H * L * (L + 1) // 2
+    ops = {
+        "in_proj": dict(fn=lambda: _C.linear(x, w["in_w"]), bytes=T * d * f + (d + kvr + r) * d * h2 + T * (d + kvr + r) * f,
+                        flops=2 * T * d * (d + kvr + r)),
+        "kv_norm": dict(fn=lambda: _C.layer_norm(kv_lat, w["ln_w"], w["ln_b"], 1e-5), bytes=2 * T * kvr * f + 2 * kvr * f),
+        "kv_up": dict(fn=lambda: _C.linear(kvn, w["kv_up"]), bytes=T * kvr * f + H * (nope + hd) * kvr * h2 +
+                      T * H * (nope + hd) * f, flops=2 * T * kvr * H * (nope + hd)),
+        "rope_qk": dict(fn=lambda: _C.mla_rope_qk(q, kv, k_rope, cos, sin, nope),
+                        bytes=(2 * T * H * r + T * r + T * H * nope + T * H * hd + 2 * L * r) * f),
+        "attention": dict(fn=lambda: _C.attention(q, k, v, _C.MASK_CAUSAL_TOP_LEFT, scale, torch.bfloat16),
+                          bytes=4 * T * d * f, flops=4 * pairs * hd),
+        "o_proj": dict(fn=lambda: _C.linear(att, w["o"]), bytes=2 * T * d * f + d * d * h2, flops=2 * T * d * d),
+    }
+    table = _kernel_table(ops, _op_times(ops, max(4, steps // 8)), "bf16")
+    dom = max(table, key=lambda k: table[k]["launch_ms"])
+    total_bytes = 2 * T * d * f + ((d + kvr + r) * d + H * (nope + hd) * kvr + d * d) * h2
+    total_flops = sum(op.get("flops", 0) for op in ops.values())
+    line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms, "bf16 weights, f32 activations/accumulate",
+                      "synthetic (seeded N(0,1) inputs, N(0,0.02) bf16 weights)",
+                      {"workload": "mla_causal_fwd", "windows": B, "seq_len": L, "d_model": d, "heads": H,
+                       "head_dim": hd, "rope_dim": r, "kv_rank": kvr, "rope_theta": cfg["theta"],
+                       "step": "mla_forward (in_proj, LayerNorm, kv_up, RoPE, causal attention, o_proj)",
+                       "launch": f"HIP graph of {sets} steps over {sets} input sets, replayed",
+                       "parallelism": "single GPU"})
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")
+    line["kernels"] = table
+    line["step_algorithmic_bytes"] = total_bytes
+    line["step_algorithmic_flops"] = total_flops
+    line["step_hbm_frac"] = total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+    line["step_mfma_frac"] = total_flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFS["bf16"]
+    if cpu:
+        line["cpu_baseline"] = cpu_baseline_mla(cfg, x_cpu, w_cpu, cos_cpu, sin_cpu)
+        line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
+    return line
+
+
+# ---------------------------------------------------------- streaming decode
+
+# 65536 streams, one bar each through 2 Mamba-3 layers (d_model 128, d_state 64, 4 heads of 64, expand 2),
+# then RMSNorm and a Linear(128 -> 1) head; fp32 weights and state. State init: ssm, k, v ~ N(0, 0.1),
+# rotary phase ~ U[0, 2 pi) (fp64), mid-sequence (started).
+DECODE = dict(streams=65536, layers=2, d_model=128, d_state=64, headdim=64, expand=2, norm_groups=8)
+
+
+def _decode_state_bytes(S: int, geo: dict) -> int:
+    H, N, D, R = geo["H"], geo["N"], geo["D"], geo["R"]
+    return S * H * ((N * D + N + D) * 4 + max(R, 1) * 8)
+
+
+def cpu_baseline_decode(cfg: dict, geo: dict, weights: list, norms: list, head, states: list, x_cpu,
+                        budget_s: float = 10.0, streams: int = 1024) -> dict:
+    """No reference step operator exists: the oracle's step restatement (one thread) for the mixer, the
+    reference CPU RMSNorm and torch CPU GEMMs, on the first `streams` streams."""
+    import numpy as np
+    import torch
+
+    from oracle import Oracle, Reference, reference_available
+
+    cores = _torch_cpu_threads()
+    orc = Oracle()
+    ref = Reference() if reference_available() else orc
+    N, G, H, D, R = geo["N"], geo["G"], geo["H"], geo["D"], geo["R"]
+    x = x_cpu[:streams].contiguous()
+    st = [{"ssm": s["ssm"][:streams].cpu().numpy().copy(), "k_prev": s["k"][:streams].cpu().numpy().copy(),
+           "v_prev": s["v"][:streams].cpu().numpy().copy(), "angle": s["angle"][:streams].cpu().numpy().copy(),
+           "started": 1} for s in states]
+    ws = [{k: v.cpu() for k, v in w.items()} for w in weights]
+    nws = [n.cpu().numpy() for n in norms]
+    hw, hb, fw = (t.cpu() for t in head)
+
+    def step():
+        hcur = x
+        for layer in range(cfg["layers"]):
+            w = ws[layer]
+            nrm = ref.rms_norm(hcur.numpy(), nws[layer], 1e-5, cfg["norm_groups"])
+            proj = torch.nn.functional.linear(torch.from_numpy(nrm), w["in_w"]).numpy()
+            p = [w[k].numpy() for k in MAMBA_PARAM_KEYS]
+            y = orc.mamba3_step(proj, st[layer], N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4)
+            hcur = hcur + torch.nn.functional.linear(torch.from_numpy(np.ascontiguousarray(y)), w["out_w"])
+        fin = torch.from_numpy(ref.rms_norm(hcur.numpy(), fw.numpy(), 1e-5, 1))
+        return torch.nn.functional.linear(fin, hw, hb)
+
+    reps, elapsed = _timed_loop(step, budget_s)
+    return {"value": reps * streams / elapsed, "unit": "stream-steps/s", "cores": cores, "kind": "port",
+            "sample": f"{reps} steps of {streams} of the {cfg['streams']} streams in {elapsed:.1f} s (rate scales "
+                      f"per stream); mixer step in the oracle's C restatement (1 thread, no reference step op "
+                      f"exists), RMSNorm in the reference build, GEMMs in torch CPU ({cores} threads)"}
+
+
+def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
+    import math
+
+    import torch
+
+    from montlok import _C
+
+    cfg = DECODE
+    S, d = cfg["streams"], cfg["d_model"]
+    geo = _mamba_geometry(d, cfg["d_state"], cfg["headdim"], cfg["expand"])
+    N, G, H, D, R, W, d_inner = (geo[k] for k in ("N", "G", "H", "D", "R", "W", "d_inner"))
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    x_cpu = torch.randn(S, d, generator=g)
+    x = x_cpu.to(dev)
+    weights = [_mamba_weights(g, d, geo, dev) for _ in range(cfg["layers"])]
+    norms = [torch.ones(d, device=dev) for _ in range(cfg["layers"])]
+    bound = 1 / math.sqrt(d)
+    head = ((torch.rand(1, d, generator=g) * 2 - 1).mul(bound).to(dev), (torch.rand(1, generator=g) * 2 - 1).mul(
+        bound).to(dev), torch.ones(d, device=dev))
+    states = []
+    for _ in range(cfg["layers"]):
+        st = _C.new_mamba3_state(S, H, N, D, R, dev)
+        st["ssm"].normal_(0.0, 0.1)
+        st["k"].normal_(0.0, 0.1)
+        st["v"].normal_(0.0, 0.1)
+        st["angle"].uniform_(0.0, 2 * math.pi)
+        st["started"] = True
+        states.append(st)
+    states_cpu = [{k: (v.cpu() if torch.is_tensor(v) else v) for k, v in st.items()} for st in states]
+    consts = (N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    result = {}
+
+    def step():
+        h = x
+        for layer in range(cfg["layers"]):
+            w = weights[layer]
+            nrm = _C.rms_norm(h, norms[layer], 1e-5, cfg["norm_groups"])
+            proj = _C.linear(nrm, w["in_w"])
+            y = _C.mamba3_siso_step(proj, states[layer], *(w[k] for k in MAMBA_PARAM_KEYS), *consts)
+            h = h + _C.linear(y, w["out_w"])
+        result["out"] = _C.linear(_C.rms_norm(h, head[2], 1e-5, 1), head[0], head[1])
+
+    # One eager step checks the graph path and leaves the state one bar further; the CPU leg starts from
+    # the initial state copied above.
+    step()
+    torch.cuda.synchronize()
+    assert torch.isfinite(result["out"]).all().item()
+    steps, ms = _time_steps([step], steps, warmup, per_graph=1)
+
+    w = weights[0]
+    nrm = _C.rms_norm(x, norms[0], 1e-5, cfg["norm_groups"])
+    proj = _C.linear(nrm, w["in_w"])
+    y = _C.mamba3_siso_step(proj, states[0], *(w[k] for k in MAMBA_PARAM_KEYS), *consts)
+    o = _C.linear(y, w["out_w"])
+    f = 4
+    state_bytes = _decode_state_bytes(S, geo)
+    ops = {
+        "rms_norm": dict(fn=lambda: _C.rms_norm(x, norms[0], 1e-5, cfg["norm_groups"]), bytes=2 * S * d * f),
+        "in_proj": dict(fn=lambda: _C.linear(nrm, w["in_w"]), bytes=(S * d + W * d + S * W) * f, flops=2 * S * d * W,
+                        precision="f32"),
+        "mamba3_siso_step": dict(fn=lambda: _C.mamba3_siso_step(proj, states[0], *(w[k] for k in MAMBA_PARAM_KEYS),
+                                                                *consts),
+                                 bytes=2 * state_bytes + (S * W + S * d_inner) * f),
+        "out_proj": dict(fn=lambda: _C.linear(y, w["out_w"]), bytes=(S * d_inner + d * d_inner + S * d) * f,
+                         flops=2 * S * d_inner * d, precision="f32"),
+        "residual_add": dict(fn=lambda: x + o, bytes=3 * S * d * f),
+    }
+    table = _kernel_table(ops, _op_times(ops, max(4, steps // 4), reps=2), "f32")
+    dom = max(table, key=lambda k: table[k]["launch_ms"])
+    total_bytes = cfg["layers"] * (2 * state_bytes + (W * d + d * d_inner) * f) + S * d * f + S * f
+    line = _base_line(S / (ms * 1e-3), "stream-steps/s", steps, warmup, ms, "f32 (fp64 rotary phase)",
+                      "synthetic (seeded N(0,1) bar inputs, Kaiming-uniform weights, state ~ N(0,0.1))",
+                      {"workload": "streaming_decode", "streams": S, "layers": cfg["layers"], "d_model": d,
+                       "d_state": N, "heads": H, "headdim": D, "rope_angles": R, "norm_groups": cfg["norm_groups"],
+                       "step": "2 x [x + out_proj(mamba3_step(in_proj(GroupedRMSNorm(x))))], RMSNorm, Linear(128->1)",
+                       "launch": "HIP graph of one step, replayed (state carried in place)",
+                       "parallelism": "single GPU"})
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32")
+    line["kernels"] = table
+    line["step_algorithmic_bytes"] = total_bytes
+    line["step_hbm_frac"] = total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+    line["state_bytes_per_layer"] = state_bytes
+    if cpu:
+        line["cpu_baseline"] = cpu_baseline_decode(cfg, geo, weights, norms, head, states_cpu, x_cpu)
+        line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
+    return line
+
+
+WORKLOADS = {"mhc": bench_mhc, "block": bench_block, "mla": bench_mla, "decode": bench_decode}
 
 
 def main() -> int:

@@ -11,13 +11,15 @@
 // The kernel is laid out for that: x streams from HBM exactly once, W (a few
 // hundred KB, L2 resident) is staged through LDS chunk by chunk.
 //
-//   block  = 4 waves, 64 rows (16 per wave); grid.y splits N only when there
+//   block  = 8 waves, 128 rows (16 per wave); grid.y splits N only when there
 //            are too few row blocks to fill the chip.
-//   A      = the wave's 16 rows of x for one K chunk (256), loaded straight
-//            from HBM into registers in the MFMA operand layout: lane l holds
-//            row l%16, k = 8*(l/16) .. +7 of every 32-wide k step.
-//   B      = a 64 x 256 chunk of W in LDS, read with one 16-byte LDS load per
-//            lane per 16x16 tile.
+//   A      = the wave's 16 rows of x for one K chunk, loaded straight from
+//            HBM into registers in the MFMA operand layout: lane l holds row
+//            l%16, k = 8*(l/16) .. +7 of every 32-wide k step. With K within
+//            one chunk (256 for bf16 weights, 128 for fp32) x is read once.
+//   B      = a 64-column chunk of W in LDS, double-buffered: the next chunk's
+//            global loads are in flight while the MFMAs consume this one.
+//            One 16-byte LDS load per lane per 16x16 tile.
 //   MFMA   = bf16 weights: v_mfma_f32_16x16x32_bf16 with x rounded to bf16
 //            (round to nearest even), fp32 accumulate; fp32 weights:
 //            v_mfma_f32_16x16x4_f32, eight per 32-wide k step, fp32 throughout.
@@ -36,23 +38,24 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16;
 
-constexpr int kRowsPerBlock = 64;
+constexpr int kThreads = 512;                  // 8 waves
+constexpr int kRowsPerBlock = 16 * (kThreads / 64);
 constexpr int kColsPerChunk = 64;
-constexpr int kKChunk = 256;
-constexpr int kSteps = kKChunk / 32;
 
+// Weight element type, K chunk staged per step, LDS row pitch (+16 bytes so
+// consecutive rows start on different banks).
 template <bool BF16W>
 struct WTraits;
-
 template <>
 struct WTraits<true> {
     using T = u16;
-    static constexpr int kPitch = kKChunk + 8;  // +16 bytes per row: rows start on different banks
+    static constexpr int kKChunk = 256;
+    static constexpr int kPitch = kKChunk + 8;
 };
-
 template <>
 struct WTraits<false> {
     using T = float;
+    static constexpr int kKChunk = 128;
     static constexpr int kPitch = kKChunk + 4;
 };
 
@@ -65,8 +68,6 @@ struct LinearArgs {
     float* out;
     int64_t out_stride;
 };
-
-__device__ __forceinline__ __bf16 bits_to_bf16(u16 v) { return __builtin_bit_cast(__bf16, v); }
 
 // Loads 8 consecutive floats x[row, k .. k+7] (zero past K or past the last row).
 template <bool VEC>
@@ -90,121 +91,187 @@ __device__ __forceinline__ void load_x8(const LinearArgs& p, int64_t row, int64_
     }
 }
 
-// Copies W[n0 .. n0+63, k0 .. k0+255] into LDS, zero past N and K.
+// A operand of one K chunk for the lane's row: step s holds k = k0 + 32s + 8g .. +7.
+template <bool BF16W>
+struct AFrag;
+template <>
+struct AFrag<true> {
+    bf16x8 v[WTraits<true>::kKChunk / 32];
+};
+template <>
+struct AFrag<false> {
+    float v[WTraits<false>::kKChunk / 32][8];
+};
+
 template <bool BF16W, bool VEC>
-__device__ __forceinline__ void stage_w(const LinearArgs& p, int64_t n0, int64_t k0,
-                                        typename WTraits<BF16W>::T* lds) {
-    using T = typename WTraits<BF16W>::T;
-    constexpr int kPitch = WTraits<BF16W>::kPitch;
-    constexpr int kPerVec = 16 / sizeof(T);  // elements per 16-byte unit
-    constexpr int kUnitsPerRow = kKChunk / kPerVec;
-    const T* w = static_cast<const T*>(p.w);
-    for (int u = threadIdx.x; u < kColsPerChunk * kUnitsPerRow; u += blockDim.x) {
-        const int r = u / kUnitsPerRow;
-        const int c = (u % kUnitsPerRow) * kPerVec;
-        const int64_t n = n0 + r;
-        const int64_t k = k0 + c;
-        T* dst = lds + r * kPitch + c;
-        if (VEC && n < p.N && k + kPerVec <= p.K) {
-            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(w + n * p.K + k);
-        } else {
+__device__ __forceinline__ void load_a(const LinearArgs& p, int64_t row, int64_t k0, int group, int steps,
+                                       AFrag<BF16W>& a) {
+    constexpr int kSteps = WTraits<BF16W>::kKChunk / 32;
 #pragma unroll
-            for (int j = 0; j < kPerVec; ++j) dst[j] = (n < p.N && k + j < p.K) ? w[n * p.K + k + j] : T(0);
+    for (int s = 0; s < kSteps; ++s) {
+        if (s < steps) {
+            float v[8];
+            load_x8<VEC>(p, row, k0 + 32 * s + 8 * group, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if constexpr (BF16W) {
+                    a.v[s][j] = static_cast<__bf16>(v[j]);
+                } else {
+                    a.v[s][j] = v[j];
+                }
+            }
         }
     }
 }
 
+// This thread's share of one W chunk W[n0 .. n0+63, k0 .. k0+kspan-1]: fixed
+// 16-byte units, fetched into registers (zero past N and K), later written to
+// LDS. Units at columns >= kspan are never read by the MFMA loop and skipped.
 template <bool BF16W, bool VEC>
-__global__ __launch_bounds__(256) void linear_kernel(LinearArgs p) {
+struct WStage {
     using T = typename WTraits<BF16W>::T;
+    static constexpr int kPer = 16 / sizeof(T);
+    static constexpr int kUnitsPerRow = WTraits<BF16W>::kKChunk / kPer;
+    static constexpr int kUnits = (kColsPerChunk * kUnitsPerRow) / kThreads;
+    uint4 reg[kUnits];
+
+    __device__ __forceinline__ void fetch(const LinearArgs& p, int64_t n0, int64_t k0, int kspan) {
+        const T* w = static_cast<const T*>(p.w);
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) {
+            const int unit = threadIdx.x + u * kThreads;
+            const int r = unit / kUnitsPerRow;
+            const int c = (unit % kUnitsPerRow) * kPer;
+            const int64_t n = n0 + r;
+            const int64_t k = k0 + c;
+            if (c >= kspan) continue;
+            if (VEC && n < p.N && k + kPer <= p.K) {
+                reg[u] = *reinterpret_cast<const uint4*>(w + n * p.K + k);
+            } else {
+                T tmp[kPer];
+#pragma unroll
+                for (int j = 0; j < kPer; ++j) tmp[j] = (n < p.N && k + j < p.K) ? w[n * p.K + k + j] : T(0);
+                reg[u] = __builtin_bit_cast(uint4, tmp);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(T* lds, int kspan) const {
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) {
+            const int unit = threadIdx.x + u * kThreads;
+            const int r = unit / kUnitsPerRow;
+            const int c = (unit % kUnitsPerRow) * kPer;
+            if (c < kspan) *reinterpret_cast<uint4*>(lds + r * WTraits<BF16W>::kPitch + c) = reg[u];
+        }
+    }
+};
+
+// Iterations run over (N chunk j of this block, K chunk kc), K fastest. W of
+// iteration i+1 (and A when K spans several chunks) is fetched before the
+// MFMAs of iteration i and written to the other LDS buffer after them: one
+// barrier per iteration.
+template <bool BF16W, bool VEC, bool MULTIK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void linear_kernel(LinearArgs p) {
+    using T = typename WTraits<BF16W>::T;
+    constexpr int KC = WTraits<BF16W>::kKChunk;
+    constexpr int kSteps = KC / 32;
     constexpr int kPitch = WTraits<BF16W>::kPitch;
-    __shared__ __attribute__((aligned(16))) T w_lds[kColsPerChunk * kPitch];
+    __shared__ __attribute__((aligned(16))) T w_lds[2][kColsPerChunk * kPitch];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int col_in_tile = lane & 15;
+    const int li = lane & 15;
     const int group = lane >> 4;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + 16 * wave;
-    const int64_t my_row = row0 + col_in_tile;  // the A row this lane feeds
+    const int64_t my_row = row0 + li;  // the A row this lane feeds
     const int64_t n_chunks = (p.N + kColsPerChunk - 1) / kColsPerChunk;
-    const int64_t k_chunks = (p.K + kKChunk - 1) / kKChunk;
+    const int64_t k_chunks = (p.K + KC - 1) / KC;
+    const int64_t my_chunks = (n_chunks - blockIdx.y + gridDim.y - 1) / gridDim.y;
+    const int64_t iters = my_chunks * k_chunks;
+    if (iters <= 0) return;
 
-    // A operand for one K chunk: 8 k steps of 8 values per lane.
-    bf16x8 a_bf[kSteps];
-    float a_f[BF16W ? 1 : kSteps][8];
+    auto kspan_of = [&](int64_t kc) -> int {
+        const int64_t rem = p.K - kc * KC;
+        const int64_t span = ((rem < KC ? rem : KC) + 31) / 32 * 32;
+        return static_cast<int>(span);
+    };
+    auto n0_of = [&](int64_t it) { return (blockIdx.y + (it / k_chunks) * gridDim.y) * kColsPerChunk; };
 
-    auto load_a = [&](int64_t k0) {
+    WStage<BF16W, VEC> stage;
+    AFrag<BF16W> a_cur;
+    AFrag<BF16W> a_next;  // only used when K spans several chunks
+    stage.fetch(p, n0_of(0), 0, kspan_of(0));
+    load_a<BF16W, VEC>(p, my_row, 0, group, kspan_of(0) / 32, a_cur);
+    stage.store(w_lds[0], kspan_of(0));
+    __syncthreads();
+
+    f32x4 acc[4];
+    for (int64_t it = 0; it < iters; ++it) {
+        const int64_t kc = it % k_chunks;
+        const int64_t n0 = n0_of(it);
+        const int steps = kspan_of(kc) / 32;
+        const bool more = it + 1 < iters;
+        const int64_t kc_next = (it + 1) % k_chunks;
+        if (more) {
+            stage.fetch(p, n0_of(it + 1), kc_next * KC, kspan_of(kc_next));
+            if constexpr (MULTIK) load_a<BF16W, VEC>(p, my_row, kc_next * KC, group, kspan_of(kc_next) / 32, a_next);
+        }
+        if (kc == 0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        const T* buf = w_lds[it & 1];
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
-            float v[8];
-            load_x8<VEC>(p, my_row, k0 + 32 * s + 8 * group, v);
-            if constexpr (BF16W) {
+            if (s < steps) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) a_bf[s][j] = static_cast<__bf16>(v[j]);
-            } else {
+                for (int t = 0; t < 4; ++t) {
+                    const T* src = buf + (16 * t + li) * kPitch + 32 * s + 8 * group;
+                    if constexpr (BF16W) {
+                        const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(src));
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur.v[s], b, acc[t], 0, 0, 0);
+                    } else {
+                        const float4 b0 = *reinterpret_cast<const float4*>(src);
+                        const float4 b1 = *reinterpret_cast<const float4*>(src + 4);
+                        const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) a_f[s][j] = v[j];
-            }
-        }
-    };
-
-    if (k_chunks == 1) load_a(0);
-
-    for (int64_t nc = blockIdx.y; nc < n_chunks; nc += gridDim.y) {
-        const int64_t n0 = nc * kColsPerChunk;
-        f32x4 acc[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-        for (int64_t kc = 0; kc < k_chunks; ++kc) {
-            const int64_t k0 = kc * kKChunk;
-            if (k_chunks > 1) load_a(k0);
-            __syncthreads();  // previous chunk's readers are done with w_lds
-            stage_w<BF16W, VEC>(p, n0, k0, w_lds);
-            __syncthreads();
-            const int steps = static_cast<int>((p.K - k0 + 31) / 32 < kSteps ? (p.K - k0 + 31) / 32 : kSteps);
-#pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
-                if (s < steps) {
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const T* src = w_lds + (16 * t + col_in_tile) * kPitch + 32 * s + 8 * group;
-                        if constexpr (BF16W) {
-                            const uint4 raw = *reinterpret_cast<const uint4*>(src);
-                            const bf16x8 b = __builtin_bit_cast(bf16x8, raw);
-                            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bf[s], b, acc[t], 0, 0, 0);
-                        } else {
-                            const float4 b0 = *reinterpret_cast<const float4*>(src);
-                            const float4 b1 = *reinterpret_cast<const float4*>(src + 4);
-                            const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-                            for (int j = 0; j < 8; ++j) {
-                                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a_f[s][j], b[j], acc[t], 0, 0, 0);
-                            }
+                        for (int j = 0; j < 8; ++j) {
+                            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a_cur.v[s][j], b[j], acc[t], 0, 0, 0);
                         }
                     }
                 }
             }
         }
-
+        if (kc == k_chunks - 1) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int64_t col = n0 + 16 * t + col_in_tile;
-            if (col < p.N) {
-                const float b = p.bias ? p.bias[col] : 0.0f;
+            for (int t = 0; t < 4; ++t) {
+                const int64_t col = n0 + 16 * t + li;
+                if (col < p.N) {
+                    const float bias = p.bias ? p.bias[col] : 0.0f;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int64_t row = row0 + 4 * group + v;
-                    if (row < p.rows) p.out[row * p.out_stride + col] = acc[t][v] + b;
+                    for (int v = 0; v < 4; ++v) {
+                        const int64_t row = row0 + 4 * group + v;
+                        if (row < p.rows) p.out[row * p.out_stride + col] = acc[t][v] + bias;
+                    }
                 }
             }
         }
+        if (more) {
+            stage.store(w_lds[(it + 1) & 1], kspan_of(kc_next));
+            if constexpr (MULTIK) a_cur = a_next;
+        }
+        __syncthreads();
     }
 }
 
 template <bool BF16W, bool VEC>
 void launch(const LinearArgs& p, dim3 grid, hipStream_t stream) {
-    hipLaunchKernelGGL((linear_kernel<BF16W, VEC>), grid, dim3(256), 0, stream, p);
+    if (p.K > WTraits<BF16W>::kKChunk) {
+        hipLaunchKernelGGL((linear_kernel<BF16W, VEC, true>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((linear_kernel<BF16W, VEC, false>), grid, dim3(kThreads), 0, stream, p);
+    }
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -227,9 +294,9 @@ extern "C" mlk_status mlk_linear(const float* x, int64_t rows, int64_t in_featur
     const int64_t row_blocks = ceil_div(rows, kRowsPerBlock);
     const int64_t n_chunks = ceil_div(out_features, kColsPerChunk);
     MLK_CHECK(row_blocks <= 0x7fffffff, "too many rows");
-    // Split N over grid.y only while there are fewer than ~1024 blocks.
+    // Split N over grid.y only while there are fewer than ~512 blocks (two per CU).
     int64_t gy = 1;
-    while (gy < n_chunks && row_blocks * gy < 1024) ++gy;
+    while (gy < n_chunks && row_blocks * gy < 512) ++gy;
     const dim3 grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(gy));
     const size_t wsize = weight_dtype == MLK_DTYPE_BF16 ? 2 : 4;
     const bool vec = aligned16(x) && x_stride % 4 == 0 && aligned16(weight) && (in_features * wsize) % 16 == 0;

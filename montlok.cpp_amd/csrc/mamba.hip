@@ -74,6 +74,22 @@ __device__ __forceinline__ float bc_norm_scale(const float* x, int64_t n, float 
     return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
 }
 
+// The same sum over x in LDS, read four at a time so the loads batch; the
+// additions stay in the same sequential order.
+__device__ __forceinline__ float bc_norm_scale_lds(const float* x, int64_t n, float eps) {
+    float ss = 0.0f;
+    const int64_t body = n - n % 4;
+    for (int64_t i = 0; i < body; i += 4) {
+        const float a0 = x[i], a1 = x[i + 1], a2 = x[i + 2], a3 = x[i + 3];
+        ss = ss + a0 * a0;
+        ss = ss + a1 * a1;
+        ss = ss + a2 * a2;
+        ss = ss + a3 * a3;
+    }
+    for (int64_t i = body; i < n; ++i) ss = fmaf(x[i], x[i], ss);
+    return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+}
+
 struct PrepArgs {
     const float* proj;
     int64_t sb, st;
@@ -93,70 +109,116 @@ struct PrepArgs {
     float* term;   // [B, L, H, max(R, 1)]
 };
 
-__global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= p.B * p.L * p.H) return;
-    const int64_t h = idx % p.H;
-    const int64_t tok = idx / p.H;
-    const int64_t b = tok / p.L;
-    const int64_t t = tok % p.L;
-    const int64_t N = p.N;
-    const int64_t GN = p.G * N;
-    const int64_t d_inner = p.H * p.D;
-    const float* row = p.proj + b * p.sb + t * p.st;
-    const int64_t g = h / (p.H / p.G);
-    const float* b_raw = row + 2 * d_inner + g * N;
-    const float* c_raw = row + 2 * d_inner + GN + g * N;
-    const float* raw_dt = row + 2 * d_inner + 2 * GN;
-    const float* raw_a = raw_dt + p.H;
-    const float* raw_trap = raw_a + p.H;
-    const float* raw_ang = raw_trap + p.H;
+// Phase A for kPrepTokens tokens per block: the [B | C | dt | A | trap |
+// angles] slice of each token's row is staged in LDS with coalesced loads,
+// then norms (one thread per token and group), coefficients (per token and
+// head), q/k (per element) and the angle terms are computed from LDS.
+constexpr int kPrepTokens = 8;
 
-    const float bs = bc_norm_scale(b_raw, N, p.b_eps);
-    const float cs = bc_norm_scale(c_raw, N, p.c_eps);
-    float* k_out = p.k + idx * N;
-    float* q_out = p.q + idx * N;
-    for (int64_t n = 0; n < N; ++n) {
-        k_out[n] = (b_raw[n] * bs) * p.b_norm_w[n] + p.b_bias[h * N + n];
-        q_out[n] = (c_raw[n] * cs) * p.c_norm_w[n] + p.c_bias[h * N + n];
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
+    extern __shared__ float seg_s[];
+    const int64_t N = p.N, G = p.G, H = p.H, R = p.R;
+    const int64_t GN = G * N;
+    const int64_t seg = 2 * GN + 3 * H + R;
+    const int64_t d_inner = H * p.D;
+    float* sc_s = seg_s + kPrepTokens * seg;  // [tokens][2G]
+    float* dt_s = sc_s + kPrepTokens * 2 * G;  // [tokens][H]
+    const int64_t BL = p.B * p.L;
+    const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * kPrepTokens;
+    const int tid = threadIdx.x;
+    auto row_of = [&](int64_t tok) { return p.proj + (tok / p.L) * p.sb + (tok % p.L) * p.st + 2 * d_inner; };
+
+    for (int64_t i = tid; i < kPrepTokens * seg; i += 256) {
+        const int64_t tt = i / seg, j = i % seg;
+        seg_s[i] = tok0 + tt < BL ? row_of(tok0 + tt)[j] : 0.0f;
     }
-    const float dt = softplus_f(raw_dt[h] + p.dt_bias[h]);
-    const float a = -fmaxf(heavy_tail_f(raw_a[h]), p.a_floor);
-    float al, be, ga;
-    step_coefficients(a * dt, dt, raw_trap[h], &al, &be, &ga);
-    p.alpha[idx] = al;
-    p.beta[idx] = be;
-    p.gamma[idx] = ga;
-    for (int64_t r = 0; r < p.R; ++r) p.term[idx * p.R + r] = (tanhf_cr(raw_ang[r]) * kPiF) * dt;
+    __syncthreads();
+    for (int64_t i = tid; i < kPrepTokens * 2 * G; i += 256) {
+        const int64_t tt = i / (2 * G), w = i % (2 * G);
+        const float* x = seg_s + tt * seg + (w < G ? w * N : GN + (w - G) * N);
+        sc_s[i] = bc_norm_scale_lds(x, N, w < G ? p.b_eps : p.c_eps);
+    }
+    for (int64_t i = tid; i < kPrepTokens * H; i += 256) {
+        const int64_t tt = i / H, h = i % H, tok = tok0 + tt;
+        const float* raw = seg_s + tt * seg + 2 * GN;
+        const float dt = softplus_f(raw[h] + p.dt_bias[h]);
+        dt_s[i] = dt;
+        if (tok < BL) {
+            const float a = -fmaxf(heavy_tail_f(raw[H + h]), p.a_floor);
+            const int64_t idx = tok * H + h;
+            step_coefficients(a * dt, dt, raw[2 * H + h], p.alpha + idx, p.beta + idx, p.gamma + idx);
+        }
+    }
+    __syncthreads();
+    for (int64_t i = tid; i < kPrepTokens * H * N; i += 256) {
+        const int64_t tt = i / (H * N), h = (i / N) % H, n = i % N, tok = tok0 + tt;
+        if (tok >= BL) continue;
+        const int64_t g = h / (H / G);
+        const float* x = seg_s + tt * seg;
+        const float* sc = sc_s + tt * 2 * G;
+        const int64_t o = (tok * H + h) * N + n;
+        p.k[o] = (x[g * N + n] * sc[g]) * p.b_norm_w[n] + p.b_bias[h * N + n];
+        p.q[o] = (x[GN + g * N + n] * sc[G + g]) * p.c_norm_w[n] + p.c_bias[h * N + n];
+    }
+    for (int64_t i = tid; i < kPrepTokens * H * R; i += 256) {
+        const int64_t tt = i / (H * R), h = (i / R) % H, r = i % R, tok = tok0 + tt;
+        if (tok >= BL) continue;
+        const float* ang = seg_s + tt * seg + 2 * GN + 3 * H;
+        p.term[(tok * H + h) * R + r] = (tanhf_cr(ang[r]) * kPiF) * dt_s[tt * H + h];
+    }
 }
 
-// Phase B + C: chain (b, h, r).
+size_t prep_lds_bytes(int64_t N, int64_t G, int64_t H, int64_t R) {
+    return sizeof(float) * static_cast<size_t>(kPrepTokens * (2 * G * N + 3 * H + R + 2 * G + H));
+}
+
+// Phase B + C for one (window, head): the angle terms of a run of tokens are
+// staged in LDS, lane r < R carries the fp64 running sum of angle r down the
+// run (rounded to fp32 at each token), then every (token, angle) pair is
+// wrapped, turned into sin/cos and applied to q and k in parallel.
+constexpr int kRotateLds = 4096;
+
 __global__ __launch_bounds__(256) void rotate_kernel(int64_t B, int64_t L, int64_t H, int64_t N, int64_t R,
                                                      const float* __restrict__ term, float* __restrict__ q,
                                                      float* __restrict__ k) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= B * H * R) return;
-    const int64_t r = idx % R;
-    const int64_t h = (idx / R) % H;
-    const int64_t b = idx / (R * H);
+    __shared__ float cum_s[kRotateLds];
+    const int64_t h = blockIdx.x % H;
+    const int64_t b = blockIdx.x / H;
+    const int tid = threadIdx.x;
+    const int64_t run_len = kRotateLds / R;
     double running = 0.0;
-    for (int64_t t = 0; t < L; ++t) {
-        const int64_t th = (b * L + t) * H + h;
-        running += static_cast<double>(term[th * R + r]);
-        const float cumulative = static_cast<float>(running);
-        const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
-        const float angle = cumulative - wraps;
-        double sd, cd;
-        sincos_d(static_cast<double>(angle), &sd, &cd);
-        const float sine = static_cast<float>(sd);
-        const float cosine = static_cast<float>(cd);
-        float* qp = q + th * N + 2 * r;
-        float* kp = k + th * N + 2 * r;
-        const float ql = qp[0], qr = qp[1], kl = kp[0], kr = kp[1];
-        qp[0] = fmaf(ql, cosine, -(qr * sine));
-        qp[1] = fmaf(ql, sine, qr * cosine);
-        kp[0] = fmaf(kl, cosine, -(kr * sine));
-        kp[1] = fmaf(kl, sine, kr * cosine);
+    for (int64_t t0 = 0; t0 < L; t0 += run_len) {
+        const int64_t n = L - t0 < run_len ? L - t0 : run_len;
+        for (int64_t i = tid; i < n * R; i += 256) {
+            const int64_t tt = i / R, r = i % R;
+            cum_s[i] = term[((b * L + t0 + tt) * H + h) * R + r];
+        }
+        __syncthreads();
+        if (tid < R) {
+            for (int64_t tt = 0; tt < n; ++tt) {
+                running += static_cast<double>(cum_s[tt * R + tid]);
+                cum_s[tt * R + tid] = static_cast<float>(running);
+            }
+        }
+        __syncthreads();
+        for (int64_t i = tid; i < n * R; i += 256) {
+            const int64_t tt = i / R, r = i % R;
+            const float cumulative = cum_s[i];
+            const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
+            double sd, cd;
+            sincos_d(static_cast<double>(cumulative - wraps), &sd, &cd);
+            const float sine = static_cast<float>(sd);
+            const float cosine = static_cast<float>(cd);
+            const int64_t th = (b * L + t0 + tt) * H + h;
+            float* qp = q + th * N + 2 * r;
+            float* kp = k + th * N + 2 * r;
+            const float ql = qp[0], qr = qp[1], kl = kp[0], kr = kp[1];
+            qp[0] = fmaf(ql, cosine, -(qr * sine));
+            qp[1] = fmaf(ql, sine, qr * cosine);
+            kp[0] = fmaf(kl, cosine, -(kr * sine));
+            kp[1] = fmaf(kl, sine, kr * cosine);
+        }
+        __syncthreads();
     }
 }
 
@@ -196,9 +258,14 @@ struct RecArgs {
     Strides3 os;
 };
 
-// The recurrence proper. Kernel parameters (not a struct) with __restrict__
-// so that the wave-uniform q/k/coefficient reads become scalar loads. NM is
-// the register capacity of the state column; EXACT means N == NM (no guards).
+// The recurrence proper: one wave per (window, head, 64 headdim columns),
+// lane = column, state column s[n] in registers, time sequential. q, k and the
+// coefficients of kStepsPerChunk tokens are staged in LDS (double-buffered)
+// and v / gate per lane in registers; the next chunk's loads are issued
+// before the current chunk is computed, so no step waits on memory. NM is
+// the register capacity of the state column; EXACT means N == NM.
+constexpr int kStepsPerChunk = 8;
+
 template <int NM, bool EXACT, bool VEC>
 __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D, int N,
                                                  const float* __restrict__ q, Strides3 qs,
@@ -208,6 +275,11 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
                                                  const float* __restrict__ alpha, const float* __restrict__ beta,
                                                  const float* __restrict__ gamma, const float* __restrict__ skip_p,
                                                  float* __restrict__ out, Strides3 os) {
+    constexpr int TC = kStepsPerChunk;
+    constexpr int QPL = (TC * NM + 63) / 64;  // staged q (and k) values per lane
+    __shared__ float q_s[2][TC * NM];
+    __shared__ float k_s[2][TC * NM];
+    __shared__ float c_s[2][TC * 4];
     const int64_t blocks_per_head = (D + 63) / 64;
     const int64_t item = blockIdx.x;
     const int64_t dblk = item % blocks_per_head;
@@ -229,53 +301,110 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
     const float* grow = gate + b * gs.b + h * gs.h + (active ? d : 0);
     float* orow = out + b * os.b + h * os.h + (active ? d : 0);
     const int64_t cbase = b * L * H + h;
-    float v_prev = 0.0f;
-    float v_cur = active ? vrow[0] : 0.0f;
-    float g_cur = active ? grow[0] : 0.0f;
-    for (int64_t t = 0; t < L; ++t) {
-        const float al = alpha[cbase + t * H];
-        const float be = beta[cbase + t * H];
-        const float ga = gamma[cbase + t * H];
-        float v_next = 0.0f, g_next = 0.0f;
-        if (active && t + 1 < L) {
-            v_next = vrow[(t + 1) * vs.t];
-            g_next = grow[(t + 1) * gs.t];
-        }
-        const float* qt = qrow + t * qs.t;
-        const float* kt = krow + t * ks.t;
-        const float* kp = t > 0 ? kt - ks.t : kt;
-        const float pv = t > 0 ? be * v_prev : 0.0f;
-        const float cv = ga * v_cur;
-        float acc0 = 0.0f, acc1 = 0.0f;
+
+    float qpre[QPL], kpre[QPL], cpre = 0.0f, vpre[TC], gpre[TC];
+    auto fetch = [&](int64_t t0) {
 #pragma unroll
-        for (int n = 0; n < NM; ++n) {
-            if (EXACT || n < N) {
-                float upd;
-                if (VEC || t > 0) {
-                    upd = fmaf(kt[n], cv, fmaf(s[n], al, kp[n] * pv));
-                } else {
-                    upd = fmaf(kt[n], cv, s[n] * al);
-                }
-                s[n] = upd;
-                if (VEC && (n & 1)) {
-                    acc1 = fmaf(upd, qt[n], acc1);
-                } else {
-                    acc0 = fmaf(upd, qt[n], acc0);
-                }
+        for (int j = 0; j < QPL; ++j) {
+            const int idx = lane + 64 * j;
+            const int tt = idx / NM, n = idx % NM;
+            const int64_t t = t0 + tt;
+            const bool ok = tt < TC && (EXACT || n < N) && t < L;
+            qpre[j] = ok ? qrow[t * qs.t + n] : 0.0f;
+            kpre[j] = ok ? krow[t * ks.t + n] : 0.0f;
+        }
+        if (lane < 3 * TC) {
+            const int which = lane / TC;
+            const int64_t t = t0 + lane % TC;
+            const float* src = which == 0 ? alpha : (which == 1 ? beta : gamma);
+            cpre = t < L ? src[cbase + t * H] : 0.0f;
+        }
+#pragma unroll
+        for (int tt = 0; tt < TC; ++tt) {
+            const int64_t t = t0 + tt;
+            vpre[tt] = (active && t < L) ? vrow[t * vs.t] : 0.0f;
+            gpre[tt] = (active && t < L) ? grow[t * gs.t] : 0.0f;
+        }
+    };
+    auto commit = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < QPL; ++j) {
+            const int idx = lane + 64 * j;
+            if (idx < TC * NM) {
+                q_s[buf][idx] = qpre[j];
+                k_s[buf][idx] = kpre[j];
             }
         }
-        const float y = fmaf(skip, v_cur, VEC ? acc0 + acc1 : acc0);
-        float o;
-        if (gate_logits) {
-            const double z = static_cast<double>(g_cur);
-            o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
-        } else {
-            o = y * g_cur;
+        if (lane < 3 * TC) c_s[buf][(lane % TC) * 4 + lane / TC] = cpre;
+    };
+
+    float vcur[TC], gcur[TC];
+    fetch(0);
+    commit(0);
+#pragma unroll
+    for (int tt = 0; tt < TC; ++tt) {
+        vcur[tt] = vpre[tt];
+        gcur[tt] = gpre[tt];
+    }
+    __syncthreads();
+    float v_last = 0.0f;
+    for (int64_t t0 = 0, c = 0; t0 < L; t0 += TC, ++c) {
+        const int buf = static_cast<int>(c & 1);
+        const bool more = t0 + TC < L;
+        if (more) fetch(t0 + TC);
+#pragma unroll
+        for (int tt = 0; tt < TC; ++tt) {
+            const int64_t t = t0 + tt;
+            if (t < L) {
+                const float al = c_s[buf][tt * 4], be = c_s[buf][tt * 4 + 1], ga = c_s[buf][tt * 4 + 2];
+                const float* qt = &q_s[buf][tt * NM];
+                const float* kt = &k_s[buf][tt * NM];
+                const float* kp = tt > 0 ? &k_s[buf][(tt - 1) * NM] : (t > 0 ? &k_s[buf ^ 1][(TC - 1) * NM] : kt);
+                const float v_cur = vcur[tt];
+                const float v_prev = tt > 0 ? vcur[tt > 0 ? tt - 1 : 0] : v_last;
+                const float pv = t > 0 ? be * v_prev : 0.0f;
+                const float cv = ga * v_cur;
+                float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+                for (int n = 0; n < NM; ++n) {
+                    if (EXACT || n < N) {
+                        float upd;
+                        if (VEC || t > 0) {
+                            upd = fmaf(kt[n], cv, fmaf(s[n], al, kp[n] * pv));
+                        } else {
+                            upd = fmaf(kt[n], cv, s[n] * al);
+                        }
+                        s[n] = upd;
+                        if (VEC && (n & 1)) {
+                            acc1 = fmaf(upd, qt[n], acc1);
+                        } else {
+                            acc0 = fmaf(upd, qt[n], acc0);
+                        }
+                    }
+                }
+                const float y = fmaf(skip, v_cur, VEC ? acc0 + acc1 : acc0);
+                float o;
+                if (gate_logits) {
+                    const double z = static_cast<double>(gcur[tt]);
+                    o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
+                } else {
+                    o = y * gcur[tt];
+                }
+                if (active) orow[t * os.t] = o;
+            }
         }
-        if (active) orow[t * os.t] = o;
-        v_prev = v_cur;
-        v_cur = v_next;
-        g_cur = g_next;
+        v_last = vcur[TC - 1];
+        if (more) {
+            // Buffer buf ^ 1 (the chunk before this one) was last read at tt = 0 above.
+            __syncthreads();
+            commit(buf ^ 1);
+#pragma unroll
+            for (int tt = 0; tt < TC; ++tt) {
+                vcur[tt] = vpre[tt];
+                gcur[tt] = gpre[tt];
+            }
+            __syncthreads();
+        }
     }
 }
 
@@ -336,97 +465,144 @@ struct StepArgs {
     float* out;     // [S, H * D]
 };
 
-// One wave per (stream, head); lanes = headdim columns (D <= 64). The q/k
-// preparation of the head is done by the wave cooperatively in LDS.
+// One block of four waves per stream; wave w owns heads w, w+4, ... and its
+// lanes are the headdim columns (D <= 64). Each wave issues the loads of its
+// first head's [N, D] state before anything else, so the per-stream set-up
+// below (B/C norms once per group, coefficients per head, the rotary phase
+// of every (head, angle) pair in parallel) runs while the state streams in.
+// Arithmetic per element is that of the sequence kernel.
+constexpr int kStepThreads = 256;
+
 template <int NM, bool VEC>
-__global__ __launch_bounds__(64) void step_kernel(StepArgs p) {
-    __shared__ float qk[2][NM];
-    __shared__ float coef[3];
-    const int64_t s_idx = blockIdx.x / p.H;
-    const int64_t h = blockIdx.x % p.H;
-    const int lane = threadIdx.x;
-    const int N = static_cast<int>(p.N);
-    const int64_t d_inner = p.H * p.D;
-    const int64_t GN = p.G * p.N;
+__global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs p) {
+    extern __shared__ float lds[];
+    const int64_t H = p.H, N = p.N, D = p.D, G = p.G, R = p.R;
+    float* q_l = lds;            // [H][N] rotated q (from C)
+    float* k_l = q_l + H * N;    // [H][N] rotated k (from B)
+    float* kp_l = k_l + H * N;   // [H][N] previous k
+    float* co = kp_l + H * N;    // [H][4] alpha, beta, gamma, dt
+    float* sc = co + 4 * H;      // [2G] B scales, then C scales
+    float* seg = sc + 2 * G;     // [2GN + 3H + R] the row's B | C | dt | A | trap | angles
+    const int64_t s_idx = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t d_inner = H * D;
+    const int64_t GN = G * N;
     const float* row = p.proj + s_idx * p.proj_ss;
-    const int64_t g = h / (p.H / p.G);
-    const float* b_raw = row + 2 * d_inner + g * p.N;
-    const float* c_raw = row + 2 * d_inner + GN + g * p.N;
-    const float* raw_dt = row + 2 * d_inner + 2 * GN;
-    const float* raw_a = raw_dt + p.H;
-    const float* raw_trap = raw_a + p.H;
-    const float* raw_ang = raw_trap + p.H;
+    const float* b_raw = seg;
+    const float* c_raw = b_raw + GN;
+    const float* raw_dt = c_raw + GN;
+    const float* raw_a = raw_dt + H;
+    const float* raw_trap = raw_a + H;
+    const float* raw_ang = raw_trap + H;
     const int started = p.started;
 
-    // Lanes 0 / 1: BCNorm scales (sequential sums); lane 2: dt and coefficients.
-    __shared__ float scales[2];
-    __shared__ float dt_s;
-    if (lane == 0) scales[0] = bc_norm_scale(b_raw, p.N, p.b_eps);
-    if (lane == 1) scales[1] = bc_norm_scale(c_raw, p.N, p.c_eps);
-    if (lane == 2) {
+    // 1. State of this wave's first head: in flight from here on.
+    float sv[NM];
+    const int64_t h_first = wave;
+    if (h_first < H && lane < D) {
+        const float* st = p.ssm + ((s_idx * H + h_first) * N) * D + lane;
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            if (n < N) sv[n] = st[static_cast<int64_t>(n) * D];
+        }
+    }
+
+    // 2. Per-stream set-up, from the row slice staged in LDS.
+    for (int64_t i = tid; i < 2 * GN + 3 * H + R; i += kStepThreads) seg[i] = row[2 * d_inner + i];
+    if (started) {
+        const float* kps = p.k_prev + s_idx * H * N;
+        for (int64_t i = tid; i < H * N; i += kStepThreads) kp_l[i] = kps[i];
+    }
+    __syncthreads();
+    if (tid < 2 * G) {
+        const int64_t g = tid % G;
+        sc[tid] = tid < G ? bc_norm_scale_lds(b_raw + g * N, N, p.b_eps)
+                          : bc_norm_scale_lds(c_raw + g * N, N, p.c_eps);
+    }
+    if (tid >= 64 && tid < 64 + H) {
+        const int64_t h = tid - 64;
         const float dt = softplus_f(raw_dt[h] + p.dt_bias[h]);
         const float a = -fmaxf(heavy_tail_f(raw_a[h]), p.a_floor);
-        step_coefficients(a * dt, dt, raw_trap[h], &coef[0], &coef[1], &coef[2]);
-        dt_s = dt;
+        step_coefficients(a * dt, dt, raw_trap[h], &co[4 * h], &co[4 * h + 1], &co[4 * h + 2]);
+        co[4 * h + 3] = dt;
     }
     __syncthreads();
-    for (int n = lane; n < N; n += 64) {
-        qk[1][n] = (b_raw[n] * scales[0]) * p.b_norm_w[n] + p.b_bias[h * p.N + n];  // k
-        qk[0][n] = (c_raw[n] * scales[1]) * p.c_norm_w[n] + p.c_bias[h * p.N + n];  // q
+    for (int64_t i = tid; i < H * N; i += kStepThreads) {
+        const int64_t h = i / N, n = i % N, g = h / (H / G);
+        k_l[i] = (b_raw[g * N + n] * sc[g]) * p.b_norm_w[n] + p.b_bias[h * N + n];
+        q_l[i] = (c_raw[g * N + n] * sc[G + g]) * p.c_norm_w[n] + p.c_bias[h * N + n];
     }
     __syncthreads();
-    // Rotary pairs: lane r < R advances the running angle and rotates pair r.
-    const int64_t Rw = p.R > 0 ? p.R : 1;
-    for (int64_t r = lane; r < p.R; r += 64) {
-        double* run = p.angle + (s_idx * p.H + h) * Rw + r;
-        const double next = *run + static_cast<double>((tanhf_cr(raw_ang[r]) * kPiF) * dt_s);
+    const int64_t Rw = R > 0 ? R : 1;
+    for (int64_t i = tid; i < H * R; i += kStepThreads) {
+        const int64_t h = i / R, r = i % R;
+        double* run = p.angle + (s_idx * H + h) * Rw + r;
+        const double next = *run + static_cast<double>((tanhf_cr(raw_ang[r]) * kPiF) * co[4 * h + 3]);
         *run = next;
         const float cumulative = static_cast<float>(next);
         const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
         double sd, cd;
         sincos_d(static_cast<double>(cumulative - wraps), &sd, &cd);
         const float sine = static_cast<float>(sd), cosine = static_cast<float>(cd);
+        float* pairs[2] = {q_l + h * N + 2 * r, k_l + h * N + 2 * r};
+#pragma unroll
         for (int w = 0; w < 2; ++w) {
-            const float l = qk[w][2 * r], rr = qk[w][2 * r + 1];
-            qk[w][2 * r] = fmaf(l, cosine, -(rr * sine));
-            qk[w][2 * r + 1] = fmaf(l, sine, rr * cosine);
+            const float l = pairs[w][0], rr = pairs[w][1];
+            pairs[w][0] = fmaf(l, cosine, -(rr * sine));
+            pairs[w][1] = fmaf(l, sine, rr * cosine);
         }
     }
     __syncthreads();
-    const int d = lane;
-    if (d >= p.D) return;
-    const float al = coef[0], be = coef[1], ga = coef[2];
-    const float* x = row + d_inner + h * p.D;
-    const float* z = row + h * p.D;
-    float* st = p.ssm + ((s_idx * p.H + h) * p.N) * p.D + d;
-    float* kps = p.k_prev + (s_idx * p.H + h) * p.N;
-    float* vps = p.v_prev + (s_idx * p.H + h) * p.D;
-    const float v_cur = x[d];
-    const float pv = started ? be * vps[d] : 0.0f;
-    const float cv = ga * v_cur;
-    float acc0 = 0.0f, acc1 = 0.0f;
+
+    // 3. Update and read out each head of this wave.
+    for (int64_t h = wave; h < H; h += kStepThreads / 64) {
+        const int d = lane;
+        if (d >= D) continue;
+        float* st = p.ssm + ((s_idx * H + h) * N) * D + d;
+        if (h != h_first) {
 #pragma unroll
-    for (int n = 0; n < NM; ++n) {
-        if (n < N) {
-            const float kc = qk[1][n];
-            const float kp = started ? kps[n] : kc;
-            const float sv = st[static_cast<int64_t>(n) * p.D];
-            const float upd = (VEC || started) ? fmaf(kc, cv, fmaf(sv, al, kp * pv)) : fmaf(kc, cv, sv * al);
-            st[static_cast<int64_t>(n) * p.D] = upd;
-            if (VEC && (n & 1)) {
-                acc1 = fmaf(upd, qk[0][n], acc1);
-            } else {
-                acc0 = fmaf(upd, qk[0][n], acc0);
+            for (int n = 0; n < NM; ++n) {
+                if (n < N) sv[n] = st[static_cast<int64_t>(n) * D];
             }
         }
+        const float al = co[4 * h], be = co[4 * h + 1], ga = co[4 * h + 2];
+        const float* x = row + d_inner + h * D;
+        const float* z = row + h * D;
+        float* vps = p.v_prev + (s_idx * H + h) * D;
+        const float* qh = q_l + h * N;
+        const float* kh = k_l + h * N;
+        const float* kph = kp_l + h * N;
+        const float v_cur = x[d];
+        const float pv = started ? be * vps[d] : 0.0f;
+        const float cv = ga * v_cur;
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            if (n < N) {
+                const float kc = kh[n];
+                const float kp = started ? kph[n] : kc;
+                const float upd = (VEC || started) ? fmaf(kc, cv, fmaf(sv[n], al, kp * pv)) : fmaf(kc, cv, sv[n] * al);
+                sv[n] = upd;
+                if (VEC && (n & 1)) {
+                    acc1 = fmaf(upd, qh[n], acc1);
+                } else {
+                    acc0 = fmaf(upd, qh[n], acc0);
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            if (n < N) st[static_cast<int64_t>(n) * D] = sv[n];
+        }
+        const float y = fmaf(p.skip[h], v_cur, VEC ? acc0 + acc1 : acc0);
+        const double zz = static_cast<double>(z[d]);
+        p.out[s_idx * d_inner + h * D + d] = static_cast<float>(static_cast<double>(y) * (zz / (1.0 + exp_d(-zz))));
+        vps[d] = v_cur;
+        float* kps = p.k_prev + (s_idx * H + h) * N;
+        for (int64_t n = d; n < N; n += D) kps[n] = kh[n];
     }
-    const float y = fmaf(p.skip[h], v_cur, VEC ? acc0 + acc1 : acc0);
-    const double zz = static_cast<double>(z[d]);
-    p.out[s_idx * d_inner + h * p.D + d] = static_cast<float>(static_cast<double>(y) * (zz / (1.0 + exp_d(-zz))));
-    // k_prev is read above by every lane before any lane replaces it: the
-    // wave executes the loop in lockstep, and the write below is after it.
-    vps[d] = v_cur;
-    for (int n = d; n < N; n += static_cast<int>(p.D)) kps[n] = qk[1][n];
 }
 
 }  // namespace
@@ -547,12 +723,14 @@ mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_
     pa.beta = beta;
     pa.gamma = gamma;
     pa.term = term;
-    hipLaunchKernelGGL(prep_kernel, dim3(ceil_div(blh, 256)), dim3(256), 0, stream, pa);
+    const size_t prep_lds = prep_lds_bytes(d_state, ngroups, nheads, num_rope_angles);
+    MLK_CHECK(prep_lds <= 64 * 1024, "Mamba-3 in_proj layout too wide for the GPU prep kernel");
+    hipLaunchKernelGGL(prep_kernel, dim3(ceil_div(batch * length, kPrepTokens)), dim3(256), prep_lds, stream, pa);
     mlk_status st = launch_status("mamba3 prep");
     if (st != MLK_OK) return st;
     if (num_rope_angles > 0) {
-        const int64_t chains = batch * nheads * num_rope_angles;
-        hipLaunchKernelGGL(rotate_kernel, dim3(ceil_div(chains, 256)), dim3(256), 0, stream, batch, length, nheads,
+        MLK_CHECK(num_rope_angles <= kRotateLds, "too many rotary angles for the GPU rotate kernel");
+        hipLaunchKernelGGL(rotate_kernel, dim3(batch * nheads), dim3(256), 0, stream, batch, length, nheads,
                            d_state, num_rope_angles, term, q, k);
         st = launch_status("mamba3 rotate");
         if (st != MLK_OK) return st;
@@ -627,13 +805,17 @@ mlk_status mlk_mamba3_siso_step(const float* projected, int64_t streams, int64_t
     p.started = started;
     p.out = out;
     const bool vec = headdim % 8 == 0;
-    const dim3 grid(static_cast<unsigned>(streams * nheads));
+    const size_t lds_bytes = sizeof(float) * static_cast<size_t>(3 * nheads * d_state + 4 * nheads + 2 * ngroups +
+                                                                 2 * ngroups * d_state + 3 * nheads + num_rope_angles);
+    MLK_CHECK(lds_bytes <= 64 * 1024, "too many heads x d_state for the GPU step");
+    MLK_CHECK(streams <= 0x7fffffff, "too many streams for one launch");
+    const dim3 grid(static_cast<unsigned>(streams));
 #define MLK_STEP(NM)                                                                                         \
     do {                                                                                                     \
         if (vec) {                                                                                           \
-            hipLaunchKernelGGL((step_kernel<NM, true>), grid, dim3(64), 0, stream, p);                       \
+            hipLaunchKernelGGL((step_kernel<NM, true>), grid, dim3(kStepThreads), lds_bytes, stream, p);     \
         } else {                                                                                             \
-            hipLaunchKernelGGL((step_kernel<NM, false>), grid, dim3(64), 0, stream, p);                      \
+            hipLaunchKernelGGL((step_kernel<NM, false>), grid, dim3(kStepThreads), lds_bytes, stream, p);    \
         }                                                                                                    \
         return launch_status("mamba3 step");                                                                 \
     } while (0)
