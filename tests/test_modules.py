@@ -1,0 +1,99 @@
+"""Drop-in modules without a GPU: the parameter contract of the reference's
+modules (state-dict names and shapes) and the refusal to run anywhere but the
+GPU path."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+from torch import nn
+
+
+def test_mamba3_parameter_contract():
+    """python/montlok/rdt/mamba3.py:109-141: names, shapes and the rotary-angle rule."""
+    from montlok.rdt import Mamba3CPUReference, Mamba3HIP
+
+    assert Mamba3CPUReference is Mamba3HIP
+    m = Mamba3HIP(64, d_state=16, expand=2, headdim=32)
+    shapes = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    assert shapes == {"in_proj.weight": (304, 64), "dt_bias": (4,), "B_bias": (4, 1, 16), "C_bias": (4, 1, 16),
+                      "B_norm.weight": (16,), "C_norm.weight": (16,), "D": (4,), "out_proj.weight": (64, 128)}
+    assert m.num_rope_angles == 4
+    assert Mamba3HIP(128, d_state=64, headdim=64).num_rope_angles == 16
+    assert Mamba3HIP(64, d_state=14, headdim=32, rope_fraction=0.5).num_rope_angles == 3
+    dt = torch.nn.functional.softplus(m.dt_bias)
+    assert bool(((dt >= 1e-4 * 0.999) & (dt <= 0.1 * 1.001)).all())
+
+
+def test_mhc_parameter_contract_and_init():
+    """reference/Model/layers/mhc.py:118-150: sigmoid(pre) = 1/n, 2 sigmoid(post) = 1, res bias 3 I."""
+    from montlok.rdt import ManifoldHyperConnectionCPU, ManifoldHyperConnectionHIP
+
+    assert ManifoldHyperConnectionCPU is ManifoldHyperConnectionHIP
+    h = ManifoldHyperConnectionHIP(128, n_streams=4)
+    shapes = {k: tuple(v.shape) for k, v in h.state_dict().items()}
+    assert shapes == {"pre_bias": (4,), "post_bias": (4,), "res_bias": (4, 4), "dyn_norm.weight": (128,),
+                      "pre_proj.weight": (4, 128), "post_proj.weight": (4, 128), "res_proj.weight": (16, 128),
+                      "pre_alpha": (), "post_alpha": (), "res_alpha": ()}
+    assert torch.allclose(torch.sigmoid(h.pre_bias), torch.full((4,), 0.25))
+    assert torch.equal(h.res_bias, torch.eye(4) * 3)
+    w = h._projection_block()
+    assert w.dtype == torch.float64 and w.shape == (24, 128)
+    assert w is h._projection_block()  # cached
+    with torch.no_grad():
+        h.pre_proj.weight.add_(1.0)  # bumps the version: the cache is rebuilt
+    assert w is not h._projection_block()
+
+
+def test_mla_parameter_contract():
+    """reference/Model/layers/mla.py:43-67 (q_lora_rank 0 and > 0)."""
+    from montlok.rdt import MLACPU, MLAHIP
+
+    assert MLACPU is MLAHIP
+    cfg = SimpleNamespace(d_model=256, n_heads=8, head_dim=32, nope_head_dim=16, rope_head_dim=16, kv_lora_rank=64,
+                          q_lora_rank=0, rope_theta=10000.0)
+    shapes = {k: tuple(v.shape) for k, v in MLAHIP(cfg).state_dict().items()}
+    assert shapes == {"q_proj.weight": (256, 256), "kv_down.weight": (64, 256), "kv_norm.weight": (64,),
+                      "kv_norm.bias": (64,), "kv_up.weight": (384, 64), "k_rope_proj.weight": (16, 256),
+                      "o_proj.weight": (256, 256)}
+    cfg.q_lora_rank = 32
+    keys = set(MLAHIP(cfg).state_dict())
+    assert {"q_down.weight", "q_norm.weight", "q_norm.bias", "q_up.weight"} <= keys and "q_proj.weight" not in keys
+    cfg.head_dim = 40
+    with pytest.raises(ValueError, match="head_dim must equal"):
+        MLAHIP(cfg)
+
+
+def test_layers_install_and_contract():
+    from montlok.rdt import GroupedRMSNormCPU, LayerNormCPU, RMSNormCPU, SwiGLUCPU, install_cpu_layers
+
+    class RMSNorm(nn.Module):  # stands for the upstream class of the same name and attributes
+        def __init__(self):
+            super().__init__()
+            self.dim, self.eps = 8, 1e-5
+            self.weight = nn.Parameter(torch.ones(8))
+
+    model = nn.Sequential(RMSNorm(), nn.LayerNorm(8), nn.Linear(8, 8))
+    assert install_cpu_layers(model) == 2
+    assert type(model[0]) is RMSNormCPU and type(model[1]) is LayerNormCPU and type(model[2]) is nn.Linear
+    assert set(GroupedRMSNormCPU(64, 8).state_dict()) == {"weight"}
+    assert set(SwiGLUCPU(64, 96, bias=True).state_dict()) == {"w_in.weight", "w_in.bias", "w_down.weight",
+                                                              "w_down.bias"}
+
+
+def test_modules_refuse_other_paths(monkeypatch):
+    """No CPU or autograd fallback: the modules raise instead of computing something else."""
+    from montlok.rdt import Mamba3HIP, RMSNormCPU, cpu_linear
+
+    x = torch.zeros(2, 3, 64)
+    with torch.no_grad(), pytest.raises(RuntimeError, match="must be on the ROCm device"):
+        Mamba3HIP(64, d_state=16, headdim=32)(x)
+    with torch.no_grad(), pytest.raises(RuntimeError, match="must be on the ROCm device"):
+        RMSNormCPU(64)(x)
+    with pytest.raises(RuntimeError, match="cpu_linear"):
+        cpu_linear(x, torch.zeros(4, 64))
+    monkeypatch.setenv("MONTLOK_CPP_LAYERS", "0")
+    with torch.no_grad(), pytest.raises(RuntimeError, match="switched off"):
+        RMSNormCPU(64)(x)
