@@ -164,14 +164,31 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     const double* w_res = a.proj_w + static_cast<int64_t>(2 * n + 4 * (t % 4) + t / 4) * D;
     const bool pp_row = t % 4 < 2;
     const double* w_pp = a.proj_w + static_cast<int64_t>((t % 4 == 0 ? 0 : n) + t / 4) * D;
+    // Every other operand is fetched up front too, so the whole block waits
+    // for one round of loads instead of one per MFMA step or phase.
+    double wa[GW][4], wb[GW][4];
+    float4 nw[GW];
+#pragma unroll
+    for (int j = 0; j < GW; ++j) {
+        const int k0 = 16 * (wave * GW + j) + 4 * q;
+        nw[j] = *reinterpret_cast<const float4*>(a.norm_w + k0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            wa[j][r] = w_res[k0 + r];
+            wb[j][r] = pp_row ? w_pp[k0 + r] : 0.0;
+        }
+    }
+    const int e_pre = l % 16;  // this lane's matrix entry in the coefficient phase
+    const float res_bias_e = a.res_bias[e_pre];
+    const float res_alpha = *a.res_alpha;
+    const float pp_alpha = e_pre < 4 ? *a.pre_alpha : *a.post_alpha;
+    const float pp_bias = e_pre < 4 ? a.pre_bias[e_pre % 4] : a.post_bias[e_pre % 4];
     double sq = 0.0;
     double4_t acc0 = {0.0, 0.0, 0.0, 0.0};
     double4_t acc1 = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < GW; ++j) {
-        const int k0 = 16 * (wave * GW + j) + 4 * q;
-        const float4 w4 = *reinterpret_cast<const float4*>(a.norm_w + k0);
-        const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
+        const float wk[4] = {nw[j].x, nw[j].y, nw[j].z, nw[j].w};
         const float s0[4] = {sv[j][0].x, sv[j][0].y, sv[j][0].z, sv[j][0].w};
         const float s1[4] = {sv[j][1].x, sv[j][1].y, sv[j][1].z, sv[j][1].w};
         const float s2[4] = {sv[j][2].x, sv[j][2].y, sv[j][2].z, sv[j][2].w};
@@ -186,10 +203,8 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
             m *= inv_n;
             sq = fma(m, m, sq);
             const double b = m * static_cast<double>(wk[r]);
-            const double a0 = w_res[k0 + r];
-            const double a1 = pp_row ? w_pp[k0 + r] : 0.0;
-            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(wa[j][r], b, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(wb[j][r], b, acc1, 0, 0, 0);
         }
     }
     {
@@ -225,12 +240,12 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
         ((part[0][1][v][src_pp] + part[1][1][v][src_pp]) + part[2][1][v][src_pp]) + part[3][1][v][src_pp];
     const double th_res = tanh_d(logit_res * scale);
     const double th_pp = tanh_d(logit_pp * scale);
-    double m = exp_d(fma(static_cast<double>(*a.res_alpha), th_res, static_cast<double>(a.res_bias[e])));
+    double m = exp_d(fma(static_cast<double>(res_alpha), th_res, static_cast<double>(res_bias_e)));
     if (e < 8) {
         const bool is_pre = e < 4;
-        const double alpha = static_cast<double>(is_pre ? *a.pre_alpha : *a.post_alpha);
-        const double bias = static_cast<double>(is_pre ? a.pre_bias[v] : a.post_bias[v]);
-        const float c = static_cast<float>((is_pre ? 1.0 : 2.0) * sigmoid_fast(fma(alpha, th_pp, bias)));
+        const float c = static_cast<float>((is_pre ? 1.0 : 2.0) *
+                                           sigmoid_fast(fma(static_cast<double>(pp_alpha), th_pp,
+                                                            static_cast<double>(pp_bias))));
         if (is_pre) pre_lds[tt][v] = c;
         if (valid_e) (is_pre ? a.pre : a.post)[token_e * n + v] = c;
     }
