@@ -21,6 +21,7 @@ bounded sample, or the oracle port when that library is absent).
 from __future__ import annotations
 
 import argparse
+import copy
 import json
 import os
 import sys
@@ -743,7 +744,211 @@ def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
     return line
 
 
-WORKLOADS = {"mhc": bench_mhc, "block": bench_block, "mla": bench_mla, "decode": bench_decode}
+# ------------------------------------------------------------------- stack
+
+# Full stack: 1024 windows x 256 tokens of 40 raw features (N(0,1) clipped to [-8, 8]) -> Linear(40 -> 256),
+# 4 mHC residual layers (n = 4, 20 Sinkhorn iterations) alternating Mamba-3 (d_state 64, 8 heads of 64,
+# expand 2) and MLA (4 heads of 64, RoPE 32, kv rank 64), collapse; bf16 GEMM weights N(0, 0.02), fp32 state.
+STACK = dict(windows=1024, seq=256, features=40, d_model=256, layers=4, n_streams=4, iters=20, d_state=64,
+             mamba_headdim=64, expand=2, heads=4, head_dim=64, rope=32, kv_rank=64)
+
+
+def _build_stack(cfg: dict, g):
+    import torch
+
+    from montlok.rdt.stack import HybridStackHIP
+
+    torch.manual_seed(int(torch.randint(0, 2 ** 31 - 1, (1,), generator=g)))
+    stack = HybridStackHIP(cfg["features"], d_model=cfg["d_model"], n_layers=cfg["layers"],
+                           n_streams=cfg["n_streams"], sinkhorn_iters=cfg["iters"], d_state=cfg["d_state"],
+                           mamba_headdim=cfg["mamba_headdim"], expand=cfg["expand"], n_heads=cfg["heads"],
+                           head_dim=cfg["head_dim"], rope_head_dim=cfg["rope"], kv_lora_rank=cfg["kv_rank"]).eval()
+    with torch.no_grad():
+        for w in stack.linear_weights():
+            w.normal_(0.0, 0.02, generator=g)
+        for hc in stack.hcs:  # data-dependent mixing: alphas 0.7, projections N(0, 1/d), mixing logits N(0, 1)
+            for a in (hc.pre_alpha, hc.post_alpha, hc.res_alpha):
+                a.fill_(0.7)
+            for w in (hc.pre_proj.weight, hc.post_proj.weight, hc.res_proj.weight):
+                w.normal_(0.0, cfg["d_model"] ** -0.5, generator=g)
+            hc.res_bias.normal_(generator=g)
+    return stack
+
+
+def cpu_baseline_stack(cfg: dict, stack, feats_cpu, budget_s: float = 12.0, windows: int = 2) -> dict:
+    """Reference CPU kernels (mHC, norms, Mamba-3 mixer, RoPE) with torch CPU GEMMs and SDPA, on `windows` of
+    the windows; the same chain as the GPU stack."""
+    import torch
+    import torch.nn.functional as F
+
+    from montlok.rdt.mla import rope_tables
+    from oracle import Oracle, Reference, reference_available
+
+    cores = _torch_cpu_threads()
+    lib = Reference() if reference_available() else Oracle()
+    kind = "reference" if isinstance(lib, Reference) else "port"
+    if kind == "reference":
+        lib.set_threads(cores)
+    x = feats_cpu[:windows].contiguous()
+    B, L, _ = x.shape
+    f32 = lambda t: t.detach().float().cpu()  # noqa: E731
+    hcs = [dict(nw=f32(h.dyn_norm.weight).numpy(), eps=h.dyn_norm.eps, w64=h._projection_block().cpu().numpy(),
+                pb=f32(h.pre_bias).numpy(), qb=f32(h.post_bias).numpy(), rb=f32(h.res_bias).numpy(),
+                al=(float(h.pre_alpha), float(h.post_alpha), float(h.res_alpha)), iters=h.sinkhorn_iters)
+           for h in stack.hcs]
+    norms = [f32(nm.weight).numpy() for nm in stack.norms]
+    mix = []
+    for i, m in enumerate(stack.mixers):
+        mix.append({k: f32(v) for k, v in m.state_dict().items()})
+    fw, fb = f32(stack.feature_proj.weight), f32(stack.feature_proj.bias)
+    mla = stack.mixers[1]
+    cos, sin = (t.numpy() for t in rope_tables(L, mla.rope_dim, mla.rope.theta))
+    m0 = stack.mixers[0]
+
+    def mamba(p, a):
+        proj = F.linear(torch.from_numpy(a), p["in_proj.weight"]).numpy()
+        y = lib.mamba3_siso_forward(proj, m0.d_state, m0.num_bc_heads, m0.nheads, m0.headdim, m0.num_rope_angles,
+                                    p["B_bias"].numpy(), p["C_bias"].numpy(), p["B_norm.weight"].numpy(),
+                                    p["C_norm.weight"].numpy(), 1e-5, 1e-5, p["dt_bias"].numpy(), p["D"].numpy(),
+                                    m0.A_floor)
+        return F.linear(torch.from_numpy(y), p["out_proj.weight"]).numpy()
+
+    def attn(p, a):
+        H, hd, nope, kvr, d = mla.n_heads, mla.head_dim, mla.nope_dim, mla.kv_lora_rank, mla.d_model
+        xa = torch.from_numpy(a)
+        projected = F.linear(xa, torch.cat([p["q_proj.weight"], p["kv_down.weight"], p["k_rope_proj.weight"]]))
+        q = projected[..., :d].reshape(B, L, H, hd).numpy()
+        kvn = lib.layer_norm(projected[..., d:d + kvr].contiguous().numpy(), p["kv_norm.weight"].numpy(),
+                             p["kv_norm.bias"].numpy(), 1e-5)
+        kv = F.linear(torch.from_numpy(kvn), p["kv_up.weight"]).reshape(B, L, H, nope + hd)
+        q, k = lib.mla_rope(q, kv.numpy(), projected[..., d + kvr:].contiguous().numpy(), cos, sin, nope)
+        o = F.scaled_dot_product_attention(torch.from_numpy(q).transpose(1, 2), torch.from_numpy(k).transpose(1, 2),
+                                           kv[..., nope:].transpose(1, 2), is_causal=True, scale=mla.scale)
+        return F.linear(o.transpose(1, 2).reshape(B, L, d), p["o_proj.weight"]).numpy()
+
+    def prep(i, streams, n_streams):
+        h = hcs[i]
+        return lib.mhc_prepare(streams, h["nw"], h["eps"], h["w64"], h["pb"], h["qb"], h["rb"], *h["al"], h["iters"],
+                               n_streams, norms[i], 1e-5)
+
+    def step():
+        hb = F.linear(x, fw, fb).numpy()
+        agg, pre, post, res = prep(0, hb, stack.n_streams)
+        out = mamba(mix[0], agg)
+        streams = hb
+        for i in range(1, len(hcs)):
+            if kind == "reference":
+                h = hcs[i]
+                streams, agg, pre, post, res = lib.mhc_combine_prepare(streams, res, post, out, h["nw"], h["eps"],
+                                                                       h["w64"], h["pb"], h["qb"], h["rb"], *h["al"],
+                                                                       h["iters"], norms[i], 1e-5)
+            else:
+                streams = lib.mhc_combine(streams, res, post, out)
+                agg, pre, post, res = prep(i, streams, 0)
+            out = mamba(mix[i], agg) if i % 2 == 0 else attn(mix[i], agg)
+        return lib.mhc_combine(streams, res, post, out, collapse=True, materialize=False)
+
+    reps, elapsed = _timed_loop(step, budget_s, cap=1000)
+    return {"value": reps * windows / elapsed, "unit": "windows/s", "cores": cores, "kind": kind,
+            "sample": f"{reps} steps over {windows} of the {cfg['windows']} windows in {elapsed:.1f} s (rate scales "
+                      f"per window); mHC, norms, Mamba-3 mixer and RoPE in the "
+                      f"{'reference ' + lib.variant if kind == 'reference' else 'oracle'} build, GEMMs and SDPA in "
+                      f"torch CPU (fp32, bf16 weights upcast), {cores} threads"}
+
+
+def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
+    import torch
+
+    from montlok import _C
+
+    cfg = STACK
+    B, L, d, n = cfg["windows"], cfg["seq"], cfg["d_model"], cfg["n_streams"]
+    T = B * L
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    feats_cpu = torch.randn(B, L, cfg["features"], generator=g).clamp_(-8.0, 8.0)
+    feats = feats_cpu.to(dev)
+    stack_cpu = _build_stack(cfg, g)
+    stack = copy.deepcopy(stack_cpu).to(dev)
+    for w in stack.linear_weights():
+        w.data = w.data.bfloat16()
+    result = {}
+
+    def step():
+        result["out"] = stack(feats)
+
+    with torch.no_grad():
+        step()
+        torch.cuda.synchronize()
+        eager = result["out"].clone()
+        assert torch.isfinite(eager).all().item()
+        steps, ms = _time_steps([step], max(steps // 10, 4), max(warmup // 10, 2), per_graph=1)
+        assert torch.equal(result["out"], eager), "graph replay differs from the eager step"
+
+        # Per-operator launches on the tensors of one eager pass.
+        c = _C
+        hc0, hc1, m0, m1 = stack.hcs[0], stack.hcs[1], stack.mixers[0], stack.mixers[1]
+        h = c.linear(feats, stack.feature_proj.weight, stack.feature_proj.bias)
+        _, prep0 = hc0._prepare(h, allow_broadcast=True, output_norm=stack.norms[0])
+        agg = prep0[0]
+        out0 = m0(agg)
+        streams1, prep1 = hc0._combine_prepare(h, prep0, out0, hc1, output_norm=stack.norms[1])
+        out1 = m1(prep1[0])
+        proj = c.linear(agg, m0.in_proj.weight)
+        y = m0.forward_projected(proj)
+        W, di = m0.in_proj.weight.shape[0], m0.d_inner
+        f, h2 = 4, 2
+        mhc_tok = lambda: T * (n * d * f + d * f + 2 * n * f + n * n * f)  # noqa: E731
+        ops = {
+            "feature_proj": dict(fn=lambda: c.linear(feats, stack.feature_proj.weight, stack.feature_proj.bias),
+                                 bytes=T * (cfg["features"] + d) * f, flops=2 * T * cfg["features"] * d),
+            "mhc_prepare_broadcast": dict(fn=lambda: hc0._prepare(h, allow_broadcast=True, output_norm=stack.norms[0]),
+                                          bytes=T * (2 * d + 2 * n + n * n) * f),
+            "mhc_combine_prepare": dict(fn=lambda: hc1._combine_prepare(streams1, prep1, out1, stack.hcs[2],
+                                                                        output_norm=stack.norms[2]),
+                                        bytes=T * (n * d + n * n + n + d) * f + T * n * d * f + mhc_tok()),
+            "mhc_combine_collapse": dict(fn=lambda: hc1._combine_collapse(streams1, prep1, out1),
+                                         bytes=T * (n * d + n * n + n + 2 * d) * f),
+            "mamba_in_proj": dict(fn=lambda: c.linear(agg, m0.in_proj.weight), bytes=T * (d + W) * f + W * d * h2,
+                                  flops=2 * T * d * W, precision="bf16"),
+            "mamba3_siso_forward": dict(fn=lambda: m0.forward_projected(proj), bytes=T * (W + di) * f,
+                                        flops=7 * T * m0.nheads * m0.d_state * m0.headdim, precision="f32"),
+            "mamba_out_proj": dict(fn=lambda: c.linear(y, m0.out_proj.weight), bytes=T * (di + d) * f + d * di * h2,
+                                   flops=2 * T * di * d, precision="bf16"),
+            "mla_forward": dict(fn=lambda: m1(prep1[0]), bytes=2 * T * d * f,
+                                flops=2 * T * d * (d + m1.kv_lora_rank + m1.rope_dim) +
+                                2 * T * m1.kv_lora_rank * m1.n_heads * (m1.nope_dim + m1.head_dim) +
+                                4 * B * m1.n_heads * (L * (L + 1) // 2) * m1.head_dim + 2 * T * d * d,
+                                precision="bf16"),
+        }
+        table = _kernel_table(ops, _op_times(ops, 4, reps=2), "bf16")
+    dom = max(table, key=lambda k: table[k]["launch_ms"])
+    flops = sum(ops[k]["flops"] for k in ("feature_proj",)) + 2 * (ops["mamba_in_proj"]["flops"] +
+                                                                   ops["mamba3_siso_forward"]["flops"] +
+                                                                   ops["mamba_out_proj"]["flops"]) + \
+        2 * ops["mla_forward"]["flops"]
+    line = _base_line(B / (ms * 1e-3), "windows/s", steps, max(warmup // 10, 2), ms,
+                      "bf16 weights, f32 activations/state/accumulate",
+                      "synthetic (seeded N(0,1) features clipped to [-8,8], N(0,0.02) bf16 weights)",
+                      {"workload": "rdt4quant_stack_4_layers", "windows": B, "seq_len": L, "features": cfg["features"],
+                       "d_model": d, "layers": cfg["layers"], "n_streams": n, "sinkhorn_iters": cfg["iters"],
+                       "mamba": f"d_state {cfg['d_state']}, {m0.nheads} heads of {cfg['mamba_headdim']}, "
+                                f"{m0.num_rope_angles} rotary angles",
+                       "mla": f"{cfg['heads']} heads of {cfg['head_dim']}, rope {cfg['rope']}, kv rank {cfg['kv_rank']}",
+                       "step": "Linear(40->256), 4 x mHC[fn = mixer(RMSNorm(agg))] alternating Mamba-3 / MLA, collapse",
+                       "launch": "HIP graph of one step, replayed", "parallelism": "single GPU"})
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")
+    line["kernels"] = table
+    line["step_flops"] = flops
+    line["step_achieved_TFs"] = flops / (ms * 1e-3) / 1e12
+    line["tokens_per_s"] = T / (ms * 1e-3)
+    if cpu:
+        line["cpu_baseline"] = cpu_baseline_stack(cfg, stack_cpu, feats_cpu)
+        line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
+    return line
+
+
+WORKLOADS = {"mhc": bench_mhc, "block": bench_block, "mla": bench_mla, "decode": bench_decode, "stack": bench_stack}
 
 
 def main() -> int:

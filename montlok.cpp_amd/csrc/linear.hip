@@ -168,9 +168,9 @@ struct WStage {
 };
 
 // Iterations run over (N chunk j of this block, K chunk kc), K fastest. W of
-// iteration i+1 (and A when K spans several chunks) is fetched before the
-// MFMAs of iteration i and written to the other LDS buffer after them: one
-// barrier per iteration.
+// iteration i+1 is fetched before the MFMAs of iteration i and written to the
+// other LDS buffer after them: one barrier per iteration. When K spans several
+// chunks, A is reloaded (from L2) at the start of each iteration.
 template <bool BF16W, bool VEC, bool MULTIK>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void linear_kernel(LinearArgs p) {
     using T = typename WTraits<BF16W>::T;
@@ -199,8 +199,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
     auto n0_of = [&](int64_t it) { return (blockIdx.y + (it / k_chunks) * gridDim.y) * kColsPerChunk; };
 
     WStage<BF16W, VEC> stage;
-    AFrag<BF16W> a_cur;
-    AFrag<BF16W> a_next;  // only used when K spans several chunks
+    AFrag<BF16W> a_cur;  // reloaded per iteration when K spans several chunks
     stage.fetch(p, n0_of(0), 0, kspan_of(0));
     load_a<BF16W, VEC>(p, my_row, 0, group, kspan_of(0) / 32, a_cur);
     stage.store(w_lds[0], kspan_of(0));
@@ -213,10 +212,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
         const int steps = kspan_of(kc) / 32;
         const bool more = it + 1 < iters;
         const int64_t kc_next = (it + 1) % k_chunks;
-        if (more) {
-            stage.fetch(p, n0_of(it + 1), kc_next * KC, kspan_of(kc_next));
-            if constexpr (MULTIK) load_a<BF16W, VEC>(p, my_row, kc_next * KC, group, kspan_of(kc_next) / 32, a_next);
+        if constexpr (MULTIK) {
+            if (it > 0) load_a<BF16W, VEC>(p, my_row, kc * KC, group, steps, a_cur);
         }
+        if (more) stage.fetch(p, n0_of(it + 1), kc_next * KC, kspan_of(kc_next));
         if (kc == 0) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -257,10 +256,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
                 }
             }
         }
-        if (more) {
-            stage.store(w_lds[(it + 1) & 1], kspan_of(kc_next));
-            if constexpr (MULTIK) a_cur = a_next;
-        }
+        if (more) stage.store(w_lds[(it + 1) & 1], kspan_of(kc_next));
         __syncthreads();
     }
 }

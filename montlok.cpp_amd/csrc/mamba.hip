@@ -117,54 +117,64 @@ constexpr int kPrepTokens = 8;
 
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
     extern __shared__ float seg_s[];
-    const int64_t N = p.N, G = p.G, H = p.H, R = p.R;
-    const int64_t GN = G * N;
-    const int64_t seg = 2 * GN + 3 * H + R;
-    const int64_t d_inner = H * p.D;
+    // Block-local index math in 32 bits (the sizes are checked at launch).
+    const int N = static_cast<int>(p.N), G = static_cast<int>(p.G), H = static_cast<int>(p.H);
+    const int R = static_cast<int>(p.R);
+    const int GN = G * N;
+    const int seg = 2 * GN + 3 * H + R;
+    const int64_t d_inner = p.H * p.D;
     float* sc_s = seg_s + kPrepTokens * seg;  // [tokens][2G]
     float* dt_s = sc_s + kPrepTokens * 2 * G;  // [tokens][H]
+    __shared__ const float* rows_s[kPrepTokens];
     const int64_t BL = p.B * p.L;
     const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * kPrepTokens;
+    const int ntok = static_cast<int>(BL - tok0 < kPrepTokens ? BL - tok0 : kPrepTokens);
     const int tid = threadIdx.x;
-    auto row_of = [&](int64_t tok) { return p.proj + (tok / p.L) * p.sb + (tok % p.L) * p.st + 2 * d_inner; };
-
-    for (int64_t i = tid; i < kPrepTokens * seg; i += 256) {
-        const int64_t tt = i / seg, j = i % seg;
-        seg_s[i] = tok0 + tt < BL ? row_of(tok0 + tt)[j] : 0.0f;
+    if (tid < ntok) {
+        const int64_t tok = tok0 + tid;
+        rows_s[tid] = p.proj + (tok / p.L) * p.sb + (tok % p.L) * p.st + 2 * d_inner;
     }
     __syncthreads();
-    for (int64_t i = tid; i < kPrepTokens * 2 * G; i += 256) {
-        const int64_t tt = i / (2 * G), w = i % (2 * G);
+    for (int i = tid; i < kPrepTokens * seg; i += 256) {
+        const int tt = i / seg, j = i - tt * seg;
+        seg_s[i] = tt < ntok ? rows_s[tt][j] : 0.0f;
+    }
+    __syncthreads();
+    for (int i = tid; i < kPrepTokens * 2 * G; i += 256) {
+        const int tt = i / (2 * G), w = i - tt * 2 * G;
         const float* x = seg_s + tt * seg + (w < G ? w * N : GN + (w - G) * N);
         sc_s[i] = bc_norm_scale_lds(x, N, w < G ? p.b_eps : p.c_eps);
     }
-    for (int64_t i = tid; i < kPrepTokens * H; i += 256) {
-        const int64_t tt = i / H, h = i % H, tok = tok0 + tt;
+    for (int i = tid; i < kPrepTokens * H; i += 256) {
+        const int tt = i / H, h = i - tt * H;
         const float* raw = seg_s + tt * seg + 2 * GN;
         const float dt = softplus_f(raw[h] + p.dt_bias[h]);
         dt_s[i] = dt;
-        if (tok < BL) {
+        if (tt < ntok) {
             const float a = -fmaxf(heavy_tail_f(raw[H + h]), p.a_floor);
-            const int64_t idx = tok * H + h;
+            const int64_t idx = (tok0 + tt) * H + h;
             step_coefficients(a * dt, dt, raw[2 * H + h], p.alpha + idx, p.beta + idx, p.gamma + idx);
         }
     }
     __syncthreads();
-    for (int64_t i = tid; i < kPrepTokens * H * N; i += 256) {
-        const int64_t tt = i / (H * N), h = (i / N) % H, n = i % N, tok = tok0 + tt;
-        if (tok >= BL) continue;
-        const int64_t g = h / (H / G);
+    const int HN = H * N;
+    const int heads_per_group = H / G;
+    for (int i = tid; i < ntok * HN; i += 256) {
+        const int tt = i / HN, rem = i - tt * HN;
+        const int h = rem / N, n = rem - h * N;
+        const int g = h / heads_per_group;
         const float* x = seg_s + tt * seg;
         const float* sc = sc_s + tt * 2 * G;
-        const int64_t o = (tok * H + h) * N + n;
+        const int64_t o = (tok0 + tt) * HN + rem;
         p.k[o] = (x[g * N + n] * sc[g]) * p.b_norm_w[n] + p.b_bias[h * N + n];
         p.q[o] = (x[GN + g * N + n] * sc[G + g]) * p.c_norm_w[n] + p.c_bias[h * N + n];
     }
-    for (int64_t i = tid; i < kPrepTokens * H * R; i += 256) {
-        const int64_t tt = i / (H * R), h = (i / R) % H, r = i % R, tok = tok0 + tt;
-        if (tok >= BL) continue;
+    const int HR = H * R;
+    for (int i = tid; i < ntok * HR; i += 256) {
+        const int tt = i / HR, rem = i - tt * HR;
+        const int h = rem / R, r = rem - h * R;
         const float* ang = seg_s + tt * seg + 2 * GN + 3 * H;
-        p.term[(tok * H + h) * R + r] = (tanhf_cr(ang[r]) * kPiF) * dt_s[tt * H + h];
+        p.term[(tok0 + tt) * HR + rem] = (tanhf_cr(ang[r]) * kPiF) * dt_s[tt * H + h];
     }
 }
 
@@ -185,24 +195,25 @@ __global__ __launch_bounds__(256) void rotate_kernel(int64_t B, int64_t L, int64
     const int64_t h = blockIdx.x % H;
     const int64_t b = blockIdx.x / H;
     const int tid = threadIdx.x;
-    const int64_t run_len = kRotateLds / R;
+    const int Ri = static_cast<int>(R);
+    const int run_len = kRotateLds / Ri;
     double running = 0.0;
     for (int64_t t0 = 0; t0 < L; t0 += run_len) {
-        const int64_t n = L - t0 < run_len ? L - t0 : run_len;
-        for (int64_t i = tid; i < n * R; i += 256) {
-            const int64_t tt = i / R, r = i % R;
+        const int n = static_cast<int>(L - t0 < run_len ? L - t0 : run_len);
+        for (int i = tid; i < n * Ri; i += 256) {
+            const int tt = i / Ri, r = i - tt * Ri;
             cum_s[i] = term[((b * L + t0 + tt) * H + h) * R + r];
         }
         __syncthreads();
-        if (tid < R) {
-            for (int64_t tt = 0; tt < n; ++tt) {
-                running += static_cast<double>(cum_s[tt * R + tid]);
-                cum_s[tt * R + tid] = static_cast<float>(running);
+        if (tid < Ri) {
+            for (int tt = 0; tt < n; ++tt) {
+                running += static_cast<double>(cum_s[tt * Ri + tid]);
+                cum_s[tt * Ri + tid] = static_cast<float>(running);
             }
         }
         __syncthreads();
-        for (int64_t i = tid; i < n * R; i += 256) {
-            const int64_t tt = i / R, r = i % R;
+        for (int i = tid; i < n * Ri; i += 256) {
+            const int tt = i / Ri, r = i - tt * Ri;
             const float cumulative = cum_s[i];
             const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
             double sd, cd;
@@ -230,11 +241,11 @@ struct Strides3 {
 __global__ __launch_bounds__(256) void coef_kernel(int64_t B, int64_t L, int64_t H, const float* adt, Strides3 as,
                                                    const float* dt, Strides3 ds, const float* trap, Strides3 ts_,
                                                    float* alpha, float* beta, float* gamma) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int idx = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);  // B*L*H < 2^31 (checked)
     if (idx >= B * L * H) return;
-    const int64_t h = idx % H;
-    const int64_t t = (idx / H) % L;
-    const int64_t b = idx / (H * L);
+    const int Hi = static_cast<int>(H), Li = static_cast<int>(L);
+    const int bt = idx / Hi, h = idx - bt * Hi;
+    const int b = bt / Li, t = bt - b * Li;
     step_coefficients(adt[b * as.b + t * as.t + h * as.h], dt[b * ds.b + t * ds.t + h * ds.h],
                       trap[b * ts_.b + t * ts_.t + h * ts_.h], alpha + idx, beta + idx, gamma + idx);
 }
@@ -259,12 +270,73 @@ struct RecArgs {
 };
 
 // The recurrence proper: one wave per (window, head, 64 headdim columns),
-// lane = column, state column s[n] in registers, time sequential. q, k and the
-// coefficients of kStepsPerChunk tokens are staged in LDS (double-buffered)
-// and v / gate per lane in registers; the next chunk's loads are issued
-// before the current chunk is computed, so no step waits on memory. NM is
-// the register capacity of the state column; EXACT means N == NM.
+// lane = column, state column s[n] in registers, time sequential. q, k, the
+// coefficients, v and gate of kStepsPerChunk tokens are staged in LDS
+// (double-buffered); the next chunk's global loads are issued before the
+// current chunk is computed, so no step waits on memory. NM is the register
+// capacity of the state column; EXACT means N == NM.
 constexpr int kStepsPerChunk = 8;
+
+template <int NM>
+struct RecChunk {
+    static constexpr int kTC = kStepsPerChunk;
+    static constexpr int kQPL = (kTC * NM + 63) / 64;  // staged q (and k) values per lane
+    float q[kQPL], k[kQPL], c, v[kTC], g[kTC];
+};
+
+template <int NM, bool EXACT>
+__device__ __forceinline__ void rec_fetch(RecChunk<NM>& r, int64_t t0, int64_t L, int N, int lane, bool active,
+                                          const float* __restrict__ qrow, int64_t qst,
+                                          const float* __restrict__ krow, int64_t kst,
+                                          const float* __restrict__ vrow, int64_t vst,
+                                          const float* __restrict__ grow, int64_t gst,
+                                          const float* __restrict__ alpha, const float* __restrict__ beta,
+                                          const float* __restrict__ gamma, int64_t cbase, int64_t H) {
+    constexpr int TC = RecChunk<NM>::kTC;
+#pragma unroll
+    for (int j = 0; j < RecChunk<NM>::kQPL; ++j) {
+        const int idx = lane + 64 * j;
+        const int tt = idx / NM, n = idx % NM;
+        const int64_t t = t0 + tt;
+        const bool ok = tt < TC && (EXACT || n < N) && t < L;
+        r.q[j] = ok ? qrow[t * qst + n] : 0.0f;
+        r.k[j] = ok ? krow[t * kst + n] : 0.0f;
+    }
+    r.c = 0.0f;
+    if (lane < 3 * TC) {
+        const int which = lane / TC;
+        const int64_t t = t0 + lane % TC;
+        const float* src = which == 0 ? alpha : (which == 1 ? beta : gamma);
+        if (t < L) r.c = src[cbase + t * H];
+    }
+#pragma unroll
+    for (int tt = 0; tt < TC; ++tt) {
+        const int64_t t = t0 + tt;
+        const bool ok = active && t < L;
+        r.v[tt] = ok ? vrow[t * vst] : 0.0f;
+        r.g[tt] = ok ? grow[t * gst] : 0.0f;
+    }
+}
+
+template <int NM>
+__device__ __forceinline__ void rec_commit(const RecChunk<NM>& r, int lane, float* q_s, float* k_s, float* c_s,
+                                           float* v_s, float* g_s) {
+    constexpr int TC = RecChunk<NM>::kTC;
+#pragma unroll
+    for (int j = 0; j < RecChunk<NM>::kQPL; ++j) {
+        const int idx = lane + 64 * j;
+        if (idx < TC * NM) {
+            q_s[idx] = r.q[j];
+            k_s[idx] = r.k[j];
+        }
+    }
+    if (lane < 3 * TC) c_s[(lane % TC) * 4 + lane / TC] = r.c;
+#pragma unroll
+    for (int tt = 0; tt < TC; ++tt) {
+        v_s[tt * 64 + lane] = r.v[tt];
+        g_s[tt * 64 + lane] = r.g[tt];
+    }
+}
 
 template <int NM, bool EXACT, bool VEC>
 __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D, int N,
@@ -276,10 +348,11 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
                                                  const float* __restrict__ gamma, const float* __restrict__ skip_p,
                                                  float* __restrict__ out, Strides3 os) {
     constexpr int TC = kStepsPerChunk;
-    constexpr int QPL = (TC * NM + 63) / 64;  // staged q (and k) values per lane
     __shared__ float q_s[2][TC * NM];
     __shared__ float k_s[2][TC * NM];
     __shared__ float c_s[2][TC * 4];
+    __shared__ float v_s[2][TC * 64];
+    __shared__ float g_s[2][TC * 64];
     const int64_t blocks_per_head = (D + 63) / 64;
     const int64_t item = blockIdx.x;
     const int64_t dblk = item % blocks_per_head;
@@ -302,107 +375,65 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
     float* orow = out + b * os.b + h * os.h + (active ? d : 0);
     const int64_t cbase = b * L * H + h;
 
-    float qpre[QPL], kpre[QPL], cpre = 0.0f, vpre[TC], gpre[TC];
-    auto fetch = [&](int64_t t0) {
-#pragma unroll
-        for (int j = 0; j < QPL; ++j) {
-            const int idx = lane + 64 * j;
-            const int tt = idx / NM, n = idx % NM;
-            const int64_t t = t0 + tt;
-            const bool ok = tt < TC && (EXACT || n < N) && t < L;
-            qpre[j] = ok ? qrow[t * qs.t + n] : 0.0f;
-            kpre[j] = ok ? krow[t * ks.t + n] : 0.0f;
-        }
-        if (lane < 3 * TC) {
-            const int which = lane / TC;
-            const int64_t t = t0 + lane % TC;
-            const float* src = which == 0 ? alpha : (which == 1 ? beta : gamma);
-            cpre = t < L ? src[cbase + t * H] : 0.0f;
-        }
-#pragma unroll
-        for (int tt = 0; tt < TC; ++tt) {
-            const int64_t t = t0 + tt;
-            vpre[tt] = (active && t < L) ? vrow[t * vs.t] : 0.0f;
-            gpre[tt] = (active && t < L) ? grow[t * gs.t] : 0.0f;
-        }
-    };
-    auto commit = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < QPL; ++j) {
-            const int idx = lane + 64 * j;
-            if (idx < TC * NM) {
-                q_s[buf][idx] = qpre[j];
-                k_s[buf][idx] = kpre[j];
-            }
-        }
-        if (lane < 3 * TC) c_s[buf][(lane % TC) * 4 + lane / TC] = cpre;
-    };
-
-    float vcur[TC], gcur[TC];
-    fetch(0);
-    commit(0);
-#pragma unroll
-    for (int tt = 0; tt < TC; ++tt) {
-        vcur[tt] = vpre[tt];
-        gcur[tt] = gpre[tt];
-    }
+    RecChunk<NM> pre;
+    rec_fetch<NM, EXACT>(pre, 0, L, N, lane, active, qrow, qs.t, krow, ks.t, vrow, vs.t, grow, gs.t, alpha, beta,
+                         gamma, cbase, H);
+    rec_commit<NM>(pre, lane, q_s[0], k_s[0], c_s[0], v_s[0], g_s[0]);
     __syncthreads();
     float v_last = 0.0f;
     for (int64_t t0 = 0, c = 0; t0 < L; t0 += TC, ++c) {
         const int buf = static_cast<int>(c & 1);
         const bool more = t0 + TC < L;
-        if (more) fetch(t0 + TC);
-#pragma unroll
-        for (int tt = 0; tt < TC; ++tt) {
+        if (more) {
+            rec_fetch<NM, EXACT>(pre, t0 + TC, L, N, lane, active, qrow, qs.t, krow, ks.t, vrow, vs.t, grow, gs.t,
+                                 alpha, beta, gamma, cbase, H);
+        }
+        const int steps = static_cast<int>(more ? TC : L - t0);
+#pragma unroll 1
+        for (int tt = 0; tt < steps; ++tt) {
             const int64_t t = t0 + tt;
-            if (t < L) {
-                const float al = c_s[buf][tt * 4], be = c_s[buf][tt * 4 + 1], ga = c_s[buf][tt * 4 + 2];
-                const float* qt = &q_s[buf][tt * NM];
-                const float* kt = &k_s[buf][tt * NM];
-                const float* kp = tt > 0 ? &k_s[buf][(tt - 1) * NM] : (t > 0 ? &k_s[buf ^ 1][(TC - 1) * NM] : kt);
-                const float v_cur = vcur[tt];
-                const float v_prev = tt > 0 ? vcur[tt > 0 ? tt - 1 : 0] : v_last;
-                const float pv = t > 0 ? be * v_prev : 0.0f;
-                const float cv = ga * v_cur;
-                float acc0 = 0.0f, acc1 = 0.0f;
+            const float al = c_s[buf][tt * 4], be = c_s[buf][tt * 4 + 1], ga = c_s[buf][tt * 4 + 2];
+            const float* qt = &q_s[buf][tt * NM];
+            const float* kt = &k_s[buf][tt * NM];
+            const float* kp = tt > 0 ? &k_s[buf][(tt - 1) * NM] : (t > 0 ? &k_s[buf ^ 1][(TC - 1) * NM] : kt);
+            const float v_cur = v_s[buf][tt * 64 + lane];
+            const float v_prev = tt > 0 ? v_s[buf][(tt - 1) * 64 + lane] : v_last;
+            const float g_cur = g_s[buf][tt * 64 + lane];
+            const float pv = t > 0 ? be * v_prev : 0.0f;
+            const float cv = ga * v_cur;
+            float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
-                for (int n = 0; n < NM; ++n) {
-                    if (EXACT || n < N) {
-                        float upd;
-                        if (VEC || t > 0) {
-                            upd = fmaf(kt[n], cv, fmaf(s[n], al, kp[n] * pv));
-                        } else {
-                            upd = fmaf(kt[n], cv, s[n] * al);
-                        }
-                        s[n] = upd;
-                        if (VEC && (n & 1)) {
-                            acc1 = fmaf(upd, qt[n], acc1);
-                        } else {
-                            acc0 = fmaf(upd, qt[n], acc0);
-                        }
+            for (int n = 0; n < NM; ++n) {
+                if (EXACT || n < N) {
+                    float upd;
+                    if (VEC || t > 0) {
+                        upd = fmaf(kt[n], cv, fmaf(s[n], al, kp[n] * pv));
+                    } else {
+                        upd = fmaf(kt[n], cv, s[n] * al);
+                    }
+                    s[n] = upd;
+                    if (VEC && (n & 1)) {
+                        acc1 = fmaf(upd, qt[n], acc1);
+                    } else {
+                        acc0 = fmaf(upd, qt[n], acc0);
                     }
                 }
-                const float y = fmaf(skip, v_cur, VEC ? acc0 + acc1 : acc0);
-                float o;
-                if (gate_logits) {
-                    const double z = static_cast<double>(gcur[tt]);
-                    o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
-                } else {
-                    o = y * gcur[tt];
-                }
-                if (active) orow[t * os.t] = o;
             }
+            const float y = fmaf(skip, v_cur, VEC ? acc0 + acc1 : acc0);
+            float o;
+            if (gate_logits) {
+                const double z = static_cast<double>(g_cur);
+                o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
+            } else {
+                o = y * g_cur;
+            }
+            if (active) orow[t * os.t] = o;
         }
-        v_last = vcur[TC - 1];
         if (more) {
-            // Buffer buf ^ 1 (the chunk before this one) was last read at tt = 0 above.
+            // The chunk before this one (buffer buf ^ 1) was last read at tt = 0 above.
+            v_last = v_s[buf][(TC - 1) * 64 + lane];
             __syncthreads();
-            commit(buf ^ 1);
-#pragma unroll
-            for (int tt = 0; tt < TC; ++tt) {
-                vcur[tt] = vpre[tt];
-                gcur[tt] = gpre[tt];
-            }
+            rec_commit<NM>(pre, lane, q_s[buf ^ 1], k_s[buf ^ 1], c_s[buf ^ 1], v_s[buf ^ 1], g_s[buf ^ 1]);
             __syncthreads();
         }
     }
@@ -529,15 +560,17 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs p) {
         co[4 * h + 3] = dt;
     }
     __syncthreads();
-    for (int64_t i = tid; i < H * N; i += kStepThreads) {
-        const int64_t h = i / N, n = i % N, g = h / (H / G);
+    const int Ni = static_cast<int>(N), heads_per_group = static_cast<int>(H / G);
+    for (int i = tid; i < H * N; i += kStepThreads) {
+        const int h = i / Ni, n = i - h * Ni, g = h / heads_per_group;
         k_l[i] = (b_raw[g * N + n] * sc[g]) * p.b_norm_w[n] + p.b_bias[h * N + n];
         q_l[i] = (c_raw[g * N + n] * sc[G + g]) * p.c_norm_w[n] + p.c_bias[h * N + n];
     }
     __syncthreads();
     const int64_t Rw = R > 0 ? R : 1;
-    for (int64_t i = tid; i < H * R; i += kStepThreads) {
-        const int64_t h = i / R, r = i % R;
+    const int Ri = static_cast<int>(R);
+    for (int i = tid; i < H * R; i += kStepThreads) {
+        const int h = i / Ri, r = i - h * Ri;
         double* run = p.angle + (s_idx * H + h) * Rw + r;
         const double next = *run + static_cast<double>((tanhf_cr(raw_ang[r]) * kPiF) * co[4 * h + 3]);
         *run = next;
@@ -638,6 +671,7 @@ mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, c
     float* beta = alpha + blh;
     float* gamma = beta + blh;
     auto s3 = [](const int64_t* x) { return Strides3{x[0], x[1], x[2]}; };
+    MLK_CHECK(blh < (int64_t{1} << 31), "too many tokens x heads for one launch");
     hipLaunchKernelGGL(coef_kernel, dim3(ceil_div(blh, 256)), dim3(256), 0, stream, batch, length, heads, adt,
                        s3(adt_strides), dt, s3(dt_strides), trap_logit, s3(trap_strides), alpha, beta, gamma);
     const mlk_status st = launch_status("mamba3 coefficients");

@@ -449,7 +449,9 @@ __global__ __launch_bounds__(kWave) void mhc_prepare_generic_kernel(GenericArgs 
 // combine
 // ---------------------------------------------------------------------------
 
-template <int N>
+// I: index type of the flat (token, 4-column chunk) index; 32-bit when it fits,
+// which keeps the per-thread division by the chunk count cheap.
+template <int N, typename I>
 __global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __restrict__ streams, int64_t tokens,
                                                                  int64_t d, int64_t sd, int64_t ts,
                                                                  const float* __restrict__ res,
@@ -457,11 +459,12 @@ __global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __
                                                                  const float* __restrict__ out,
                                                                  float* __restrict__ new_streams,
                                                                  float* __restrict__ collapsed) {
-    const int64_t chunks = d / 4;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (idx >= tokens * chunks) return;
-    const int64_t token = idx / chunks;
-    const int64_t k = (idx % chunks) * 4;
+    const I chunks = static_cast<I>(d / 4);
+    const I idx = static_cast<I>(blockIdx.x) * kBlock + threadIdx.x;
+    if (static_cast<int64_t>(idx) >= tokens * static_cast<int64_t>(chunks)) return;
+    const I token_i = idx / chunks;
+    const int64_t token = token_i;
+    const int64_t k = static_cast<int64_t>(idx - token_i * chunks) * 4;
     const float4 o = *reinterpret_cast<const float4*>(out + token * d + k);
     float4 s[N];
 #pragma unroll
@@ -498,6 +501,7 @@ __global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __
 }
 
 // Any n, d, stride and alignment: one thread per (token, k).
+template <typename I>
 __global__ __launch_bounds__(kBlock) void mhc_combine_scalar_kernel(const float* __restrict__ streams,
                                                                     int64_t tokens, int n, int64_t d, int64_t sd,
                                                                     int64_t ts, const float* __restrict__ res,
@@ -505,10 +509,11 @@ __global__ __launch_bounds__(kBlock) void mhc_combine_scalar_kernel(const float*
                                                                     const float* __restrict__ out,
                                                                     float* __restrict__ new_streams,
                                                                     float* __restrict__ collapsed) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (idx >= tokens * d) return;
-    const int64_t token = idx / d;
-    const int64_t k = idx % d;
+    const I idx = static_cast<I>(blockIdx.x) * kBlock + threadIdx.x;
+    if (static_cast<int64_t>(idx) >= tokens * d) return;
+    const I token_i = idx / static_cast<I>(d);
+    const int64_t token = token_i;
+    const int64_t k = idx - token_i * static_cast<I>(d);
     const double o = static_cast<double>(out[token * d + k]);
     const float* s = streams + token * ts + k;
     double mean = 0.0;
@@ -533,10 +538,16 @@ mlk_status launch_combine(const float* streams, int64_t tokens, int64_t n, int64
                      al16(collapsed) && n >= 1 && n <= 8;
     if (vec) {
         const int64_t blocks = ceil_div(tokens * (d / 4), kBlock);
+        const bool narrow = tokens * (d / 4) < (int64_t{1} << 31);
 #define MLK_COMBINE(NN)                                                                                        \
     case NN:                                                                                                   \
-        hipLaunchKernelGGL(mhc_combine_vec_kernel<NN>, dim3(blocks), dim3(kBlock), 0, stream, streams, tokens, d, \
-                           sd, ts, res, post, out, new_streams, collapsed);                                    \
+        if (narrow) {                                                                                          \
+            hipLaunchKernelGGL((mhc_combine_vec_kernel<NN, uint32_t>), dim3(blocks), dim3(kBlock), 0, stream,  \
+                               streams, tokens, d, sd, ts, res, post, out, new_streams, collapsed);            \
+        } else {                                                                                               \
+            hipLaunchKernelGGL((mhc_combine_vec_kernel<NN, int64_t>), dim3(blocks), dim3(kBlock), 0, stream,   \
+                               streams, tokens, d, sd, ts, res, post, out, new_streams, collapsed);            \
+        }                                                                                                      \
         break;
         switch (n) {
             MLK_COMBINE(1)
@@ -553,8 +564,13 @@ mlk_status launch_combine(const float* streams, int64_t tokens, int64_t n, int64
         return launch_status("mhc_combine");
     }
     const int64_t blocks = ceil_div(tokens * d, kBlock);
-    hipLaunchKernelGGL(mhc_combine_scalar_kernel, dim3(blocks), dim3(kBlock), 0, stream, streams, tokens,
-                       static_cast<int>(n), d, sd, ts, res, post, out, new_streams, collapsed);
+    if (tokens * d < (int64_t{1} << 31)) {
+        hipLaunchKernelGGL(mhc_combine_scalar_kernel<uint32_t>, dim3(blocks), dim3(kBlock), 0, stream, streams,
+                           tokens, static_cast<int>(n), d, sd, ts, res, post, out, new_streams, collapsed);
+    } else {
+        hipLaunchKernelGGL(mhc_combine_scalar_kernel<int64_t>, dim3(blocks), dim3(kBlock), 0, stream, streams,
+                           tokens, static_cast<int>(n), d, sd, ts, res, post, out, new_streams, collapsed);
+    }
     return launch_status("mhc_combine");
 }
 

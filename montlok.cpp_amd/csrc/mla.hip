@@ -51,16 +51,22 @@ struct RopeArgs {
 
 // One thread per (token, head, lane j): j < nope copies k_nope; nope <= j <
 // nope + rope/2 rotates the pair (i, i + rope/2), i = j - nope, of k and q.
+// I: index type of the flat thread index, 32-bit when it fits (cheap divisions).
+template <typename I>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs p) {
-    const int64_t per_head = p.nope_dim + (p.head_dim - p.nope_dim) / 2;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= p.batch * p.length * p.heads * per_head) return;
-    const int64_t j = idx % per_head;
-    const int64_t th = idx / per_head;  // token * heads + h
-    const int64_t h = th % p.heads;
-    const int64_t token = th / p.heads;
-    const int64_t pos = token % p.length;
-    const int64_t seq = token / p.length;
+    const I per_head = static_cast<I>(p.nope_dim + (p.head_dim - p.nope_dim) / 2);
+    const I idx = static_cast<I>(blockIdx.x) * 256 + threadIdx.x;
+    if (static_cast<int64_t>(idx) >= p.batch * p.length * p.heads * static_cast<int64_t>(per_head)) return;
+    const I th_i = idx / per_head;  // token * heads + h
+    const int64_t j = idx - th_i * per_head;
+    const I heads = static_cast<I>(p.heads), length = static_cast<I>(p.length);
+    const I token_i = th_i / heads;
+    const int64_t th = th_i;
+    const int64_t h = th_i - token_i * heads;
+    const I seq_i = token_i / length;
+    const int64_t token = token_i;
+    const int64_t pos = token_i - seq_i * length;
+    const int64_t seq = seq_i;
     const int64_t rope_dim = p.head_dim - p.nope_dim;
     const int64_t half = rope_dim / 2;
     float* kh = p.k + th * p.head_dim;
@@ -381,8 +387,12 @@ extern "C" mlk_status mlk_mla_rope_qk(float* q, int64_t q_token_stride, int64_t 
     RopeArgs p{q, q_token_stride, q_length, kv, k_rope, k_rope_token_stride, cosine, sine, k,
                batch, length, heads, head_dim, nope_dim};
     const int64_t threads = batch * length * heads * (nope_dim + rope_dim / 2);
-    hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>(ceil_div(threads, 256))), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), p);
+    const dim3 grid(static_cast<unsigned>(ceil_div(threads, 256)));
+    if (threads < (int64_t{1} << 31)) {
+        hipLaunchKernelGGL(rope_kernel<uint32_t>, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), p);
+    } else {
+        hipLaunchKernelGGL(rope_kernel<int64_t>, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), p);
+    }
     return launch_status("mla rope");
 }
 

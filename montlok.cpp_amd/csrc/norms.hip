@@ -230,12 +230,14 @@ __global__ __launch_bounds__(kBlock) void layer_norm_scalar_kernel(const float* 
     }
 }
 
+template <typename I>
 __global__ __launch_bounds__(kBlock) void swiglu_kernel(const float* __restrict__ x, int64_t rows, int64_t hidden,
                                                         int64_t row_stride, float* __restrict__ out) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (i >= rows * hidden) return;
-    const int64_t row = i / hidden;
-    const int64_t k = i % hidden;
+    const I i = static_cast<I>(blockIdx.x) * kBlock + threadIdx.x;
+    if (static_cast<int64_t>(i) >= rows * hidden) return;
+    const I row_i = i / static_cast<I>(hidden);
+    const int64_t row = row_i;
+    const int64_t k = i - row_i * static_cast<I>(hidden);
     const double z = static_cast<double>(x[row * row_stride + k]);
     const double u = static_cast<double>(x[row * row_stride + hidden + k]);
     out[i] = static_cast<float>((z / (1.0 + exp(-z))) * u);
@@ -313,7 +315,13 @@ mlk_status mlk_swiglu(const float* x, int64_t rows, int64_t hidden, int64_t row_
     MLK_CHECK(rows == 0 || (x != nullptr && out != nullptr), "null tensor pointer");
     if (rows == 0) return MLK_OK;
     const int64_t blocks = ceil_div(rows * hidden, kBlock);
-    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(kBlock), 0, stream, x, rows, hidden, row_stride, out);
+    if (rows * hidden < (int64_t{1} << 31)) {
+        hipLaunchKernelGGL(swiglu_kernel<uint32_t>, dim3(blocks), dim3(kBlock), 0, stream, x, rows, hidden, row_stride,
+                           out);
+    } else {
+        hipLaunchKernelGGL(swiglu_kernel<int64_t>, dim3(blocks), dim3(kBlock), 0, stream, x, rows, hidden, row_stride,
+                           out);
+    }
     return launch_status("swiglu");
 }
 

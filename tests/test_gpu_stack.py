@@ -1,0 +1,81 @@
+"""GPU parity of the hybrid stack (feature projection, 4 mHC residual layers
+alternating Mamba-3 and MLA, collapse) against the same chain of oracle ops:
+fp32 weights within 1e-5, bf16 weights within 2e-2 (normwise)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16_TOL, assert_close
+from test_gpu_modules import _mamba_oracle, _mla_oracle, _np
+
+pytestmark = pytest.mark.gpu
+
+
+def _randomise(stack, bf16: bool):
+    torch.manual_seed(5)
+    with torch.no_grad():
+        for hc in stack.hcs:
+            for a in (hc.pre_alpha, hc.post_alpha, hc.res_alpha):
+                a.fill_(0.7)
+            for p in (hc.pre_proj.weight, hc.post_proj.weight, hc.res_proj.weight):
+                p.normal_(0.0, stack.d_model ** -0.5)
+            hc.res_bias.normal_()
+        for n in stack.norms:
+            n.weight.normal_(1.0, 0.1)
+        for m in stack.mixers:
+            if hasattr(m, "B_bias"):
+                m.B_bias.add_(0.3 * torch.randn_like(m.B_bias))
+        if bf16:
+            for w in stack.linear_weights():
+                w.normal_(0.0, 0.02)
+                w.copy_(w.bfloat16().float())
+
+
+def _oracle_stack(oracle, stack, feats):
+    from montlok.rdt.mla import rope_tables
+
+    B, L, _ = feats.shape
+    cos, sin = (t.numpy() for t in rope_tables(L, stack.mixers[1].rope_dim))
+    h = oracle.linear(feats, _np(stack.feature_proj.weight), _np(stack.feature_proj.bias))
+
+    def mixer(i, x):
+        m = stack.mixers[i]
+        return _mamba_oracle(oracle, m, x) if i % 2 == 0 else _mla_oracle(oracle, m, x, L, 1, cos, sin)
+
+    def prepare(i, streams, n_streams):
+        hc = stack.hcs[i]
+        return oracle.mhc_prepare(streams, _np(hc.dyn_norm.weight), hc.dyn_norm.eps,
+                                  hc._projection_block().cpu().numpy(), _np(hc.pre_bias), _np(hc.post_bias),
+                                  _np(hc.res_bias), float(hc.pre_alpha), float(hc.post_alpha), float(hc.res_alpha),
+                                  hc.sinkhorn_iters, n_streams, _np(stack.norms[i].weight), stack.norms[i].eps)
+
+    agg, pre, post, res = prepare(0, h, stack.n_streams)
+    out = mixer(0, agg)
+    streams = h
+    for i in range(1, len(stack.hcs)):
+        streams = oracle.mhc_combine(streams, res, post, out)
+        agg, pre, post, res = prepare(i, streams, 0)
+        out = mixer(i, agg)
+    return oracle.mhc_combine(streams, res, post, out, collapse=True, materialize=False)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_hybrid_stack(dev, oracle, bf16):
+    from montlok.rdt.stack import HybridStackHIP
+
+    stack = HybridStackHIP(40, d_model=64, n_layers=4, n_streams=4, d_state=16, mamba_headdim=32, n_heads=2,
+                           head_dim=32, rope_head_dim=16, kv_lora_rank=32).eval()
+    _randomise(stack, bf16)
+    feats = np.clip(np.random.default_rng(6).standard_normal((2, 32, 40)), -8, 8).astype(np.float32)
+    expect = _oracle_stack(oracle, stack, feats)
+    stack = stack.to(dev)
+    if bf16:
+        for w in stack.linear_weights():
+            w.data = w.data.bfloat16()
+    with torch.no_grad():
+        out = stack(torch.from_numpy(feats).to(dev))
+    assert out.shape == (2, 32, 64)
+    assert_close(out, expect, tol=BF16_TOL if bf16 else 1e-5, name=f"hybrid stack bf16={bf16}")
