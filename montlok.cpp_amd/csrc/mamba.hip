@@ -109,12 +109,13 @@ struct PrepArgs {
     float* term;   // [B, L, H, max(R, 1)]
 };
 
-// Phase A for kPrepTokens tokens per block: the [B | C | dt | A | trap |
-// angles] slice of each token's row is staged in LDS with coalesced loads,
-// then norms (one thread per token and group), coefficients (per token and
-// head), q/k (per element) and the angle terms are computed from LDS.
-constexpr int kPrepTokens = 8;
-
+// Phase A for kPrepTokens tokens per block (32 when that still leaves at least
+// 1024 blocks, else 8): the [B | C | dt | A | trap | angles] slice of each
+// token's row and the B/C norm weights and biases are staged in LDS with
+// coalesced loads, then norms (one thread per token and group), coefficients
+// (per token and head), q/k (per element) and the angle terms are computed
+// from LDS.
+template <int kPrepTokens>
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
     extern __shared__ float seg_s[];
     // Block-local index math in 32 bits (the sizes are checked at launch).
@@ -125,6 +126,8 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
     const int64_t d_inner = p.H * p.D;
     float* sc_s = seg_s + kPrepTokens * seg;  // [tokens][2G]
     float* dt_s = sc_s + kPrepTokens * 2 * G;  // [tokens][H]
+    float* bw_s = dt_s + kPrepTokens * H;      // [N] B norm weight, then [N] C norm weight
+    float* bb_s = bw_s + 2 * N;                // [H][N] B bias, then [H][N] C bias
     __shared__ const float* rows_s[kPrepTokens];
     const int64_t BL = p.B * p.L;
     const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * kPrepTokens;
@@ -138,6 +141,14 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
     for (int i = tid; i < kPrepTokens * seg; i += 256) {
         const int tt = i / seg, j = i - tt * seg;
         seg_s[i] = tt < ntok ? rows_s[tt][j] : 0.0f;
+    }
+    for (int i = tid; i < N; i += 256) {
+        bw_s[i] = p.b_norm_w[i];
+        bw_s[N + i] = p.c_norm_w[i];
+    }
+    for (int i = tid; i < H * N; i += 256) {
+        bb_s[i] = p.b_bias[i];
+        bb_s[H * N + i] = p.c_bias[i];
     }
     __syncthreads();
     for (int i = tid; i < kPrepTokens * 2 * G; i += 256) {
@@ -166,8 +177,8 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
         const float* x = seg_s + tt * seg;
         const float* sc = sc_s + tt * 2 * G;
         const int64_t o = (tok0 + tt) * HN + rem;
-        p.k[o] = (x[g * N + n] * sc[g]) * p.b_norm_w[n] + p.b_bias[h * N + n];
-        p.q[o] = (x[GN + g * N + n] * sc[G + g]) * p.c_norm_w[n] + p.c_bias[h * N + n];
+        p.k[o] = (x[g * N + n] * sc[g]) * bw_s[n] + bb_s[rem];
+        p.q[o] = (x[GN + g * N + n] * sc[G + g]) * bw_s[N + n] + bb_s[HN + rem];
     }
     const int HR = H * R;
     for (int i = tid; i < ntok * HR; i += 256) {
@@ -178,8 +189,9 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
     }
 }
 
-size_t prep_lds_bytes(int64_t N, int64_t G, int64_t H, int64_t R) {
-    return sizeof(float) * static_cast<size_t>(kPrepTokens * (2 * G * N + 3 * H + R + 2 * G + H));
+size_t prep_lds_bytes(int tokens_per_block, int64_t N, int64_t G, int64_t H, int64_t R) {
+    return sizeof(float) *
+           static_cast<size_t>(tokens_per_block * (2 * G * N + 3 * H + R + 2 * G + H) + 2 * N + 2 * H * N);
 }
 
 // Phase B + C for one (window, head): the angle terms of a run of tokens are
@@ -338,7 +350,14 @@ __device__ __forceinline__ void rec_commit(const RecChunk<NM>& r, int lane, floa
     }
 }
 
-template <int NM, bool EXACT, bool VEC>
+// Lane layout. VEC is the reference's vector path (headdim a multiple of 8)
+// with even/odd state-row accumulators (montlok_kernel.h:300-322), y =
+// acc_even + acc_odd; otherwise one accumulator. Default: 64 columns per
+// wave, one lane per column holding every state row. PAIR (VEC with headdim
+// <= 32, where half a wave would idle): 32 columns per wave, two lanes per
+// column; the lane of parity p owns the rows n = p (mod 2) and their
+// accumulator, and the pair's two sums are added in the reference's order.
+template <int NM, bool EXACT, bool VEC, bool PAIR>
 __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D, int N,
                                                  const float* __restrict__ q, Strides3 qs,
                                                  const float* __restrict__ k, Strides3 ks,
@@ -348,25 +367,28 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
                                                  const float* __restrict__ gamma, const float* __restrict__ skip_p,
                                                  float* __restrict__ out, Strides3 os) {
     constexpr int TC = kStepsPerChunk;
+    constexpr int kCols = PAIR ? 32 : 64;     // columns per wave
+    constexpr int kRows = PAIR ? NM / 2 : NM;  // state rows per lane
     __shared__ float q_s[2][TC * NM];
     __shared__ float k_s[2][TC * NM];
     __shared__ float c_s[2][TC * 4];
     __shared__ float v_s[2][TC * 64];
     __shared__ float g_s[2][TC * 64];
-    const int64_t blocks_per_head = (D + 63) / 64;
+    const int64_t blocks_per_head = (D + kCols - 1) / kCols;
     const int64_t item = blockIdx.x;
     const int64_t dblk = item % blocks_per_head;
     const int64_t bh = item / blocks_per_head;
     const int64_t h = bh % H;
     const int64_t b = bh / H;
     const int lane = threadIdx.x;
-    const int64_t d = dblk * 64 + lane;
+    const int par = PAIR ? lane >> 5 : 0;
+    const int64_t d = dblk * kCols + (PAIR ? (lane & 31) : lane);
     const bool active = d < D;
     if (EXACT) N = NM;
 
-    float s[NM];
+    float s[kRows];
 #pragma unroll
-    for (int n = 0; n < NM; ++n) s[n] = 0.0f;
+    for (int m = 0; m < kRows; ++m) s[m] = 0.0f;
     const float skip = skip_p[h];
     const float* qrow = q + b * qs.b + h * qs.h;
     const float* krow = k + b * ks.b + h * ks.h;
@@ -403,23 +425,31 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
             const float cv = ga * v_cur;
             float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
-            for (int n = 0; n < NM; ++n) {
+            for (int m = 0; m < kRows; ++m) {
+                const int n = PAIR ? 2 * m + par : m;
                 if (EXACT || n < N) {
                     float upd;
                     if (VEC || t > 0) {
-                        upd = fmaf(kt[n], cv, fmaf(s[n], al, kp[n] * pv));
+                        upd = fmaf(kt[n], cv, fmaf(s[m], al, kp[n] * pv));
                     } else {
-                        upd = fmaf(kt[n], cv, s[n] * al);
+                        upd = fmaf(kt[n], cv, s[m] * al);
                     }
-                    s[n] = upd;
-                    if (VEC && (n & 1)) {
+                    s[m] = upd;
+                    if (!PAIR && VEC && (n & 1)) {
                         acc1 = fmaf(upd, qt[n], acc1);
                     } else {
                         acc0 = fmaf(upd, qt[n], acc0);
                     }
                 }
             }
-            const float y = fmaf(skip, v_cur, VEC ? acc0 + acc1 : acc0);
+            float sum;
+            if constexpr (PAIR) {
+                const float other = __shfl_xor(acc0, 32);
+                sum = par == 0 ? acc0 + other : other + acc0;  // acc_even + acc_odd
+            } else {
+                sum = VEC ? acc0 + acc1 : acc0;
+            }
+            const float y = fmaf(skip, v_cur, sum);
             float o;
             if (gate_logits) {
                 const double z = static_cast<double>(g_cur);
@@ -427,7 +457,7 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
             } else {
                 o = y * g_cur;
             }
-            if (active) orow[t * os.t] = o;
+            if (active && par == 0) orow[t * os.t] = o;
         }
         if (more) {
             // The chunk before this one (buffer buf ^ 1) was last read at tt = 0 above.
@@ -442,18 +472,21 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
 mlk_status launch_rec(const RecArgs& a, hipStream_t stream) {
     if (a.B * a.L * a.H == 0 || a.D == 0) return MLK_OK;
     const bool vec = a.D % 8 == 0;
-    const int64_t grid = a.B * a.H * ((a.D + 63) / 64);
+    const bool pair = vec && a.D <= 32;
+    const int64_t grid = a.B * a.H * ((a.D + (pair ? 31 : 63)) / (pair ? 32 : 64));
     const int N = static_cast<int>(a.N);
+#define MLK_REC_LAUNCH(NM, EXACT, VEC, PAIR)                                                                     \
+    hipLaunchKernelGGL((rec_kernel<NM, EXACT, VEC, PAIR>), dim3(grid), dim3(64), 0, stream, a.L, a.H, a.D, N, a.q, \
+                       a.qs, a.k, a.ks, a.v, a.vs, a.gate, a.gs, a.gate_logits, a.alpha, a.beta, a.gamma, a.skip, \
+                       a.out, a.os)
 #define MLK_REC(NM, EXACT)                                                                                         \
     do {                                                                                                           \
-        if (vec) {                                                                                                 \
-            hipLaunchKernelGGL((rec_kernel<NM, EXACT, true>), dim3(grid), dim3(64), 0, stream, a.L, a.H, a.D, N,   \
-                               a.q, a.qs, a.k, a.ks, a.v, a.vs, a.gate, a.gs, a.gate_logits, a.alpha, a.beta,      \
-                               a.gamma, a.skip, a.out, a.os);                                                      \
+        if (pair) {                                                                                                \
+            MLK_REC_LAUNCH(NM, EXACT, true, true);                                                                 \
+        } else if (vec) {                                                                                          \
+            MLK_REC_LAUNCH(NM, EXACT, true, false);                                                                \
         } else {                                                                                                   \
-            hipLaunchKernelGGL((rec_kernel<NM, EXACT, false>), dim3(grid), dim3(64), 0, stream, a.L, a.H, a.D, N,  \
-                               a.q, a.qs, a.k, a.ks, a.v, a.vs, a.gate, a.gs, a.gate_logits, a.alpha, a.beta,      \
-                               a.gamma, a.skip, a.out, a.os);                                                      \
+            MLK_REC_LAUNCH(NM, EXACT, false, false);                                                               \
         }                                                                                                          \
         return launch_status("mamba3 recurrence");                                                                 \
     } while (0)
@@ -468,6 +501,7 @@ mlk_status launch_rec(const RecArgs& a, hipStream_t stream) {
     if (N <= 64) MLK_REC(64, false);
     if (N <= 128) MLK_REC(128, false);
 #undef MLK_REC
+#undef MLK_REC_LAUNCH
     set_error("d_state above 128 is not supported by the GPU recurrence");
     return MLK_ERR_UNSUPPORTED;
 }
@@ -757,9 +791,14 @@ mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_
     pa.beta = beta;
     pa.gamma = gamma;
     pa.term = term;
-    const size_t prep_lds = prep_lds_bytes(d_state, ngroups, nheads, num_rope_angles);
+    const int tpb = ceil_div(batch * length, 32) >= 1024 ? 32 : 8;
+    const size_t prep_lds = prep_lds_bytes(tpb, d_state, ngroups, nheads, num_rope_angles);
     MLK_CHECK(prep_lds <= 64 * 1024, "Mamba-3 in_proj layout too wide for the GPU prep kernel");
-    hipLaunchKernelGGL(prep_kernel, dim3(ceil_div(batch * length, kPrepTokens)), dim3(256), prep_lds, stream, pa);
+    if (tpb == 32) {
+        hipLaunchKernelGGL(prep_kernel<32>, dim3(ceil_div(batch * length, 32)), dim3(256), prep_lds, stream, pa);
+    } else {
+        hipLaunchKernelGGL(prep_kernel<8>, dim3(ceil_div(batch * length, 8)), dim3(256), prep_lds, stream, pa);
+    }
     mlk_status st = launch_status("mamba3 prep");
     if (st != MLK_OK) return st;
     if (num_rope_angles > 0) {
