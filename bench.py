@@ -557,26 +557,18 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
 
     x = xs[0]
     projected = _C.linear(x, w["in_w"])
-    q = projected[..., :d].unflatten(-1, (H, hd))
-    kv_lat = projected[..., d:d + kvr]
-    k_rope = projected[..., d + kvr:]
-    kvn = _C.layer_norm(kv_lat, w["ln_w"], w["ln_b"], 1e-5)
-    kv = _C.linear(kvn, w["kv_up"]).view(B, L, H, nope + hd)
-    k = _C.mla_rope_qk(q, kv, k_rope, cos, sin, nope)
-    v = kv[..., nope:]
-    att = _C.attention(q, k, v, _C.MASK_CAUSAL_TOP_LEFT, scale, torch.bfloat16).view(B, L, d)
+    att = _C._fused_attend(projected, B, L, d, H, hd, nope, kvr, w["ln_w"], w["ln_b"], 1e-5, w["kv_up"], cos, sin,
+                           scale).view(B, L, d)
     f, h2 = 4, 2
     pairs = B * H * L * (L + 1) // 2
     ops = {
         "in_proj": dict(fn=lambda: _C.linear(x, w["in_w"]), bytes=T * d * f + (d + kvr + r) * d * h2 + T * (d + kvr + r) * f,
                         flops=2 * T * d * (d + kvr + r)),
-        "kv_norm": dict(fn=lambda: _C.layer_norm(kv_lat, w["ln_w"], w["ln_b"], 1e-5), bytes=2 * T * kvr * f + 2 * kvr * f),
-        "kv_up": dict(fn=lambda: _C.linear(kvn, w["kv_up"]), bytes=T * kvr * f + H * (nope + hd) * kvr * h2 +
-                      T * H * (nope + hd) * f, flops=2 * T * kvr * H * (nope + hd)),
-        "rope_qk": dict(fn=lambda: _C.mla_rope_qk(q, kv, k_rope, cos, sin, nope),
-                        bytes=(2 * T * H * r + T * r + T * H * nope + T * H * hd + 2 * L * r) * f),
-        "attention": dict(fn=lambda: _C.attention(q, k, v, _C.MASK_CAUSAL_TOP_LEFT, scale, torch.bfloat16),
-                          bytes=4 * T * d * f, flops=4 * pairs * hd),
+        # LayerNorm + kv_up + RoPE + causal attention in one kernel: q, the latent and k_rope in, attention out.
+        "mla_attend": dict(fn=lambda: _C._fused_attend(projected, B, L, d, H, hd, nope, kvr, w["ln_w"], w["ln_b"], 1e-5,
+                                                       w["kv_up"], cos, sin, scale),
+                           bytes=T * (d + kvr + r) * f + H * (nope + hd) * kvr * h2 + T * d * f,
+                           flops=2 * T * kvr * H * (nope + hd) + 4 * pairs * hd),
         "o_proj": dict(fn=lambda: _C.linear(att, w["o"]), bytes=2 * T * d * f + d * d * h2, flops=2 * T * d * d),
     }
     table = _kernel_table(ops, _op_times(ops, max(4, steps // 8)), "bf16")
@@ -587,7 +579,7 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
                       "synthetic (seeded N(0,1) inputs, N(0,0.02) bf16 weights)",
                       {"workload": "mla_causal_fwd", "windows": B, "seq_len": L, "d_model": d, "heads": H,
                        "head_dim": hd, "rope_dim": r, "kv_rank": kvr, "rope_theta": cfg["theta"],
-                       "step": "mla_forward (in_proj, LayerNorm, kv_up, RoPE, causal attention, o_proj)",
+                       "step": "mla_forward: in_proj GEMM, fused LayerNorm + kv_up + RoPE + causal attention, o_proj GEMM",
                        "launch": f"HIP graph of {sets} steps over {sets} input sets, replayed",
                        "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")

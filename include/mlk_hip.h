@@ -134,6 +134,23 @@ mlk_status mlk_attention(const float* q, int64_t q_token_stride, int64_t q_head_
                          int64_t head_dim, int32_t mask, double scale, int32_t precision, float* out,
                          mlk_stream_t stream);
 
+/* The part of mla_forward between its two projections (montlok.cpp:1196-1209)
+ * for the full causal sequence, fused per (window, head): LayerNorm of the
+ * latent rows, this head's kv_up slice (bf16 weights), k = cat(k_nope,
+ * rope(k_rope)), q's rope lanes rotated, top-left causal attention.
+ * projected: in_proj output [B, L, W] with q at column q_offset + h*head_dim,
+ * the latent at kv_offset and k_rope at k_rope_offset; kv_up_weight: bf16
+ * [H*(nope+hd), kv_rank]; cos/sin: [L, rope]; out: [B, L, H, head_dim]. The
+ * result equals mla_rope_qk + mlk_attention (bf16) on the separately
+ * computed kv, bit for bit. Built for head_dim 32 / nope 16 (L <= 128) and
+ * head_dim 64 / nope 32 (L <= 256), kv_rank 64; MLK_ERR_UNSUPPORTED
+ * otherwise. No reference operator of its own. */
+mlk_status mlk_mla_attend(const float* projected, int64_t batch, int64_t length, int64_t proj_token_stride,
+                          int64_t q_offset, int64_t kv_offset, int64_t k_rope_offset, int64_t heads,
+                          int64_t head_dim, int64_t nope_dim, int64_t kv_rank, const float* kv_norm_w,
+                          const float* kv_norm_b, double kv_norm_eps, const void* kv_up_weight, const float* cosine,
+                          const float* sine, double scale, float* out, mlk_stream_t stream);
+
 /* ----------------------------------------------------------------- mHC -- */
 
 /* mhc_prepare(streams, norm_w, eps, proj_w, pre_bias, post_bias, res_bias,

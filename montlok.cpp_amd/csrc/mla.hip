@@ -367,6 +367,343 @@ void dispatch_attn(const AttnArgs& p, bool vec, hipStream_t stream) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
+// ---------------------------------------------------- fused latent attention
+
+// The part of mla_forward between the two projections, for one (window,
+// head) per block: LayerNorm of the window's latent rows, this head's slice
+// of kv_up on the matrix cores, k = cat(k_nope, rope(k_rope)), q's rope lanes
+// rotated, causal attention, all staged in LDS, so neither the normalised
+// latent, kv, k nor the rotated q goes through HBM. Every value is computed
+// with the operations of the separate kernels (layer_norm_vec_kernel with 16
+// lanes per row, linear_kernel's bf16 MFMA over k steps of 32, rope_kernel's
+// fp64 rotation, attn_kernel's softmax), so the output is bit-identical to
+// the unfused path. Blocks are mapped so that the heads of one window run on
+// one XCD and share its L2 copy of the window's latent rows.
+struct MlaAttendArgs {
+    const float* proj;  // in_proj output rows [B, L, W]
+    int64_t proj_ts;    // W
+    int64_t q_off, kv_off, kr_off;
+    const float* ln_w;
+    const float* ln_b;  // may be null
+    double ln_eps;
+    const u16* w_up;  // [H * (nope + hd), kv_rank] bf16
+    const float* cosine;
+    const float* sine;
+    float* out;  // [B, L, H, hd]
+    int64_t batch, heads, length;
+    float scale_log2;
+};
+
+template <int HD, int NOPE, int KV, int NW, int TPW>
+__global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
+    constexpr int THREADS = 64 * NW;
+    constexpr int ROPE = HD - NOPE, HALF = ROPE / 2;
+    constexpr int LMAX = 16 * NW * TPW;  // NW waves x TPW query tiles x 16
+    constexpr int UPW = NOPE + HD;       // kv_up rows of one head
+    constexpr int XP = KV + 8;           // LDS pitches in bf16 elements (+16 bytes)
+    constexpr int KP = HD + 8;
+    constexpr int VP = LMAX + 8;
+    constexpr int HC = HD / 32;
+    constexpr int OT = HD / 16;
+    static_assert(HD <= KV && KV == 64 && HD % 32 == 0 && UPW % 16 == 0 && NOPE % 4 == 0 && HALF % 4 == 0,
+                  "geometry");
+    __shared__ __attribute__((aligned(16))) u16 xq_s[LMAX * XP];  // LN(kv_latent); later q (pitch KP)
+    __shared__ __attribute__((aligned(16))) u16 wu_s[UPW * XP];
+    __shared__ __attribute__((aligned(16))) u16 k_s[LMAX * KP];
+    __shared__ __attribute__((aligned(16))) u16 vt_s[HD * VP];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int L = static_cast<int>(p.length);
+    const int H = static_cast<int>(p.heads);
+    int64_t b, h;
+    {
+        const int64_t id = blockIdx.x;
+        if (p.batch % 8 == 0) {  // XCD x = id % 8 takes windows x, x + 8, ...
+            const int64_t k = id / 8;
+            b = id % 8 + 8 * (k / H);
+            h = k % H;
+        } else {
+            b = id / H;
+            h = id % H;
+        }
+    }
+    const float* rows = p.proj + b * L * p.proj_ts;
+    auto rot = [](double x1, double x2, double c1, double s1, double c2, double s2, u16& o1, u16& o2) {
+        o1 = AttnElem<true>::from(static_cast<float>(__dsub_rn(__dmul_rn(x1, c1), __dmul_rn(x2, s1))));
+        o2 = AttnElem<true>::from(static_cast<float>(__dadd_rn(__dmul_rn(x2, c2), __dmul_rn(x1, s2))));
+    };
+
+    // 1. LayerNorm of the latent rows: 16 lanes per row, 4 columns each (all loads issued first).
+    {
+        constexpr int PASSES = LMAX / (THREADS / 16);
+        const int lr = tid >> 4, lc = tid & 15;
+        float4 xs[PASSES];
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int row = ps * (THREADS / 16) + lr;
+            xs[ps] = row < L ? *reinterpret_cast<const float4*>(rows + row * p.proj_ts + p.kv_off + 4 * lc)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const float4 wv = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
+        const float4 bv = p.ln_b ? *reinterpret_cast<const float4*>(p.ln_b + 4 * lc) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const double inv_dim = 1.0 / static_cast<double>(KV);
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int row = ps * (THREADS / 16) + lr;
+            const float4 x = xs[ps];
+            double sum = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
+                         (static_cast<double>(x.z) + static_cast<double>(x.w));
+            for (int mask = 8; mask > 0; mask >>= 1) sum += shfl_xor_d(sum, mask);
+            const double mean = sum * inv_dim;
+            const double a0 = static_cast<double>(x.x) - mean, a1 = static_cast<double>(x.y) - mean;
+            const double a2 = static_cast<double>(x.z) - mean, a3 = static_cast<double>(x.w) - mean;
+            double sumsq = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+            for (int mask = 8; mask > 0; mask >>= 1) sumsq += shfl_xor_d(sumsq, mask);
+            const double rstd = 1.0 / sqrt(fma(sumsq, inv_dim, p.ln_eps));
+            const bool active = row < L;
+            const u16 o0 = active ? AttnElem<true>::from(static_cast<float>((a0 * rstd) * wv.x + static_cast<double>(bv.x))) : u16(0);
+            const u16 o1 = active ? AttnElem<true>::from(static_cast<float>((a1 * rstd) * wv.y + static_cast<double>(bv.y))) : u16(0);
+            const u16 o2 = active ? AttnElem<true>::from(static_cast<float>((a2 * rstd) * wv.z + static_cast<double>(bv.z))) : u16(0);
+            const u16 o3 = active ? AttnElem<true>::from(static_cast<float>((a3 * rstd) * wv.w + static_cast<double>(bv.w))) : u16(0);
+            *reinterpret_cast<uint2*>(xq_s + row * XP + 4 * lc) =
+                make_uint2(static_cast<uint32_t>(o0) | (static_cast<uint32_t>(o1) << 16),
+                           static_cast<uint32_t>(o2) | (static_cast<uint32_t>(o3) << 16));
+        }
+    }
+    // kv_up rows of this head.
+    for (int u = tid; u < UPW * (KV / 8); u += THREADS) {
+        const int r = u / (KV / 8), c = (u % (KV / 8)) * 8;
+        *reinterpret_cast<uint4*>(wu_s + r * XP + c) =
+            *reinterpret_cast<const uint4*>(p.w_up + (h * UPW + r) * static_cast<int64_t>(KV) + c);
+    }
+    // 3. Rotated k_rope into k_s, four pairs per thread (rows beyond L: zero).
+    {
+        constexpr int QU = HALF / 4;  // quads of pairs per row
+        constexpr int ITER = (LMAX * QU + THREADS - 1) / THREADS;
+#pragma unroll
+        for (int it = 0; it < ITER; ++it) {
+            const int u = tid + it * THREADS;
+            if (u < LMAX * QU) {
+                const int row = u / QU, i0 = 4 * (u % QU);
+                u16 o1[4] = {0, 0, 0, 0}, o2[4] = {0, 0, 0, 0};
+                if (row < L) {
+                    const float* kr = rows + row * p.proj_ts + p.kr_off;
+                    const float* c = p.cosine + row * ROPE;
+                    const float* sn = p.sine + row * ROPE;
+                    float x1[4], x2[4], c1[4], c2[4], s1[4], s2[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        x1[j] = kr[i0 + j];
+                        x2[j] = kr[i0 + j + HALF];
+                        c1[j] = c[i0 + j];
+                        c2[j] = c[i0 + j + HALF];
+                        s1[j] = sn[i0 + j];
+                        s2[j] = sn[i0 + j + HALF];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) rot(x1[j], x2[j], c1[j], s1[j], c2[j], s2[j], o1[j], o2[j]);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    k_s[row * KP + NOPE + i0 + j] = o1[j];
+                    k_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. kv = LN(latent) . W_up^T for this head: k_nope into k_s, v transposed into vt_s.
+    {
+        constexpr int RT = LMAX / 16, CT = UPW / 16;
+        for (int tix = wave; tix < RT * CT; tix += NW) {
+            const int rt = tix / CT, ct = tix % CT;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KV / 32; ++ks) {
+                const bf16x8 a = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const uint4*>(xq_s + (16 * rt + li) * XP + 32 * ks + 8 * g));
+                const bf16x8 bw = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const uint4*>(wu_s + (16 * ct + li) * XP + 32 * ks + 8 * g));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bw, acc, 0, 0, 0);
+            }
+            const int col = 16 * ct + li;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = 16 * rt + 4 * g + v;
+                const u16 e = AttnElem<true>::from(acc[v]);
+                if (col < NOPE) {
+                    k_s[row * KP + col] = e;
+                } else {
+                    vt_s[(col - NOPE) * VP + row] = e;
+                }
+            }
+        }
+    }
+    // q of this head, loaded now (registers) and written over the latent after the barrier.
+    constexpr int QN = NOPE / 4, QR = HALF / 4, QUNITS = QN + QR;  // float4 units per row
+    constexpr int QITER = (LMAX * QUNITS + THREADS - 1) / THREADS;
+    float4 qa[QITER], qb4[QITER];
+#pragma unroll
+    for (int it = 0; it < QITER; ++it) {
+        const int u = tid + it * THREADS;
+        const int row = u / QUNITS, q4 = u % QUNITS;
+        qa[it] = qb4[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (u < LMAX * QUNITS && row < L) {
+            const float* qr = rows + row * p.proj_ts + p.q_off + h * HD;
+            if (q4 < QN) {
+                qa[it] = *reinterpret_cast<const float4*>(qr + 4 * q4);
+            } else {
+                const int i0 = 4 * (q4 - QN);
+                qa[it] = *reinterpret_cast<const float4*>(qr + NOPE + i0);
+                qb4[it] = *reinterpret_cast<const float4*>(qr + NOPE + i0 + HALF);
+            }
+        }
+    }
+    __syncthreads();  // xq_s (the latent) is free from here on
+#pragma unroll
+    for (int it = 0; it < QITER; ++it) {
+        const int u = tid + it * THREADS;
+        if (u >= LMAX * QUNITS) continue;
+        const int row = u / QUNITS, q4 = u % QUNITS;
+        const float a4[4] = {qa[it].x, qa[it].y, qa[it].z, qa[it].w};
+        if (q4 < QN) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xq_s[row * KP + 4 * q4 + j] = AttnElem<true>::from(a4[j]);
+        } else {
+            const int i0 = 4 * (q4 - QN);
+            const float b4[4] = {qb4[it].x, qb4[it].y, qb4[it].z, qb4[it].w};
+            u16 o1[4] = {0, 0, 0, 0}, o2[4] = {0, 0, 0, 0};
+            if (row < L) {
+                const float* c = p.cosine + row * ROPE;
+                const float* sn = p.sine + row * ROPE;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    rot(a4[j], b4[j], c[i0 + j], sn[i0 + j], c[i0 + j + HALF], sn[i0 + j + HALF], o1[j], o2[j]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xq_s[row * KP + NOPE + i0 + j] = o1[j];
+                xq_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
+            }
+        }
+    }
+    __syncthreads();
+
+    // 5. Causal attention (top-left), keys and values from LDS, 64 keys per softmax step.
+    int tiles[TPW];  // tile t and its mirror 2*NW-1-t balance the causal triangle
+#pragma unroll
+    for (int j = 0; j < TPW / 2; ++j) {
+        tiles[2 * j] = wave + 2 * NW * j;
+        tiles[2 * j + 1] = 2 * NW - 1 - wave + 2 * NW * j;
+    }
+    bf16x8 qb[TPW][HC];
+    float m_run[TPW], l_run[TPW];
+    f32x4 acc[TPW][OT];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        const int q0 = 16 * tiles[i];
+#pragma unroll
+        for (int c = 0; c < HC; ++c) {
+            qb[i][c] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xq_s + (q0 + li) * KP + 32 * c + 8 * g));
+        }
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < OT; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int kbase = 0; kbase < L; kbase += kKeysPerChunk) {
+#pragma unroll
+        for (int i = 0; i < TPW; ++i) {
+            const int q0 = 16 * tiles[i];
+            if (q0 >= L || kbase > q0 + 15) continue;
+            f32x4 sc[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                sc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < HC; ++c) {
+                    const bf16x8 a = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4*>(k_s + (kbase + 16 * t + li) * KP + 32 * c + 8 * g));
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[i][c], sc[t], 0, 0, 0);
+                }
+            }
+            const int qpos = q0 + li;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int key = kbase + 16 * t + 4 * g + v;
+                    const float x = (key < L && key <= qpos) ? sc[t][v] * p.scale_log2 : -INFINITY;
+                    sc[t][v] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+            mx = xor_max(mx, 16);
+            mx = xor_max(mx, 32);
+            const float m_new = fmaxf(m_run[i], mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
+            m_run[i] = m_new;
+            float psum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
+                    sc[t][v] = e;
+                    psum += e;
+                }
+            }
+            l_run[i] = l_run[i] * corr + psum;
+#pragma unroll
+            for (int t = 0; t < OT; ++t) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[i][t][v] *= corr;
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                bf16x8 pb;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    pb[v] = static_cast<__bf16>(sc[2 * half][v]);
+                    pb[4 + v] = static_cast<__bf16>(sc[2 * half + 1][v]);
+                }
+#pragma unroll
+                for (int t = 0; t < OT; ++t) {
+                    const u16* vrow = vt_s + (16 * t + li) * VP + kbase + 32 * half + 4 * g;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
+                    const uint4 raw = {lo.x, lo.y, hi.x, hi.y};
+                    acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, raw), pb, acc[i][t],
+                                                                         0, 0, 0);
+                }
+            }
+        }
+    }
+    // 6. Normalise and store [B, L, H, hd].
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        const int qi = 16 * tiles[i] + li;
+        float l = xor_sum(l_run[i], 16);
+        l = xor_sum(l, 32);
+        if (qi >= L) continue;
+        const float inv = 1.0f / l;
+        float* orow = p.out + ((b * L + qi) * p.heads + h) * HD;
+#pragma unroll
+        for (int t = 0; t < OT; ++t) {
+            *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) =
+                make_float4(acc[i][t][0] * inv, acc[i][t][1] * inv, acc[i][t][2] * inv, acc[i][t][3] * inv);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace mlk
 
@@ -438,4 +775,37 @@ extern "C" mlk_status mlk_attention(const float* q, int64_t q_token_stride, int6
         dispatch_attn<false>(p, vec, s);
     }
     return launch_status("attention");
+}
+
+extern "C" mlk_status mlk_mla_attend(const float* projected, int64_t batch, int64_t length, int64_t proj_token_stride,
+                                     int64_t q_offset, int64_t kv_offset, int64_t k_rope_offset, int64_t heads,
+                                     int64_t head_dim, int64_t nope_dim, int64_t kv_rank, const float* kv_norm_w,
+                                     const float* kv_norm_b, double kv_norm_eps, const void* kv_up_weight,
+                                     const float* cosine, const float* sine, double scale, float* out,
+                                     mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 1 && heads > 0, "invalid MLA geometry");
+    const bool cfg32 = head_dim == 32 && nope_dim == 16 && kv_rank == 64 && length <= 128;
+    const bool cfg64 = head_dim == 64 && nope_dim == 32 && kv_rank == 64 && length <= 256;
+    if (!cfg32 && !cfg64) {
+        set_error("mla_attend: geometry without a fused kernel (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    MLK_CHECK(proj_token_stride % 4 == 0 && q_offset % 4 == 0 && kv_offset % 4 == 0 && aligned16(projected) &&
+                  aligned16(kv_norm_w) && (kv_norm_b == nullptr || aligned16(kv_norm_b)) && aligned16(kv_up_weight) &&
+                  aligned16(out),
+              "mla_attend: operands must be 16-byte aligned");
+    if (batch == 0) return MLK_OK;
+    MLK_CHECK(projected && kv_norm_w && kv_up_weight && cosine && sine && out, "null tensor pointer");
+    MLK_CHECK(batch * heads <= 0x7fffffff, "too many windows x heads for one launch");
+    MlaAttendArgs p{projected, proj_token_stride, q_offset, kv_offset, k_rope_offset, kv_norm_w, kv_norm_b,
+                    static_cast<double>(static_cast<float>(kv_norm_eps)), static_cast<const u16*>(kv_up_weight),
+                    cosine, sine, out, batch, heads, length, static_cast<float>(scale * 1.4426950408889634)};
+    const dim3 grid(static_cast<unsigned>(batch * heads));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (cfg32) {
+        hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2>), grid, dim3(256), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2>), grid, dim3(512), 0, s, p);
+    }
+    return launch_status("mla_attend");
 }

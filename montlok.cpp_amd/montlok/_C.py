@@ -44,6 +44,8 @@ def _load():
         "mlk_swiglu": [_vp, _i64, _i64, _i64, _vp, _vp],
         "mlk_linear": [_vp, _i64, _i64, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp],
         "mlk_mla_rope_qk": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
+        "mlk_mla_attend": [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp,
+                           _vp, _dbl, _vp, _vp],
         "mlk_attention": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, C.c_int32,
                           _dbl, C.c_int32, _vp, _vp],
         "mlk_mhc_prepare": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
@@ -555,7 +557,42 @@ def mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_no
     """montlok.cpp:1159-1211: projection, latent LayerNorm, kv_up, RoPE, attention and output projection.
 
     Weights may be float32 or bfloat16; with bf16 weights the attention contractions run on bf16 matrix
-    cores as well (fp32 softmax and accumulation)."""
+    cores as well (fp32 softmax and accumulation), and for the full causal sequence the part between the
+    two projections runs as one fused kernel (same result, bit for bit)."""
+    return _mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight,
+                        out_weight, cosine, sine, n_heads, head_dim, nope_dim, kv_lora_rank, n_last, causal, scale,
+                        allow_fused=True)
+
+
+def _fused_attend(projected, batch, length, q_width, n_heads, head_dim, nope_dim, kv_lora_rank, kv_norm_weight,
+                  kv_norm_bias, kv_norm_eps, kv_up_weight, cosine, sine, scale):
+    """The fused LayerNorm/kv_up/RoPE/attention kernel, or None where it is not built for the geometry."""
+    rope = head_dim - nope_dim
+    geometry = (head_dim, nope_dim, kv_lora_rank) in ((32, 16, 64), (64, 32, 64)) and \
+        length <= (128 if head_dim == 32 else 256)
+    if not geometry or kv_up_weight.dtype != torch.bfloat16 or projected.stride(-1) != 1:
+        return None
+    w = _dense_parameter(kv_norm_weight, kv_lora_rank, "kv_norm.weight")
+    b = None if kv_norm_bias is None or kv_norm_bias.numel() == 0 else _dense_parameter(kv_norm_bias, kv_lora_rank,
+                                                                                       "kv_norm.bias")
+    up = _weight(kv_up_weight, "kv_up_weight")
+    _check(tuple(cosine.shape) == (length, rope) and cosine.is_contiguous(), "cos must be contiguous [L,rope_dim]")
+    _check(sine.shape == cosine.shape and sine.is_contiguous(), "sin must be contiguous [L,rope_dim]")
+    out = torch.empty((batch, length, n_heads, head_dim), dtype=torch.float32, device=projected.device)
+    ts = projected.stride(1) if length > 1 else projected.size(-1)
+    lib = _load()
+    status = lib.mlk_mla_attend(_ptr(projected), batch, length, ts, 0, q_width, q_width + kv_lora_rank, n_heads,
+                                head_dim, nope_dim, kv_lora_rank, _ptr(w), _ptr(b), float(kv_norm_eps), _ptr(up),
+                                _ptr(cosine), _ptr(sine), float(scale), _ptr(out), _stream())
+    if status == 3:  # MLK_ERR_UNSUPPORTED
+        return None
+    if status != 0:
+        raise RuntimeError(lib.mlk_last_error().decode())
+    return out
+
+
+def _mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight,
+                 cosine, sine, n_heads, head_dim, nope_dim, kv_lora_rank, n_last, causal, scale, allow_fused):
     _require_f32_gpu(x, "x")
     _check(x.dim() == 3, "x must be [B,L,d_model]")
     batch, length, d_model = x.shape
@@ -565,6 +602,11 @@ def mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_no
     precision = torch.bfloat16 if _weight(in_proj_weight, "in_proj_weight").dtype == torch.bfloat16 else torch.float32
     full = n_last == length
     projected = linear(x, in_proj_weight)
+    if allow_fused and full and causal and precision == torch.bfloat16:
+        attended = _fused_attend(projected, batch, length, d_model, n_heads, head_dim, nope_dim, kv_lora_rank,
+                                 kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, cosine, sine, scale)
+        if attended is not None:
+            return linear(attended.view(batch, length, d_model), out_weight)
     q_width = d_model if full else 0
     if full:
         q = projected[..., :q_width]
@@ -616,7 +658,7 @@ def exported_symbols() -> list[str]:
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent", "mlk_mamba3_siso_forward",
-            "mlk_mamba3_siso_step", "mlk_linear", "mlk_mla_rope_qk", "mlk_attention"]
+            "mlk_mamba3_siso_step", "mlk_linear", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend"]
 
 
 def math_check(x: torch.Tensor) -> dict:

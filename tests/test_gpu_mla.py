@@ -199,3 +199,33 @@ def test_mla_errors(dev):
     with pytest.raises(RuntimeError, match="k_rope must be \\[B,L,rope_dim\\]"):
         _C.mla_rope_qk(q, kv, torch.zeros(1, 4, 6, device=dev), torch.zeros(4, 8, device=dev),
                        torch.zeros(4, 8, device=dev), 8)
+
+
+@pytest.mark.parametrize("B,L,H,hd,nope", [(16, 128, 8, 32, 16),   # MLA block geometry
+                                           (8, 256, 4, 64, 32),    # full-stack MLA geometry
+                                           (3, 100, 8, 32, 16),    # windows not a multiple of 8, ragged length
+                                           (2, 77, 4, 64, 32)])
+def test_fused_attend_equals_separate_kernels(dev, B, L, H, hd, nope):
+    """With bf16 weights the full causal mla_forward runs LayerNorm, kv_up, RoPE and attention in one
+    kernel; it must give the separate kernels' result bit for bit."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(B * L + hd)
+    d, kvr, rope = H * hd, 64, hd - nope
+    bf = torch.bfloat16
+    x = torch.randn(B, L, d, generator=g).to(dev)
+    in_w = (torch.randn(d + kvr + rope, d, generator=g) * 0.02).to(dev, bf)
+    up_w = (torch.randn(H * (nope + hd), kvr, generator=g) * 0.02).to(dev, bf)
+    o_w = (torch.randn(d, d, generator=g) * 0.02).to(dev, bf)
+    ln_w = (1 + 0.1 * torch.randn(kvr, generator=g)).to(dev)
+    ln_b = (0.1 * torch.randn(kvr, generator=g)).to(dev)
+    cos, sin = (t.to(dev) for t in rope_tables_t(L, rope))
+    args = (x, in_w, x.new_empty(0), ln_w, ln_b, 1e-5, up_w, o_w, cos, sin, H, hd, nope, kvr, L, True, hd ** -0.5)
+    fused = _C._mla_forward(*args, allow_fused=True)
+    separate = _C._mla_forward(*args, allow_fused=False)
+    assert_bitwise(fused, separate.cpu().numpy(), "fused vs separate MLA attention")
+
+
+def rope_tables_t(length: int, rope_dim: int):
+    cos, sin = rope_tables(length, rope_dim)
+    return torch.from_numpy(cos), torch.from_numpy(sin)
