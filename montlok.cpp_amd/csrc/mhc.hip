@@ -42,6 +42,8 @@
 namespace mlk {
 namespace {
 
+typedef float nt_f4 __attribute__((ext_vector_type(4)));  // for non-temporal vector loads and stores
+
 typedef double double4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBlock = 256;
@@ -468,17 +470,43 @@ __global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __
     const float4 o = *reinterpret_cast<const float4*>(out + token * d + k);
     float4 s[N];
 #pragma unroll
-    for (int j = 0; j < N; ++j) s[j] = *reinterpret_cast<const float4*>(streams + token * ts + j * sd + k);
-    const float* r = res + token * N * N;
-    const float* p = post + token * N;
+    for (int j = 0; j < N; ++j) {
+        // Streams are read once and the new streams written once: non-temporal.
+        const nt_f4 x = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(streams + token * ts + j * sd + k));
+        s[j] = make_float4(x[0], x[1], x[2], x[3]);
+    }
+    // The token's coefficients: shared by every thread of the token, fetched
+    // as whole 16-byte rows when n = 4 (one request per row, not per value).
+    float rv[N * N], pv[N];
+    if constexpr (N == 4) {
+        const float4* r4 = reinterpret_cast<const float4*>(res + token * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 x = r4[i];
+            rv[4 * i] = x.x;
+            rv[4 * i + 1] = x.y;
+            rv[4 * i + 2] = x.z;
+            rv[4 * i + 3] = x.w;
+        }
+        const float4 y = *reinterpret_cast<const float4*>(post + token * 4);
+        pv[0] = y.x;
+        pv[1] = y.y;
+        pv[2] = y.z;
+        pv[3] = y.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N * N; ++i) rv[i] = res[token * N * N + i];
+#pragma unroll
+        for (int i = 0; i < N; ++i) pv[i] = post[token * N + i];
+    }
     double mean[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const double pi = static_cast<double>(p[i]);
+        const double pi = static_cast<double>(pv[i]);
         double acc[4] = {pi * o.x, pi * o.y, pi * o.z, pi * o.w};
 #pragma unroll
         for (int j = 0; j < N; ++j) {
-            const double rij = static_cast<double>(r[i * N + j]);
+            const double rij = static_cast<double>(rv[i * N + j]);
             acc[0] = fma(rij, static_cast<double>(s[j].x), acc[0]);
             acc[1] = fma(rij, static_cast<double>(s[j].y), acc[1]);
             acc[2] = fma(rij, static_cast<double>(s[j].z), acc[2]);
@@ -486,7 +514,10 @@ __global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __
         }
         const float4 nv = make_float4(static_cast<float>(acc[0]), static_cast<float>(acc[1]),
                                       static_cast<float>(acc[2]), static_cast<float>(acc[3]));
-        if (new_streams != nullptr) *reinterpret_cast<float4*>(new_streams + (token * N + i) * d + k) = nv;
+        if (new_streams != nullptr) {
+            const nt_f4 x = {nv.x, nv.y, nv.z, nv.w};
+            __builtin_nontemporal_store(x, reinterpret_cast<nt_f4*>(new_streams + (token * N + i) * d + k));
+        }
         mean[0] += static_cast<double>(nv.x);
         mean[1] += static_cast<double>(nv.y);
         mean[2] += static_cast<double>(nv.z);
@@ -535,7 +566,7 @@ mlk_status launch_combine(const float* streams, int64_t tokens, int64_t n, int64
     if (tokens == 0) return MLK_OK;
     auto al16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     const bool vec = d % 4 == 0 && sd % 4 == 0 && ts % 4 == 0 && al16(streams) && al16(out) && al16(new_streams) &&
-                     al16(collapsed) && n >= 1 && n <= 8;
+                     al16(collapsed) && n >= 1 && n <= 8 && (n != 4 || (al16(res) && al16(post)));
     if (vec) {
         const int64_t blocks = ceil_div(tokens * (d / 4), kBlock);
         const bool narrow = tokens * (d / 4) < (int64_t{1} << 31);
