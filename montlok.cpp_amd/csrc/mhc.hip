@@ -133,6 +133,7 @@ template <int D>
 __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     constexpr int n = 4;
     constexpr int GW = D / 64;  // groups of 16 k per wave; group g covers k in [16g, 16g + 16)
+    __shared__ __attribute__((aligned(16))) double w_lds[(2 * n + n * n) * (D + 2)];
     __shared__ double part[4][2][4][64];
     __shared__ double part_sq[4][64];
     __shared__ double agg_sq[4][64];
@@ -163,33 +164,33 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     // lane (t, q), so tile 0 row i carries res entry (i % 4, i / 4) and lane q
     // ends with res row q; tile 1 row i carries pre[i / 4] (i % 4 == 0) or
     // post[i / 4] (i % 4 == 1), zero rows otherwise.
-    const double* w_res = a.proj_w + static_cast<int64_t>(2 * n + 4 * (t % 4) + t / 4) * D;
+    // The projection block is staged in LDS once per block with coalesced
+    // 16-byte loads (per-lane gathers of it from L2 cost as many cache lines
+    // as the streams themselves); every other operand is fetched up front as
+    // well, so the block waits for one round of loads.
+    constexpr int WP = D + 2;  // row pitch in doubles: consecutive rows start 4 banks apart
+    for (int u = threadIdx.x; u < (2 * n + n * n) * (D / 2); u += kBlock) {
+        const int row = u / (D / 2), c = 2 * (u % (D / 2));
+        *reinterpret_cast<double2*>(w_lds + row * WP + c) = *reinterpret_cast<const double2*>(a.proj_w + row * D + c);
+    }
+    const double* w_res = w_lds + (2 * n + 4 * (t % 4) + t / 4) * WP;
     const bool pp_row = t % 4 < 2;
-    const double* w_pp = a.proj_w + static_cast<int64_t>((t % 4 == 0 ? 0 : n) + t / 4) * D;
-    // Every other operand is fetched up front too, so the whole block waits
-    // for one round of loads instead of one per MFMA step or phase.
-    double wa[GW][4], wb[GW][4];
+    const double* w_pp = w_lds + ((t % 4 == 0 ? 0 : n) + t / 4) * WP;
     float4 nw[GW];
 #pragma unroll
-    for (int j = 0; j < GW; ++j) {
-        const int k0 = 16 * (wave * GW + j) + 4 * q;
-        nw[j] = *reinterpret_cast<const float4*>(a.norm_w + k0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            wa[j][r] = w_res[k0 + r];
-            wb[j][r] = pp_row ? w_pp[k0 + r] : 0.0;
-        }
-    }
+    for (int j = 0; j < GW; ++j) nw[j] = *reinterpret_cast<const float4*>(a.norm_w + 16 * (wave * GW + j) + 4 * q);
     const int e_pre = l % 16;  // this lane's matrix entry in the coefficient phase
     const float res_bias_e = a.res_bias[e_pre];
     const float res_alpha = *a.res_alpha;
     const float pp_alpha = e_pre < 4 ? *a.pre_alpha : *a.post_alpha;
     const float pp_bias = e_pre < 4 ? a.pre_bias[e_pre % 4] : a.post_bias[e_pre % 4];
+    __syncthreads();  // w_lds filled
     double sq = 0.0;
     double4_t acc0 = {0.0, 0.0, 0.0, 0.0};
     double4_t acc1 = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < GW; ++j) {
+        const int k0 = 16 * (wave * GW + j) + 4 * q;
         const float wk[4] = {nw[j].x, nw[j].y, nw[j].z, nw[j].w};
         const float s0[4] = {sv[j][0].x, sv[j][0].y, sv[j][0].z, sv[j][0].w};
         const float s1[4] = {sv[j][1].x, sv[j][1].y, sv[j][1].z, sv[j][1].w};
@@ -205,8 +206,8 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
             m *= inv_n;
             sq = fma(m, m, sq);
             const double b = m * static_cast<double>(wk[r]);
-            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(wa[j][r], b, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(wb[j][r], b, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(w_res[k0 + r], b, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(pp_row ? w_pp[k0 + r] : 0.0, b, acc1, 0, 0, 0);
         }
     }
     {
@@ -610,7 +611,7 @@ mlk_status launch_prepare(const PrepareArgs& a, int64_t n, int64_t d, hipStream_
     auto al16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     const bool fast = n == 4 && (d == 64 || d == 128 || d == 256 || d == 512) && a.sd % 4 == 0 && a.ts % 4 == 0 &&
                       al16(a.streams) && al16(a.norm_w) && al16(a.agg_norm_w) && al16(a.agg) && al16(a.pre) &&
-                      al16(a.post) && al16(a.res);
+                      al16(a.post) && al16(a.res) && al16(a.proj_w);
     if (fast) {
         const int64_t blocks = ceil_div(a.tokens, 16);
         switch (d) {
