@@ -786,7 +786,7 @@ def cpu_baseline_stack(cfg: dict, stack, feats_cpu, budget_s: float = 12.0, wind
     f32 = lambda t: t.detach().float().cpu()  # noqa: E731
     hcs = [dict(nw=f32(h.dyn_norm.weight).numpy(), eps=h.dyn_norm.eps, w64=h._projection_block().cpu().numpy(),
                 pb=f32(h.pre_bias).numpy(), qb=f32(h.post_bias).numpy(), rb=f32(h.res_bias).numpy(),
-                al=(float(h.pre_alpha), float(h.post_alpha), float(h.res_alpha)), iters=h.sinkhorn_iters)
+                al=(h.pre_alpha.item(), h.post_alpha.item(), h.res_alpha.item()), iters=h.sinkhorn_iters)
            for h in stack.hcs]
     norms = [f32(nm.weight).numpy() for nm in stack.norms]
     mix = []
