@@ -148,37 +148,56 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     const float* base = a.streams + (valid ? token : 0) * a.ts;
     const double inv_n = 1.0 / n;
 
+    // The projection block is staged in LDS once per block with coalesced
+    // 16-byte loads (per-lane gathers of it from L2 cost as many cache lines
+    // as the streams themselves). Its loads go out first, into registers, so
+    // the LDS stores wait for them alone; then every other operand is fetched,
+    // so the block waits for one round of loads. All loop bounds are compile
+    // time: each load is issued without waiting for the one before.
+    constexpr int WP = D + 2;  // row pitch in doubles: consecutive rows start 4 banks apart
+    constexpr int kWPairs = (2 * n + n * n) * (D / 2);
+    static_assert(kWPairs % kBlock == 0, "projection block must split evenly over the block");
+    constexpr int kWPer = kWPairs / kBlock;
+    double2 wreg[kWPer];
+#pragma unroll
+    for (int c = 0; c < kWPer; ++c) {
+        const int u = threadIdx.x + c * kBlock;
+        wreg[c] = *reinterpret_cast<const double2*>(a.proj_w + 2 * u);  // row u / (D/2), column 2 (u % (D/2))
+    }
     // MFMA step s = 4g + r multiplies k = 16g + 4q + r: lane (t, q) owns the
-    // float4 at 16g + 4q of every group g of its wave.
+    // float4 at 16g + 4q of every group g of its wave. Lanes of tokens past
+    // the end read token 0 (in bounds): an MFMA column and every lane
+    // reduction below stay within one token, and those tokens' results are
+    // never stored.
     float4 sv[GW][n];
 #pragma unroll
     for (int j = 0; j < GW; ++j) {
         const int k0 = 16 * (wave * GW + j) + 4 * q;
 #pragma unroll
-        for (int i = 0; i < n; ++i) {
-            sv[j][i] = valid ? *reinterpret_cast<const float4*>(base + i * a.sd + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int i = 0; i < n; ++i) sv[j][i] = *reinterpret_cast<const float4*>(base + i * a.sd + k0);
+    }
+    float4 nw[GW];
+#pragma unroll
+    for (int j = 0; j < GW; ++j) nw[j] = *reinterpret_cast<const float4*>(a.norm_w + 16 * (wave * GW + j) + 4 * q);
+    // agg_norm_w is read unconditionally (norm_w stands in when absent) so
+    // that no branch separates these loads from the others.
+    const float* anw_src = a.agg_norm_w != nullptr ? a.agg_norm_w : a.norm_w;
+    float4 anw[GW];
+#pragma unroll
+    for (int j = 0; j < GW; ++j) anw[j] = *reinterpret_cast<const float4*>(anw_src + 16 * (wave * GW + j) + 4 * q);
+#pragma unroll
+    for (int c = 0; c < kWPer; ++c) {
+        const int u = threadIdx.x + c * kBlock;
+        *reinterpret_cast<double2*>(w_lds + (u / (D / 2)) * WP + 2 * (u % (D / 2))) = wreg[c];
     }
     // A operand: projection row for tile row i = l % 16. The accumulator of
     // the 16x16x4 f64 MFMA puts tile rows q, q+4, q+8, q+12 of token t in
     // lane (t, q), so tile 0 row i carries res entry (i % 4, i / 4) and lane q
     // ends with res row q; tile 1 row i carries pre[i / 4] (i % 4 == 0) or
     // post[i / 4] (i % 4 == 1), zero rows otherwise.
-    // The projection block is staged in LDS once per block with coalesced
-    // 16-byte loads (per-lane gathers of it from L2 cost as many cache lines
-    // as the streams themselves); every other operand is fetched up front as
-    // well, so the block waits for one round of loads.
-    constexpr int WP = D + 2;  // row pitch in doubles: consecutive rows start 4 banks apart
-    for (int u = threadIdx.x; u < (2 * n + n * n) * (D / 2); u += kBlock) {
-        const int row = u / (D / 2), c = 2 * (u % (D / 2));
-        *reinterpret_cast<double2*>(w_lds + row * WP + c) = *reinterpret_cast<const double2*>(a.proj_w + row * D + c);
-    }
     const double* w_res = w_lds + (2 * n + 4 * (t % 4) + t / 4) * WP;
     const bool pp_row = t % 4 < 2;
     const double* w_pp = w_lds + ((t % 4 == 0 ? 0 : n) + t / 4) * WP;
-    float4 nw[GW];
-#pragma unroll
-    for (int j = 0; j < GW; ++j) nw[j] = *reinterpret_cast<const float4*>(a.norm_w + 16 * (wave * GW + j) + 4 * q);
     const int e_pre = l % 16;  // this lane's matrix entry in the coefficient phase
     const float res_bias_e = a.res_bias[e_pre];
     const float res_alpha = *a.res_alpha;
@@ -196,6 +215,14 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
         const float s1[4] = {sv[j][1].x, sv[j][1].y, sv[j][1].z, sv[j][1].w};
         const float s2[4] = {sv[j][2].x, sv[j][2].y, sv[j][2].z, sv[j][2].w};
         const float s3[4] = {sv[j][3].x, sv[j][3].y, sv[j][3].z, sv[j][3].w};
+        // This group's A operands, read up front as 16-byte pairs (rows and
+        // k0 are 16-byte aligned in LDS).
+        const double2 r01 = *reinterpret_cast<const double2*>(w_res + k0);
+        const double2 r23 = *reinterpret_cast<const double2*>(w_res + k0 + 2);
+        const double2 p01 = *reinterpret_cast<const double2*>(w_pp + k0);
+        const double2 p23 = *reinterpret_cast<const double2*>(w_pp + k0 + 2);
+        const double wr[4] = {r01.x, r01.y, r23.x, r23.y};
+        const double wp[4] = {pp_row ? p01.x : 0.0, pp_row ? p01.y : 0.0, pp_row ? p23.x : 0.0, pp_row ? p23.y : 0.0};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             // m = ((s0 + s1) + s2) + s3, then * (1/n): the reference's order.
@@ -206,8 +233,8 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
             m *= inv_n;
             sq = fma(m, m, sq);
             const double b = m * static_cast<double>(wk[r]);
-            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(w_res[k0 + r], b, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(pp_row ? w_pp[k0 + r] : 0.0, b, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(wr[r], b, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(wp[r], b, acc1, 0, 0, 0);
         }
     }
     {
@@ -244,13 +271,16 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     const double th_res = tanh_d(logit_res * scale);
     const double th_pp = tanh_d(logit_pp * scale);
     double m = exp_d(fma(static_cast<double>(res_alpha), th_res, static_cast<double>(res_bias_e)));
+    const bool is_pre = e < 4;
+    const float c = static_cast<float>((is_pre ? 1.0 : 2.0) *
+                                       sigmoid_fast(fma(static_cast<double>(pp_alpha), th_pp,
+                                                        static_cast<double>(pp_bias))));
+    // The res chain (tanh, exp) runs here beside the pre/post chain; left to
+    // itself the compiler sinks it past the barrier, after the agg pass.
+    asm volatile("" : "+v"(m));
     if (e < 8) {
-        const bool is_pre = e < 4;
-        const float c = static_cast<float>((is_pre ? 1.0 : 2.0) *
-                                           sigmoid_fast(fma(static_cast<double>(pp_alpha), th_pp,
-                                                            static_cast<double>(pp_bias))));
         if (is_pre) pre_lds[tt][v] = c;
-        if (valid_e) (is_pre ? a.pre : a.post)[token_e * n + v] = c;
+        if (valid_e) __builtin_nontemporal_store(c, (is_pre ? a.pre : a.post) + token_e * n + v);
     }
     __syncthreads();
 
@@ -290,8 +320,7 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
         const double ascale = 1.0 / sqrt(total / static_cast<double>(D) + a.agg_norm_eps);
 #pragma unroll
         for (int j = 0; j < GW; ++j) {
-            const int k0 = 16 * (wave * GW + j) + 4 * q;
-            const float4 w4 = *reinterpret_cast<const float4*>(a.agg_norm_w + k0);
+            const float4 w4 = anw[j];
             float4& o = aggv[j];
             o.x = static_cast<float>((static_cast<double>(o.x) * ascale) * static_cast<double>(w4.x));
             o.y = static_cast<float>((static_cast<double>(o.y) * ascale) * static_cast<double>(w4.y));
@@ -302,19 +331,31 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     if (valid) {
 #pragma unroll
         for (int j = 0; j < GW; ++j) {
-            *reinterpret_cast<float4*>(agg_row + 16 * (wave * GW + j) + 4 * q) = aggv[j];
+            __builtin_nontemporal_store(nt_f4{aggv[j].x, aggv[j].y, aggv[j].z, aggv[j].w},
+                                        reinterpret_cast<nt_f4*>(agg_row + 16 * (wave * GW + j) + 4 * q));
         }
     }
 
     // Sinkhorn, one entry per lane (token tt, entry e): row sums over the quad,
     // column sums over the 16-lane group, reciprocals then products as in the
     // reference (1 / s, then m * (1 / s)).
+    // Only a first-round row sum can be infinite: after a row normalisation
+    // every entry is at most 1 (+1 ulp), so later sums stay below 5. When no
+    // entry of the wave reaches 2^1020, four of them cannot overflow and the
+    // loop runs without the reciprocal's infinity test (same results).
     const int rounds = a.iters > 1 ? a.iters : 1;
-    for (int it = 0; it < rounds; ++it) {
-        m *= recip_pos(quad_sum(m));
-        m *= recip_pos(column_sum(m));
+    if (__all(m < 0x1p1020)) {
+        for (int it = 0; it < rounds; ++it) {
+            m *= recip_finite(quad_sum(m));
+            m *= recip_finite(column_sum(m));
+        }
+    } else {
+        for (int it = 0; it < rounds; ++it) {
+            m *= recip_pos(quad_sum(m));
+            m *= recip_pos(column_sum(m));
+        }
     }
-    if (valid_e) a.res[token_e * 16 + e] = static_cast<float>(m);
+    if (valid_e) __builtin_nontemporal_store(static_cast<float>(m), a.res + token_e * 16 + e);
 }
 
 // ---------------------------------------------------------------------------

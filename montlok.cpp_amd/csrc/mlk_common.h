@@ -86,14 +86,17 @@ __device__ __forceinline__ double exp_d(double x) {
 // 1 / x for positive normal x (also 1 / inf = 0): the hardware reciprocal
 // (relative error ~5e-8) refined by two Newton steps r += r (1 - x r). Over
 // 2^18 inputs in [0.5, 4) the result equalled the IEEE quotient every time;
-// it is within a double ulp by construction.
-__device__ __forceinline__ double recip_pos(double x) {
+// it is within a double ulp by construction. recip_finite is the same steps
+// without the infinity test, for callers that know x is finite.
+__device__ __forceinline__ double recip_finite(double x) {
     double r = __builtin_amdgcn_rcp(x);
-    if (__builtin_isinf(x)) return 0.0;
     double e = fma(-x, r, 1.0);
     r = fma(r, e, r);
     e = fma(-x, r, 1.0);
     return fma(r, e, r);
+}
+__device__ __forceinline__ double recip_pos(double x) {
+    return __builtin_isinf(x) ? 0.0 : recip_finite(x);
 }
 
 // tanh(x) = sign(x) (1 - t) / (1 + t), t = exp(-2 |x|) in (0, 1]: absolute
