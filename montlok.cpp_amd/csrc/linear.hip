@@ -69,11 +69,13 @@ struct LinearArgs {
     int64_t out_stride;
 };
 
-// Loads 8 consecutive floats x[row, k .. k+7] (zero past K or past the last row).
+// Loads 8 consecutive floats x[row, k .. k+7] (zero past K or past the last
+// row). Rows past the end read the last row (in bounds) and are zeroed by the
+// caller, so full-width loads need no branch around them.
 template <bool VEC>
 __device__ __forceinline__ void load_x8(const LinearArgs& p, int64_t row, int64_t k, float (&v)[8]) {
-    if (row < p.rows && k + 8 <= p.K) {
-        const float* src = p.x + row * p.x_stride + k;
+    if (k + 8 <= p.K) {
+        const float* src = p.x + (row < p.rows ? row : p.rows - 1) * p.x_stride + k;
         if constexpr (VEC) {
             const float4 lo = *reinterpret_cast<const float4*>(src);
             const float4 hi = *reinterpret_cast<const float4*>(src + 4);
@@ -112,12 +114,13 @@ __device__ __forceinline__ void load_a(const LinearArgs& p, int64_t row, int64_t
         if (s < steps) {
             float v[8];
             load_x8<VEC>(p, row, k0 + 32 * s + 8 * group, v);
+            const bool live = row < p.rows;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if constexpr (BF16W) {
-                    a.v[s][j] = static_cast<__bf16>(v[j]);
+                    a.v[s][j] = static_cast<__bf16>(live ? v[j] : 0.0f);
                 } else {
-                    a.v[s][j] = v[j];
+                    a.v[s][j] = live ? v[j] : 0.0f;
                 }
             }
         }
@@ -125,8 +128,10 @@ __device__ __forceinline__ void load_a(const LinearArgs& p, int64_t row, int64_t
 }
 
 // This thread's share of one W chunk W[n0 .. n0+63, k0 .. k0+kspan-1]: fixed
-// 16-byte units, fetched into registers (zero past N and K), later written to
-// LDS. Units at columns >= kspan are never read by the MFMA loop and skipped.
+// 16-byte units, fetched into registers, later written to LDS (zero past N
+// and K). Rows past N read row N - 1 (in bounds) and are zeroed at the store,
+// so full-width fetches need no branch. Units at columns >= kspan are never
+// read by the MFMA loop and skipped.
 template <bool BF16W, bool VEC>
 struct WStage {
     using T = typename WTraits<BF16W>::T;
@@ -145,8 +150,8 @@ struct WStage {
             const int64_t n = n0 + r;
             const int64_t k = k0 + c;
             if (c >= kspan) continue;
-            if (VEC && n < p.N && k + kPer <= p.K) {
-                reg[u] = *reinterpret_cast<const uint4*>(w + n * p.K + k);
+            if (VEC && k + kPer <= p.K) {
+                reg[u] = *reinterpret_cast<const uint4*>(w + (n < p.N ? n : p.N - 1) * p.K + k);
             } else {
                 T tmp[kPer];
 #pragma unroll
@@ -156,13 +161,16 @@ struct WStage {
         }
     }
 
-    __device__ __forceinline__ void store(T* lds, int kspan) const {
+    __device__ __forceinline__ void store(const LinearArgs& p, int64_t n0, T* lds, int kspan) const {
 #pragma unroll
         for (int u = 0; u < kUnits; ++u) {
             const int unit = threadIdx.x + u * kThreads;
             const int r = unit / kUnitsPerRow;
             const int c = (unit % kUnitsPerRow) * kPer;
-            if (c < kspan) *reinterpret_cast<uint4*>(lds + r * WTraits<BF16W>::kPitch + c) = reg[u];
+            if (c < kspan) {
+                *reinterpret_cast<uint4*>(lds + r * WTraits<BF16W>::kPitch + c) =
+                    n0 + r < p.N ? reg[u] : uint4{0u, 0u, 0u, 0u};
+            }
         }
     }
 };
@@ -202,7 +210,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
     AFrag<BF16W> a_cur;  // reloaded per iteration when K spans several chunks
     stage.fetch(p, n0_of(0), 0, kspan_of(0));
     load_a<BF16W, VEC>(p, my_row, 0, group, kspan_of(0) / 32, a_cur);
-    stage.store(w_lds[0], kspan_of(0));
+    stage.store(p, n0_of(0), w_lds[0], kspan_of(0));
     __syncthreads();
 
     f32x4 acc[4];
@@ -216,6 +224,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
             if (it > 0) load_a<BF16W, VEC>(p, my_row, kc * KC, group, steps, a_cur);
         }
         if (more) stage.fetch(p, n0_of(it + 1), kc_next * KC, kspan_of(kc_next));
+        float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // fetched with the chunk, used after its MFMAs
+        if (p.bias != nullptr) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int64_t col = n0 + 16 * t + li;
+                bias[t] = p.bias[col < p.N ? col : p.N - 1];
+            }
+        }
         if (kc == 0) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -247,16 +263,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
             for (int t = 0; t < 4; ++t) {
                 const int64_t col = n0 + 16 * t + li;
                 if (col < p.N) {
-                    const float bias = p.bias ? p.bias[col] : 0.0f;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int64_t row = row0 + 4 * group + v;
-                        if (row < p.rows) p.out[row * p.out_stride + col] = acc[t][v] + bias;
+                        if (row < p.rows) p.out[row * p.out_stride + col] = acc[t][v] + bias[t];
                     }
                 }
             }
         }
-        if (more) stage.store(w_lds[(it + 1) & 1], kspan_of(kc_next));
+        if (more) stage.store(p, n0_of(it + 1), w_lds[(it + 1) & 1], kspan_of(kc_next));
         __syncthreads();
     }
 }

@@ -437,7 +437,13 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
         o2 = AttnElem<true>::from(static_cast<float>(__dadd_rn(__dmul_rn(x2, c2), __dmul_rn(x1, s2))));
     };
 
-    // 1. LayerNorm of the latent rows: 16 lanes per row, 4 columns each (all loads issued first).
+    // 1. LayerNorm of the latent rows: 16 lanes per row, 4 columns each, and
+    // this head's kv_up rows. Every load is issued before the first use, with
+    // compile-time trip counts and no branch around it: rows past L read row
+    // L - 1 (in bounds) and their outputs are zeroed.
+    constexpr int WUN = UPW * (KV / 8);  // 16-byte units of this head's kv_up rows
+    constexpr int WUI = (WUN + THREADS - 1) / THREADS;
+    uint4 wur[WUI];
     {
         constexpr int PASSES = LMAX / (THREADS / 16);
         const int lr = tid >> 4, lc = tid & 15;
@@ -445,8 +451,14 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
 #pragma unroll
         for (int ps = 0; ps < PASSES; ++ps) {
             const int row = ps * (THREADS / 16) + lr;
-            xs[ps] = row < L ? *reinterpret_cast<const float4*>(rows + row * p.proj_ts + p.kv_off + 4 * lc)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int rc = row < L ? row : L - 1;
+            xs[ps] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.kv_off + 4 * lc);
+        }
+#pragma unroll
+        for (int it = 0; it < WUI; ++it) {
+            const int u = min(tid + it * THREADS, WUN - 1);
+            const int r = u / (KV / 8), c = (u % (KV / 8)) * 8;
+            wur[it] = *reinterpret_cast<const uint4*>(p.w_up + (h * UPW + r) * static_cast<int64_t>(KV) + c);
         }
         const float4 wv = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
         const float4 bv = p.ln_b ? *reinterpret_cast<const float4*>(p.ln_b + 4 * lc) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -474,44 +486,47 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
                            static_cast<uint32_t>(o2) | (static_cast<uint32_t>(o3) << 16));
         }
     }
-    // kv_up rows of this head.
-    for (int u = tid; u < UPW * (KV / 8); u += THREADS) {
-        const int r = u / (KV / 8), c = (u % (KV / 8)) * 8;
-        *reinterpret_cast<uint4*>(wu_s + r * XP + c) =
-            *reinterpret_cast<const uint4*>(p.w_up + (h * UPW + r) * static_cast<int64_t>(KV) + c);
+#pragma unroll
+    for (int it = 0; it < WUI; ++it) {
+        const int u = tid + it * THREADS;
+        if (u < WUN) {
+            const int r = u / (KV / 8), c = (u % (KV / 8)) * 8;
+            *reinterpret_cast<uint4*>(wu_s + r * XP + c) = wur[it];
+        }
     }
     // 3. Rotated k_rope into k_s, four pairs per thread (rows beyond L: zero).
     {
         constexpr int QU = HALF / 4;  // quads of pairs per row
-        constexpr int ITER = (LMAX * QU + THREADS - 1) / THREADS;
+        static_assert((LMAX * QU) % THREADS == 0, "rope units must split evenly");
+        constexpr int ITER = LMAX * QU / THREADS;
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
             const int u = tid + it * THREADS;
-            if (u < LMAX * QU) {
-                const int row = u / QU, i0 = 4 * (u % QU);
-                u16 o1[4] = {0, 0, 0, 0}, o2[4] = {0, 0, 0, 0};
-                if (row < L) {
-                    const float* kr = rows + row * p.proj_ts + p.kr_off;
-                    const float* c = p.cosine + row * ROPE;
-                    const float* sn = p.sine + row * ROPE;
-                    float x1[4], x2[4], c1[4], c2[4], s1[4], s2[4];
+            const int row = u / QU, i0 = 4 * (u % QU);
+            const int rc = row < L ? row : L - 1;
+            const float* kr = rows + rc * p.proj_ts + p.kr_off;
+            const float* c = p.cosine + rc * ROPE;
+            const float* sn = p.sine + rc * ROPE;
+            float x1[4], x2[4], c1[4], c2[4], s1[4], s2[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        x1[j] = kr[i0 + j];
-                        x2[j] = kr[i0 + j + HALF];
-                        c1[j] = c[i0 + j];
-                        c2[j] = c[i0 + j + HALF];
-                        s1[j] = sn[i0 + j];
-                        s2[j] = sn[i0 + j + HALF];
-                    }
+            for (int j = 0; j < 4; ++j) {
+                x1[j] = kr[i0 + j];
+                x2[j] = kr[i0 + j + HALF];
+                c1[j] = c[i0 + j];
+                c2[j] = c[i0 + j + HALF];
+                s1[j] = sn[i0 + j];
+                s2[j] = sn[i0 + j + HALF];
+            }
+            u16 o1[4], o2[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) rot(x1[j], x2[j], c1[j], s1[j], c2[j], s2[j], o1[j], o2[j]);
-                }
+            for (int j = 0; j < 4; ++j) {
+                rot(x1[j], x2[j], c1[j], s1[j], c2[j], s2[j], o1[j], o2[j]);
+                if (row >= L) o1[j] = o2[j] = 0;
+            }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    k_s[row * KP + NOPE + i0 + j] = o1[j];
-                    k_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
-                }
+            for (int j = 0; j < 4; ++j) {
+                k_s[row * KP + NOPE + i0 + j] = o1[j];
+                k_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
             }
         }
     }
@@ -544,53 +559,64 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
             }
         }
     }
-    // q of this head, loaded now (registers) and written over the latent after the barrier.
-    constexpr int QN = NOPE / 4, QR = HALF / 4, QUNITS = QN + QR;  // float4 units per row
-    constexpr int QITER = (LMAX * QUNITS + THREADS - 1) / THREADS;
-    float4 qa[QITER], qb4[QITER];
+    // q of this head, loaded now (registers) and written over the latent
+    // after the barrier: the nope part in float4 units, the rope part in
+    // units of four pairs with their cos/sin, each with an exact compile-time
+    // trip count so every load is issued before the barrier. Rows past L read
+    // row L - 1 (in bounds) and are written as zeros.
+    constexpr int QN = NOPE / 4, QR = HALF / 4;
+    static_assert((LMAX * QN) % THREADS == 0 && (LMAX * QR) % THREADS == 0, "q units must split evenly");
+    constexpr int NI = LMAX * QN / THREADS, RI = LMAX * QR / THREADS;
+    float4 qn[NI], qx1[RI], qx2[RI];
+    float qc1[RI][4], qs1[RI][4], qc2[RI][4], qs2[RI][4];
 #pragma unroll
-    for (int it = 0; it < QITER; ++it) {
+    for (int it = 0; it < NI; ++it) {
         const int u = tid + it * THREADS;
-        const int row = u / QUNITS, q4 = u % QUNITS;
-        qa[it] = qb4[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (u < LMAX * QUNITS && row < L) {
-            const float* qr = rows + row * p.proj_ts + p.q_off + h * HD;
-            if (q4 < QN) {
-                qa[it] = *reinterpret_cast<const float4*>(qr + 4 * q4);
-            } else {
-                const int i0 = 4 * (q4 - QN);
-                qa[it] = *reinterpret_cast<const float4*>(qr + NOPE + i0);
-                qb4[it] = *reinterpret_cast<const float4*>(qr + NOPE + i0 + HALF);
-            }
+        const int row = u / QN, rc = row < L ? row : L - 1;
+        qn[it] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.q_off + h * HD + 4 * (u % QN));
+    }
+#pragma unroll
+    for (int it = 0; it < RI; ++it) {
+        const int u = tid + it * THREADS;
+        const int row = u / QR, rc = row < L ? row : L - 1, i0 = 4 * (u % QR);
+        const float* qr = rows + rc * p.proj_ts + p.q_off + h * HD + NOPE + i0;
+        qx1[it] = *reinterpret_cast<const float4*>(qr);
+        qx2[it] = *reinterpret_cast<const float4*>(qr + HALF);
+        const float* c = p.cosine + rc * ROPE + i0;
+        const float* sn = p.sine + rc * ROPE + i0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            qc1[it][j] = c[j];
+            qs1[it][j] = sn[j];
+            qc2[it][j] = c[j + HALF];
+            qs2[it][j] = sn[j + HALF];
         }
     }
     __syncthreads();  // xq_s (the latent) is free from here on
 #pragma unroll
-    for (int it = 0; it < QITER; ++it) {
+    for (int it = 0; it < NI; ++it) {
         const int u = tid + it * THREADS;
-        if (u >= LMAX * QUNITS) continue;
-        const int row = u / QUNITS, q4 = u % QUNITS;
-        const float a4[4] = {qa[it].x, qa[it].y, qa[it].z, qa[it].w};
-        if (q4 < QN) {
+        const int row = u / QN, q4 = u % QN;
+        const float a4[4] = {qn[it].x, qn[it].y, qn[it].z, qn[it].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xq_s[row * KP + 4 * q4 + j] = AttnElem<true>::from(a4[j]);
-        } else {
-            const int i0 = 4 * (q4 - QN);
-            const float b4[4] = {qb4[it].x, qb4[it].y, qb4[it].z, qb4[it].w};
-            u16 o1[4] = {0, 0, 0, 0}, o2[4] = {0, 0, 0, 0};
-            if (row < L) {
-                const float* c = p.cosine + row * ROPE;
-                const float* sn = p.sine + row * ROPE;
+        for (int j = 0; j < 4; ++j) xq_s[row * KP + 4 * q4 + j] = row < L ? AttnElem<true>::from(a4[j]) : u16(0);
+    }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    rot(a4[j], b4[j], c[i0 + j], sn[i0 + j], c[i0 + j + HALF], sn[i0 + j + HALF], o1[j], o2[j]);
-                }
-            }
+    for (int it = 0; it < RI; ++it) {
+        const int u = tid + it * THREADS;
+        const int row = u / QR, i0 = 4 * (u % QR);
+        const float a4[4] = {qx1[it].x, qx1[it].y, qx1[it].z, qx1[it].w};
+        const float b4[4] = {qx2[it].x, qx2[it].y, qx2[it].z, qx2[it].w};
+        u16 o1[4], o2[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                xq_s[row * KP + NOPE + i0 + j] = o1[j];
-                xq_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
-            }
+        for (int j = 0; j < 4; ++j) {
+            rot(a4[j], b4[j], qc1[it][j], qs1[it][j], qc2[it][j], qs2[it][j], o1[j], o2[j]);
+            if (row >= L) o1[j] = o2[j] = 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xq_s[row * KP + NOPE + i0 + j] = o1[j];
+            xq_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
         }
     }
     __syncthreads();

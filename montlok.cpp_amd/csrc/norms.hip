@@ -37,41 +37,51 @@ __global__ __launch_bounds__(kBlock) void rms_norm_vec_kernel(const float* __res
     const int64_t row = active ? gid / groups : 0;
     const int64_t g = active ? gid % groups : 0;
     const float* xg = x + row * row_stride + g * gs;
-    float4 v[CPL];
+    const float* wg = w + g * gs;
+    // Every load is issued before the first use, without a branch around it:
+    // lanes past the last group read group 0 (in bounds); all LPG lanes of a
+    // group share `active`, so those sums never meet a live group's.
+    float4 v[CPL], wv[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) v[c] = *reinterpret_cast<const float4*>(xg + static_cast<int64_t>(c * LPG + li) * 4);
+    if constexpr (ADD) {
+        float4 r[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            r[c] = *reinterpret_cast<const float4*>(right + row * row_stride + g * gs + static_cast<int64_t>(c * LPG + li) * 4);
+        }
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            v[c].x += r[c].x;
+            v[c].y += r[c].y;
+            v[c].z += r[c].z;
+            v[c].w += r[c].w;
+            if (active) {
+                *reinterpret_cast<float4*>(residual + row * dim + g * gs + static_cast<int64_t>(c * LPG + li) * 4) = v[c];
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) wv[c] = *reinterpret_cast<const float4*>(wg + static_cast<int64_t>(c * LPG + li) * 4);
     double sumsq = 0.0;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const int64_t off = static_cast<int64_t>(c * LPG + li) * 4;
-        if (active) {
-            v[c] = *reinterpret_cast<const float4*>(xg + off);
-            if constexpr (ADD) {
-                const float4 r = *reinterpret_cast<const float4*>(right + row * row_stride + g * gs + off);
-                v[c].x += r.x;
-                v[c].y += r.y;
-                v[c].z += r.z;
-                v[c].w += r.w;
-                *reinterpret_cast<float4*>(residual + row * dim + g * gs + off) = v[c];
-            }
-        } else {
-            v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
         const double a = v[c].x, b = v[c].y, cc = v[c].z, d = v[c].w;
         sumsq += (a * a + b * b) + (cc * cc + d * d);
     }
     sumsq = group_sum_d<LPG>(sumsq);
     if (!active) return;
     const double scale = 1.0 / sqrt(sumsq / static_cast<double>(gs) + eps);
-    const float* wg = w + g * gs;
     float* og = out + row * dim + g * gs;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int64_t off = static_cast<int64_t>(c * LPG + li) * 4;
-        const float4 wv = *reinterpret_cast<const float4*>(wg + off);
+        const float4 wv_c = wv[c];
         float4 o;
-        o.x = static_cast<float>((static_cast<double>(v[c].x) * scale) * static_cast<double>(wv.x));
-        o.y = static_cast<float>((static_cast<double>(v[c].y) * scale) * static_cast<double>(wv.y));
-        o.z = static_cast<float>((static_cast<double>(v[c].z) * scale) * static_cast<double>(wv.z));
-        o.w = static_cast<float>((static_cast<double>(v[c].w) * scale) * static_cast<double>(wv.w));
+        o.x = static_cast<float>((static_cast<double>(v[c].x) * scale) * static_cast<double>(wv_c.x));
+        o.y = static_cast<float>((static_cast<double>(v[c].y) * scale) * static_cast<double>(wv_c.y));
+        o.z = static_cast<float>((static_cast<double>(v[c].z) * scale) * static_cast<double>(wv_c.z));
+        o.w = static_cast<float>((static_cast<double>(v[c].w) * scale) * static_cast<double>(wv_c.w));
         *reinterpret_cast<float4*>(og + off) = o;
     }
 }
@@ -165,11 +175,21 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __r
     const int li = threadIdx.x % lpg;
     const bool active = row < rows;
     const float* xr = x + (active ? row : 0) * row_stride;
-    float4 v[CPL];
+    // Loads first, unconditional (rows past the end read row 0; a row's lanes
+    // share `active`), weights and bias with them.
+    float4 v[CPL], wv[CPL], bv[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) v[c] = *reinterpret_cast<const float4*>(xr + (c * lpg + li) * 4);
+    const float* bsrc = bias != nullptr ? bias : w;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        wv[c] = *reinterpret_cast<const float4*>(w + (c * lpg + li) * 4);
+        bv[c] = *reinterpret_cast<const float4*>(bsrc + (c * lpg + li) * 4);
+        if (bias == nullptr) bv[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     double sum = 0.0;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        v[c] = active ? *reinterpret_cast<const float4*>(xr + (c * lpg + li) * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
         sum += (static_cast<double>(v[c].x) + static_cast<double>(v[c].y)) +
                (static_cast<double>(v[c].z) + static_cast<double>(v[c].w));
     }
@@ -190,14 +210,11 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __r
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int off = (c * lpg + li) * 4;
-        const float4 wv = *reinterpret_cast<const float4*>(w + off);
-        float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (bias != nullptr) bv = *reinterpret_cast<const float4*>(bias + off);
         float4 o;
-        o.x = static_cast<float>(((static_cast<double>(v[c].x) - mean) * rstd) * wv.x + static_cast<double>(bv.x));
-        o.y = static_cast<float>(((static_cast<double>(v[c].y) - mean) * rstd) * wv.y + static_cast<double>(bv.y));
-        o.z = static_cast<float>(((static_cast<double>(v[c].z) - mean) * rstd) * wv.z + static_cast<double>(bv.z));
-        o.w = static_cast<float>(((static_cast<double>(v[c].w) - mean) * rstd) * wv.w + static_cast<double>(bv.w));
+        o.x = static_cast<float>(((static_cast<double>(v[c].x) - mean) * rstd) * wv[c].x + static_cast<double>(bv[c].x));
+        o.y = static_cast<float>(((static_cast<double>(v[c].y) - mean) * rstd) * wv[c].y + static_cast<double>(bv[c].y));
+        o.z = static_cast<float>(((static_cast<double>(v[c].z) - mean) * rstd) * wv[c].z + static_cast<double>(bv[c].z));
+        o.w = static_cast<float>(((static_cast<double>(v[c].w) - mean) * rstd) * wv[c].w + static_cast<double>(bv[c].w));
         *reinterpret_cast<float4*>(outr + off) = o;
     }
 }
