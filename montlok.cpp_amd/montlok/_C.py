@@ -480,6 +480,66 @@ def stage1_forward(inputs, layers, mamba_norm_eps, mamba_norm_groups, ffn_norm_e
     return hidden
 
 
+def stage2_tail_forward(backbone, depth, n_streams, attn_hc, attn_hc_eps, attn_sinkhorn_iters, attn_norm_weight,
+                        attn_norm_eps, mla, kv_norm_eps, n_heads, head_dim, nope_dim, kv_lora_rank, attn_scale, ffn_hc,
+                        ffn_hc_eps, ffn_sinkhorn_iters, ffn_norm_weight, ffn_norm_eps, ffn):
+    """montlok.cpp:1217-1359: the recurrent stage-2 mHC tail, `depth` applications of one layer.
+
+    The backbone [B, L, d] is expanded to n_streams as a broadcast view; each step runs MLA on the
+    aggregated input, writes the attention residual fused with the FFN residual's coefficients, runs the
+    SwiGLU MLP and writes that residual fused with the next attention residual's coefficients. The last
+    step evaluates only the final query and returns the collapsed hidden state [B, 1, d].
+
+    Packs (as model.py:160-232 builds them): each mHC pack holds dyn-norm weight, fp64 projection block,
+    pre/post/res bias and pre/post/res alpha; the MLA pack holds the full and tail in_proj weights, q weight,
+    kv-norm weight and bias (empty = none), kv_up weight, o_proj weight, cos and sin; the FFN pack holds the
+    in weight and bias and the out weight and bias (empty = none). MONTLOK_STAGE2_INPLACE and
+    MONTLOK_STAGE2_REUSE_COEFF change only where the reference keeps its buffers, not the values, so they
+    have no counterpart here."""
+    _check(depth > 0, "depth must be positive")
+    _check(n_streams > 0, "n_streams must be positive")
+    _check(len(attn_hc) == 8 and len(ffn_hc) == 8, "each mHC tensor pack must contain dyn/proj/biases/alphas")
+    _check(len(mla) == 9, "MLA tensor pack must contain full/tail/q/norm/kv/out/rope tensors")
+    _check(len(ffn) == 4, "FFN tensor pack must contain in/out weights and biases")
+
+    def prepare(streams, hc, eps, iters, broadcast, norm_weight, norm_eps):
+        return mhc_prepare(streams, hc[0], eps, hc[1], hc[2], hc[3], hc[4], hc[5], hc[6], hc[7], iters, broadcast,
+                           norm_weight, norm_eps)
+
+    def combine_prepare(streams, res, post, out, hc, eps, iters, norm_weight, norm_eps):
+        return mhc_combine_prepare(streams, res, post, out, hc[0], eps, hc[1], hc[2], hc[3], hc[4], hc[5], hc[6],
+                                   hc[7], iters, norm_weight, norm_eps)
+
+    def run_mla(inputs, n_last):
+        projection = mla[0] if n_last == inputs.size(1) else mla[1]
+        return mla_forward(inputs, projection, mla[2], mla[3], mla[4], kv_norm_eps, mla[5], mla[6], mla[7], mla[8],
+                           n_heads, head_dim, nope_dim, kv_lora_rank, n_last, True, attn_scale)
+
+    def ffn_mlp(inputs):
+        return swiglu_mlp(inputs, ffn[0], ffn[1] if ffn[1].numel() else None, ffn[2],
+                          ffn[3] if ffn[3].numel() else None)
+
+    agg, _, post, res = prepare(backbone, attn_hc, attn_hc_eps, attn_sinkhorn_iters, n_streams, attn_norm_weight,
+                                attn_norm_eps)
+    streams = backbone
+    for step in range(depth):
+        if step + 1 == depth:
+            attn_out = run_mla(agg, 1)
+            last = streams.size(1) - 1
+            tail_streams = streams.narrow(1, last, 1).contiguous()
+            written = mhc_combine(tail_streams, res.narrow(1, last, 1).contiguous(),
+                                  post.narrow(1, last, 1).contiguous(), attn_out)
+            f_agg, _, f_post, f_res = prepare(written, ffn_hc, ffn_hc_eps, ffn_sinkhorn_iters, 0, ffn_norm_weight,
+                                              ffn_norm_eps)
+            return mhc_combine_collapse(written, f_res, f_post, ffn_mlp(f_agg))
+        attn_out = run_mla(agg, agg.size(1))
+        streams, f_agg, _, f_post, f_res = combine_prepare(streams, res, post, attn_out, ffn_hc, ffn_hc_eps,
+                                                           ffn_sinkhorn_iters, ffn_norm_weight, ffn_norm_eps)
+        streams, agg, _, post, res = combine_prepare(streams, f_res, f_post, ffn_mlp(f_agg), attn_hc, attn_hc_eps,
+                                                     attn_sinkhorn_iters, attn_norm_weight, attn_norm_eps)
+    raise AssertionError("unreachable stage-2 loop")
+
+
 def new_mamba3_state(streams: int, nheads: int, d_state: int, headdim: int, num_rope_angles: int, device) -> dict:
     """Zero carried state for mamba3_siso_step."""
     return {"ssm": torch.zeros(streams, nheads, d_state, headdim, device=device),
@@ -635,6 +695,37 @@ def build_info() -> dict:
     _call("mlk_build_info", buf, len(buf))
     info = json.loads(buf.value.decode())
     info["library"] = str(LIB_PATH)
+    return info
+
+
+def cpu_features() -> dict:
+    """Instruction-set features of the host CPU, with the reference's keys (montlok.cpp:1361-1378), read
+    from /proc/cpuinfo (empty brand and all flags false where that file is absent)."""
+    import platform
+
+    brand, flags = "", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, value = line.partition(":")
+                key = key.strip()
+                if key == "model name" and not brand:
+                    brand = value.strip()
+                elif key in ("flags", "Features") and not flags:
+                    flags = set(value.split())
+    except OSError:
+        pass
+    machine = platform.machine().lower()
+    info = {"brand": brand,
+            "arch": "x86-64" if machine in ("x86_64", "amd64") else ("arm64" if machine in ("aarch64", "arm64")
+                                                                     else "other")}
+    for key, flag in (("sse2", "sse2"), ("sse4_2", "sse4_2"), ("avx", "avx"), ("fma", "fma"), ("avx2", "avx2"),
+                      ("avx512f", "avx512f"), ("avx512dq", "avx512dq"), ("avx512bw", "avx512bw"),
+                      ("avx512vl", "avx512vl")):
+        info[key] = flag in flags
+    # The OS saves the wide registers when it exposes the features (xsave state enabled).
+    info["os_avx"] = info["avx"] and "osxsave" in flags
+    info["os_avx512"] = info["os_avx"] and info["avx512f"]
     return info
 
 

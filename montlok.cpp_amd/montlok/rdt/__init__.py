@@ -25,6 +25,10 @@ _EXPORTS = {
     "GroupedRMSNormCPU": "layers",
     "LayerNormCPU": "layers",
     "SwiGLUCPU": "layers",
+    "RMSNormHIP": "layers",
+    "GroupedRMSNormHIP": "layers",
+    "LayerNormHIP": "layers",
+    "SwiGLUHIP": "layers",
     "install_cpu_layers": "layers",
     "cpu_linear": "linear",
 }

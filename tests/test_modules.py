@@ -97,3 +97,33 @@ def test_modules_refuse_other_paths(monkeypatch):
     monkeypatch.setenv("MONTLOK_CPP_LAYERS", "0")
     with torch.no_grad(), pytest.raises(RuntimeError, match="switched off"):
         RMSNormCPU(64)(x)
+
+
+def test_stage2_tail_argument_checks():
+    """montlok.cpp:1239-1245: the packed tail op rejects a bad depth, stream count or pack before any launch."""
+    from montlok import _C
+
+    x = torch.zeros(1, 2, 8)
+    hc, mla, ffn = [x] * 8, [x] * 9, [x] * 4
+    common = dict(attn_hc_eps=1e-5, attn_sinkhorn_iters=20, attn_norm_weight=x, attn_norm_eps=1e-5, kv_norm_eps=1e-5,
+                  n_heads=1, head_dim=8, nope_dim=4, kv_lora_rank=8, attn_scale=1.0, ffn_hc_eps=1e-5,
+                  ffn_sinkhorn_iters=20, ffn_norm_weight=x, ffn_norm_eps=1e-5)
+    cases = [((0, 4, hc, mla, hc, ffn), "depth must be positive"),
+             ((1, 0, hc, mla, hc, ffn), "n_streams must be positive"),
+             ((1, 4, hc[:7], mla, hc, ffn), "each mHC tensor pack must contain dyn/proj/biases/alphas"),
+             ((1, 4, hc, mla[:8], hc, ffn), "MLA tensor pack must contain full/tail/q/norm/kv/out/rope tensors"),
+             ((1, 4, hc, mla, hc, ffn[:3]), "FFN tensor pack must contain in/out weights and biases")]
+    for (depth, n, a_hc, a_mla, f_hc, a_ffn), message in cases:
+        with pytest.raises(RuntimeError, match=message):
+            _C.stage2_tail_forward(x, depth, n, attn_hc=a_hc, mla=a_mla, ffn_hc=f_hc, ffn=a_ffn, **common)
+
+
+def test_cpu_features_keys():
+    """montlok.cpp:1361-1378: the same keys as the reference's host-CPU description."""
+    from montlok import _C
+
+    info = _C.cpu_features()
+    assert set(info) == {"brand", "arch", "sse2", "sse4_2", "avx", "fma", "avx2", "avx512f", "avx512dq", "avx512bw",
+                         "avx512vl", "os_avx", "os_avx512"}
+    assert isinstance(info["brand"], str) and info["arch"] in ("x86-64", "arm64", "other")
+    assert all(isinstance(info[k], bool) for k in info if k not in ("brand", "arch"))
