@@ -16,24 +16,21 @@
 //
 // Kernels
 //   prepare_n4<D> (n = 4, d = D in {64, 128, 256, 512}): one 256-thread block
-//     per 16 tokens. Lane l of every wave is (token t = l % 16, k-lane
-//     q = l / 16). The 24 dot products of each token run on the fp64 matrix
-//     cores, v_mfma_f64_16x16x4_f64: A = 16 projection rows x 4 k, B = 4 k x
-//     16 tokens, two row tiles (tile 0 = the 16 res rows, tile 1 = 4 pre + 4
-//     post rows + 8 zero rows). The k range is split over the block's four
-//     waves (wave w owns steps [w*S/4, (w+1)*S/4), S = D/4, step s covering
-//     k = 4s + q); partial tiles are summed through LDS by wave 0 in wave
-//     order. norm_w and the RMS scale are applied on the B side and after the
-//     sum: logit = scale * sum_k W[r,k] * (w_k * m_k). The accumulator of the
-//     16x16x4 f64 MFMA holds tile rows q, q+4, q+8, q+12 of token t in lane
-//     (t, q); the projection rows are permuted on the A side so that after the
-//     tanh every lane holds one full row of its token's 4x4 Sinkhorn matrix
-//     (and lanes q = 0 / 1 the pre / post logits): row sums are lane-local,
-//     column sums gather the four
-//     lanes of the token with the reference's sequential order, and the
-//     reciprocals are IEEE divisions like the reference's 1 / s.
-//     Traffic per token: n*d*4 bytes read twice (the second read, for agg,
-//     hits L2) + d*4 written + 36 floats of coefficients.
+//     per 16 tokens. In the load and MFMA phase lane l of every wave is
+//     (token t = l % 16, k-lane q = l / 16). The 24 dot products of each token
+//     run on the fp64 matrix cores, v_mfma_f64_16x16x4_f64: A = 16 projection
+//     rows x 4 k, B = 4 k x 16 tokens, two row tiles (tile 0 = the 16 res rows,
+//     tile 1 = 4 pre + 4 post rows + 8 zero rows). The k range is split over
+//     the block's four waves (wave w owns k in [w*D/4, (w+1)*D/4)); partial
+//     tiles go through LDS and are summed in wave order. norm_w and the RMS
+//     scale are applied on the B side and after the sum:
+//     logit = scale * sum_k W[r,k] * (w_k * m_k). In the coefficient phase
+//     each wave takes 4 tokens with one res entry per lane (token 4w + l / 16,
+//     entry l % 16; lanes with entry < 8 also produce pre or post). Sinkhorn
+//     row sums are quad sums and column sums 16-lane sums (DPP, the
+//     reference's association), the reciprocals the IEEE quotient 1 / s.
+//     Traffic per token: n*d*4 bytes read once + d*4 written + 36 floats of
+//     coefficients (non-temporal stores).
 //   prepare_generic: one wave per token, every sum in the reference's own
 //     order (bit-exact with it); used for other n or d. Slow, small shapes.
 //   combine<N>: one thread per (token, float4 of d), HBM-bound.
