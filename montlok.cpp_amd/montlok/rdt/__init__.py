@@ -30,6 +30,11 @@ _EXPORTS = {
     "LayerNormHIP": "layers",
     "SwiGLUHIP": "layers",
     "install_cpu_layers": "layers",
+    "RDT4QuantCPU": "model",
+    "RDT4QuantHIP": "model",
+    "MultiAssetRDTCPU": "model",
+    "MultiAssetRDTHIP": "model",
+    "RDTModelConfig": "model",
     "cpu_linear": "linear",
 }
 

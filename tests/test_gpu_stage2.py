@@ -86,8 +86,9 @@ def _oracle_tail(oracle, layer, backbone: np.ndarray, depth: int) -> np.ndarray:
 
     def ffn(x):
         f = layer.ffn
-        h = oracle.linear(x, _np(f.w_in.weight), _np(f.w_in.bias))
-        return oracle.linear(oracle.swiglu(h), _np(f.w_down.weight), _np(f.w_down.bias))
+        bias = (lambda b: None if b is None else _np(b))  # noqa: E731
+        h = oracle.linear(x, _np(f.w_in.weight), bias(f.w_in.bias))
+        return oracle.linear(oracle.swiglu(h), _np(f.w_down.weight), bias(f.w_down.bias))
 
     agg, _, post, res = prepare(layer.attn_hc, layer.attn_norm, backbone, n)
     streams = backbone

@@ -127,3 +127,79 @@ def test_cpu_features_keys():
                          "avx512vl", "os_avx", "os_avx512"}
     assert isinstance(info["brand"], str) and info["arch"] in ("x86-64", "arm64", "other")
     assert all(isinstance(info[k], bool) for k in info if k not in ("brand", "arch"))
+
+
+def _tiny_model_config(**overrides):
+    model = dict(d_model=64, n_heads=2, head_dim=32, rope_head_dim=16, nope_head_dim=16, kv_lora_rank=64,
+                 ffn_hidden=128, n_prelude=0, n_coda=0, core_type="two_stage", stage1_mamba_layers=1,
+                 stage2_attn_layers=1, recurrent_steps=2, recurrent_drift_mode="mhc", mhc_n_streams=4,
+                 mhc_sinkhorn_iters=20, mamba_d_state=16, mamba_headdim=32, mamba_expand=2, mamba_chunk_size=64,
+                 use_official_mamba=True, use_morphological_rope=False, bidirectional=False, max_seq_len=64,
+                 grad_ckpt_blocks=False, grad_ckpt_recurrent=True)
+    model.update(overrides)
+    return {"model": model, "horizons_minutes": [15, 60, 240]}
+
+
+def test_model_state_dict_contract():
+    """The upstream two-stage module tree (Model/two_stage.py:58-168, Model/blocks.py:120-131,
+    Model/layers/mamba3_layer.py:383-445) under RDT4QuantCPU (model.py:289-305): every key and shape a
+    checkpoint carries, written out from those modules."""
+    from montlok.rdt import RDT4QuantCPU, RDT4QuantHIP
+
+    assert RDT4QuantCPU is RDT4QuantHIP
+    m = RDT4QuantHIP(7, _tiny_model_config())
+    shapes = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    s1, s2 = "recurrent.stage1.0.", "recurrent.stage2.0."
+    hc = {"pre_bias": (4,), "post_bias": (4,), "res_bias": (4, 4), "dyn_norm.weight": (64,),
+          "pre_proj.weight": (4, 64), "post_proj.weight": (4, 64), "res_proj.weight": (16, 64), "pre_alpha": (),
+          "post_alpha": (), "res_alpha": ()}
+    expect = {"projection.weight": (64, 7), "projection.bias": (64,), "input_norm.weight": (64,),
+              "input_norm.bias": (64,),
+              s1 + "mamba.norm.weight": (64,), s1 + "mamba.mamba.in_proj.weight": (2 * 128 + 2 * 16 + 3 * 4 + 4, 64),
+              s1 + "mamba.mamba.dt_bias": (4,), s1 + "mamba.mamba.B_bias": (4, 1, 16),
+              s1 + "mamba.mamba.C_bias": (4, 1, 16), s1 + "mamba.mamba.B_norm.weight": (16,),
+              s1 + "mamba.mamba.C_norm.weight": (16,), s1 + "mamba.mamba.D": (4,),
+              s1 + "mamba.mamba.out_proj.weight": (64, 128), s1 + "ffn_norm.weight": (64,),
+              s1 + "ffn.w_in.weight": (256, 64), s1 + "ffn.w_down.weight": (64, 128),
+              s2 + "attn_norm.weight": (64,), s2 + "attn.q_proj.weight": (64, 64),
+              s2 + "attn.kv_down.weight": (64, 64), s2 + "attn.kv_norm.weight": (64,),
+              s2 + "attn.kv_norm.bias": (64,), s2 + "attn.kv_up.weight": (2 * 48, 64),
+              s2 + "attn.k_rope_proj.weight": (16, 64), s2 + "attn.o_proj.weight": (64, 64),
+              s2 + "ffn_norm.weight": (64,), s2 + "ffn.w_in.weight": (256, 64), s2 + "ffn.w_down.weight": (64, 128),
+              "final_norm.weight": (64,), "head.weight": (9, 64), "head.bias": (9,)}
+    for k, v in hc.items():
+        expect[s2 + "attn_hc." + k] = v
+        expect[s2 + "ffn_hc." + k] = v
+    assert shapes == expect
+    m.load_state_dict(m.state_dict(), strict=True)
+
+
+def test_multi_asset_model_contract():
+    """model.py:393-406: the stock inputs' projection, norm, embeddings and per-domain heads."""
+    from montlok.rdt import MultiAssetRDTCPU, MultiAssetRDTHIP
+
+    assert MultiAssetRDTCPU is MultiAssetRDTHIP
+    m = MultiAssetRDTHIP(_tiny_model_config(), asset_count=5)
+    shapes = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    assert shapes["projection.weight"] == (64, 57)
+    assert shapes["stock_projection.weight"] == (64, 23) and shapes["stock_norm.bias"] == (64,)
+    assert shapes["asset_embedding.weight"] == (5, 64) and shapes["period_embedding.weight"] == (2, 64)
+    assert shapes["stock_heads.equity_daily.weight"] == (9, 64) and shapes["stock_heads.token_hour.bias"] == (9,)
+
+
+def test_model_config_refusals():
+    """Configurations the reference hands to upstream PyTorch are refused, never computed another way."""
+    from montlok.rdt import RDT4QuantHIP
+
+    for overrides, message in ((dict(core_type="interleaved"), "core_type"),
+                               (dict(recurrent_drift_mode="none"), "recurrent_drift_mode"),
+                               (dict(n_prelude=2), "prelude/coda"), (dict(use_morphological_rope=True), "morphological"),
+                               (dict(use_mol=True), "mixture-of-LoRA")):
+        with pytest.raises(NotImplementedError, match=message):
+            RDT4QuantHIP(7, _tiny_model_config(**overrides))
+    with pytest.raises(ValueError, match="use_official_mamba"):
+        RDT4QuantHIP(7, _tiny_model_config(use_official_mamba=False))
+    m = RDT4QuantHIP(7, _tiny_model_config())
+    with pytest.raises(RuntimeError, match="ROCm device|switched off"):
+        with torch.no_grad():
+            m(torch.zeros(1, 4, 7), 1)
