@@ -17,18 +17,25 @@
 //                   sum over time in double, rounded to fp32 per step, wrapped
 //                   to [0, 2pi) with a separately rounded 2pi*floor product,
 //                   sin/cos in double, rotation of pair (2r, 2r+1) of q and k.
-//   rec_kernel<NM>  one wave per (window, head, 64 headdim columns): lane d
-//                   owns state column S[:, d] (N <= NM floats in VGPRs); q_t,
-//                   k_t, k_{t-1} and the coefficients are wave-uniform (scalar
-//                   loads). Per step and state row n:
+//   rec_kernel<NM>  the time-sequential recurrence: one wave per (window,
+//                   head, 64 headdim columns), lane d owns state column S[:, d]
+//                   (N <= NM floats in VGPRs); q_t, k_t, k_{t-1}, the
+//                   coefficients, v and the gate of 8-step chunks are staged in
+//                   LDS, double-buffered. Per step and state row n:
 //                     s = fma(k_t[n], gamma*v_t[d], fma(s, alpha, k_{t-1}[n] * beta*v_{t-1}[d]))
 //                     acc_{n%2} = fma(s, q_t[n], acc)
 //                   (even/odd accumulators when headdim % 8 == 0, one
 //                   otherwise, as the reference's vector and scalar paths),
 //                   y = fma(D, v_t[d], acc0 + acc1), out = y * silu(z) in double
-//                   rounded once (or y * gate).
-//   The recurrence is FP32-VALU bound: ~4N flops... 7 flop per state element
-//   per token; q/k/coefficients come through the scalar cache.
+//                   rounded once (or y * gate). Bit for bit the reference's
+//                   association; fp32-VALU bound, ~7 flop per state element
+//                   per token.
+//   rec_chunk_kernel the chunked scan on the fp32 matrix cores (32-token
+//                   chunks, state carried in registers), used when there are
+//                   few (window, head) pairs; see the comment above it.
+#include <cstdlib>
+#include <cstring>
+
 #include "mlk_common.h"
 
 namespace mlk {
@@ -469,8 +476,341 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
     }
 }
 
+// ---------------------------------------------------------------------------
+// The recurrence in chunked form, on the fp32 matrix cores
+// ---------------------------------------------------------------------------
+//
+// Over a chunk of C tokens (chunk-local indices t, s in [0, C)), unrolling
+// S_t = a_t S_{t-1} + b_t k_{t-1} v_{t-1}^T + g_t k_t v_t^T gives
+//   y_t = sum_{s<=t} W[t][s] (q_t . k_s) v_s          intra-chunk
+//       + Din(t) S_in^T q_t                            carried state
+//       + Wp(t) (q_t . k_p) v_p                        the previous chunk's last token p
+//   W[t][s] = g_s prod_{r=s+1..t} a_r + [s < t] b_{s+1} prod_{r=s+2..t} a_r
+//   Din(t)  = prod_{r=0..t} a_r,  Wp(t) = b_0 prod_{r=1..t} a_r
+// and the state after the chunk is
+//   S_out = Din(C-1) S_in + sum_s W[C-1][s] k_s v_s^T + Wp(C-1) k_p v_p^T.
+// The products of the stored fp32 coefficients are formed in double, one lane
+// per s walking t forward (no exp or log: exactly the products the
+// time-sequential form multiplies by), and each weight is rounded to fp32
+// once. One wave per (window, head), all D <= 64 columns:
+//   G^T = K Q^T        v_mfma_f32_16x16x4_f32, A = K rows, B = Q rows (float4
+//                      loads: instruction v of a 16-wide k block takes
+//                      k = 4g + v in lane group g on both sides);
+//   P = W o G          the accumulator layout of G^T (s = 4g + v, t = lane % 16)
+//                      is the A-operand layout of P for Y = P V;
+//   Y = P V + Q S_in   V staged in LDS; S_in lives in registers in the
+//                      accumulator layout (n = 4g + v, d = lane % 16), which is
+//                      the B-operand layout of Q S_in and the C operand of the
+//                      state update S_out = Din S_in + K^T (w o V).
+// Every fp32 sum is in an order of its own, so results agree with the
+// time-sequential kernel to rounding (the fp32 tolerance), not bit for bit.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int C, int NT, int DT>
+__global__ __launch_bounds__(64) void rec_chunk_kernel(RecArgs a) {
+    constexpr int N = 16 * NT, D = 16 * DT;
+    constexpr int CT = C / 16;
+    constexpr int WP = C + 4;  // row pitches in floats: 16-byte rows, 16 consecutive rows on distinct banks
+    constexpr int NP = N + 4;
+    constexpr int VP = D + 4;
+    __shared__ __attribute__((aligned(16))) float w_s[C * WP];
+    __shared__ __attribute__((aligned(16))) float q_sh[C * NP];
+    __shared__ __attribute__((aligned(16))) float k_sh[C * NP];
+    __shared__ __attribute__((aligned(16))) float v_sh[C * VP];
+    __shared__ __attribute__((aligned(16))) float g_sh[C * VP];
+    __shared__ float coef[3][C];
+    __shared__ float din_s[C], wp_s[C], ck_s[C];
+    __shared__ float kp_s[N];
+
+    const int lane = threadIdx.x, g = lane >> 4, li = lane & 15;
+    const int64_t L = a.L, H = a.H;
+    const int64_t h = blockIdx.x % H, b = blockIdx.x / H;
+    const float* qrow = a.q + b * a.qs.b + h * a.qs.h;
+    const float* krow = a.k + b * a.ks.b + h * a.ks.h;
+    const float* vrow = a.v + b * a.vs.b + h * a.vs.h;
+    const float* grow = a.gate + b * a.gs.b + h * a.gs.h;
+    float* orow = a.out + b * a.os.b + h * a.os.h;
+    const int64_t cbase = b * L * H + h;
+    const float skip = a.skip[h];
+
+    f32x4_t S[NT][DT];
+    float vp_d[DT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) S[nt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vp_d[dt] = 0.0f;
+
+    for (int64_t c0 = 0; c0 < L; c0 += C) {
+        const int Lc = static_cast<int>(L - c0 < C ? L - c0 : C);
+        const bool first = c0 == 0, last = c0 + C >= L;
+        // 1. The chunk's operands into LDS, every load of a batch issued before
+        //    the first wait (rows past the end read the last row; their
+        //    coefficients are zero, so they carry no weight).
+        {
+            constexpr int QU = C * N / 4 / 64;  // float4 units of Q (and K) per lane
+            float4 qq[QU], kk[QU];
+            constexpr int CU = (3 * C + 63) / 64;  // coefficient entries (alpha, beta, gamma of C tokens) per lane
+            float cf[CU];
+#pragma unroll
+            for (int j = 0; j < QU; ++j) {
+                const int u = lane + 64 * j, s = u / (N / 4), n4 = 4 * (u % (N / 4));
+                const int64_t t = c0 + (s < Lc ? s : Lc - 1);
+                qq[j] = *reinterpret_cast<const float4*>(qrow + t * a.qs.t + n4);
+                kk[j] = *reinterpret_cast<const float4*>(krow + t * a.ks.t + n4);
+            }
+#pragma unroll
+            for (int j = 0; j < CU; ++j) {
+                const int u = lane + 64 * j, which = u / C, s = u % C;
+                const float* src = which == 0 ? a.alpha : (which == 1 ? a.beta : a.gamma);
+                cf[j] = u < 3 * C && s < Lc ? src[cbase + (c0 + s) * H] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < QU; ++j) {
+                const int u = lane + 64 * j, s = u / (N / 4), n4 = 4 * (u % (N / 4));
+                *reinterpret_cast<float4*>(q_sh + s * NP + n4) = qq[j];
+                *reinterpret_cast<float4*>(k_sh + s * NP + n4) = kk[j];
+            }
+#pragma unroll
+            for (int j = 0; j < CU; ++j) {
+                const int u = lane + 64 * j;
+                if (u < 3 * C) coef[u / C][u % C] = cf[j];
+            }
+            constexpr int VU = C * D / 64;
+            float vv[VU], gg[VU];
+#pragma unroll
+            for (int j = 0; j < VU; ++j) {
+                const int u = lane + 64 * j, s = u / D, d = u % D;
+                const int64_t t = c0 + (s < Lc ? s : Lc - 1);
+                vv[j] = vrow[t * a.vs.t + d];
+                gg[j] = grow[t * a.gs.t + d];
+            }
+#pragma unroll
+            for (int j = 0; j < VU; ++j) {
+                const int u = lane + 64 * j;
+                v_sh[(u / D) * VP + u % D] = vv[j];
+                g_sh[(u / D) * VP + u % D] = gg[j];
+            }
+        }
+        __syncthreads();
+        // 2. Weights: lane s walks t forward; lane 0 also writes Din and Wp.
+        if (lane < C) {
+            const int s = lane;
+            const double gam = coef[2][s];
+            const double bet = s + 1 < C ? static_cast<double>(coef[1][s + 1]) : 0.0;
+            const double a0 = coef[0][0], b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
+            double d = 1.0, e = 1.0;
+#pragma unroll
+            for (int t = 0; t < C; ++t) {
+                float w = 0.0f;
+                const double at = coef[0][t];
+                if (t >= s) {
+                    if (t > s) d *= at;
+                    if (t > s + 1) e *= at;
+                    double val = gam * d;
+                    if (t > s) val = fma(bet, e, val);
+                    w = static_cast<float>(val);
+                }
+                w_s[t * WP + s] = w;
+                if (s == 0) {
+                    din_s[t] = static_cast<float>(a0 * d);
+                    wp_s[t] = static_cast<float>(b0 * d);
+                }
+            }
+            // 3. The previous chunk's last token: ck[t] = Wp(t) (q_t . k_p), computed by lane t.
+            float dot = 0.0f;
+            if (!first) {
+#pragma unroll
+                for (int n = 0; n < N; ++n) dot = fmaf(q_sh[s * NP + n], kp_s[n], dot);
+            }
+            ck_s[s] = dot;
+        }
+        __syncthreads();
+        if (lane < C) ck_s[lane] *= wp_s[lane];
+        __syncthreads();
+
+        // 4. Outputs, 16 tokens at a time; every operand from LDS. Independent
+        //    accumulators (the s tiles of G, the d tiles of Y) are interleaved so
+        //    that consecutive MFMAs do not wait on each other.
+#pragma unroll
+        for (int tt = 0; tt < CT; ++tt) {
+            const int t0 = 16 * tt;
+            if (t0 >= Lc) break;
+            float4 qf[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) qf[nt] = *reinterpret_cast<const float4*>(q_sh + (t0 + li) * NP + 16 * nt + 4 * g);
+            f32x4_t P[CT];
+#pragma unroll
+            for (int st = 0; st < CT; ++st) P[st] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float4 k4[CT];
+#pragma unroll
+                for (int st = 0; st < CT; ++st) {
+                    if (st <= tt) k4[st] = *reinterpret_cast<const float4*>(k_sh + (16 * st + li) * NP + 16 * nt + 4 * g);
+                }
+#pragma unroll
+                for (int st = 0; st < CT; ++st) {
+                    if (st > tt) continue;
+                    P[st] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[st].x, qf[nt].x, P[st], 0, 0, 0);
+                }
+#pragma unroll
+                for (int st = 0; st < CT; ++st) {
+                    if (st > tt) continue;
+                    P[st] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[st].y, qf[nt].y, P[st], 0, 0, 0);
+                }
+#pragma unroll
+                for (int st = 0; st < CT; ++st) {
+                    if (st > tt) continue;
+                    P[st] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[st].z, qf[nt].z, P[st], 0, 0, 0);
+                }
+#pragma unroll
+                for (int st = 0; st < CT; ++st) {
+                    if (st > tt) continue;
+                    P[st] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[st].w, qf[nt].w, P[st], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < CT; ++st) {  // P = W o G
+                if (st > tt) continue;
+                const float4 w4 = *reinterpret_cast<const float4*>(w_s + (t0 + li) * WP + 16 * st + 4 * g);
+                P[st] = f32x4_t{w4.x * P[st][0], w4.y * P[st][1], w4.z * P[st][2], w4.w * P[st][3]};
+            }
+            f32x4_t Y[DT], Yi[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                Y[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                Yi[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int st = 0; st < CT; ++st) {
+                if (st > tt) continue;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float vb[DT];
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) vb[dt] = v_sh[(16 * st + 4 * g + v) * VP + 16 * dt + li];
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) Y[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[st][v], vb[dt], Y[dt], 0, 0, 0);
+                }
+            }
+            if (!first) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const float qv[4] = {qf[nt].x, qf[nt].y, qf[nt].z, qf[nt].w};
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt) {
+                            Yi[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[v], S[nt][dt][v], Yi[dt], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int d = 16 * dt + li;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int t = t0 + 4 * g + v;
+                    if (t >= Lc) continue;
+                    float y = Y[dt][v];
+                    if (!first) y = fmaf(ck_s[t], vp_d[dt], fmaf(din_s[t], Yi[dt][v], y));
+                    y = fmaf(skip, v_sh[t * VP + d], y);
+                    const float gt = g_sh[t * VP + d];
+                    float o;
+                    if (a.gate_logits) {
+                        const double z = static_cast<double>(gt);
+                        o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
+                    } else {
+                        o = y * gt;
+                    }
+                    orow[(c0 + t) * a.os.t + d] = o;
+                }
+            }
+        }
+        if (last) break;
+
+        // 5. State after the chunk (every token of a non-final chunk is valid);
+        //    the NT x DT state tiles are independent accumulators, interleaved.
+        {
+            const float dl = din_s[C - 1], wl = wp_s[C - 1];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        float x = S[nt][dt][v] * dl;
+                        if (!first) x = fmaf(wl * kp_s[16 * nt + 4 * g + v], vp_d[dt], x);
+                        S[nt][dt][v] = x;
+                    }
+#pragma unroll
+            for (int st = 0; st < CT; ++st) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int srow = 16 * st + 4 * g + v;
+                    const float wv = w_s[(C - 1) * WP + srow];
+                    float kA[NT], bv[DT];
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) kA[nt] = k_sh[srow * NP + 16 * nt + li];
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) bv[dt] = wv * v_sh[srow * VP + 16 * dt + li];
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt)
+                            S[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kA[nt], bv[dt], S[nt][dt], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();  // kp_s and this chunk's LDS operands are read above
+        if (lane < N) kp_s[lane] = k_sh[(C - 1) * NP + lane];
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) vp_d[dt] = v_sh[(C - 1) * VP + 16 * dt + li];
+        __syncthreads();
+    }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+bool chunked_scan_enabled() {
+    const char* mode = std::getenv("MLK_MAMBA3_SCAN");
+    return mode == nullptr || std::strcmp(mode, "sequential") != 0;
+}
+
+template <int C>
+bool launch_rec_chunk(const RecArgs& a, hipStream_t stream) {
+    const int NT = static_cast<int>(a.N / 16), DT = static_cast<int>(a.D / 16);
+    const dim3 grid(static_cast<unsigned>(a.B * a.H));
+#define MLK_CHUNK(NTV, DTV)                                                                               \
+    if (NT == NTV && DT == DTV) {                                                                         \
+        hipLaunchKernelGGL((rec_chunk_kernel<C, NTV, DTV>), grid, dim3(64), 0, stream, a);              \
+        return true;                                                                                      \
+    }
+    MLK_CHUNK(1, 2) MLK_CHUNK(1, 4) MLK_CHUNK(2, 2) MLK_CHUNK(2, 4) MLK_CHUNK(4, 2) MLK_CHUNK(4, 4)
+#undef MLK_CHUNK
+    return false;
+}
+
 mlk_status launch_rec(const RecArgs& a, hipStream_t stream) {
     if (a.B * a.L * a.H == 0 || a.D == 0) return MLK_OK;
+    // Chunked scan on the matrix cores when there are at most 2048 (window,
+    // head) pairs, i.e. at most two waves per SIMD: there the time-sequential
+    // kernel's L dependent steps per wave leave the chip idle (measured
+    // 0.058 vs 0.088 ms at 64 x 64 tokens, 8 heads, d_state 64). With more
+    // pairs the sequential kernel fills the chip and is faster (1.17 vs 1.24
+    // ms at 1024 x 256 tokens, 8 heads). d_state in {16, 32, 64}, headdim in
+    // {32, 64}, 16-byte aligned q/k rows; MLK_MAMBA3_SCAN=sequential forces
+    // the reference's own association.
+    if (chunked_scan_enabled() && a.B * a.H <= 2048 && (a.N == 16 || a.N == 32 || a.N == 64) &&
+        (a.D == 32 || a.D == 64) &&
+        a.qs.t % 4 == 0 && a.qs.b % 4 == 0 && a.qs.h % 4 == 0 && a.ks.t % 4 == 0 && a.ks.b % 4 == 0 &&
+        a.ks.h % 4 == 0 && aligned16(a.q) && aligned16(a.k)) {
+        const bool ok = launch_rec_chunk<32>(a, stream);
+        if (ok) return launch_status("mamba3 chunked recurrence");
+    }
     const bool vec = a.D % 8 == 0;
     const bool pair = vec && a.D <= 32;
     const int64_t grid = a.B * a.H * ((a.D + (pair ? 31 : 63)) / (pair ? 32 : 64));

@@ -3,9 +3,12 @@ post-processing + recurrence, and the one-token step with carried state.
 
 Against the golden vectors of the compiled reference and the CPU oracle on
 the same seeded inputs; gate: normwise relative error <= 1e-5 (fp32). The
-step is checked against the sequence op (stepping T tokens from a zero state
-equals the forward over T tokens, bit for bit) and against the oracle's step
-at the streaming-decode geometry (d_model 128, d_state 64, 4 heads).
+chunked scan on the matrix cores (the default for d_state 16/32/64 and
+headdim 32/64) is checked against the time-sequential kernel and the oracle.
+The step is checked against the time-sequential sequence kernel (stepping T
+tokens from a zero state equals the forward over T tokens, bit for bit) and
+against the oracle's step at the streaming-decode geometry (d_model 128,
+d_state 64, 4 heads).
 """
 
 from __future__ import annotations
@@ -125,7 +128,8 @@ def test_recurrent_strided_views(dev, oracle):
 
 
 @pytest.mark.parametrize("N,G,H,D,R", [(16, 1, 4, 16, 4), (64, 1, 4, 64, 16), (6, 1, 3, 12, 1)])
-def test_step_equals_sequence(dev, N, G, H, D, R):
+def test_step_equals_sequence(dev, monkeypatch, N, G, H, D, R):
+    """T steps equal the time-sequential sequence kernel bit for bit, and the chunked scan to rounding."""
     from montlok import _C
 
     rng = np.random.default_rng(N + D)
@@ -133,11 +137,34 @@ def test_step_equals_sequence(dev, N, G, H, D, R):
     proj, p = _random_layer(rng, S, T, N, G, H, D, R)
     plist = [_t(p[k], dev) for k in ("b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")]
     tp = _t(proj, dev)
+    chunked = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "sequential")
     seq = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
     state = _C.new_mamba3_state(S, H, N, D, R, dev)
     for t in range(T):
         y = _C.mamba3_siso_step(tp[:, t].contiguous(), state, *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
         assert_bitwise(y, seq[:, t].cpu().numpy(), f"step {t}")
+    assert_close(chunked, seq, tol=1e-6, name="chunked scan vs time-sequential")
+
+
+@pytest.mark.parametrize("B,L,N,H,D", [(2, 200, 64, 2, 64), (3, 64, 32, 2, 32), (2, 70, 16, 3, 64), (4, 31, 64, 1, 32)])
+def test_chunked_scan_vs_sequential(dev, oracle, monkeypatch, B, L, N, H, D):
+    """The chunked scan (full, partial and single chunks, both chunk lengths) against the time-sequential
+    kernel and the oracle, 1e-6 normwise."""
+    from montlok import _C
+
+    rng = np.random.default_rng(L + N)
+    R = N // 4
+    proj, p = _random_layer(rng, B, L, N, 1, H, D, R)
+    plist = [_t(p[k], dev) for k in ("b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")]
+    tp = _t(proj, dev)
+    chunked = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, 1, H, D, R, 1e-5, 1e-5, 1e-4)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "sequential")
+    seq = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, 1, H, D, R, 1e-5, 1e-5, 1e-4)
+    assert_close(chunked, seq, tol=1e-6, name="chunked vs sequential")
+    expect = oracle.mamba3_siso_forward(proj, N, 1, H, D, R, p["b_bias"], p["c_bias"], p["b_norm_w"], p["c_norm_w"],
+                                        1e-5, 1e-5, p["dt_bias"], p["skip"], 1e-4)
+    assert_close(chunked, expect, tol=1e-6, name="chunked vs oracle")
 
 
 def test_step_decode_geometry_vs_oracle(dev, oracle):
