@@ -97,6 +97,13 @@ struct PrepareArgs {
     float* pre;
     float* post;
     float* res;
+    // Fused write of the previous residual (mhc_combine_prepare): its res
+    // [T, 16] and post [T, 4] coefficients, the mixer output [T, D], and the
+    // new streams [T, 4, D] written on the way.
+    const float* c_res;
+    const float* c_post;
+    const float* c_out;
+    float* c_new;
 };
 
 // Values held by lanes (t, 0..3) of a wave, gathered into every lane of
@@ -126,7 +133,7 @@ __device__ __forceinline__ float bcast_row0(float v) {
     return __int_as_float(e[0]);
 }
 
-template <int D>
+template <int D, bool FUSED>
 __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     constexpr int n = 4;
     constexpr int GW = D / 64;  // groups of 16 k per wave; group g covers k in [16g, 16g + 16)
@@ -173,6 +180,47 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
 #pragma unroll
         for (int i = 0; i < n; ++i) sv[j][i] = *reinterpret_cast<const float4*>(base + i * a.sd + k0);
     }
+    if constexpr (FUSED) {
+        // The previous residual's write on this lane's k-slice of all n
+        // streams, in mhc_combine's arithmetic (post_i * out + sum_j res_ij *
+        // s_j in double, one rounding): the new streams are stored once and
+        // are the streams this prepare reads.
+        const int64_t tok = valid ? token : 0;
+        const float4 r0 = reinterpret_cast<const float4*>(a.c_res + tok * 16)[0];
+        const float4 r1 = reinterpret_cast<const float4*>(a.c_res + tok * 16)[1];
+        const float4 r2 = reinterpret_cast<const float4*>(a.c_res + tok * 16)[2];
+        const float4 r3 = reinterpret_cast<const float4*>(a.c_res + tok * 16)[3];
+        const float4 pv = *reinterpret_cast<const float4*>(a.c_post + tok * 4);
+        float4 ov[GW];
+#pragma unroll
+        for (int j = 0; j < GW; ++j) ov[j] = *reinterpret_cast<const float4*>(a.c_out + tok * D + 16 * (wave * GW + j) + 4 * q);
+        // new_i = post_i * out + res_i0 s_0 + res_i1 s_1 + res_i2 s_2 + res_i3 s_3 (double, this order, one rounding)
+        auto mix = [](float p, float4 r, float o, float s0, float s1, float s2, float s3) -> float {
+            double acc = static_cast<double>(p) * static_cast<double>(o);
+            acc = fma(static_cast<double>(r.x), static_cast<double>(s0), acc);
+            acc = fma(static_cast<double>(r.y), static_cast<double>(s1), acc);
+            acc = fma(static_cast<double>(r.z), static_cast<double>(s2), acc);
+            acc = fma(static_cast<double>(r.w), static_cast<double>(s3), acc);
+            return static_cast<float>(acc);
+        };
+#pragma unroll
+        for (int j = 0; j < GW; ++j) {
+            const int k0 = 16 * (wave * GW + j) + 4 * q;
+            const float4 s0 = sv[j][0], s1 = sv[j][1], s2 = sv[j][2], s3 = sv[j][3], o = ov[j];
+            const float4 n0 = make_float4(mix(pv.x, r0, o.x, s0.x, s1.x, s2.x, s3.x), mix(pv.x, r0, o.y, s0.y, s1.y, s2.y, s3.y),
+                                          mix(pv.x, r0, o.z, s0.z, s1.z, s2.z, s3.z), mix(pv.x, r0, o.w, s0.w, s1.w, s2.w, s3.w));
+            const float4 n1 = make_float4(mix(pv.y, r1, o.x, s0.x, s1.x, s2.x, s3.x), mix(pv.y, r1, o.y, s0.y, s1.y, s2.y, s3.y),
+                                          mix(pv.y, r1, o.z, s0.z, s1.z, s2.z, s3.z), mix(pv.y, r1, o.w, s0.w, s1.w, s2.w, s3.w));
+            const float4 n2 = make_float4(mix(pv.z, r2, o.x, s0.x, s1.x, s2.x, s3.x), mix(pv.z, r2, o.y, s0.y, s1.y, s2.y, s3.y),
+                                          mix(pv.z, r2, o.z, s0.z, s1.z, s2.z, s3.z), mix(pv.z, r2, o.w, s0.w, s1.w, s2.w, s3.w));
+            const float4 n3 = make_float4(mix(pv.w, r3, o.x, s0.x, s1.x, s2.x, s3.x), mix(pv.w, r3, o.y, s0.y, s1.y, s2.y, s3.y),
+                                          mix(pv.w, r3, o.z, s0.z, s1.z, s2.z, s3.z), mix(pv.w, r3, o.w, s0.w, s1.w, s2.w, s3.w));
+            sv[j][0] = n0;
+            sv[j][1] = n1;
+            sv[j][2] = n2;
+            sv[j][3] = n3;
+        }
+    }
     float4 nw[GW];
 #pragma unroll
     for (int j = 0; j < GW; ++j) nw[j] = *reinterpret_cast<const float4*>(a.norm_w + 16 * (wave * GW + j) + 4 * q);
@@ -201,6 +249,21 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
     const float pp_alpha = e_pre < 4 ? *a.pre_alpha : *a.post_alpha;
     const float pp_bias = e_pre < 4 ? a.pre_bias[e_pre % 4] : a.post_bias[e_pre % 4];
     __syncthreads();  // w_lds filled
+    if constexpr (FUSED) {
+        // The new streams, stored here rather than where they are computed so
+        // that no register of the staging above stays live across the branch.
+        if (valid) {
+#pragma unroll
+            for (int j = 0; j < GW; ++j) {
+                float* dst = a.c_new + token * n * D + 16 * (wave * GW + j) + 4 * q;
+#pragma unroll
+                for (int i = 0; i < n; ++i) {
+                    __builtin_nontemporal_store(nt_f4{sv[j][i].x, sv[j][i].y, sv[j][i].z, sv[j][i].w},
+                                                reinterpret_cast<nt_f4*>(dst + i * D));
+                }
+            }
+        }
+    }
     double sq = 0.0;
     double4_t acc0 = {0.0, 0.0, 0.0, 0.0};
     double4_t acc1 = {0.0, 0.0, 0.0, 0.0};
@@ -644,28 +707,41 @@ mlk_status launch_combine(const float* streams, int64_t tokens, int64_t n, int64
     return launch_status("mhc_combine");
 }
 
-mlk_status launch_prepare(const PrepareArgs& a, int64_t n, int64_t d, hipStream_t stream) {
-    if (a.tokens == 0) return MLK_OK;
+bool prepare_fast(const PrepareArgs& a, int64_t n, int64_t d) {
     auto al16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    const bool fast = n == 4 && (d == 64 || d == 128 || d == 256 || d == 512) && a.sd % 4 == 0 && a.ts % 4 == 0 &&
-                      al16(a.streams) && al16(a.norm_w) && al16(a.agg_norm_w) && al16(a.agg) && al16(a.pre) &&
-                      al16(a.post) && al16(a.res) && al16(a.proj_w);
-    if (fast) {
+    return n == 4 && (d == 64 || d == 128 || d == 256 || d == 512) && a.sd % 4 == 0 && a.ts % 4 == 0 &&
+           al16(a.streams) && al16(a.norm_w) && al16(a.agg_norm_w) && al16(a.agg) && al16(a.pre) && al16(a.post) &&
+           al16(a.res) && al16(a.proj_w);
+}
+
+// The fused combine + prepare kernel: n = 4, d <= 256 (d = 512 has no
+// registers to spare), every operand 16-byte aligned.
+bool prepare_fusable(const PrepareArgs& a, int64_t n, int64_t d) {
+    auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    return prepare_fast(a, n, d) && d <= 256 && al16(a.c_res) && al16(a.c_post) && al16(a.c_out) && al16(a.c_new);
+}
+
+mlk_status launch_prepare(const PrepareArgs& a, int64_t n, int64_t d, hipStream_t stream, bool fused = false) {
+    if (a.tokens == 0) return MLK_OK;
+    if (fused || prepare_fast(a, n, d)) {
         const int64_t blocks = ceil_div(a.tokens, 16);
+#define MLK_PREP(DV)                                                                                              \
+    case DV:                                                                                                      \
+        if (fused) {                                                                                              \
+            hipLaunchKernelGGL((mhc_prepare_n4_kernel<(DV <= 256 ? DV : 256), true>), dim3(blocks), dim3(kBlock), \
+                               0, stream, a);                                                                     \
+        } else {                                                                                                  \
+            hipLaunchKernelGGL((mhc_prepare_n4_kernel<DV, false>), dim3(blocks), dim3(kBlock), 0, stream, a);     \
+        }                                                                                                         \
+        break;
         switch (d) {
-            case 64:
-                hipLaunchKernelGGL(mhc_prepare_n4_kernel<64>, dim3(blocks), dim3(kBlock), 0, stream, a);
-                break;
-            case 128:
-                hipLaunchKernelGGL(mhc_prepare_n4_kernel<128>, dim3(blocks), dim3(kBlock), 0, stream, a);
-                break;
-            case 256:
-                hipLaunchKernelGGL(mhc_prepare_n4_kernel<256>, dim3(blocks), dim3(kBlock), 0, stream, a);
-                break;
-            default:
-                hipLaunchKernelGGL(mhc_prepare_n4_kernel<512>, dim3(blocks), dim3(kBlock), 0, stream, a);
-                break;
+            MLK_PREP(64)
+            MLK_PREP(128)
+            MLK_PREP(256)
+            MLK_PREP(512)
+            default: break;
         }
+#undef MLK_PREP
         return launch_status("mhc_prepare");
     }
     GenericArgs g{a, static_cast<int>(n), d};
@@ -745,6 +821,38 @@ mlk_status mlk_mhc_combine_prepare(const float* streams, int64_t tokens, int64_t
     MLK_CHECK(new_streams != nullptr || tokens == 0, "new_streams must be given");
     mlk_status st = check_prepare(tokens, n, d, proj_w, sinkhorn_iters);
     if (st != MLK_OK) return st;
+    if (tokens == 0) return MLK_OK;
+    // n = 4 and d <= 256: one kernel writes the new streams and prepares the
+    // next residual from them in registers (the new streams are not read back).
+    PrepareArgs a{};
+    a.streams = streams;
+    a.tokens = tokens;
+    a.sd = stream_stride;
+    a.ts = token_stride;
+    a.norm_w = norm_w;
+    a.eps = static_cast<double>(static_cast<float>(eps));
+    a.proj_w = proj_w;
+    a.pre_bias = pre_bias;
+    a.post_bias = post_bias;
+    a.res_bias = res_bias;
+    a.pre_alpha = pre_alpha;
+    a.post_alpha = post_alpha;
+    a.res_alpha = res_alpha;
+    a.iters = static_cast<int>(sinkhorn_iters < (1 << 20) ? sinkhorn_iters : (1 << 20));
+    a.agg_norm_w = agg_norm_w;
+    a.agg_norm_eps = static_cast<double>(static_cast<float>(agg_norm_eps));
+    a.agg = agg_out;
+    a.pre = pre_out;
+    a.post = post_out;
+    a.res = res_out;
+    a.c_res = res;
+    a.c_post = post;
+    a.c_out = out;
+    a.c_new = new_streams;
+    if (prepare_fusable(a, n, d)) {
+        MLK_CHECK(res && post && out, "null tensor pointer");
+        return launch_prepare(a, n, d, stream, true);
+    }
     st = launch_combine(streams, tokens, n, d, stream_stride, token_stride, res, post, out, new_streams, nullptr,
                         stream);
     if (st != MLK_OK) return st;
