@@ -97,6 +97,28 @@ __device__ __forceinline__ float bc_norm_scale_lds(const float* x, int64_t n, fl
     return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
 }
 
+// bc_norm_scale_lds for a compile-time row length N (a multiple of 8), eight
+// elements in flight at a time: the same sequential order of additions.
+template <int N>
+__device__ __forceinline__ float bc_norm_scale_rows(const float* x, float eps) {
+    static_assert(N % 8 == 0, "row length");
+    float ss = 0.0f;
+#pragma unroll 1
+    for (int i = 0; i < N; i += 8) {
+        const float4 u = *reinterpret_cast<const float4*>(x + i);
+        const float4 w = *reinterpret_cast<const float4*>(x + i + 4);
+        ss = ss + u.x * u.x;
+        ss = ss + u.y * u.y;
+        ss = ss + u.z * u.z;
+        ss = ss + u.w * u.w;
+        ss = ss + w.x * w.x;
+        ss = ss + w.y * w.y;
+        ss = ss + w.z * w.z;
+        ss = ss + w.w * w.w;
+    }
+    return 1.0f / sqrtf(ss / static_cast<float>(N) + eps);
+}
+
 struct PrepArgs {
     const float* proj;
     int64_t sb, st;
@@ -773,11 +795,442 @@ __global__ __launch_bounds__(64) void rec_chunk_kernel(RecArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The whole forward in one kernel: in_proj post-processing + chunked scan
+// ---------------------------------------------------------------------------
+//
+// One block of DT waves per (window, head); wave w owns headdim columns
+// [16w, 16w + 16). Per 32-token chunk, straight from the in_proj rows:
+//   a. the head's B and C group rows, its dt/A/trap logits and the angles into
+//      LDS; this wave's v (x) and gate (z) columns into registers, laid out as
+//      the operands below take them (token 16st + 4g + v, column 16w + li);
+//   b. the BCNorm scales (one lane per token and group), (alpha, beta, gamma,
+//      dt) per token, tanh(angle) * pi;
+//   c. q and k (scale, norm weight, bias) in place; the fp64 running angle
+//      sums (one lane per angle, carried across chunks in a register); the
+//      decay weights W, Din, Wp;
+//   d. the rotation of each (2r, 2r + 1) pair of q and k;
+//   e. the G^T = K Q^T tiles, one wave per tile, masked by W into LDS; the
+//      previous chunk's last-token term ck;
+//   f. each wave's output columns, Y = P V + Din Q S_in + ck v_p, skip, gate;
+//   g. each wave's state columns, S_out = Din S_in + Wp k_p v_p^T + K^T (w o V).
+// Steps a-d are prep_kernel's and rotate_kernel's arithmetic per token, and
+// e-g rec_chunk_kernel's products in the same order, so the output equals the
+// prep -> rotate -> rec_chunk_kernel sequence bit for bit; q and k never leave
+// LDS. Blocks are ordered so that the heads of one window run on one XCD and
+// share its L2 copy of the window's B/C rows.
+struct ScanArgs {
+    const float* proj;  // [B, L, W] rows: [z | x | B | C | dt | A | trap | angles]
+    int64_t sb, st;
+    int64_t B, L, G, H, R;
+    const float* b_bias;  // [H, N]
+    const float* c_bias;
+    const float* b_norm_w;  // [N]
+    const float* c_norm_w;
+    float b_eps, c_eps;
+    const float* dt_bias;  // [H]
+    float a_floor;
+    const float* skip;  // [H]
+    const float* gate;  // z columns of proj (gate_logits), or an explicit gate [B, L, H*D]
+    int64_t gsb, gst;
+    int gate_logits;
+    float* out;  // [B, L, H*D] contiguous
+};
+
+// Three waves per SIMD for the four-wave blocks (the register budget the
+// compiler meets without spilling at d_state 64); the others as they fall.
+template <int C, int NT, int DT>
+__global__ __launch_bounds__(64 * DT) __attribute__((amdgpu_waves_per_eu(DT == 4 ? 3 : 1)))
+void scan_fused_kernel(ScanArgs a) {
+    static_assert(C == 32, "the BCNorm step takes one lane per (token, B|C) pair of a 64-lane wave");
+    constexpr int N = 16 * NT, D = 16 * DT, NTH = 64 * DT;
+    constexpr int CT = C / 16;
+    constexpr int NP = N + 4, WP = C + 4;
+    constexpr int NPAIR = CT * (CT + 1) / 2;
+    constexpr int RM = N / 2;  // rotary angles at most
+    static_assert(NTH % N == 0, "a thread keeps one q/k column across the chunk");
+    __shared__ __attribute__((aligned(16))) float q_sh[C * NP];
+    __shared__ __attribute__((aligned(16))) float k_sh[C * NP];
+    __shared__ __attribute__((aligned(16))) float w_s[C * WP];
+    __shared__ f32x4_t p_s[NPAIR * 64];
+    __shared__ float ang_s[C * RM];  // angle logits, then tanh(angle) * pi
+    __shared__ float cum_s[C * RM];  // cumulative angles
+    __shared__ float raw_s[3][C];    // dt, A, trap logits
+    __shared__ __attribute__((aligned(16))) float coef[4][C];  // alpha, beta, gamma, dt
+    __shared__ float sc_s[2][C];     // B and C norm scales
+    __shared__ float ck_s[C];
+    __shared__ float kp_s[2][N];
+    __shared__ float nrm_s[4][N];    // B norm weight, C norm weight, this head's B bias, C bias
+    // Din(t) and Wp(t) live in the padding columns C and C + 1 of the W rows.
+    constexpr int kDin = C, kWp = C + 1;
+
+    const int64_t H = a.H, L = a.L, G = a.G;
+    const int R = static_cast<int>(a.R);
+    // Block -> (window, head) in 32-bit arithmetic (B * H < 2^31, checked at launch).
+    const unsigned Hu = static_cast<unsigned>(a.H), nblk = static_cast<unsigned>(a.B * a.H);
+    unsigned lin = blockIdx.x;
+    if (nblk % 8 == 0) lin = (lin % 8) * (nblk / 8) + lin / 8;
+    const int64_t b = lin / Hu, h = lin % Hu;
+    const int64_t d_inner = H * D, GN = G * N;
+    const float* base = a.proj + b * a.sb;
+    const float* brow = base + 2 * d_inner + static_cast<int64_t>(static_cast<unsigned>(h) / (Hu / static_cast<unsigned>(a.G))) * N;
+    const float* crow = brow + GN;
+    const float* mrow = base + 2 * d_inner + 2 * GN + h;  // dt; A at +H, trap at +2H
+    const float* arow = base + 2 * d_inner + 2 * GN + 3 * H;
+    const float* xrow = base + d_inner + h * D;
+    const float* zrow = a.gate + b * a.gsb + h * D;
+    float* orow = a.out + b * L * d_inner + h * D;
+    const float skip = a.skip[h], dt_bias = a.dt_bias[h];
+
+    for (int i = threadIdx.x; i < N; i += NTH) {
+        nrm_s[0][i] = a.b_norm_w[i];
+        nrm_s[1][i] = a.c_norm_w[i];
+        nrm_s[2][i] = a.b_bias[h * N + i];
+        nrm_s[3][i] = a.c_bias[h * N + i];
+    }
+    // (token, angle) work items i < C * R map to t = i / R by a multiply-shift,
+    // exact for i < 2^10 and R <= 32.
+    const unsigned rmagic = R > 0 ? (65536u + static_cast<unsigned>(R) - 1u) / static_cast<unsigned>(R) : 0u;
+
+    f32x4_t S[NT];  // S[16nt + 4g + v][col]
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) S[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float vp = 0.0f;        // v of the previous chunk's last token, this lane's column
+    double running = 0.0;   // lane r < R: the running angle sum
+    float vx[CT][4], zx[CT][4];
+
+    for (int64_t c0 = 0; c0 < L; c0 += C) {
+        // The thread index is made opaque per chunk so that the per-lane index
+        // arithmetic of the phases below is recomputed here (a few integer
+        // operations) rather than hoisted out of the loop and held in VGPRs.
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        const int lane = tid & 63, g = lane >> 4, li = lane & 15;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int col = 16 * wave + li, n_own = tid % N;
+        const int Lc = static_cast<int>(L - c0 < C ? L - c0 : C);
+        const bool first = c0 == 0, last = c0 + C >= L;
+        const int par = static_cast<int>((c0 / C) & 1);
+        // a. Every global load of the chunk issued before the first wait
+        //    (tokens past the end read the last token; they carry no weight).
+        //    Offsets are 32-bit from the chunk's first row (checked at launch).
+        {
+            constexpr int BU = C * N / NTH;
+            constexpr int MU = (3 * C + NTH - 1) / NTH;
+            constexpr int AU = (C * RM + NTH - 1) / NTH;
+            const int st32 = static_cast<int>(a.st), gst32 = static_cast<int>(a.gst);
+            const float* bc = brow + c0 * a.st;
+            const float* cc = crow + c0 * a.st;
+            const float* mc = mrow + c0 * a.st;
+            const float* ac = arow + c0 * a.st;
+            const float* xc = xrow + c0 * a.st;
+            const float* zc = zrow + c0 * a.gst;
+            float bx[BU], cx[BU], mx[MU], ax[AU];
+#pragma unroll
+            for (int j = 0; j < BU; ++j) {
+                const int t = (tid + NTH * j) / N;
+                const unsigned off = static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + n_own);
+                bx[j] = bc[off];
+                cx[j] = cc[off];
+            }
+#pragma unroll
+            for (int j = 0; j < MU; ++j) {
+                const int u = tid + NTH * j;
+                const int which = u < 3 * C ? u / C : 0, t = u % C;
+                mx[j] = mc[static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + which * static_cast<int>(H))];
+            }
+            if (R > 0) {
+#pragma unroll
+                for (int j = 0; j < AU; ++j) {
+                    const unsigned u = static_cast<unsigned>(tid + NTH * j);
+                    const unsigned uc = u < static_cast<unsigned>(C * R) ? u : static_cast<unsigned>(C * R - 1);
+                    const int t = static_cast<int>((uc * rmagic) >> 16), r = static_cast<int>(uc) - t * R;
+                    ax[j] = ac[static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + r)];
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < CT; ++st)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int t = 16 * st + 4 * g + v;
+                    const int tc = t < Lc ? t : Lc - 1;
+                    vx[st][v] = xc[static_cast<unsigned>(tc * st32 + col)];
+                    zx[st][v] = zc[static_cast<unsigned>(tc * gst32 + col)];
+                }
+#pragma unroll
+            for (int j = 0; j < BU; ++j) {
+                const int t = (tid + NTH * j) / N;
+                k_sh[t * NP + n_own] = bx[j];
+                q_sh[t * NP + n_own] = cx[j];
+            }
+#pragma unroll
+            for (int j = 0; j < MU; ++j) {
+                const int u = tid + NTH * j;
+                if (u < 3 * C) raw_s[u / C][u % C] = mx[j];
+            }
+            if (R > 0) {
+#pragma unroll
+                for (int j = 0; j < AU; ++j) {
+                    const unsigned u = static_cast<unsigned>(tid + NTH * j);
+                    const int t = static_cast<int>((u * rmagic) >> 16), r = static_cast<int>(u) - t * R;
+                    if (u < static_cast<unsigned>(C * R)) ang_s[t * RM + r] = ax[j];
+                }
+            }
+        }
+        __syncthreads();
+        // b. Norm scales, coefficients, tanh(angle) * pi.
+        if (tid < 2 * C) {
+            const int t = tid % C;
+            const bool isb = tid < C;
+            sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? k_sh : q_sh) + t * NP, isb ? a.b_eps : a.c_eps);
+        }
+        {
+            const int ct = NTH >= 128 ? tid - 64 : tid;
+            if (ct >= 0 && ct < C) {
+                const float dt = softplus_f(raw_s[0][ct] + dt_bias);
+                const float am = -fmaxf(heavy_tail_f(raw_s[1][ct]), a.a_floor);
+                float al, be, ga;
+                step_coefficients(am * dt, dt, raw_s[2][ct], &al, &be, &ga);
+                const bool valid = ct < Lc;
+                coef[0][ct] = valid ? al : 0.0f;
+                coef[1][ct] = valid ? be : 0.0f;
+                coef[2][ct] = valid ? ga : 0.0f;
+                coef[3][ct] = dt;
+            }
+        }
+#pragma unroll 1
+        for (int i = tid; i < C * R; i += NTH) {
+            const int t = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - t * R;
+            ang_s[t * RM + r] = tanhf_cr(ang_s[t * RM + r]) * kPiF;
+        }
+        __syncthreads();
+        // c. q and k (all values read before any is written back); the
+        //    running angle sums into cum_s; the decay weights.
+        {
+            constexpr int QU = C * N / NTH;
+            float kv[QU], qv[QU], skb[QU], sqb[QU];
+#pragma unroll
+            for (int j = 0; j < QU; ++j) {
+                const int t = (tid + NTH * j) / N, i = t * NP + n_own;
+                kv[j] = k_sh[i];
+                qv[j] = q_sh[i];
+                skb[j] = sc_s[0][t];
+                sqb[j] = sc_s[1][t];
+            }
+            const float bw = nrm_s[0][n_own], cw = nrm_s[1][n_own], bb = nrm_s[2][n_own], cb = nrm_s[3][n_own];
+#pragma unroll
+            for (int j = 0; j < QU; ++j) {
+                const int t = (tid + NTH * j) / N, i = t * NP + n_own;
+                k_sh[i] = (kv[j] * skb[j]) * bw + bb;
+                q_sh[i] = (qv[j] * sqb[j]) * cw + cb;
+            }
+        }
+        if (tid < R) {
+#pragma unroll
+            for (int t0 = 0; t0 < C; t0 += 16) {
+                float term[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) term[i] = ang_s[(t0 + i) * RM + tid] * coef[3][t0 + i];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    running += static_cast<double>(term[i]);
+                    cum_s[(t0 + i) * RM + tid] = static_cast<float>(running);
+                }
+            }
+        }
+        {
+            // Lane s < C of the weight wave walks t forward; lanes C and C + 1
+            // run lane 0's product chain and write Din and Wp. The conditions
+            // are selects; the alpha values of the next 8 tokens are read
+            // while the current 8 are processed.
+            const int wl = NTH >= 128 ? tid - 64 : tid;
+            if (wl >= 0 && wl < C + 2) {
+                const int s = wl < C ? wl : 0;
+                const double gam = coef[2][s];
+                const double bet = s + 1 < C ? static_cast<double>(coef[1][s + 1]) : 0.0;
+                const double a0 = coef[0][0], b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
+                float* dst = w_s + (wl < C ? wl : (wl == C ? kDin : kWp));
+                const bool wlane = wl < C;
+                const double scale = wl == C ? a0 : b0;
+                const float4* a4p = reinterpret_cast<const float4*>(&coef[0][0]);
+                float4 n0 = a4p[0], n1 = a4p[1];
+                double dd = 1.0, e = 1.0;
+#pragma unroll 1
+                for (int t0 = 0; t0 < C; t0 += 8) {
+                    const float al[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+                    if (t0 + 8 < C) {
+                        n0 = a4p[(t0 + 8) / 4];
+                        n1 = a4p[(t0 + 8) / 4 + 1];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int t = t0 + i;
+                        const double at = al[i];
+                        dd = t > s ? dd * at : dd;
+                        e = t > s + 1 ? e * at : e;
+                        const double val = t > s ? fma(bet, e, gam * dd) : gam * dd;
+                        dst[t * WP] = wlane ? (t >= s ? static_cast<float>(val) : 0.0f) : static_cast<float>(scale * dd);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // d. Rotation of the (2r, 2r + 1) pairs.
+#pragma unroll 1
+        for (int i = tid; i < C * R; i += NTH) {
+            const int t = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - t * R;
+            {
+                const float cumulative = cum_s[t * RM + r];
+                const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
+                double sd, cd;
+                sincos_d(static_cast<double>(cumulative - wraps), &sd, &cd);
+                const float sine = static_cast<float>(sd), cosine = static_cast<float>(cd);
+                float* qp = q_sh + t * NP + 2 * r;
+                float* kq = k_sh + t * NP + 2 * r;
+                const float ql = qp[0], qr = qp[1], kl = kq[0], kr = kq[1];
+                qp[0] = fmaf(ql, cosine, -(qr * sine));
+                qp[1] = fmaf(ql, sine, qr * cosine);
+                kq[0] = fmaf(kl, cosine, -(kr * sine));
+                kq[1] = fmaf(kl, sine, kr * cosine);
+            }
+        }
+        __syncthreads();
+        // e. Masked G^T tiles into LDS (tile pair p on wave p % DT); ck; k_p.
+        {
+            int p = 0;
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt) {
+#pragma unroll
+                for (int st = 0; st <= tt; ++st, ++p) {
+                    if (p % DT != wave || 16 * tt >= Lc) continue;
+                    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const float4 k4 = *reinterpret_cast<const float4*>(k_sh + (16 * st + li) * NP + 16 * nt + 4 * g);
+                        const float4 q4 = *reinterpret_cast<const float4*>(q_sh + (16 * tt + li) * NP + 16 * nt + 4 * g);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, q4.x, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, q4.y, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, q4.z, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, q4.w, acc, 0, 0, 0);
+                    }
+                    const float4 w4 = *reinterpret_cast<const float4*>(w_s + (16 * tt + li) * WP + 16 * st + 4 * g);
+                    p_s[p * 64 + lane] = f32x4_t{w4.x * acc[0], w4.y * acc[1], w4.z * acc[2], w4.w * acc[3]};
+                }
+            }
+        }
+        if (wave == DT - 1 && lane < C) {
+            float dot = 0.0f;
+            if (!first) {
+#pragma unroll
+                for (int n = 0; n < N; ++n) dot = fmaf(q_sh[lane * NP + n], kp_s[par][n], dot);
+            }
+            ck_s[lane] = dot * w_s[lane * WP + kWp];
+        }
+        if (tid < N) kp_s[par ^ 1][tid] = k_sh[(C - 1) * NP + tid];
+        __syncthreads();
+        // f. This wave's output columns.
+        {
+            int p0 = 0;  // index of pair (tt, 0)
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt) {
+                const int t0 = 16 * tt;
+                if (t0 < Lc) {
+                    f32x4_t Y = f32x4_t{0.f, 0.f, 0.f, 0.f}, Yi = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int st = 0; st <= tt; ++st) {
+                        const f32x4_t P = p_s[(p0 + st) * 64 + lane];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(P[v], vx[st][v], Y, 0, 0, 0);
+                    }
+                    if (!first) {
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt) {
+                            const float4 q4 = *reinterpret_cast<const float4*>(q_sh + (t0 + li) * NP + 16 * nt + 4 * g);
+                            const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) Yi = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[v], S[nt][v], Yi, 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int t = t0 + 4 * g + v;
+                        if (t >= Lc) continue;
+                        float y = Y[v];
+                        if (!first) y = fmaf(ck_s[t], vp, fmaf(w_s[t * WP + kDin], Yi[v], y));
+                        y = fmaf(skip, vx[tt][v], y);
+                        const float gt = zx[tt][v];
+                        float o;
+                        if (a.gate_logits) {
+                            const double z = static_cast<double>(gt);
+                            o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
+                        } else {
+                            o = y * gt;
+                        }
+                        orow[(c0 + t) * d_inner + col] = o;
+                    }
+                }
+                p0 += tt + 1;
+            }
+        }
+        if (last) break;
+        // g. This wave's state columns after the chunk (all C tokens valid).
+        {
+            const float dl = w_s[(C - 1) * WP + kDin], wl = w_s[(C - 1) * WP + kWp];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float x = S[nt][v] * dl;
+                    if (!first) x = fmaf(wl * kp_s[par][16 * nt + 4 * g + v], vp, x);
+                    S[nt][v] = x;
+                }
+#pragma unroll
+            for (int st = 0; st < CT; ++st) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int srow = 16 * st + 4 * g + v;
+                    const float bv = w_s[(C - 1) * WP + srow] * vx[st][v];
+                    float kA[NT];
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) kA[nt] = k_sh[srow * NP + 16 * nt + li];
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) S[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kA[nt], bv, S[nt], 0, 0, 0);
+                }
+            }
+            vp = __shfl(vx[CT - 1][3], 48 + li, 64);
+        }
+        __syncthreads();
+    }
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
-bool chunked_scan_enabled() {
+// MLK_MAMBA3_SCAN selects the forward's scan: unset (or "fused") the fused
+// kernel where the geometry allows it; "unfused" prep -> rotate -> recurrence
+// kernel (chunked or time-sequential by the rule in launch_rec); "sequential"
+// prep -> rotate -> the time-sequential kernel, the reference's association.
+enum class ScanMode { kFused, kUnfused, kSequential };
+
+ScanMode scan_mode() {
     const char* mode = std::getenv("MLK_MAMBA3_SCAN");
-    return mode == nullptr || std::strcmp(mode, "sequential") != 0;
+    if (mode == nullptr) return ScanMode::kFused;
+    if (std::strcmp(mode, "sequential") == 0) return ScanMode::kSequential;
+    if (std::strcmp(mode, "unfused") == 0) return ScanMode::kUnfused;
+    return ScanMode::kFused;
+}
+
+bool launch_scan_fused(const ScanArgs& s, int64_t N, int64_t D, hipStream_t stream) {
+    const int NT = static_cast<int>(N / 16), DT = static_cast<int>(D / 16);
+    const dim3 grid(static_cast<unsigned>(s.B * s.H));
+#define MLK_FUSED(NTV, DTV)                                                                                  \
+    if (NT == NTV && DT == DTV) {                                                                            \
+        hipLaunchKernelGGL((scan_fused_kernel<32, NTV, DTV>), grid, dim3(64 * DTV), 0, stream, s);          \
+        return true;                                                                                         \
+    }
+    MLK_FUSED(1, 1) MLK_FUSED(1, 2) MLK_FUSED(1, 4) MLK_FUSED(2, 1) MLK_FUSED(2, 2) MLK_FUSED(2, 4)
+    MLK_FUSED(4, 1) MLK_FUSED(4, 2) MLK_FUSED(4, 4)
+#undef MLK_FUSED
+    return false;
 }
 
 template <int C>
@@ -804,7 +1257,7 @@ mlk_status launch_rec(const RecArgs& a, hipStream_t stream) {
     // ms at 1024 x 256 tokens, 8 heads). d_state in {16, 32, 64}, headdim in
     // {32, 64}, 16-byte aligned q/k rows; MLK_MAMBA3_SCAN=sequential forces
     // the reference's own association.
-    if (chunked_scan_enabled() && a.B * a.H <= 2048 && (a.N == 16 || a.N == 32 || a.N == 64) &&
+    if (scan_mode() != ScanMode::kSequential && a.B * a.H <= 2048 && (a.N == 16 || a.N == 32 || a.N == 64) &&
         (a.D == 32 || a.D == 64) &&
         a.qs.t % 4 == 0 && a.qs.b % 4 == 0 && a.qs.h % 4 == 0 && a.ks.t % 4 == 0 && a.ks.b % 4 == 0 &&
         a.ks.h % 4 == 0 && aligned16(a.q) && aligned16(a.k)) {
@@ -1098,6 +1551,40 @@ mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_
     if (blh == 0) return MLK_OK;
     MLK_CHECK(projected && b_bias && c_bias && b_norm_w && c_norm_w && dt_bias && skip && out && workspace,
               "null tensor pointer");
+    if (scan_mode() == ScanMode::kFused && (d_state == 16 || d_state == 32 || d_state == 64) &&
+        (headdim == 16 || headdim == 32 || headdim == 64) && batch * nheads < (int64_t{1} << 31)) {
+        ScanArgs s{};
+        s.proj = projected;
+        s.sb = proj_batch_stride;
+        s.st = proj_token_stride;
+        s.B = batch;
+        s.L = length;
+        s.G = ngroups;
+        s.H = nheads;
+        s.R = num_rope_angles;
+        s.b_bias = b_bias;
+        s.c_bias = c_bias;
+        s.b_norm_w = b_norm_w;
+        s.c_norm_w = c_norm_w;
+        s.b_eps = static_cast<float>(b_eps);
+        s.c_eps = static_cast<float>(c_eps);
+        s.dt_bias = dt_bias;
+        s.a_floor = static_cast<float>(a_floor);
+        s.skip = skip;
+        if (gate == nullptr) {
+            s.gate = projected;
+            s.gsb = proj_batch_stride;
+            s.gst = proj_token_stride;
+            s.gate_logits = 1;
+        } else {
+            s.gate = gate;
+            s.gsb = gate_batch_stride;
+            s.gst = gate_token_stride;
+            s.gate_logits = 0;
+        }
+        s.out = out;
+        if (launch_scan_fused(s, d_state, headdim, stream)) return launch_status("mamba3 fused scan");
+    }
     const int64_t rw = num_rope_angles > 0 ? num_rope_angles : 1;
     float* q = static_cast<float*>(workspace);
     float* k = q + blh * d_state;

@@ -3,8 +3,10 @@ post-processing + recurrence, and the one-token step with carried state.
 
 Against the golden vectors of the compiled reference and the CPU oracle on
 the same seeded inputs; gate: normwise relative error <= 1e-5 (fp32). The
-chunked scan on the matrix cores (the default for d_state 16/32/64 and
-headdim 32/64) is checked against the time-sequential kernel and the oracle.
+forward's one-kernel chunked scan (the default for d_state 16/32/64 and
+headdim 16/32/64) equals the unfused prep -> rotate -> chunked-recurrence
+kernels bit for bit, and is checked against the time-sequential kernel and
+the oracle at 1e-6; so is the recurrent op's chunked scan.
 The step is checked against the time-sequential sequence kernel (stepping T
 tokens from a zero state equals the forward over T tokens, bit for bit) and
 against the oracle's step at the streaming-decode geometry (d_model 128,
@@ -165,6 +167,72 @@ def test_chunked_scan_vs_sequential(dev, oracle, monkeypatch, B, L, N, H, D):
     expect = oracle.mamba3_siso_forward(proj, N, 1, H, D, R, p["b_bias"], p["c_bias"], p["b_norm_w"], p["c_norm_w"],
                                         1e-5, 1e-5, p["dt_bias"], p["skip"], 1e-4)
     assert_close(chunked, expect, tol=1e-6, name="chunked vs oracle")
+
+
+@pytest.mark.parametrize("B,L,N,G,H,D", [(2, 200, 64, 1, 2, 64), (3, 64, 32, 1, 2, 32), (64, 32, 16, 1, 4, 32),
+                                         (2, 70, 16, 1, 3, 64), (4, 31, 64, 2, 2, 32), (8, 33, 32, 2, 4, 64)])
+def test_fused_scan_equals_unfused_chunked(dev, monkeypatch, B, L, N, G, H, D):
+    """The one-kernel forward (in_proj post-processing and chunked scan, q/k kept in LDS) equals the
+    prep -> rotate -> chunked-recurrence kernels bit for bit: the same arithmetic per token, the same
+    matrix-core products in the same order."""
+    from montlok import _C
+
+    rng = np.random.default_rng(B + L + N + D)
+    R = N // 4 + 1
+    proj, p = _random_layer(rng, B, L, N, G, H, D, R)
+    plist = [_t(p[k], dev) for k in ("b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")]
+    tp = _t(proj, dev)
+    fused = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "unfused")
+    unfused = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    assert_bitwise(fused, unfused.cpu().numpy(), "fused vs unfused chunked scan")
+    z = tp[..., :H * D].double()
+    gate = (z * torch.sigmoid(z)).float()
+    monkeypatch.delenv("MLK_MAMBA3_SCAN")
+    fused_g = _C.mamba3_siso_forward(tp, gate, *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "unfused")
+    unfused_g = _C.mamba3_siso_forward(tp, gate, *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    assert_bitwise(fused_g, unfused_g.cpu().numpy(), "fused vs unfused, explicit gate")
+
+
+@pytest.mark.parametrize("B,L,N,G,H,D,R", [(5, 40, 16, 1, 4, 16, 4), (3, 77, 64, 2, 4, 16, 32), (2, 33, 32, 1, 3, 16, 0)])
+def test_fused_scan_headdim16_vs_sequential(dev, oracle, monkeypatch, B, L, N, G, H, D, R):
+    """headdim 16 (one wave per head, no unfused chunked counterpart), with grouped B/C, every angle
+    slot used, and no rotary angles: against the time-sequential kernel and the oracle, 1e-6 normwise."""
+    from montlok import _C
+
+    rng = np.random.default_rng(B * L + N)
+    proj, p = _random_layer(rng, B, L, N, G, H, D, R)
+    plist = [_t(p[k], dev) for k in ("b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")]
+    tp = _t(proj, dev)
+    fused = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "sequential")
+    seq = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    assert_close(fused, seq, tol=1e-6, name="fused vs sequential")
+    expect = oracle.mamba3_siso_forward(proj, N, G, H, D, R, p["b_bias"], p["c_bias"], p["b_norm_w"], p["c_norm_w"],
+                                        1e-5, 1e-5, p["dt_bias"], p["skip"], 1e-4)
+    assert_close(fused, expect, tol=1e-6, name="fused vs oracle")
+
+
+@pytest.mark.parametrize("B,L,H,N,D", [(3, 70, 4, 64, 64), (16, 32, 2, 16, 32)])
+def test_recurrent_chunked_vs_sequential(dev, oracle, monkeypatch, B, L, H, N, D):
+    """mamba3_siso_recurrent on contiguous q/k takes the chunked scan (few window x head pairs);
+    against the time-sequential kernel and the oracle, 1e-6 normwise."""
+    from montlok import _C
+
+    rng = np.random.default_rng(B * L + H)
+    f = lambda *s: _t(rng.standard_normal(s).astype(np.float32), dev)  # noqa: E731
+    q, k, v, gate = f(B, L, H, N) * 0.3, f(B, L, H, N) * 0.3, f(B, L, H, D), f(B, L, H, D)
+    dt = torch.nn.functional.softplus(f(B, L, H) - 2)
+    adt, trap, skip = -dt * 0.7, f(B, L, H), f(H)
+    chunked = _C.mamba3_siso_recurrent(q, k, v, gate, adt, dt, trap, skip)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "sequential")
+    seq = _C.mamba3_siso_recurrent(q, k, v, gate, adt, dt, trap, skip)
+    assert_close(chunked, seq, tol=1e-6, name="recurrent chunked vs sequential")
+    al, be, ga = oracle.step_coefficients(adt.cpu().numpy(), dt.cpu().numpy(), trap.cpu().numpy())
+    expect = oracle.siso(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), gate.cpu().numpy(), al, be, ga,
+                         skip.cpu().numpy())
+    assert_close(chunked, expect, tol=1e-6, name="recurrent chunked vs oracle")
 
 
 def test_step_decode_geometry_vs_oracle(dev, oracle):
