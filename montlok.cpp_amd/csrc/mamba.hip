@@ -1039,19 +1039,18 @@ void scan_fused_kernel(ScanArgs a) {
             }
         }
         {
-            // Lane s < C of the weight wave walks t forward; lanes C and C + 1
-            // run lane 0's product chain and write Din and Wp. The conditions
-            // are selects; the alpha values of the next 8 tokens are read
-            // while the current 8 are processed.
+            // Lane s < C of the weight wave walks t forward. Lanes C and C + 1
+            // write Din(t) = a_0 prod_{0<r<=t} a_r and Wp(t) = b_0 prod_{0<r<=t} a_r
+            // as the weights of a column s = 0 with gamma = a_0 (b_0) and no
+            // beta term, so every lane runs the same selects. The alpha
+            // values of the next 8 tokens are read while 8 are processed.
             const int wl = NTH >= 128 ? tid - 64 : tid;
             if (wl >= 0 && wl < C + 2) {
                 const int s = wl < C ? wl : 0;
-                const double gam = coef[2][s];
-                const double bet = s + 1 < C ? static_cast<double>(coef[1][s + 1]) : 0.0;
-                const double a0 = coef[0][0], b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
+                const double b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
+                const double gam = wl < C ? static_cast<double>(coef[2][s]) : (wl == C ? static_cast<double>(coef[0][0]) : b0);
+                const double bet = wl + 1 < C ? static_cast<double>(coef[1][wl + 1]) : 0.0;
                 float* dst = w_s + (wl < C ? wl : (wl == C ? kDin : kWp));
-                const bool wlane = wl < C;
-                const double scale = wl == C ? a0 : b0;
                 const float4* a4p = reinterpret_cast<const float4*>(&coef[0][0]);
                 float4 n0 = a4p[0], n1 = a4p[1];
                 double dd = 1.0, e = 1.0;
@@ -1069,7 +1068,7 @@ void scan_fused_kernel(ScanArgs a) {
                         dd = t > s ? dd * at : dd;
                         e = t > s + 1 ? e * at : e;
                         const double val = t > s ? fma(bet, e, gam * dd) : gam * dd;
-                        dst[t * WP] = wlane ? (t >= s ? static_cast<float>(val) : 0.0f) : static_cast<float>(scale * dd);
+                        dst[t * WP] = t >= s ? static_cast<float>(val) : 0.0f;
                     }
                 }
             }
@@ -1128,8 +1127,18 @@ void scan_fused_kernel(ScanArgs a) {
         }
         if (tid < N) kp_s[par ^ 1][tid] = k_sh[(C - 1) * NP + tid];
         __syncthreads();
-        // f. This wave's output columns.
+        // f. This wave's output columns. The gate factors depend on z only and
+        //    are formed first, branch-free, so that their fp64 work can issue
+        //    while the matrix cores run the products below.
         {
+            double gz[CT][4];
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const double z = static_cast<double>(zx[tt][v]);
+                    gz[tt][v] = a.gate_logits ? z / (1.0 + exp_d(-z)) : z;
+                }
             int p0 = 0;  // index of pair (tt, 0)
 #pragma unroll
             for (int tt = 0; tt < CT; ++tt) {
@@ -1154,19 +1163,12 @@ void scan_fused_kernel(ScanArgs a) {
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int t = t0 + 4 * g + v;
-                        if (t >= Lc) continue;
                         float y = Y[v];
                         if (!first) y = fmaf(ck_s[t], vp, fmaf(w_s[t * WP + kDin], Yi[v], y));
                         y = fmaf(skip, vx[tt][v], y);
-                        const float gt = zx[tt][v];
-                        float o;
-                        if (a.gate_logits) {
-                            const double z = static_cast<double>(gt);
-                            o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
-                        } else {
-                            o = y * gt;
-                        }
-                        orow[(c0 + t) * d_inner + col] = o;
+                        const float o = a.gate_logits ? static_cast<float>(static_cast<double>(y) * gz[tt][v])
+                                                      : y * zx[tt][v];
+                        if (t < Lc) orow[(c0 + t) * d_inner + col] = o;
                     }
                 }
                 p0 += tt + 1;
