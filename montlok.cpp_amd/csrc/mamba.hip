@@ -35,6 +35,7 @@
 //                   few (window, head) pairs; see the comment above it.
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "mlk_common.h"
 
@@ -883,6 +884,7 @@ void scan_fused_kernel(ScanArgs a) {
     const float skip = a.skip[h], dt_bias = a.dt_bias[h];
 
     for (int i = threadIdx.x; i < N; i += NTH) {
+        kp_s[0][i] = 0.0f;  // k_p before the first chunk
         nrm_s[0][i] = a.b_norm_w[i];
         nrm_s[1][i] = a.c_norm_w[i];
         nrm_s[2][i] = a.b_bias[h * N + i];
@@ -899,7 +901,15 @@ void scan_fused_kernel(ScanArgs a) {
     double running = 0.0;   // lane r < R: the running angle sum
     float vx[CT][4], zx[CT][4];
 
-    for (int64_t c0 = 0; c0 < L; c0 += C) {
+    // One chunk; `last` is compile-time, so a full chunk runs without the edge
+    // conditions (no partial tiles) and its products and gate arithmetic form
+    // long straight-line blocks the scheduler can interleave. The first chunk
+    // runs the same code: its carried state, k_p and v_p are zero, so the terms
+    // they enter are exact zeros, and a select keeps its outputs those of a
+    // scan with no carried state.
+    auto chunk = [&](auto last_c, int64_t c0) {
+        constexpr bool last = decltype(last_c)::value;
+        const bool first = c0 == 0;
         // The thread index is made opaque per chunk so that the per-lane index
         // arithmetic of the phases below is recomputed here (a few integer
         // operations) rather than hoisted out of the loop and held in VGPRs.
@@ -908,8 +918,7 @@ void scan_fused_kernel(ScanArgs a) {
         const int lane = tid & 63, g = lane >> 4, li = lane & 15;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int col = 16 * wave + li, n_own = tid % N;
-        const int Lc = static_cast<int>(L - c0 < C ? L - c0 : C);
-        const bool first = c0 == 0, last = c0 + C >= L;
+        const int Lc = last ? static_cast<int>(L - c0) : C;
         const int par = static_cast<int>((c0 / C) & 1);
         // a. Every global load of the chunk issued before the first wait
         //    (tokens past the end read the last token; they carry no weight).
@@ -984,6 +993,14 @@ void scan_fused_kernel(ScanArgs a) {
             const bool isb = tid < C;
             sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? k_sh : q_sh) + t * NP, isb ? a.b_eps : a.c_eps);
         }
+        // The coefficient wave (wave 1, or wave 0 when the block has one wave)
+        // goes on to the decay weights. Lane s < C walks t = s + 1, s + 2, ...
+        // (lanes drop out past the chunk end), carrying the products
+        // prod_{s<r<=t} alpha_r and prod_{s+1<r<=t} alpha_r in fp64; its alpha
+        // values are read 8 steps ahead. W[t][s] for t < s is never read (the
+        // G tiles mask it). Lanes C and C + 1 write Din(t) = a_0 prod_{0<r<=t}
+        // a_r and Wp(t) = b_0 prod_{0<r<=t} a_r as the weights of a column s = 0
+        // with gamma = a_0 (b_0) and no beta term. tanh runs on the other waves.
         {
             const int ct = NTH >= 128 ? tid - 64 : tid;
             if (ct >= 0 && ct < C) {
@@ -997,11 +1014,60 @@ void scan_fused_kernel(ScanArgs a) {
                 coef[2][ct] = valid ? ga : 0.0f;
                 coef[3][ct] = dt;
             }
-        }
+            if (ct >= 0 && ct < 64) {
+                // The coefficients above were written by other lanes of this wave.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            const int wl = ct;
+            if (wl >= 0 && wl < C + 2) {
+                const int s = wl < C ? wl : 0;
+                const double b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
+                const double gam = wl < C ? static_cast<double>(coef[2][s]) : (wl == C ? static_cast<double>(coef[0][0]) : b0);
+                const double bet = wl + 1 < C ? static_cast<double>(coef[1][wl + 1]) : 0.0;
+                float* dst = w_s + (wl < C ? wl : (wl == C ? kDin : kWp));
+                dst[s * WP] = static_cast<float>(gam * 1.0);  // t = s
+                // Steps k = 0 .. C - 2 handle t = s + 1 + k; alpha of t is read
+                // from a clamped slot (the steps past the end are not stored).
+                float nx[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + i, C - 1)];
+                double dd = 1.0, e = 1.0;
 #pragma unroll 1
-        for (int i = tid; i < C * R; i += NTH) {
-            const int t = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - t * R;
-            ang_s[t * RM + r] = tanhf_cr(ang_s[t * RM + r]) * kPiF;
+                for (int k0 = 0; k0 < C - 1; k0 += 8) {
+                    float al[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) al[i] = nx[i];
+                    if (k0 + 8 < C - 1) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + k0 + 8 + i, C - 1)];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int k = k0 + i, t = s + 1 + k;
+                        if (k < C - 1) {
+                            const double at = al[i];
+                            dd *= at;
+                            if (k > 0) e *= at;
+                            if (t < C) dst[t * WP] = static_cast<float>(fma(bet, e, gam * dd));
+                        }
+                    }
+                }
+            }
+        }
+        {
+            // tanh(angle) * pi on the waves other than the coefficient wave.
+            const int tl = NTH >= 128 ? (tid < 64 ? tid : tid - 64) : tid;
+            const bool tw = NTH < 128 || tid < 64 || tid >= 128;
+            constexpr int TN = NTH >= 128 ? NTH - 64 : NTH;
+            if (tw) {
+#pragma unroll 1
+                for (int i = tl; i < C * R; i += TN) {
+                    const int t = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - t * R;
+                    ang_s[t * RM + r] = tanhf_cr(ang_s[t * RM + r]) * kPiF;
+                }
+            }
         }
         __syncthreads();
         // c. q and k (all values read before any is written back); the
@@ -1035,41 +1101,6 @@ void scan_fused_kernel(ScanArgs a) {
                 for (int i = 0; i < 16; ++i) {
                     running += static_cast<double>(term[i]);
                     cum_s[(t0 + i) * RM + tid] = static_cast<float>(running);
-                }
-            }
-        }
-        {
-            // Lane s < C of the weight wave walks t forward. Lanes C and C + 1
-            // write Din(t) = a_0 prod_{0<r<=t} a_r and Wp(t) = b_0 prod_{0<r<=t} a_r
-            // as the weights of a column s = 0 with gamma = a_0 (b_0) and no
-            // beta term, so every lane runs the same selects. The alpha
-            // values of the next 8 tokens are read while 8 are processed.
-            const int wl = NTH >= 128 ? tid - 64 : tid;
-            if (wl >= 0 && wl < C + 2) {
-                const int s = wl < C ? wl : 0;
-                const double b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
-                const double gam = wl < C ? static_cast<double>(coef[2][s]) : (wl == C ? static_cast<double>(coef[0][0]) : b0);
-                const double bet = wl + 1 < C ? static_cast<double>(coef[1][wl + 1]) : 0.0;
-                float* dst = w_s + (wl < C ? wl : (wl == C ? kDin : kWp));
-                const float4* a4p = reinterpret_cast<const float4*>(&coef[0][0]);
-                float4 n0 = a4p[0], n1 = a4p[1];
-                double dd = 1.0, e = 1.0;
-#pragma unroll 1
-                for (int t0 = 0; t0 < C; t0 += 8) {
-                    const float al[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
-                    if (t0 + 8 < C) {
-                        n0 = a4p[(t0 + 8) / 4];
-                        n1 = a4p[(t0 + 8) / 4 + 1];
-                    }
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int t = t0 + i;
-                        const double at = al[i];
-                        dd = t > s ? dd * at : dd;
-                        e = t > s + 1 ? e * at : e;
-                        const double val = t > s ? fma(bet, e, gam * dd) : gam * dd;
-                        dst[t * WP] = t >= s ? static_cast<float>(val) : 0.0f;
-                    }
                 }
             }
         }
@@ -1113,16 +1144,19 @@ void scan_fused_kernel(ScanArgs a) {
                         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, q4.w, acc, 0, 0, 0);
                     }
                     const float4 w4 = *reinterpret_cast<const float4*>(w_s + (16 * tt + li) * WP + 16 * st + 4 * g);
-                    p_s[p * 64 + lane] = f32x4_t{w4.x * acc[0], w4.y * acc[1], w4.z * acc[2], w4.w * acc[3]};
+                    f32x4_t pv = f32x4_t{w4.x * acc[0], w4.y * acc[1], w4.z * acc[2], w4.w * acc[3]};
+                    if (st == tt) {  // W[t][s] is defined for s <= t only
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) pv[v] = 4 * g + v <= li ? pv[v] : 0.0f;
+                    }
+                    p_s[p * 64 + lane] = pv;
                 }
             }
         }
         if (wave == DT - 1 && lane < C) {
             float dot = 0.0f;
-            if (!first) {
 #pragma unroll
-                for (int n = 0; n < N; ++n) dot = fmaf(q_sh[lane * NP + n], kp_s[par][n], dot);
-            }
+            for (int n = 0; n < N; ++n) dot = fmaf(q_sh[lane * NP + n], kp_s[par][n], dot);
             ck_s[lane] = dot * w_s[lane * WP + kWp];
         }
         if (tid < N) kp_s[par ^ 1][tid] = k_sh[(C - 1) * NP + tid];
@@ -1137,7 +1171,8 @@ void scan_fused_kernel(ScanArgs a) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const double z = static_cast<double>(zx[tt][v]);
-                    gz[tt][v] = a.gate_logits ? z / (1.0 + exp_d(-z)) : z;
+                    const double sz = z / (1.0 + exp_d(-z));
+                    gz[tt][v] = a.gate_logits ? sz : z;
                 }
             int p0 = 0;  // index of pair (tt, 0)
 #pragma unroll
@@ -1151,30 +1186,29 @@ void scan_fused_kernel(ScanArgs a) {
 #pragma unroll
                         for (int v = 0; v < 4; ++v) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(P[v], vx[st][v], Y, 0, 0, 0);
                     }
-                    if (!first) {
 #pragma unroll
-                        for (int nt = 0; nt < NT; ++nt) {
-                            const float4 q4 = *reinterpret_cast<const float4*>(q_sh + (t0 + li) * NP + 16 * nt + 4 * g);
-                            const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const float4 q4 = *reinterpret_cast<const float4*>(q_sh + (t0 + li) * NP + 16 * nt + 4 * g);
+                        const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
-                            for (int v = 0; v < 4; ++v) Yi = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[v], S[nt][v], Yi, 0, 0, 0);
-                        }
+                        for (int v = 0; v < 4; ++v) Yi = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[v], S[nt][v], Yi, 0, 0, 0);
                     }
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int t = t0 + 4 * g + v;
-                        float y = Y[v];
-                        if (!first) y = fmaf(ck_s[t], vp, fmaf(w_s[t * WP + kDin], Yi[v], y));
+                        const float yc = fmaf(ck_s[t], vp, fmaf(w_s[t * WP + kDin], Yi[v], Y[v]));
+                        float y = first ? Y[v] : yc;
                         y = fmaf(skip, vx[tt][v], y);
-                        const float o = a.gate_logits ? static_cast<float>(static_cast<double>(y) * gz[tt][v])
-                                                      : y * zx[tt][v];
-                        if (t < Lc) orow[(c0 + t) * d_inner + col] = o;
+                        // With an explicit gate gz = z, and the double product of two
+                        // floats rounded once is the fp32 product y * gate.
+                        const float o = static_cast<float>(static_cast<double>(y) * gz[tt][v]);
+                        if (!last || t < Lc) orow[(c0 + t) * d_inner + col] = o;
                     }
                 }
                 p0 += tt + 1;
             }
         }
-        if (last) break;
+        if constexpr (last) return;
         // g. This wave's state columns after the chunk (all C tokens valid).
         {
             const float dl = w_s[(C - 1) * WP + kDin], wl = w_s[(C - 1) * WP + kWp];
@@ -1183,26 +1217,31 @@ void scan_fused_kernel(ScanArgs a) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     float x = S[nt][v] * dl;
-                    if (!first) x = fmaf(wl * kp_s[par][16 * nt + 4 * g + v], vp, x);
+                    x = fmaf(wl * kp_s[par][16 * nt + 4 * g + v], vp, x);  // k_p, v_p are zero in the first chunk
                     S[nt][v] = x;
                 }
 #pragma unroll
             for (int st = 0; st < CT; ++st) {
+                float kA[4][NT], bv[4];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int srow = 16 * st + 4 * g + v;
-                    const float bv = w_s[(C - 1) * WP + srow] * vx[st][v];
-                    float kA[NT];
+                    bv[v] = w_s[(C - 1) * WP + srow] * vx[st][v];
 #pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) kA[nt] = k_sh[srow * NP + 16 * nt + li];
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) S[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kA[nt], bv, S[nt], 0, 0, 0);
+                    for (int nt = 0; nt < NT; ++nt) kA[v][nt] = k_sh[srow * NP + 16 * nt + li];
                 }
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) S[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kA[v][nt], bv[v], S[nt], 0, 0, 0);
             }
             vp = __shfl(vx[CT - 1][3], 48 + li, 64);
         }
         __syncthreads();
-    }
+    };
+    int64_t c0 = 0;
+    for (; c0 + C < L; c0 += C) chunk(std::false_type{}, c0);
+    chunk(std::true_type{}, c0);
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
