@@ -13,10 +13,11 @@
 //
 //   block  = 8 waves, 128 rows (16 per wave); grid.y splits N only when there
 //            are too few row blocks to fill the chip.
-//   A      = the wave's 16 rows of x for one K chunk, loaded straight from
-//            HBM into registers in the MFMA operand layout: lane l holds row
-//            l%16, k = 8*(l/16) .. +7 of every 32-wide k step. With K within
-//            one chunk (256 for bf16 weights, 128 for fp32) x is read once.
+//   x      = the wave's 16 rows of x, loaded straight from HBM into registers
+//            in the MFMA operand layout: lane l holds row l%16, k = 8*(l/16)
+//            .. +7 of every 32-wide k step. With K within two chunks (512 for
+//            bf16 weights, 256 for fp32) all of K stays in registers and x is
+//            read once; beyond that (linear_kernel) it is reloaded per chunk.
 //   B      = a 64-column chunk of W in LDS, double-buffered: the next chunk's
 //            global loads are in flight while the MFMAs consume this one.
 //            One 16-byte LDS load per lane per 16x16 tile.
@@ -276,12 +277,153 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
     }
 }
 
+// The tiled form for K within two chunks: each wave owns RT tiles of 16 rows
+// (128 * RT rows per block) and holds its x fragments for all of K (KS
+// chunks) in registers, so x is read once whatever N is, and every W fragment
+// read from LDS feeds RT products. Iterations run over (N chunk, K chunk), W
+// of the next one in flight as above. The products are formed transposed
+// (W as the A operand, x as B; the same fragments the lanes hold above), so
+// the accumulator of lane (g, l) holds row l, columns 4g .. 4g + 3 of a tile
+// and leaves as one 16-byte store (scalar stores at a ragged N edge or an
+// unaligned output).
+template <bool BF16W, bool VEC, int RT, int KS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT * KS > 1 ? 2 : 4, RT * KS > 1 ? 2 : 4)))
+void linear_tiles_kernel(LinearArgs p) {
+    using T = typename WTraits<BF16W>::T;
+    constexpr int KC = WTraits<BF16W>::kKChunk;
+    constexpr int kSteps = KC / 32;
+    constexpr int kPitch = WTraits<BF16W>::kPitch;
+    __shared__ __attribute__((aligned(16))) T w_lds[2][kColsPerChunk * kPitch];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int li = lane & 15;
+    const int group = lane >> 4;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * (kRowsPerBlock * RT) + 16 * RT * wave;
+    const int64_t n_chunks = (p.N + kColsPerChunk - 1) / kColsPerChunk;
+    const int64_t my_chunks = (n_chunks - blockIdx.y + gridDim.y - 1) / gridDim.y;
+    if (my_chunks <= 0) return;
+    const int64_t iters = my_chunks * KS;
+    const bool vec_out = (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0;
+
+    auto kspan_of = [&](int kc) -> int {
+        const int64_t rem = p.K - static_cast<int64_t>(kc) * KC;
+        const int64_t span = ((rem < KC ? rem : KC) + 31) / 32 * 32;
+        return static_cast<int>(span);
+    };
+    auto n0_of = [&](int64_t it) { return (blockIdx.y + (it / KS) * gridDim.y) * kColsPerChunk; };
+
+    WStage<BF16W, VEC> stage;
+    AFrag<BF16W> a[RT][KS];
+    stage.fetch(p, n0_of(0), 0, kspan_of(0));
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int kc = 0; kc < KS; ++kc)
+            load_a<BF16W, VEC>(p, row0 + 16 * rt + li, static_cast<int64_t>(kc) * KC, group, kspan_of(kc) / 32,
+                               a[rt][kc]);
+    stage.store(p, n0_of(0), w_lds[0], kspan_of(0));
+    __syncthreads();
+
+    f32x4 acc[RT][4];
+    for (int64_t c = 0; c < my_chunks; ++c) {
+        const int64_t n0 = n0_of(c * KS);
+        f32x4 bias[4];  // columns n0 + 16t + 4g .. + 3
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t col = n0 + 16 * t + 4 * group + v;
+                bias[t][v] = p.bias != nullptr ? p.bias[col < p.N ? col : p.N - 1] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[rt][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kc = 0; kc < KS; ++kc) {
+            const int64_t it = c * KS + kc;
+            const bool more = it + 1 < iters;
+            const int kc_next = (kc + 1) % KS;
+            if (more) stage.fetch(p, n0_of(it + 1), static_cast<int64_t>(kc_next) * KC, kspan_of(kc_next));
+            const int steps = kspan_of(kc) / 32;
+            const T* buf = w_lds[it & 1];
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                if (s < steps) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const T* src = buf + (16 * t + li) * kPitch + 32 * s + 8 * group;
+                        if constexpr (BF16W) {
+                            const bf16x8 bv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(src));
+#pragma unroll
+                            for (int rt = 0; rt < RT; ++rt)
+                                acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bv, a[rt][kc].v[s], acc[rt][t], 0, 0, 0);
+                        } else {
+                            const float4 b0 = *reinterpret_cast<const float4*>(src);
+                            const float4 b1 = *reinterpret_cast<const float4*>(src + 4);
+                            const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                                for (int rt = 0; rt < RT; ++rt)
+                                    acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j], a[rt][kc].v[s][j], acc[rt][t], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+            if (kc == KS - 1) {
+                const bool full = vec_out && n0 + kColsPerChunk <= p.N;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const int64_t row = row0 + 16 * rt + li;
+                    if (row < p.rows) {
+                        float* orow = p.out + row * p.out_stride + n0 + 4 * group;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const f32x4 y = acc[rt][t] + bias[t];
+                            if (full) {
+                                *reinterpret_cast<f32x4*>(orow + 16 * t) = y;
+                            } else {
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) {
+                                    if (n0 + 16 * t + 4 * group + v < p.N) orow[16 * t + v] = y[v];
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+            if (more) stage.store(p, n0_of(it + 1), w_lds[(it + 1) & 1], kspan_of(kc_next));
+            __syncthreads();
+        }
+    }
+}
+
 template <bool BF16W, bool VEC>
-void launch(const LinearArgs& p, dim3 grid, hipStream_t stream) {
-    if (p.K > WTraits<BF16W>::kKChunk) {
-        hipLaunchKernelGGL((linear_kernel<BF16W, VEC, true>), grid, dim3(kThreads), 0, stream, p);
-    } else {
+void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t stream) {
+    constexpr int KC = WTraits<BF16W>::kKChunk;
+    // gy splits N only while there are fewer than ~512 blocks (two per CU).
+    // Two row tiles per wave (half the LDS reads of W per row) measured
+    // slower at 262144 x 256 -> 1192 (0.64 vs 0.58 ms): the register budget
+    // leaves one block per CU.
+    const int64_t row_blocks = ceil_div(rows, kRowsPerBlock);
+    int64_t gy = 1;
+    while (gy < n_chunks && row_blocks * gy < 512) ++gy;
+    const dim3 grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(gy));
+    // fp32 weights within one K chunk keep the row-layout kernel (measured
+    // faster there: 7.2 vs 8.6 us at 2048 x 64 -> 304, 71 vs 79 us at
+    // 65536 x 128 -> 257); bf16 weights take the tiled kernel (27.6 vs 29.3 us
+    // at 32768 x 256 -> 336).
+    if (p.K <= KC && !BF16W) {
         hipLaunchKernelGGL((linear_kernel<BF16W, VEC, false>), grid, dim3(kThreads), 0, stream, p);
+    } else if (p.K <= KC) {
+        hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 1>), grid, dim3(kThreads), 0, stream, p);
+    } else if (p.K <= 2 * KC) {
+        hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 2>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((linear_kernel<BF16W, VEC, true>), grid, dim3(kThreads), 0, stream, p);
     }
 }
 
@@ -302,20 +444,15 @@ extern "C" mlk_status mlk_linear(const float* x, int64_t rows, int64_t in_featur
     if (rows == 0) return MLK_OK;
     MLK_CHECK(x && weight && out, "null tensor pointer");
     LinearArgs p{x, rows, in_features, x_stride, weight, bias, out_features, out, out_stride};
-    const int64_t row_blocks = ceil_div(rows, kRowsPerBlock);
     const int64_t n_chunks = ceil_div(out_features, kColsPerChunk);
-    MLK_CHECK(row_blocks <= 0x7fffffff, "too many rows");
-    // Split N over grid.y only while there are fewer than ~512 blocks (two per CU).
-    int64_t gy = 1;
-    while (gy < n_chunks && row_blocks * gy < 512) ++gy;
-    const dim3 grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(gy));
+    MLK_CHECK(ceil_div(rows, kRowsPerBlock) <= 0x7fffffff, "too many rows");
     const size_t wsize = weight_dtype == MLK_DTYPE_BF16 ? 2 : 4;
     const bool vec = aligned16(x) && x_stride % 4 == 0 && aligned16(weight) && (in_features * wsize) % 16 == 0;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (weight_dtype == MLK_DTYPE_BF16) {
-        vec ? launch<true, true>(p, grid, s) : launch<true, false>(p, grid, s);
+        vec ? launch<true, true>(p, rows, n_chunks, s) : launch<true, false>(p, rows, n_chunks, s);
     } else {
-        vec ? launch<false, true>(p, grid, s) : launch<false, false>(p, grid, s);
+        vec ? launch<false, true>(p, rows, n_chunks, s) : launch<false, false>(p, rows, n_chunks, s);
     }
     return launch_status("linear");
 }
