@@ -31,8 +31,13 @@
 //                   association; fp32-VALU bound, ~7 flop per state element
 //                   per token.
 //   rec_chunk_kernel the chunked scan on the fp32 matrix cores (32-token
-//                   chunks, state carried in registers), used when there are
-//                   few (window, head) pairs; see the comment above it.
+//                   chunks, state carried in registers), used by the
+//                   recurrent op when there are few (window, head) pairs; see
+//                   the comment above it.
+//   scan_fused_kernel the forward in one kernel: the prep and rotate steps
+//                   above and rec_chunk_kernel's scan per (window, head)
+//                   straight from the in_proj rows, q and k kept in LDS; the
+//                   forward's default for d_state 16/32/64, headdim 16/32/64.
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
