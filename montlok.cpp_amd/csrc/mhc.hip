@@ -205,7 +205,6 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
         };
 #pragma unroll
         for (int j = 0; j < GW; ++j) {
-            const int k0 = 16 * (wave * GW + j) + 4 * q;
             const float4 s0 = sv[j][0], s1 = sv[j][1], s2 = sv[j][2], s3 = sv[j][3], o = ov[j];
             const float4 n0 = make_float4(mix(pv.x, r0, o.x, s0.x, s1.x, s2.x, s3.x), mix(pv.x, r0, o.y, s0.y, s1.y, s2.y, s3.y),
                                           mix(pv.x, r0, o.z, s0.z, s1.z, s2.z, s3.z), mix(pv.x, r0, o.w, s0.w, s1.w, s2.w, s3.w));
