@@ -1500,7 +1500,10 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs p) {
         }
 #pragma unroll
         for (int n = 0; n < NM; ++n) {
-            if (n < N) st[static_cast<int64_t>(n) * D] = sv[n];
+            // Non-temporal: the state is not read again this step, and leaving it
+            // out of the caches keeps the projections' operands there (decode step
+            // 4.30 -> 4.22 ms at 65536 streams, this kernel 1.87 -> 1.89 ms).
+            if (n < N) __builtin_nontemporal_store(sv[n], st + static_cast<int64_t>(n) * D);
         }
         const float y = fmaf(p.skip[h], v_cur, VEC ? acc0 + acc1 : acc0);
         const double zz = static_cast<double>(z[d]);
