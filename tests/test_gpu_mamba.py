@@ -170,7 +170,8 @@ def test_chunked_scan_vs_sequential(dev, oracle, monkeypatch, B, L, N, H, D):
 
 
 @pytest.mark.parametrize("B,L,N,G,H,D", [(2, 200, 64, 1, 2, 64), (3, 64, 32, 1, 2, 32), (64, 32, 16, 1, 4, 32),
-                                         (2, 70, 16, 1, 3, 64), (4, 31, 64, 2, 2, 32), (8, 33, 32, 2, 4, 64)])
+                                         (2, 70, 16, 1, 3, 64), (4, 31, 64, 2, 2, 32), (8, 33, 32, 2, 4, 64),
+                                         (3, 1, 64, 1, 2, 64), (5, 65, 16, 1, 2, 32)])
 def test_fused_scan_equals_unfused_chunked(dev, monkeypatch, B, L, N, G, H, D):
     """The one-kernel forward (in_proj post-processing and chunked scan, q/k kept in LDS) equals the
     prep -> rotate -> chunked-recurrence kernels bit for bit: the same arithmetic per token, the same
