@@ -26,6 +26,10 @@
 //            v_mfma_f32_16x16x4_f32, eight per 32-wide k step, fp32 throughout.
 //   D      = lane l, register v holds row 4*(l/16)+v, column l%16 of a tile.
 //
+// Shapes with fewer 128-row blocks x 64-column chunks than CUs (a few
+// thousand rows) take linear_small_kernel instead: one wave per 16 x 16
+// output tile, operands straight from L2, no LDS.
+//
 // K is reduced in an order of its own (the 8 k of a lane, then the four lane
 // groups inside the MFMA); for fp32 weights the result differs from a
 // sequential fp32 dot product by rounding only.
@@ -401,9 +405,128 @@ void linear_tiles_kernel(LinearArgs p) {
     }
 }
 
+// The small-problem form, for shapes whose 128-row blocks cannot fill the
+// chip (a few thousand rows): one wave per 16 x 16 output tile, so the grid
+// has rows/16 x N/16 waves. Both operands come straight from memory (L2) in
+// the MFMA fragment layout, every load of the tile issued before the first
+// product, no LDS and no barrier. KS 32-wide k steps are held in registers
+// (K <= 32 KS, K a multiple of 8: an 8-wide segment lies wholly inside or
+// wholly past K, and segments past K read column 0 and are zeroed). As in the
+// tiled form the products are transposed (W as the A operand), leaving lane
+// (g, l) with row l, columns 4g .. 4g + 3. fp32 weights accumulate the even
+// and odd k of each lane in two chains, summed at the end.
+template <bool BF16W, int KS>
+__global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
+    const int lane = threadIdx.x;
+    const int li = lane & 15;
+    const int group = lane >> 4;
+    const int64_t n_tiles = (p.N + 15) / 16;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x / n_tiles) * 16;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x % n_tiles) * 16;
+    const int64_t xr = row0 + li < p.rows ? row0 + li : p.rows - 1;
+    const int64_t wr = n0 + li < p.N ? n0 + li : p.N - 1;
+    const float* xrow = p.x + xr * p.x_stride;
+    float xv[KS][8];
+    bool live[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const int k = 32 * s + 8 * group;
+        live[s] = k < p.K;
+        const float* src = xrow + (live[s] ? k : 0);
+        const float4 lo = *reinterpret_cast<const float4*>(src);
+        const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+        xv[s][0] = lo.x; xv[s][1] = lo.y; xv[s][2] = lo.z; xv[s][3] = lo.w;
+        xv[s][4] = hi.x; xv[s][5] = hi.y; xv[s][6] = hi.z; xv[s][7] = hi.w;
+    }
+    f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p.bias != nullptr) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t col = n0 + 4 * group + v;
+            bias[v] = p.bias[col < p.N ? col : p.N - 1];
+        }
+    }
+    f32x4 y;
+    if constexpr (BF16W) {
+        const u16* wrow = static_cast<const u16*>(p.w) + wr * p.K;
+        uint4 wv[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const int k = 32 * s + 8 * group;
+            wv[s] = *reinterpret_cast<const uint4*>(wrow + (live[s] ? k : 0));
+        }
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            bf16x8 a;
+            bf16x8 b = __builtin_bit_cast(bf16x8, live[s] ? wv[s] : uint4{0u, 0u, 0u, 0u});
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] = static_cast<__bf16>(live[s] ? xv[s][j] : 0.0f);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a, acc, 0, 0, 0);
+        }
+        y = acc;
+    } else {
+        const float* wrow = static_cast<const float*>(p.w) + wr * p.K;
+        float wv[KS][8];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const float* src = wrow + (live[s] ? 32 * s + 8 * group : 0);
+            const float4 lo = *reinterpret_cast<const float4*>(src);
+            const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+            wv[s][0] = lo.x; wv[s][1] = lo.y; wv[s][2] = lo.z; wv[s][3] = lo.w;
+            wv[s][4] = hi.x; wv[s][5] = hi.y; wv[s][6] = hi.z; wv[s][7] = hi.w;
+        }
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(live[s] ? wv[s][j] : 0.0f, live[s] ? xv[s][j] : 0.0f,
+                                                            acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(live[s] ? wv[s][j + 1] : 0.0f,
+                                                            live[s] ? xv[s][j + 1] : 0.0f, acc1, 0, 0, 0);
+            }
+        }
+        y = acc0 + acc1;
+    }
+    y += bias;
+    const int64_t row = row0 + li;
+    if (row < p.rows) {
+        float* dst = p.out + row * p.out_stride + n0 + 4 * group;
+        if ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 && n0 + 16 <= p.N) {
+            *reinterpret_cast<f32x4*>(dst) = y;
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (n0 + 4 * group + v < p.N) dst[v] = y[v];
+            }
+        }
+    }
+}
+
+template <bool BF16W, int KS>
+void launch_small(const LinearArgs& p, int64_t tiles, hipStream_t stream) {
+    hipLaunchKernelGGL((linear_small_kernel<BF16W, KS>), dim3(static_cast<unsigned>(tiles)), dim3(64), 0, stream, p);
+}
+
 template <bool BF16W, bool VEC>
 void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t stream) {
     constexpr int KC = WTraits<BF16W>::kKChunk;
+    // Shapes too small to give the 128-row blocks one per CU (256 CUs) take
+    // one wave per 16 x 16 tile (2048 x 128 -> 64: 16 blocks of the tiled
+    // form, 512 waves here).
+    const int64_t tiles = ceil_div(rows, 16) * ceil_div(p.N, 16);
+    if (VEC && p.K % 8 == 0 && p.K <= 256 && ceil_div(rows, kRowsPerBlock) * n_chunks < 256 && tiles <= 0x7fffffff) {
+        if (p.K <= 64) {
+            launch_small<BF16W, 2>(p, tiles, stream);
+        } else if (p.K <= 128) {
+            launch_small<BF16W, 4>(p, tiles, stream);
+        } else {
+            launch_small<BF16W, 8>(p, tiles, stream);
+        }
+        return;
+    }
     // gy splits N only while there are fewer than ~512 blocks (two per CU).
     // Two row tiles per wave (half the LDS reads of W per row) measured
     // slower at 262144 x 256 -> 1192 (0.64 vs 0.58 ms): the register budget

@@ -35,7 +35,10 @@ SHAPES = [(2048, 64, 304, False),    # RMSNorm->Mamba-3 block in_proj
           (333, 300, 70, False),     # K beyond one 256-wide chunk
           (4100, 520, 1, True),      # one output column, two K chunks
           (1, 256, 336, False),      # a single row
-          (64, 512, 1192, False)]    # full-stack Mamba in_proj width
+          (64, 512, 1192, False),    # full-stack Mamba in_proj width
+          (300, 96, 70, True),       # one wave per tile: ragged rows and N, K past the last 32-wide step
+          (50, 200, 33, True),       # ... K = 200 (eight steps, the last two partly or wholly past K)
+          (16, 8, 16, False)]        # ... a single 8-wide k segment
 
 
 @pytest.mark.parametrize("M,K,N,with_bias", SHAPES)
