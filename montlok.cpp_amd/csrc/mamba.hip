@@ -858,7 +858,7 @@ void scan_fused_kernel(ScanArgs a) {
     static_assert(NTH % N == 0, "a thread keeps one q/k column across the chunk");
     __shared__ __attribute__((aligned(16))) float q_sh[C * NP];
     __shared__ __attribute__((aligned(16))) float k_sh[C * NP];
-    __shared__ __attribute__((aligned(16))) float w_s[C * WP];
+    __shared__ __attribute__((aligned(16))) float w_s[(C + 1) * WP];  // row C: sink of the walk's steps past the chunk
     __shared__ f32x4_t p_s[NPAIR * 64];
     __shared__ float ang_s[C * RM];  // angle logits, then tanh(angle) * pi
     __shared__ float cum_s[C * RM];  // cumulative angles
@@ -1032,10 +1032,14 @@ void scan_fused_kernel(ScanArgs a) {
                 const double b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
                 const double gam = wl < C ? static_cast<double>(coef[2][s]) : (wl == C ? static_cast<double>(coef[0][0]) : b0);
                 const double bet = wl + 1 < C ? static_cast<double>(coef[1][wl + 1]) : 0.0;
-                float* dst = w_s + (wl < C ? wl : (wl == C ? kDin : kWp));
-                dst[s * WP] = static_cast<float>(gam * 1.0);  // t = s
-                // Steps k = 0 .. C - 2 handle t = s + 1 + k; alpha of t is read
-                // from a clamped slot (the steps past the end are not stored).
+                const int colw = wl < C ? wl : (wl == C ? kDin : kWp);
+                w_s[s * WP + colw] = static_cast<float>(gam * 1.0);  // t = s
+                // Step k handles t = s + 1 + k; alpha of t is read from a
+                // clamped slot. Steps with t >= C (and the one step past
+                // k = C - 2 that rounds the walk up to whole batches of 8) store
+                // into the sink row C, so no step is predicated. Each group of 4
+                // steps runs the two product chains first, then the 4
+                // independent weights, then the 4 stores.
                 float nx[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + i, C - 1)];
@@ -1050,13 +1054,23 @@ void scan_fused_kernel(ScanArgs a) {
                         for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + k0 + 8 + i, C - 1)];
                     }
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int k = k0 + i, t = s + 1 + k;
-                        if (k < C - 1) {
-                            const double at = al[i];
+                    for (int i0 = 0; i0 < 8; i0 += 4) {
+                        double ddv[4], ev[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const double at = al[i0 + i];
                             dd *= at;
-                            if (k > 0) e *= at;
-                            if (t < C) dst[t * WP] = static_cast<float>(fma(bet, e, gam * dd));
+                            if (k0 + i0 + i > 0) e *= at;
+                            ddv[i] = dd;
+                            ev[i] = e;
+                        }
+                        float wv[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) wv[i] = static_cast<float>(fma(bet, ev[i], gam * ddv[i]));
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int t = s + 1 + k0 + i0 + i;
+                            w_s[(t < C ? t : C) * WP + colw] = wv[i];
                         }
                     }
                 }
@@ -1180,6 +1194,13 @@ void scan_fused_kernel(ScanArgs a) {
                     const double sz = z / (1.0 + exp_d(-z));
                     gz[tt][v] = a.gate_logits ? sz : z;
                 }
+            // Held here: left to itself the compiler sinks each gate into the
+            // predicated store of its output (the last chunk's stores are
+            // guarded), where the eight fp64 chains run one after another.
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(gz[tt][v]));
             int p0 = 0;  // index of pair (tt, 0)
 #pragma unroll
             for (int tt = 0; tt < CT; ++tt) {
