@@ -394,8 +394,12 @@ struct MlaAttendArgs {
     float scale_log2;
 };
 
+// The four-wave form keeps three blocks per CU (its LDS allows three): the
+// register budget is held to 168 so that the up-front loads do not cost a
+// block.
 template <int HD, int NOPE, int KV, int NW, int TPW>
-__global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 3 : 1)))
+void mla_attend_kernel(MlaAttendArgs p) {
     constexpr int THREADS = 64 * NW;
     constexpr int ROPE = HD - NOPE, HALF = ROPE / 2;
     constexpr int LMAX = 16 * NW * TPW;  // NW waves x TPW query tiles x 16
@@ -437,45 +441,104 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
         o2 = AttnElem<true>::from(static_cast<float>(__dadd_rn(__dmul_rn(x2, c2), __dmul_rn(x1, s2))));
     };
 
-    // 1. LayerNorm of the latent rows: 16 lanes per row, 4 columns each, and
-    // this head's kv_up rows. Every load is issued before the first use, with
-    // compile-time trip counts and no branch around it: rows past L read row
-    // L - 1 (in bounds) and their outputs are zeroed.
+    // 1. Every global operand of the block is fetched first, with compile-time
+    // trip counts and no branch around a load (rows past L read row L - 1, in
+    // bounds, and their values are zeroed where they are stored), so the block
+    // waits for one round of memory latency rather than one per phase: the
+    // latent rows (16 lanes per row, 4 columns each), this head's kv_up rows,
+    // k_rope and q of this head, and the cos/sin of their rows, which the k
+    // and q rotations share (both map unit u to row u / (HALF / 4) and the
+    // pairs from 4 (u % (HALF / 4)) on).
     constexpr int WUN = UPW * (KV / 8);  // 16-byte units of this head's kv_up rows
     constexpr int WUI = (WUN + THREADS - 1) / THREADS;
+    constexpr int PASSES = LMAX / (THREADS / 16);
+    constexpr int QU = HALF / 4;  // quads of rotary pairs per row
+    static_assert((LMAX * QU) % THREADS == 0, "rope units must split evenly");
+    constexpr int RI = LMAX * QU / THREADS;
+    constexpr int QN = NOPE / 4;
+    static_assert((LMAX * QN) % THREADS == 0, "q units must split evenly");
+    constexpr int NI = LMAX * QN / THREADS;
+    const int lr = tid >> 4, lc = tid & 15;
+    float4 xs[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+        const int row = ps * (THREADS / 16) + lr;
+        const int rc = row < L ? row : L - 1;
+        xs[ps] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.kv_off + 4 * lc);
+    }
     uint4 wur[WUI];
+#pragma unroll
+    for (int it = 0; it < WUI; ++it) {
+        const int u = min(tid + it * THREADS, WUN - 1);
+        const int r = u / (KV / 8), c = (u % (KV / 8)) * 8;
+        wur[it] = *reinterpret_cast<const uint4*>(p.w_up + (h * UPW + r) * static_cast<int64_t>(KV) + c);
+    }
+    float4 kx1[RI], kx2[RI], qx1[RI], qx2[RI], rc1[RI], rc2[RI], rs1[RI], rs2[RI];
+#pragma unroll
+    for (int it = 0; it < RI; ++it) {
+        const int u = tid + it * THREADS;
+        const int row = u / QU, rc = row < L ? row : L - 1, i0 = 4 * (u % QU);
+        const float* kr = rows + rc * p.proj_ts + p.kr_off + i0;
+        const float* qr = rows + rc * p.proj_ts + p.q_off + h * HD + NOPE + i0;
+        kx1[it] = *reinterpret_cast<const float4*>(kr);
+        kx2[it] = *reinterpret_cast<const float4*>(kr + HALF);
+        qx1[it] = *reinterpret_cast<const float4*>(qr);
+        qx2[it] = *reinterpret_cast<const float4*>(qr + HALF);
+        rc1[it] = *reinterpret_cast<const float4*>(p.cosine + rc * ROPE + i0);
+        rc2[it] = *reinterpret_cast<const float4*>(p.cosine + rc * ROPE + i0 + HALF);
+        rs1[it] = *reinterpret_cast<const float4*>(p.sine + rc * ROPE + i0);
+        rs2[it] = *reinterpret_cast<const float4*>(p.sine + rc * ROPE + i0 + HALF);
+    }
+    float4 qn[NI];
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+        const int u = tid + it * THREADS;
+        const int row = u / QN, rc = row < L ? row : L - 1;
+        qn[it] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.q_off + h * HD + 4 * (u % QN));
+    }
+    const float4 wv = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
+    const float4 bv = p.ln_b ? *reinterpret_cast<const float4*>(p.ln_b + 4 * lc) : make_float4(0.f, 0.f, 0.f, 0.f);
+
+    // LayerNorm of the latent rows into xq_s (bf16), the kv_up rows into wu_s.
+    // The passes (rows) advance together, one reduction level at a time, so
+    // that their cross-lane exchanges overlap; each row's arithmetic is that
+    // of layer_norm_vec_kernel with 16 lanes per row.
     {
-        constexpr int PASSES = LMAX / (THREADS / 16);
-        const int lr = tid >> 4, lc = tid & 15;
-        float4 xs[PASSES];
+        const double inv_dim = 1.0 / static_cast<double>(KV);
+        double mean[PASSES], sumsq[PASSES];  // the centred values are recomputed where used
 #pragma unroll
         for (int ps = 0; ps < PASSES; ++ps) {
-            const int row = ps * (THREADS / 16) + lr;
-            const int rc = row < L ? row : L - 1;
-            xs[ps] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.kv_off + 4 * lc);
+            const float4 x = xs[ps];
+            mean[ps] = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
+                       (static_cast<double>(x.z) + static_cast<double>(x.w));
         }
+        auto row_sums = [](double (&v)[PASSES]) {  // butterfly over the row's 16 lanes: xor 8, 4, 2, 1
 #pragma unroll
-        for (int it = 0; it < WUI; ++it) {
-            const int u = min(tid + it * THREADS, WUN - 1);
-            const int r = u / (KV / 8), c = (u % (KV / 8)) * 8;
-            wur[it] = *reinterpret_cast<const uint4*>(p.w_up + (h * UPW + r) * static_cast<int64_t>(KV) + c);
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<8>(v[ps]);
+#pragma unroll
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<4>(v[ps]);
+#pragma unroll
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<2>(v[ps]);
+#pragma unroll
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<1>(v[ps]);
+        };
+        row_sums(mean);
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const float4 x = xs[ps];
+            mean[ps] *= inv_dim;
+            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
+            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
+            sumsq[ps] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
         }
-        const float4 wv = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
-        const float4 bv = p.ln_b ? *reinterpret_cast<const float4*>(p.ln_b + 4 * lc) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const double inv_dim = 1.0 / static_cast<double>(KV);
+        row_sums(sumsq);
 #pragma unroll
         for (int ps = 0; ps < PASSES; ++ps) {
             const int row = ps * (THREADS / 16) + lr;
             const float4 x = xs[ps];
-            double sum = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
-                         (static_cast<double>(x.z) + static_cast<double>(x.w));
-            for (int mask = 8; mask > 0; mask >>= 1) sum += shfl_xor_d(sum, mask);
-            const double mean = sum * inv_dim;
-            const double a0 = static_cast<double>(x.x) - mean, a1 = static_cast<double>(x.y) - mean;
-            const double a2 = static_cast<double>(x.z) - mean, a3 = static_cast<double>(x.w) - mean;
-            double sumsq = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
-            for (int mask = 8; mask > 0; mask >>= 1) sumsq += shfl_xor_d(sumsq, mask);
-            const double rstd = 1.0 / sqrt(fma(sumsq, inv_dim, p.ln_eps));
+            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
+            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
+            const double rstd = 1.0 / sqrt(fma(sumsq[ps], inv_dim, p.ln_eps));
             const bool active = row < L;
             const u16 o0 = active ? AttnElem<true>::from(static_cast<float>((a0 * rstd) * wv.x + static_cast<double>(bv.x))) : u16(0);
             const u16 o1 = active ? AttnElem<true>::from(static_cast<float>((a1 * rstd) * wv.y + static_cast<double>(bv.y))) : u16(0);
@@ -495,39 +558,26 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
         }
     }
     // 3. Rotated k_rope into k_s, four pairs per thread (rows beyond L: zero).
-    {
-        constexpr int QU = HALF / 4;  // quads of pairs per row
-        static_assert((LMAX * QU) % THREADS == 0, "rope units must split evenly");
-        constexpr int ITER = LMAX * QU / THREADS;
 #pragma unroll
-        for (int it = 0; it < ITER; ++it) {
-            const int u = tid + it * THREADS;
-            const int row = u / QU, i0 = 4 * (u % QU);
-            const int rc = row < L ? row : L - 1;
-            const float* kr = rows + rc * p.proj_ts + p.kr_off;
-            const float* c = p.cosine + rc * ROPE;
-            const float* sn = p.sine + rc * ROPE;
-            float x1[4], x2[4], c1[4], c2[4], s1[4], s2[4];
+    for (int it = 0; it < RI; ++it) {
+        const int u = tid + it * THREADS;
+        const int row = u / QU, i0 = 4 * (u % QU);
+        const float x1[4] = {kx1[it].x, kx1[it].y, kx1[it].z, kx1[it].w};
+        const float x2[4] = {kx2[it].x, kx2[it].y, kx2[it].z, kx2[it].w};
+        const float c1[4] = {rc1[it].x, rc1[it].y, rc1[it].z, rc1[it].w};
+        const float c2[4] = {rc2[it].x, rc2[it].y, rc2[it].z, rc2[it].w};
+        const float s1[4] = {rs1[it].x, rs1[it].y, rs1[it].z, rs1[it].w};
+        const float s2[4] = {rs2[it].x, rs2[it].y, rs2[it].z, rs2[it].w};
+        u16 o1[4], o2[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x1[j] = kr[i0 + j];
-                x2[j] = kr[i0 + j + HALF];
-                c1[j] = c[i0 + j];
-                c2[j] = c[i0 + j + HALF];
-                s1[j] = sn[i0 + j];
-                s2[j] = sn[i0 + j + HALF];
-            }
-            u16 o1[4], o2[4];
+        for (int j = 0; j < 4; ++j) {
+            rot(x1[j], x2[j], c1[j], s1[j], c2[j], s2[j], o1[j], o2[j]);
+            if (row >= L) o1[j] = o2[j] = 0;
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                rot(x1[j], x2[j], c1[j], s1[j], c2[j], s2[j], o1[j], o2[j]);
-                if (row >= L) o1[j] = o2[j] = 0;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                k_s[row * KP + NOPE + i0 + j] = o1[j];
-                k_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
-            }
+        for (int j = 0; j < 4; ++j) {
+            k_s[row * KP + NOPE + i0 + j] = o1[j];
+            k_s[row * KP + NOPE + i0 + j + HALF] = o2[j];
         }
     }
     __syncthreads();
@@ -559,40 +609,9 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
             }
         }
     }
-    // q of this head, loaded now (registers) and written over the latent
-    // after the barrier: the nope part in float4 units, the rope part in
-    // units of four pairs with their cos/sin, each with an exact compile-time
-    // trip count so every load is issued before the barrier. Rows past L read
-    // row L - 1 (in bounds) and are written as zeros.
-    constexpr int QN = NOPE / 4, QR = HALF / 4;
-    static_assert((LMAX * QN) % THREADS == 0 && (LMAX * QR) % THREADS == 0, "q units must split evenly");
-    constexpr int NI = LMAX * QN / THREADS, RI = LMAX * QR / THREADS;
-    float4 qn[NI], qx1[RI], qx2[RI];
-    float qc1[RI][4], qs1[RI][4], qc2[RI][4], qs2[RI][4];
-#pragma unroll
-    for (int it = 0; it < NI; ++it) {
-        const int u = tid + it * THREADS;
-        const int row = u / QN, rc = row < L ? row : L - 1;
-        qn[it] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.q_off + h * HD + 4 * (u % QN));
-    }
-#pragma unroll
-    for (int it = 0; it < RI; ++it) {
-        const int u = tid + it * THREADS;
-        const int row = u / QR, rc = row < L ? row : L - 1, i0 = 4 * (u % QR);
-        const float* qr = rows + rc * p.proj_ts + p.q_off + h * HD + NOPE + i0;
-        qx1[it] = *reinterpret_cast<const float4*>(qr);
-        qx2[it] = *reinterpret_cast<const float4*>(qr + HALF);
-        const float* c = p.cosine + rc * ROPE + i0;
-        const float* sn = p.sine + rc * ROPE + i0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            qc1[it][j] = c[j];
-            qs1[it][j] = sn[j];
-            qc2[it][j] = c[j + HALF];
-            qs2[it][j] = sn[j + HALF];
-        }
-    }
     __syncthreads();  // xq_s (the latent) is free from here on
+    // 4. q of this head over the latent: the nope part as loaded, the rope
+    // part rotated (rows beyond L: zero).
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
         const int u = tid + it * THREADS;
@@ -604,13 +623,17 @@ __global__ __launch_bounds__(64 * NW) void mla_attend_kernel(MlaAttendArgs p) {
 #pragma unroll
     for (int it = 0; it < RI; ++it) {
         const int u = tid + it * THREADS;
-        const int row = u / QR, i0 = 4 * (u % QR);
+        const int row = u / QU, i0 = 4 * (u % QU);
         const float a4[4] = {qx1[it].x, qx1[it].y, qx1[it].z, qx1[it].w};
         const float b4[4] = {qx2[it].x, qx2[it].y, qx2[it].z, qx2[it].w};
+        const float c1[4] = {rc1[it].x, rc1[it].y, rc1[it].z, rc1[it].w};
+        const float c2[4] = {rc2[it].x, rc2[it].y, rc2[it].z, rc2[it].w};
+        const float s1[4] = {rs1[it].x, rs1[it].y, rs1[it].z, rs1[it].w};
+        const float s2[4] = {rs2[it].x, rs2[it].y, rs2[it].z, rs2[it].w};
         u16 o1[4], o2[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            rot(a4[j], b4[j], qc1[it][j], qs1[it][j], qc2[it][j], qs2[it][j], o1[j], o2[j]);
+            rot(a4[j], b4[j], c1[j], s1[j], c2[j], s2[j], o1[j], o2[j]);
             if (row >= L) o1[j] = o2[j] = 0;
         }
 #pragma unroll
@@ -814,6 +837,10 @@ extern "C" mlk_status mlk_mla_attend(const float* projected, int64_t batch, int6
     const bool cfg64 = head_dim == 64 && nope_dim == 32 && kv_rank == 64 && length <= 256;
     if (!cfg32 && !cfg64) {
         set_error("mla_attend: geometry without a fused kernel (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    if (k_rope_offset % 4 != 0 || !aligned16(cosine) || !aligned16(sine)) {
+        set_error("mla_attend: k_rope and the cos/sin tables are read as 16-byte vectors (use the separate operators)");
         return MLK_ERR_UNSUPPORTED;
     }
     MLK_CHECK(proj_token_stride % 4 == 0 && q_offset % 4 == 0 && kv_offset % 4 == 0 && aligned16(projected) &&

@@ -42,6 +42,30 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kWave = 64;
 
 __device__ __forceinline__ double shfl_xor_d(double v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// A double moved between lanes by one DPP control (GFX9 encodings: quad_perm
+// 0x00-0xFF, row_mirror 0x140, row_half_mirror 0x141), both halves alike.
+template <int CTRL>
+__device__ __forceinline__ double mov_dpp_d(double v) {
+    const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+
+// The value of lane l ^ MASK, MASK in {1, 2, 4, 8} (a partner inside the
+// lane's row of 16), by DPP moves instead of the LDS crossbar: quad_perm
+// [1,0,3,2] for 1, [2,3,0,1] for 2; row_half_mirror (l ^ 7) then quad_perm
+// [3,2,1,0] (l ^ 3) for 4; row_mirror (l ^ 15) then row_half_mirror for 8.
+// The same partner as shfl_xor_d(v, MASK), so sums built from it agree bit
+// for bit.
+template <int MASK>
+__device__ __forceinline__ double xor_row_d(double v) {
+    static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "partner must lie in the 16-lane row");
+    if constexpr (MASK == 1) return mov_dpp_d<0xB1>(v);
+    if constexpr (MASK == 2) return mov_dpp_d<0x4E>(v);
+    if constexpr (MASK == 4) return mov_dpp_d<0x1B>(mov_dpp_d<0x141>(v));
+    return mov_dpp_d<0x141>(mov_dpp_d<0x140>(v));
+}
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 __device__ __forceinline__ double shfl_d(double v, int src) { return __shfl(v, src, kWave); }
 
