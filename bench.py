@@ -407,34 +407,36 @@ def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
     norm_w = torch.ones(d, device=dev)
     wts = _mamba_weights(g, d, geo, dev)
     mp = [wts[k] for k in MAMBA_PARAM_KEYS]
-    out = torch.empty_like(x)
     consts = (N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    res = [None]
 
     def step():
-        h = _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"])
-        y = _C.mamba3_siso_layer(h, wts["in_w"], wts["out_w"], *mp, *consts)
-        torch.add(x, y, out=out)
+        # GroupedRMSNorm + in_proj in one launch, the scan, out_proj + residual in one launch:
+        # bit-identical to rms_norm -> mamba3_siso_layer -> x + y.
+        proj = _C.rms_norm_linear(x, norm_w, 1e-5, cfg["norm_groups"], wts["in_w"])
+        y = _C.mamba3_siso_forward(proj, None, *mp, *consts)
+        res[0] = _C.linear_residual(y, wts["out_w"], None, x)
 
     step()
     torch.cuda.synchronize()
-    eager = out.clone()
+    eager = res[0].clone()
+    unfused = x + _C.mamba3_siso_layer(_C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"]), wts["in_w"], wts["out_w"],
+                                       *mp, *consts)
+    assert torch.equal(eager, unfused), "fused block step differs from the separate operators"
     steps, ms = _time_steps([step], steps, warmup, per_graph=16)
-    assert torch.equal(out, eager), "graph replay differs from the eager step"
+    assert torch.equal(res[0], eager), "graph replay differs from the eager step"
 
     h = _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"])
     proj = _C.linear(h, wts["in_w"])
     y = _C.mamba3_siso_forward(proj, None, *mp, *consts)
-    o = _C.linear(y, wts["out_w"])
     f = 4
     ops = {
-        "rms_norm": dict(fn=lambda: _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"]), bytes=2 * T * d * f + d * f),
-        "in_proj": dict(fn=lambda: _C.linear(h, wts["in_w"]), bytes=(T * d + W * d + T * W) * f,
-                        flops=2 * T * d * W),
+        "rms_norm_in_proj": dict(fn=lambda: _C.rms_norm_linear(x, norm_w, 1e-5, cfg["norm_groups"], wts["in_w"]),
+                                 bytes=(T * d + d + W * d + T * W) * f, flops=2 * T * d * W),
         "mamba3_siso_forward": dict(fn=lambda: _C.mamba3_siso_forward(proj, None, *mp, *consts),
                                     bytes=(T * W + T * d_inner) * f, flops=7 * T * H * N * D),
-        "out_proj": dict(fn=lambda: _C.linear(y, wts["out_w"]), bytes=(T * d_inner + d * d_inner + T * d) * f,
-                         flops=2 * T * d_inner * d),
-        "residual_add": dict(fn=lambda: torch.add(x, o, out=out), bytes=3 * T * d * f),
+        "out_proj_residual": dict(fn=lambda: _C.linear_residual(y, wts["out_w"], None, x),
+                                  bytes=(T * d_inner + d * d_inner + 2 * T * d) * f, flops=2 * T * d_inner * d),
     }
     table = _kernel_table(ops, _op_times(ops, max(4, steps // 16)), "f32")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
@@ -445,6 +447,8 @@ def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
                       {"workload": "rmsnorm_mamba3_block", "windows": B, "seq_len": L, "d_model": d, "heads": H,
                        "d_state": N, "headdim": D, "rope_angles": R, "expand": cfg["expand"],
                        "norm_groups": cfg["norm_groups"], "step": "x + out_proj(mamba3(in_proj(GroupedRMSNorm(x))))",
+                       "launches": "rms_norm_linear (GroupedRMSNorm + in_proj), mamba3_siso_forward, "
+                                   "linear_residual (out_proj + x)",
                        "launch": "HIP graph of 16 steps, replayed", "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32")
     line["kernels"] = table

@@ -105,6 +105,33 @@ mlk_status mlk_linear(const float* x, int64_t rows, int64_t in_features, int64_t
                       int32_t weight_dtype, const float* bias, int64_t out_features, float* out,
                       int64_t out_stride, mlk_stream_t stream);
 
+/* linear followed by a residual add: out = residual + (x W^T + bias), the
+ * add a separate fp32 rounding, so the result is bit-identical to mlk_linear
+ * into a buffer and then residual + that buffer (the x = x + f(norm(x))
+ * steps of python/montlok/rdt/reference/Model/blocks.py:66-75). residual:
+ * fp32 rows `res_stride` floats apart. No single counterpart in the
+ * reference's op table: it fuses linear (montlok.cpp:1458) with the caller's
+ * residual add. */
+mlk_status mlk_linear_residual(const float* x, int64_t rows, int64_t in_features, int64_t x_stride,
+                               const void* weight, int32_t weight_dtype, const float* bias, int64_t out_features,
+                               const float* residual, int64_t res_stride, float* out, int64_t out_stride,
+                               mlk_stream_t stream);
+
+/* rms_norm(x, norm_weight, eps, groups) then linear(., weight, bias) in one
+ * launch, without the normalised intermediate: bit-identical to mlk_rms_norm
+ * into a buffer followed by mlk_linear on it. Built for the shapes that take
+ * the one-wave-per-tile linear (fewer 128-row blocks x 64-column chunks than
+ * CUs, in_features <= 256 and a multiple of 8), groups of 8, 16, 32 or 64
+ * floats and 16-byte aligned x rows, norm weight and weight rows; other
+ * shapes return MLK_ERR_UNSUPPORTED and the caller runs the two operators.
+ * No single counterpart in the reference's op table: it fuses rms_norm
+ * (montlok.cpp:1481) with the in_proj linear that follows it (stage1_forward,
+ * montlok.cpp:1030-1034). */
+mlk_status mlk_rms_norm_linear(const float* x, int64_t rows, int64_t in_features, int64_t x_stride,
+                               const float* norm_weight, double eps, int64_t groups, const void* weight,
+                               int32_t weight_dtype, const float* bias, int64_t out_features, float* out,
+                               int64_t out_stride, mlk_stream_t stream);
+
 /* ----------------------------------------------------------------- MLA -- */
 
 /* mla_rope_qk(q, kv, k_rope, cos, sin, nope_dim) -- montlok.cpp:1093-1154,

@@ -72,6 +72,14 @@ struct LinearArgs {
     int64_t N;
     float* out;
     int64_t out_stride;
+    // Optional residual added to the result (out = residual + (x W^T + b),
+    // the add as a separate fp32 rounding), rows res_stride apart.
+    const float* residual;
+    int64_t res_stride;
+    // Optional grouped RMSNorm of x before the product (linear_small_kernel
+    // only): weight and eps as the rms_norm operator takes them.
+    const float* norm_w;
+    double norm_eps;
 };
 
 // Loads 8 consecutive floats x[row, k .. k+7] (zero past K or past the last
@@ -271,7 +279,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int64_t row = row0 + 4 * group + v;
-                        if (row < p.rows) p.out[row * p.out_stride + col] = acc[t][v] + bias[t];
+                        if (row < p.rows) {
+                            const float y = acc[t][v] + bias[t];
+                            p.out[row * p.out_stride + col] =
+                                p.residual != nullptr ? p.residual[row * p.res_stride + col] + y : y;
+                        }
                     }
                 }
             }
@@ -308,7 +320,9 @@ void linear_tiles_kernel(LinearArgs p) {
     const int64_t my_chunks = (n_chunks - blockIdx.y + gridDim.y - 1) / gridDim.y;
     if (my_chunks <= 0) return;
     const int64_t iters = my_chunks * KS;
-    const bool vec_out = (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0;
+    const bool vec_out = (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 &&
+                         (p.residual == nullptr ||
+                          ((reinterpret_cast<uintptr_t>(p.residual) & 15) == 0 && p.res_stride % 4 == 0));
 
     auto kspan_of = [&](int kc) -> int {
         const int64_t rem = p.K - static_cast<int64_t>(kc) * KC;
@@ -384,15 +398,19 @@ void linear_tiles_kernel(LinearArgs p) {
                     const int64_t row = row0 + 16 * rt + li;
                     if (row < p.rows) {
                         float* orow = p.out + row * p.out_stride + n0 + 4 * group;
+                        const float* rrow = p.residual != nullptr ? p.residual + row * p.res_stride + n0 + 4 * group : nullptr;
 #pragma unroll
                         for (int t = 0; t < 4; ++t) {
-                            const f32x4 y = acc[rt][t] + bias[t];
+                            f32x4 y = acc[rt][t] + bias[t];
                             if (full) {
+                                if (p.residual != nullptr) y = *reinterpret_cast<const f32x4*>(rrow + 16 * t) + y;
                                 *reinterpret_cast<f32x4*>(orow + 16 * t) = y;
                             } else {
 #pragma unroll
                                 for (int v = 0; v < 4; ++v) {
-                                    if (n0 + 16 * t + 4 * group + v < p.N) orow[16 * t + v] = y[v];
+                                    if (n0 + 16 * t + 4 * group + v < p.N) {
+                                        orow[16 * t + v] = p.residual != nullptr ? rrow[16 * t + v] + y[v] : y[v];
+                                    }
                                 }
                             }
                         }
@@ -415,7 +433,17 @@ void linear_tiles_kernel(LinearArgs p) {
 // tiled form the products are transposed (W as the A operand), leaving lane
 // (g, l) with row l, columns 4g .. 4g + 3. fp32 weights accumulate the even
 // and odd k of each lane in two chains, summed at the end.
-template <bool BF16W, int KS>
+//
+// GS > 0 applies the grouped RMSNorm of x (groups of GS floats, GS in 8, 16,
+// 32, 64) to the loaded fragments first, with the arithmetic of
+// rms_norm_vec_kernel: per 4-float chunk the fp64 partial (a^2 + b^2) +
+// (c^2 + d^2), the group's chunks combined by the same butterfly (chunk c of
+// the group is lane (c / 2) % 4's half c % 2 of its segment, so the levels
+// are: the two steps of a 64-group in registers, lanes 32 apart, lanes 16
+// apart, the two halves in registers), scale = 1 / sqrt(sum / GS + eps),
+// x * scale * w rounded once. The normalised x is bit-identical to the
+// rms_norm operator's output, so the product is that of rms_norm then linear.
+template <bool BF16W, int KS, int GS>
 __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
     const int lane = threadIdx.x;
     const int li = lane & 15;
@@ -437,6 +465,56 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
         const float4 hi = *reinterpret_cast<const float4*>(src + 4);
         xv[s][0] = lo.x; xv[s][1] = lo.y; xv[s][2] = lo.z; xv[s][3] = lo.w;
         xv[s][4] = hi.x; xv[s][5] = hi.y; xv[s][6] = hi.z; xv[s][7] = hi.w;
+    }
+    if constexpr (GS > 0) {
+        static_assert(GS == 8 || GS == 16 || GS == 32 || (GS == 64 && KS % 2 == 0), "RMSNorm group size");
+        float nw[KS][8];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const float* src = p.norm_w + (live[s] ? 32 * s + 8 * group : 0);
+            const float4 lo = *reinterpret_cast<const float4*>(src);
+            const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+            nw[s][0] = lo.x; nw[s][1] = lo.y; nw[s][2] = lo.z; nw[s][3] = lo.w;
+            nw[s][4] = hi.x; nw[s][5] = hi.y; nw[s][6] = hi.z; nw[s][7] = hi.w;
+        }
+        double part[KS][2];
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const double a = xv[s][4 * hf], b = xv[s][4 * hf + 1], c = xv[s][4 * hf + 2], d = xv[s][4 * hf + 3];
+                part[s][hf] = (a * a + b * b) + (c * c + d * d);
+            }
+        if constexpr (GS == 64) {
+#pragma unroll
+            for (int s = 0; s < KS; s += 2)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const double q = part[s][hf] + part[s + 1][hf];
+                    part[s][hf] = q;
+                    part[s + 1][hf] = q;
+                }
+        }
+        if constexpr (GS >= 32) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) part[s][hf] += shfl_xor_d(part[s][hf], 32);
+        }
+        if constexpr (GS >= 16) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) part[s][hf] += shfl_xor_d(part[s][hf], 16);
+        }
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const double scale = 1.0 / sqrt((part[s][0] + part[s][1]) / static_cast<double>(GS) + p.norm_eps);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xv[s][j] = static_cast<float>((static_cast<double>(xv[s][j]) * scale) * static_cast<double>(nw[s][j]));
+            }
+        }
     }
     f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
     if (p.bias != nullptr) {
@@ -494,20 +572,43 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
     const int64_t row = row0 + li;
     if (row < p.rows) {
         float* dst = p.out + row * p.out_stride + n0 + 4 * group;
-        if ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 && n0 + 16 <= p.N) {
+        const float* res = p.residual != nullptr ? p.residual + row * p.res_stride + n0 + 4 * group : nullptr;
+        if ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 && n0 + 16 <= p.N &&
+            (res == nullptr || ((reinterpret_cast<uintptr_t>(p.residual) & 15) == 0 && p.res_stride % 4 == 0))) {
+            if (res != nullptr) y = *reinterpret_cast<const f32x4*>(res) + y;
             *reinterpret_cast<f32x4*>(dst) = y;
         } else {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                if (n0 + 4 * group + v < p.N) dst[v] = y[v];
+                if (n0 + 4 * group + v < p.N) dst[v] = res != nullptr ? res[v] + y[v] : y[v];
             }
         }
     }
 }
 
-template <bool BF16W, int KS>
+template <bool BF16W, int KS, int GS = 0>
 void launch_small(const LinearArgs& p, int64_t tiles, hipStream_t stream) {
-    hipLaunchKernelGGL((linear_small_kernel<BF16W, KS>), dim3(static_cast<unsigned>(tiles)), dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((linear_small_kernel<BF16W, KS, GS>), dim3(static_cast<unsigned>(tiles)), dim3(64), 0, stream,
+                       p);
+}
+
+// The small form with the RMSNorm prologue: K steps by K, group size by gs.
+template <bool BF16W, int GS>
+void launch_small_norm(const LinearArgs& p, int64_t tiles, hipStream_t stream) {
+    if (p.K <= 64) {
+        launch_small<BF16W, 2, GS>(p, tiles, stream);
+    } else if (p.K <= 128) {
+        launch_small<BF16W, 4, GS>(p, tiles, stream);
+    } else {
+        launch_small<BF16W, 8, GS>(p, tiles, stream);
+    }
+}
+
+// Shapes too small to give the 128-row blocks one per CU (256 CUs), with K
+// held in at most eight 32-wide steps.
+bool small_shape(int64_t rows, int64_t K, int64_t N) {
+    return K % 8 == 0 && K <= 256 && ceil_div(rows, kRowsPerBlock) * ceil_div(N, kColsPerChunk) < 256 &&
+           ceil_div(rows, 16) * ceil_div(N, 16) <= 0x7fffffff;
 }
 
 template <bool BF16W, bool VEC>
@@ -517,7 +618,7 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
     // one wave per 16 x 16 tile (2048 x 128 -> 64: 16 blocks of the tiled
     // form, 512 waves here).
     const int64_t tiles = ceil_div(rows, 16) * ceil_div(p.N, 16);
-    if (VEC && p.K % 8 == 0 && p.K <= 256 && ceil_div(rows, kRowsPerBlock) * n_chunks < 256 && tiles <= 0x7fffffff) {
+    if (VEC && small_shape(rows, p.K, p.N)) {
         if (p.K <= 64) {
             launch_small<BF16W, 2>(p, tiles, stream);
         } else if (p.K <= 128) {
@@ -578,4 +679,64 @@ extern "C" mlk_status mlk_linear(const float* x, int64_t rows, int64_t in_featur
         vec ? launch<false, true>(p, rows, n_chunks, s) : launch<false, false>(p, rows, n_chunks, s);
     }
     return launch_status("linear");
+}
+
+extern "C" mlk_status mlk_linear_residual(const float* x, int64_t rows, int64_t in_features, int64_t x_stride,
+                                          const void* weight, int32_t weight_dtype, const float* bias,
+                                          int64_t out_features, const float* residual, int64_t res_stride,
+                                          float* out, int64_t out_stride, mlk_stream_t stream) {
+    MLK_CHECK(rows >= 0 && in_features > 0 && out_features > 0, "invalid linear geometry");
+    MLK_CHECK(x_stride >= in_features, "x row stride must be at least in_features");
+    MLK_CHECK(out_stride >= out_features, "out row stride must be at least out_features");
+    MLK_CHECK(res_stride >= out_features, "residual row stride must be at least out_features");
+    MLK_CHECK(weight_dtype == MLK_DTYPE_F32 || weight_dtype == MLK_DTYPE_BF16, "weight dtype must be f32 or bf16");
+    if (rows == 0) return MLK_OK;
+    MLK_CHECK(x && weight && out && residual, "null tensor pointer");
+    MLK_CHECK(ceil_div(rows, kRowsPerBlock) <= 0x7fffffff, "too many rows");
+    LinearArgs p{x, rows, in_features, x_stride, weight, bias, out_features, out, out_stride, residual, res_stride};
+    const int64_t n_chunks = ceil_div(out_features, kColsPerChunk);
+    const size_t wsize = weight_dtype == MLK_DTYPE_BF16 ? 2 : 4;
+    const bool vec = aligned16(x) && x_stride % 4 == 0 && aligned16(weight) && (in_features * wsize) % 16 == 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (weight_dtype == MLK_DTYPE_BF16) {
+        vec ? launch<true, true>(p, rows, n_chunks, s) : launch<true, false>(p, rows, n_chunks, s);
+    } else {
+        vec ? launch<false, true>(p, rows, n_chunks, s) : launch<false, false>(p, rows, n_chunks, s);
+    }
+    return launch_status("linear_residual");
+}
+
+extern "C" mlk_status mlk_rms_norm_linear(const float* x, int64_t rows, int64_t in_features, int64_t x_stride,
+                                          const float* norm_weight, double eps, int64_t groups, const void* weight,
+                                          int32_t weight_dtype, const float* bias, int64_t out_features, float* out,
+                                          int64_t out_stride, mlk_stream_t stream) {
+    MLK_CHECK(rows >= 0 && in_features > 0 && out_features > 0, "invalid linear geometry");
+    MLK_CHECK(groups > 0 && in_features % groups == 0, "groups must divide the normalised dimension");
+    MLK_CHECK(x_stride >= in_features, "x row stride must be at least in_features");
+    MLK_CHECK(out_stride >= out_features, "out row stride must be at least out_features");
+    MLK_CHECK(weight_dtype == MLK_DTYPE_F32 || weight_dtype == MLK_DTYPE_BF16, "weight dtype must be f32 or bf16");
+    const int64_t gs = in_features / groups;
+    const size_t wsize = weight_dtype == MLK_DTYPE_BF16 ? 2 : 4;
+    const bool vec = aligned16(x) && x_stride % 4 == 0 && aligned16(weight) && (in_features * wsize) % 16 == 0 &&
+                     aligned16(norm_weight);
+    if (!vec || !(gs == 8 || gs == 16 || gs == 32 || gs == 64) || !small_shape(rows, in_features, out_features)) {
+        set_error("rms_norm_linear: shape without the fused form (use rms_norm then linear)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    if (rows == 0) return MLK_OK;
+    MLK_CHECK(x && norm_weight && weight && out, "null tensor pointer");
+    LinearArgs p{x, rows, in_features, x_stride, weight, bias, out_features, out, out_stride, nullptr, 0,
+                 norm_weight, static_cast<double>(static_cast<float>(eps))};
+    const int64_t tiles = ceil_div(rows, 16) * ceil_div(out_features, 16);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+#define MLK_NORM_GS(G)                                                                             \
+    (weight_dtype == MLK_DTYPE_BF16 ? launch_small_norm<true, G>(p, tiles, s) : launch_small_norm<false, G>(p, tiles, s))
+    switch (gs) {
+        case 8: MLK_NORM_GS(8); break;
+        case 16: MLK_NORM_GS(16); break;
+        case 32: MLK_NORM_GS(32); break;
+        default: MLK_NORM_GS(64); break;
+    }
+#undef MLK_NORM_GS
+    return launch_status("rms_norm_linear");
 }

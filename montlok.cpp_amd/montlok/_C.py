@@ -43,6 +43,8 @@ def _load():
         "mlk_layer_norm": [_vp, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp],
         "mlk_swiglu": [_vp, _i64, _i64, _i64, _vp, _vp],
         "mlk_linear": [_vp, _i64, _i64, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp],
+        "mlk_linear_residual": [_vp, _i64, _i64, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp, _i64, _vp],
+        "mlk_rms_norm_linear": [_vp, _i64, _i64, _i64, _vp, _dbl, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp],
         "mlk_mla_rope_qk": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
         "mlk_mla_attend": [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp,
                            _vp, _dbl, _vp, _vp],
@@ -213,6 +215,54 @@ def linear(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None 
     out = torch.empty((count, n), dtype=torch.float32, device=input.device)
     _linear_into(rows, count, stride, w, b, out, n)
     return out.view(*input.shape[:-1], n)
+
+
+def linear_residual(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                    residual: torch.Tensor) -> torch.Tensor:
+    """residual + linear(input, weight, bias) in one launch, bit-identical to the two steps (the
+    x = x + f(x) update of python/montlok/rdt/reference/Model/blocks.py:66-75)."""
+    _require_f32_gpu(input, "input")
+    _require_f32_gpu(residual, "residual")
+    w = _weight(weight)
+    n, k = w.shape
+    _check(input.dim() >= 1 and input.size(-1) == k, f"input must end in in_features={k}")
+    _check(tuple(residual.shape) == tuple(input.shape[:-1]) + (n,), "residual must have the output's shape")
+    b = None
+    if bias is not None and bias.numel() > 0:
+        b = _dense_parameter(bias, n, "bias")
+    rows, count, stride = _rows(input, k)
+    res = residual.reshape(count, n).contiguous()
+    out = torch.empty((count, n), dtype=torch.float32, device=input.device)
+    _call("mlk_linear_residual", _ptr(rows), count, k, stride, _ptr(w), _WEIGHT_DTYPES[w.dtype], _ptr(b), n,
+          _ptr(res), n, _ptr(out), n, _stream())
+    return out.view(*input.shape[:-1], n)
+
+
+def rms_norm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, groups: int, weight: torch.Tensor,
+                    bias: torch.Tensor | None = None) -> torch.Tensor:
+    """linear(rms_norm(x, norm_weight, eps, groups), weight, bias), one launch where the fused form is
+    built (small row counts), else the two operators; the results are identical either way."""
+    _require_f32_gpu(x, "x")
+    _check(x.dim() >= 1, "x must have at least one dimension")
+    dim = x.size(-1)
+    _check(groups > 0 and dim % groups == 0, "groups must divide the normalised dimension")
+    nw = _dense_parameter(norm_weight, dim, "weight")
+    w = _weight(weight)
+    n, k = w.shape
+    _check(k == dim, f"input must end in in_features={k}")
+    b = None
+    if bias is not None and bias.numel() > 0:
+        b = _dense_parameter(bias, n, "bias")
+    rows, count, stride = _rows(x, dim)
+    out = torch.empty((count, n), dtype=torch.float32, device=x.device)
+    lib = _load()
+    status = lib.mlk_rms_norm_linear(_ptr(rows), count, k, stride, _ptr(nw), float(eps), int(groups), _ptr(w),
+                                     _WEIGHT_DTYPES[w.dtype], _ptr(b), n, _ptr(out), n, _stream())
+    if status == 3:  # MLK_ERR_UNSUPPORTED: no fused form for this shape
+        return linear(rms_norm(x, norm_weight, eps, groups), weight, bias)
+    if status != 0:
+        raise RuntimeError(lib.mlk_last_error().decode())
+    return out.view(*x.shape[:-1], n)
 
 
 def swiglu_mlp(input, in_weight, in_bias=None, out_weight=None, out_bias=None):
@@ -749,7 +799,8 @@ def exported_symbols() -> list[str]:
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent", "mlk_mamba3_siso_forward",
-            "mlk_mamba3_siso_step", "mlk_linear", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend"]
+            "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear", "mlk_mla_rope_qk",
+            "mlk_attention", "mlk_mla_attend"]
 
 
 def math_check(x: torch.Tensor) -> dict:

@@ -173,3 +173,65 @@ def test_stage1_forward_two_layers(dev, oracle):
         else:
             hidden, mamba_in = oracle.add_rms_norm(hidden, ffn, packs_np[i + 1][0], 1e-5, groups)
     assert_close(out, hidden, name="stage1_forward")
+
+
+# linear followed by the residual add, across the kernel forms: one wave per tile (small row
+# counts), the row-layout form (fp32 weights, K within a chunk), the tiled form (bf16 weights,
+# K within two chunks) and the K-chunked form (K beyond two chunks).
+RESIDUAL_SHAPES = [(2048, 128, 64, False), (300, 96, 70, True), (20000, 128, 100, True), (9000, 256, 336, False),
+                   (5000, 520, 40, True)]
+
+
+@pytest.mark.parametrize("M,K,N,with_bias", RESIDUAL_SHAPES)
+@pytest.mark.parametrize("wdt", ["f32", "bf16"])
+def test_linear_residual_equals_linear_then_add(dev, M, K, N, with_bias, wdt):
+    from montlok import _C
+
+    g = torch.Generator(device="cpu").manual_seed(M + K + N)
+    x = torch.randn(M, K, generator=g).to(dev)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dev)
+    if wdt == "bf16":
+        w = w.bfloat16()
+    b = torch.randn(N, generator=g).to(dev) if with_bias else None
+    r = torch.randn(M, N, generator=g).to(dev)
+    fused = _C.linear_residual(x, w, b, r)
+    separate = r + _C.linear(x, w, b)
+    assert torch.equal(fused, separate), f"{M}x{K}->{N} {wdt}"
+
+
+@pytest.mark.parametrize("M,K,N,groups", [(2048, 64, 304, 8), (300, 64, 70, 4), (1000, 128, 96, 2), (77, 128, 33, 8),
+                                          (500, 256, 64, 4), (64, 256, 300, 16), (250, 96, 50, 12),
+                                          (300, 128, 40, 4)])
+@pytest.mark.parametrize("wdt", ["f32", "bf16"])
+def test_rms_norm_linear_equals_the_two_operators(dev, M, K, N, groups, wdt):
+    """Groups of 8, 16, 32 and 64 floats on the fused form, bit for bit against rms_norm then linear."""
+    from montlok import _C
+
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + K + N + groups)
+    x = (torch.randn(M, K, generator=g) * 3).to(dev)
+    nw = (torch.rand(K, generator=g) + 0.5).to(dev)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dev)
+    if wdt == "bf16":
+        w = w.bfloat16()
+    b = torch.randn(N, generator=g).to(dev)
+    fused = _C.rms_norm_linear(x, nw, 1e-5, groups, w, b)
+    separate = _C.linear(_C.rms_norm(x, nw, 1e-5, groups), w, b)
+    assert torch.equal(fused, separate), f"{M}x{K}->{N} groups {groups} {wdt}"
+
+
+def test_rms_norm_linear_beyond_the_fused_form(dev):
+    """Row counts that fill the chip, and groups of 4 floats, run the two operators."""
+    from montlok import _C
+    from montlok._C import _load
+
+    g = torch.Generator(device="cpu").manual_seed(9)
+    for M, K, groups in ((40000, 64, 8), (100, 64, 16)):
+        x = torch.randn(M, K, generator=g).to(dev)
+        nw = (torch.rand(K, generator=g) + 0.5).to(dev)
+        w = (torch.randn(48, K, generator=g) / 8).to(dev)
+        out = torch.empty(M, 48, device=dev)
+        status = _load().mlk_rms_norm_linear(x.data_ptr(), M, K, K, nw.data_ptr(), 1e-5, groups, w.data_ptr(), 0, None,
+                                             48, out.data_ptr(), 48, torch.cuda.current_stream().cuda_stream)
+        assert status == 3
+        fused = _C.rms_norm_linear(x, nw, 1e-5, groups, w)
+        assert torch.equal(fused, _C.linear(_C.rms_norm(x, nw, 1e-5, groups), w))
