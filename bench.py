@@ -560,18 +560,21 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
     assert torch.equal(outs[0], eager), "graph replay differs from the eager step"
 
     x = xs[0]
-    projected = _C.linear(x, w["in_w"])
-    att = _C._fused_attend(projected, B, L, d, H, hd, nope, kvr, w["ln_w"], w["ln_b"], 1e-5, w["kv_up"], cos, sin,
-                           scale).view(B, L, d)
+    projected = _C.linear(x, w["in_w"]).view(T, d + kvr + r)
+    latent = _C._latent_normed(projected, d, kvr, w["ln_w"], w["ln_b"], 1e-5)
+    att = _C._attend_normed(projected, latent, B, L, d, H, hd, nope, kvr, w["kv_up"], cos, sin, scale).view(B, L, d)
     f, h2 = 4, 2
     pairs = B * H * L * (L + 1) // 2
     ops = {
         "in_proj": dict(fn=lambda: _C.linear(x, w["in_w"]), bytes=T * d * f + (d + kvr + r) * d * h2 + T * (d + kvr + r) * f,
                         flops=2 * T * d * (d + kvr + r)),
-        # LayerNorm + kv_up + RoPE + causal attention in one kernel: q, the latent and k_rope in, attention out.
-        "mla_attend": dict(fn=lambda: _C._fused_attend(projected, B, L, d, H, hd, nope, kvr, w["ln_w"], w["ln_b"], 1e-5,
-                                                       w["kv_up"], cos, sin, scale),
-                           bytes=T * (d + kvr + r) * f + H * (nope + hd) * kvr * h2 + T * d * f,
+        # The latent's LayerNorm once per row, to bf16.
+        "latent_layer_norm": dict(fn=lambda: _C._latent_normed(projected, d, kvr, w["ln_w"], w["ln_b"], 1e-5),
+                                  bytes=T * kvr * (f + h2) + 2 * kvr * f),
+        # kv_up + RoPE + causal attention in one kernel: q, the normalised latent and k_rope in, attention out.
+        "mla_attend": dict(fn=lambda: _C._attend_normed(projected, latent, B, L, d, H, hd, nope, kvr, w["kv_up"], cos,
+                                                        sin, scale),
+                           bytes=T * (d + r) * f + T * kvr * h2 + H * (nope + hd) * kvr * h2 + T * d * f,
                            flops=2 * T * kvr * H * (nope + hd) + 4 * pairs * hd),
         "o_proj": dict(fn=lambda: _C.linear(att, w["o"]), bytes=2 * T * d * f + d * d * h2, flops=2 * T * d * d),
     }
@@ -583,7 +586,8 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
                       "synthetic (seeded N(0,1) inputs, N(0,0.02) bf16 weights)",
                       {"workload": "mla_causal_fwd", "windows": B, "seq_len": L, "d_model": d, "heads": H,
                        "head_dim": hd, "rope_dim": r, "kv_rank": kvr, "rope_theta": cfg["theta"],
-                       "step": "mla_forward: in_proj GEMM, fused LayerNorm + kv_up + RoPE + causal attention, o_proj GEMM",
+                       "step": "mla_forward: in_proj GEMM, latent LayerNorm (once per row, bf16), fused kv_up + RoPE + "
+                               "causal attention, o_proj GEMM",
                        "launch": f"HIP graph of {sets} steps over {sets} input sets, replayed",
                        "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")

@@ -392,12 +392,15 @@ struct MlaAttendArgs {
     float* out;  // [B, L, H, hd]
     int64_t batch, heads, length;
     float scale_log2;
+    const u16* latent;  // LNIN form: LayerNorm(kv_latent) rows [B * L, kv_rank], bf16
 };
 
 // The four-wave form keeps three blocks per CU (its LDS allows three): the
 // register budget is held to 168 so that the up-front loads do not cost a
 // block.
-template <int HD, int NOPE, int KV, int NW, int TPW>
+// LNIN: the latent rows arrive normalised, in bf16 (the in_proj's LayerNorm
+// epilogue, the same arithmetic as below), and the block skips its LayerNorm.
+template <int HD, int NOPE, int KV, int NW, int TPW, bool LNIN>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 3 : 1)))
 void mla_attend_kernel(MlaAttendArgs p) {
     constexpr int THREADS = 64 * NW;
@@ -459,12 +462,24 @@ void mla_attend_kernel(MlaAttendArgs p) {
     static_assert((LMAX * QN) % THREADS == 0, "q units must split evenly");
     constexpr int NI = LMAX * QN / THREADS;
     const int lr = tid >> 4, lc = tid & 15;
-    float4 xs[PASSES];
+    constexpr int LATI = LMAX * (KV / 8) / THREADS;  // LNIN: 16-byte units of the bf16 latent rows per thread
+    static_assert(!LNIN || (LMAX * (KV / 8)) % THREADS == 0, "latent units must split evenly");
+    float4 xs[LNIN ? 1 : PASSES];
+    uint4 lat[LNIN ? LATI : 1];
+    if constexpr (LNIN) {
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-        const int row = ps * (THREADS / 16) + lr;
-        const int rc = row < L ? row : L - 1;
-        xs[ps] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.kv_off + 4 * lc);
+        for (int it = 0; it < LATI; ++it) {
+            const int u = tid + it * THREADS;
+            const int row = u / (KV / 8), rc = row < L ? row : L - 1;
+            lat[it] = *reinterpret_cast<const uint4*>(p.latent + (b * L + rc) * static_cast<int64_t>(KV) + 8 * (u % (KV / 8)));
+        }
+    } else {
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int row = ps * (THREADS / 16) + lr;
+            const int rc = row < L ? row : L - 1;
+            xs[ps] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.kv_off + 4 * lc);
+        }
     }
     uint4 wur[WUI];
 #pragma unroll
@@ -496,57 +511,66 @@ void mla_attend_kernel(MlaAttendArgs p) {
         const int row = u / QN, rc = row < L ? row : L - 1;
         qn[it] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.q_off + h * HD + 4 * (u % QN));
     }
-    const float4 wv = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
-    const float4 bv = p.ln_b ? *reinterpret_cast<const float4*>(p.ln_b + 4 * lc) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (LNIN) {
+#pragma unroll
+        for (int it = 0; it < LATI; ++it) {
+            const int u = tid + it * THREADS;
+            const int row = u / (KV / 8);
+            *reinterpret_cast<uint4*>(xq_s + row * XP + 8 * (u % (KV / 8))) = row < L ? lat[it] : uint4{0u, 0u, 0u, 0u};
+        }
+    } else {
+        const float4 wv = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
+        const float4 bv = p.ln_b ? *reinterpret_cast<const float4*>(p.ln_b + 4 * lc) : make_float4(0.f, 0.f, 0.f, 0.f);
 
-    // LayerNorm of the latent rows into xq_s (bf16), the kv_up rows into wu_s.
-    // The passes (rows) advance together, one reduction level at a time, so
-    // that their cross-lane exchanges overlap; each row's arithmetic is that
-    // of layer_norm_vec_kernel with 16 lanes per row.
-    {
-        const double inv_dim = 1.0 / static_cast<double>(KV);
-        double mean[PASSES], sumsq[PASSES];  // the centred values are recomputed where used
+        // LayerNorm of the latent rows into xq_s (bf16), the kv_up rows into wu_s.
+        // The passes (rows) advance together, one reduction level at a time, so
+        // that their cross-lane exchanges overlap; each row's arithmetic is that
+        // of layer_norm_vec_kernel with 16 lanes per row.
+        {
+            const double inv_dim = 1.0 / static_cast<double>(KV);
+            double mean[PASSES], sumsq[PASSES];  // the centred values are recomputed where used
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            const float4 x = xs[ps];
-            mean[ps] = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
-                       (static_cast<double>(x.z) + static_cast<double>(x.w));
-        }
-        auto row_sums = [](double (&v)[PASSES]) {  // butterfly over the row's 16 lanes: xor 8, 4, 2, 1
+            for (int ps = 0; ps < PASSES; ++ps) {
+                const float4 x = xs[ps];
+                mean[ps] = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
+                           (static_cast<double>(x.z) + static_cast<double>(x.w));
+            }
+            auto row_sums = [](double (&v)[PASSES]) {  // butterfly over the row's 16 lanes: xor 8, 4, 2, 1
 #pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<8>(v[ps]);
+                for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<8>(v[ps]);
 #pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<4>(v[ps]);
+                for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<4>(v[ps]);
 #pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<2>(v[ps]);
+                for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<2>(v[ps]);
 #pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<1>(v[ps]);
-        };
-        row_sums(mean);
+                for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<1>(v[ps]);
+            };
+            row_sums(mean);
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            const float4 x = xs[ps];
-            mean[ps] *= inv_dim;
-            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
-            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
-            sumsq[ps] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
-        }
-        row_sums(sumsq);
+            for (int ps = 0; ps < PASSES; ++ps) {
+                const float4 x = xs[ps];
+                mean[ps] *= inv_dim;
+                const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
+                const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
+                sumsq[ps] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+            }
+            row_sums(sumsq);
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            const int row = ps * (THREADS / 16) + lr;
-            const float4 x = xs[ps];
-            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
-            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
-            const double rstd = 1.0 / sqrt(fma(sumsq[ps], inv_dim, p.ln_eps));
-            const bool active = row < L;
-            const u16 o0 = active ? AttnElem<true>::from(static_cast<float>((a0 * rstd) * wv.x + static_cast<double>(bv.x))) : u16(0);
-            const u16 o1 = active ? AttnElem<true>::from(static_cast<float>((a1 * rstd) * wv.y + static_cast<double>(bv.y))) : u16(0);
-            const u16 o2 = active ? AttnElem<true>::from(static_cast<float>((a2 * rstd) * wv.z + static_cast<double>(bv.z))) : u16(0);
-            const u16 o3 = active ? AttnElem<true>::from(static_cast<float>((a3 * rstd) * wv.w + static_cast<double>(bv.w))) : u16(0);
-            *reinterpret_cast<uint2*>(xq_s + row * XP + 4 * lc) =
-                make_uint2(static_cast<uint32_t>(o0) | (static_cast<uint32_t>(o1) << 16),
-                           static_cast<uint32_t>(o2) | (static_cast<uint32_t>(o3) << 16));
+            for (int ps = 0; ps < PASSES; ++ps) {
+                const int row = ps * (THREADS / 16) + lr;
+                const float4 x = xs[ps];
+                const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
+                const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
+                const double rstd = 1.0 / sqrt(fma(sumsq[ps], inv_dim, p.ln_eps));
+                const bool active = row < L;
+                const u16 o0 = active ? AttnElem<true>::from(static_cast<float>((a0 * rstd) * wv.x + static_cast<double>(bv.x))) : u16(0);
+                const u16 o1 = active ? AttnElem<true>::from(static_cast<float>((a1 * rstd) * wv.y + static_cast<double>(bv.y))) : u16(0);
+                const u16 o2 = active ? AttnElem<true>::from(static_cast<float>((a2 * rstd) * wv.z + static_cast<double>(bv.z))) : u16(0);
+                const u16 o3 = active ? AttnElem<true>::from(static_cast<float>((a3 * rstd) * wv.w + static_cast<double>(bv.w))) : u16(0);
+                *reinterpret_cast<uint2*>(xq_s + row * XP + 4 * lc) =
+                    make_uint2(static_cast<uint32_t>(o0) | (static_cast<uint32_t>(o1) << 16),
+                               static_cast<uint32_t>(o2) | (static_cast<uint32_t>(o3) << 16));
+            }
         }
     }
 #pragma unroll
@@ -856,9 +880,45 @@ extern "C" mlk_status mlk_mla_attend(const float* projected, int64_t batch, int6
     const dim3 grid(static_cast<unsigned>(batch * heads));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (cfg32) {
-        hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, false>), grid, dim3(256), 0, s, p);
     } else {
-        hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2>), grid, dim3(512), 0, s, p);
+        hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, false>), grid, dim3(512), 0, s, p);
     }
     return launch_status("mla_attend");
+}
+
+extern "C" mlk_status mlk_mla_attend_normed(const float* projected, int64_t batch, int64_t length,
+                                            int64_t proj_token_stride, int64_t q_offset, int64_t k_rope_offset,
+                                            int64_t heads, int64_t head_dim, int64_t nope_dim, int64_t kv_rank,
+                                            const void* latent_normed, const void* kv_up_weight,
+                                            const float* cosine, const float* sine, double scale, float* out,
+                                            mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 1 && heads > 0, "invalid MLA geometry");
+    const bool cfg32 = head_dim == 32 && nope_dim == 16 && kv_rank == 64 && length <= 128;
+    const bool cfg64 = head_dim == 64 && nope_dim == 32 && kv_rank == 64 && length <= 256;
+    if (!cfg32 && !cfg64) {
+        set_error("mla_attend: geometry without a fused kernel (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    if (k_rope_offset % 4 != 0 || !aligned16(cosine) || !aligned16(sine)) {
+        set_error("mla_attend: k_rope and the cos/sin tables are read as 16-byte vectors (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    MLK_CHECK(proj_token_stride % 4 == 0 && q_offset % 4 == 0 && aligned16(projected) && aligned16(latent_normed) &&
+                  aligned16(kv_up_weight) && aligned16(out),
+              "mla_attend: operands must be 16-byte aligned");
+    if (batch == 0) return MLK_OK;
+    MLK_CHECK(projected && latent_normed && kv_up_weight && cosine && sine && out, "null tensor pointer");
+    MLK_CHECK(batch * heads <= 0x7fffffff, "too many windows x heads for one launch");
+    MlaAttendArgs p{projected, proj_token_stride, q_offset, 0, k_rope_offset, nullptr, nullptr, 0.0,
+                    static_cast<const u16*>(kv_up_weight), cosine, sine, out, batch, heads, length,
+                    static_cast<float>(scale * 1.4426950408889634), static_cast<const u16*>(latent_normed)};
+    const dim3 grid(static_cast<unsigned>(batch * heads));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (cfg32) {
+        hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, true>), grid, dim3(256), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, true>), grid, dim3(512), 0, s, p);
+    }
+    return launch_status("mla_attend_normed");
 }

@@ -163,12 +163,14 @@ mlk_status launch_rms(const float* x, const float* right, const float* w, int64_
 
 // LayerNorm: one wave per row, the row held in registers as float4 chunks
 // when possible (two passes over registers: mean, then centred squares).
-template <int CPL>
+// BF16OUT: the float results rounded once more to bf16 (round to nearest
+// even), written as bf16 rows of dim.
+template <int CPL, bool BF16OUT = false>
 __global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __restrict__ x,
                                                                 const float* __restrict__ w,
                                                                 const float* __restrict__ bias, int64_t rows,
                                                                 int64_t dim, int64_t row_stride, double eps,
-                                                                float* __restrict__ out) {
+                                                                void* __restrict__ out) {
     // LPG lanes per row: dim = 4 * CPL * LPG with LPG = 64 / rows-per-wave.
     const int lpg = static_cast<int>(dim / (4 * CPL));
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / lpg) + threadIdx.x / lpg;
@@ -206,7 +208,6 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __r
     for (int mask = lpg / 2; mask > 0; mask >>= 1) sumsq += shfl_xor_d(sumsq, mask);
     if (!active) return;
     const double rstd = 1.0 / sqrt(fma(sumsq, inv_dim, eps));
-    float* outr = out + row * dim;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int off = (c * lpg + li) * 4;
@@ -215,7 +216,13 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __r
         o.y = static_cast<float>(((static_cast<double>(v[c].y) - mean) * rstd) * wv[c].y + static_cast<double>(bv[c].y));
         o.z = static_cast<float>(((static_cast<double>(v[c].z) - mean) * rstd) * wv[c].z + static_cast<double>(bv[c].z));
         o.w = static_cast<float>(((static_cast<double>(v[c].w) - mean) * rstd) * wv[c].w + static_cast<double>(bv[c].w));
-        *reinterpret_cast<float4*>(outr + off) = o;
+        if constexpr (BF16OUT) {
+            auto h = [](float f) { return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f))); };
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + row * dim + off) =
+                make_uint2(h(o.x) | (h(o.y) << 16), h(o.z) | (h(o.w) << 16));
+        } else {
+            *reinterpret_cast<float4*>(static_cast<float*>(out) + row * dim + off) = o;
+        }
     }
 }
 
@@ -324,6 +331,25 @@ mlk_status mlk_layer_norm(const float* x, int64_t rows, int64_t dim, int64_t row
     hipLaunchKernelGGL(layer_norm_scalar_kernel, dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias, rows, dim,
                        row_stride, eps_f, out);
     return launch_status("layer_norm");
+}
+
+mlk_status mlk_layer_norm_bf16(const float* x, int64_t rows, int64_t dim, int64_t row_stride, const float* weight,
+                               const float* bias, double eps, void* out, mlk_stream_t stream) {
+    MLK_CHECK(rows >= 0 && dim >= 1, "x must have at least one dimension");
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
+                         (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0) && row_stride % 4 == 0;
+    const int64_t chunks = dim / 4;
+    if (!aligned || dim % 4 != 0 || chunks > 64 || (chunks & (chunks - 1)) != 0) {
+        set_error("layer_norm_bf16: rows without the vector form (use layer_norm)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    if (rows == 0) return MLK_OK;
+    MLK_CHECK(x != nullptr && weight != nullptr && out != nullptr, "null tensor pointer");
+    const int64_t blocks = ceil_div(rows, kBlock / chunks);
+    hipLaunchKernelGGL((layer_norm_vec_kernel<1, true>), dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias, rows,
+                       dim, row_stride, static_cast<double>(static_cast<float>(eps)), out);
+    return launch_status("layer_norm_bf16");
 }
 
 mlk_status mlk_swiglu(const float* x, int64_t rows, int64_t hidden, int64_t row_stride, float* out,

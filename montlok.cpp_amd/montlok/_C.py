@@ -45,6 +45,9 @@ def _load():
         "mlk_linear": [_vp, _i64, _i64, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp],
         "mlk_linear_residual": [_vp, _i64, _i64, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp, _i64, _vp],
         "mlk_rms_norm_linear": [_vp, _i64, _i64, _i64, _vp, _dbl, _i64, _vp, C.c_int32, _vp, _i64, _vp, _i64, _vp],
+        "mlk_layer_norm_bf16": [_vp, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp],
+        "mlk_mla_attend_normed": [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _dbl,
+                                  _vp, _vp],
         "mlk_mla_rope_qk": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
         "mlk_mla_attend": [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp,
                            _vp, _dbl, _vp, _vp],
@@ -701,6 +704,67 @@ def _fused_attend(projected, batch, length, q_width, n_heads, head_dim, nope_dim
     return out
 
 
+def _latent_normed(projected: torch.Tensor, q_width: int, kv_lora_rank: int, kv_norm_weight, kv_norm_bias,
+                   kv_norm_eps: float):
+    """LayerNorm of the latent columns of the in_proj rows [count, W], once per row, rounded to bf16
+    (the form the fused attention takes); None where the rows have no vector form."""
+    count, n = projected.shape
+    lw = _dense_parameter(kv_norm_weight, kv_lora_rank, "kv_norm.weight")
+    lb = None if kv_norm_bias is None or kv_norm_bias.numel() == 0 else _dense_parameter(kv_norm_bias, kv_lora_rank,
+                                                                                        "kv_norm.bias")
+    latent = torch.empty((count, kv_lora_rank), dtype=torch.bfloat16, device=projected.device)
+    lib = _load()
+    status = lib.mlk_layer_norm_bf16(_ptr(projected) + 4 * q_width, count, kv_lora_rank, n, _ptr(lw), _ptr(lb),
+                                     float(kv_norm_eps), _ptr(latent), _stream())
+    if status == 3:  # MLK_ERR_UNSUPPORTED
+        return None
+    if status != 0:
+        raise RuntimeError(lib.mlk_last_error().decode())
+    return latent
+
+
+def _attend_normed(projected: torch.Tensor, latent: torch.Tensor, batch, length, q_width, n_heads, head_dim,
+                   nope_dim, kv_lora_rank, kv_up_weight, cosine, sine, scale):
+    """The fused attention reading the normalised bf16 latent; None where it is not built."""
+    rope = head_dim - nope_dim
+    up = _weight(kv_up_weight, "kv_up_weight")
+    _check(tuple(cosine.shape) == (length, rope) and cosine.is_contiguous(), "cos must be contiguous [L,rope_dim]")
+    _check(sine.shape == cosine.shape and sine.is_contiguous(), "sin must be contiguous [L,rope_dim]")
+    n = projected.size(-1)
+    out = torch.empty((batch, length, n_heads, head_dim), dtype=torch.float32, device=projected.device)
+    lib = _load()
+    status = lib.mlk_mla_attend_normed(_ptr(projected), batch, length, n, 0, q_width + kv_lora_rank, n_heads,
+                                       head_dim, nope_dim, kv_lora_rank, _ptr(latent), _ptr(up), _ptr(cosine),
+                                       _ptr(sine), float(scale), _ptr(out), _stream())
+    if status == 3:
+        return None
+    if status != 0:
+        raise RuntimeError(lib.mlk_last_error().decode())
+    return out
+
+
+def _fused_attend_ln(x, in_proj_weight, batch, length, q_width, n_heads, head_dim, nope_dim, kv_lora_rank,
+                     kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, cosine, sine, scale):
+    """in_proj, the latent LayerNorm once per row into bf16, then the fused attention reading the
+    normalised latent (rather than normalising it again in every head's block): bit-identical to linear
+    followed by _fused_attend. None where a kernel is not built for the geometry."""
+    geometry = (head_dim, nope_dim, kv_lora_rank) in ((32, 16, 64), (64, 32, 64)) and \
+        length <= (128 if head_dim == 32 else 256)
+    if not geometry or kv_up_weight.dtype != torch.bfloat16:
+        return None
+    w = _weight(in_proj_weight, "in_proj_weight")
+    n, k = w.shape
+    _check(x.size(-1) == k, f"input must end in in_features={k}")
+    rows, count, stride = _rows(x, k)
+    projected = torch.empty((count, n), dtype=torch.float32, device=x.device)
+    _linear_into(rows, count, stride, w, None, projected, n)
+    latent = _latent_normed(projected, q_width, kv_lora_rank, kv_norm_weight, kv_norm_bias, kv_norm_eps)
+    if latent is None:
+        return None
+    return _attend_normed(projected, latent, batch, length, q_width, n_heads, head_dim, nope_dim, kv_lora_rank,
+                          kv_up_weight, cosine, sine, scale)
+
+
 def _mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight,
                  cosine, sine, n_heads, head_dim, nope_dim, kv_lora_rank, n_last, causal, scale, allow_fused):
     _require_f32_gpu(x, "x")
@@ -711,6 +775,12 @@ def _mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_n
     _check(n_last == 1 or n_last == length, "native MLA supports the final query or the full sequence")
     precision = torch.bfloat16 if _weight(in_proj_weight, "in_proj_weight").dtype == torch.bfloat16 else torch.float32
     full = n_last == length
+    if allow_fused and full and causal and precision == torch.bfloat16:
+        attended = _fused_attend_ln(x, in_proj_weight, batch, length, d_model, n_heads, head_dim, nope_dim,
+                                    kv_lora_rank, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, cosine,
+                                    sine, scale)
+        if attended is not None:
+            return linear(attended.view(batch, length, d_model), out_weight)
     projected = linear(x, in_proj_weight)
     if allow_fused and full and causal and precision == torch.bfloat16:
         attended = _fused_attend(projected, batch, length, d_model, n_heads, head_dim, nope_dim, kv_lora_rank,
@@ -799,8 +869,8 @@ def exported_symbols() -> list[str]:
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent", "mlk_mamba3_siso_forward",
-            "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear", "mlk_mla_rope_qk",
-            "mlk_attention", "mlk_mla_attend"]
+            "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear",
+            "mlk_layer_norm_bf16", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend", "mlk_mla_attend_normed"]
 
 
 def math_check(x: torch.Tensor) -> dict:

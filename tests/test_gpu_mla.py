@@ -204,7 +204,8 @@ def test_mla_errors(dev):
 @pytest.mark.parametrize("B,L,H,hd,nope", [(16, 128, 8, 32, 16),   # MLA block geometry
                                            (8, 256, 4, 64, 32),    # full-stack MLA geometry
                                            (3, 100, 8, 32, 16),    # windows not a multiple of 8, ragged length
-                                           (2, 77, 4, 64, 32)])
+                                           (2, 77, 4, 64, 32),
+                                           (48, 128, 8, 32, 16), (60, 100, 8, 32, 16)])
 def test_fused_attend_equals_separate_kernels(dev, B, L, H, hd, nope):
     """With bf16 weights the full causal mla_forward runs LayerNorm, kv_up, RoPE and attention in one
     kernel; it must give the separate kernels' result bit for bit."""
@@ -229,3 +230,26 @@ def test_fused_attend_equals_separate_kernels(dev, B, L, H, hd, nope):
 def rope_tables_t(length: int, rope_dim: int):
     cos, sin = rope_tables(length, rope_dim)
     return torch.from_numpy(cos), torch.from_numpy(sin)
+
+
+@pytest.mark.parametrize("B,L,H,hd,nope", [(16, 128, 8, 32, 16), (8, 256, 4, 64, 32), (3, 100, 8, 32, 16),
+                                           (2, 77, 4, 64, 32)])
+def test_latent_layernorm_once_per_row(dev, B, L, H, hd, nope):
+    """The latent LayerNorm'd once per row into bf16 feeds the attention that skips its own LayerNorm: the
+    result equals the attention that normalises in every head's block, bit for bit."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(B + L + hd)
+    d, kvr, rope = H * hd, 64, hd - nope
+    bf = torch.bfloat16
+    x = torch.randn(B, L, d, generator=g).to(dev)
+    in_w = (torch.randn(d + kvr + rope, d, generator=g) * 0.02).to(dev, bf)
+    up_w = (torch.randn(H * (nope + hd), kvr, generator=g) * 0.02).to(dev, bf)
+    ln_w = (1 + 0.1 * torch.randn(kvr, generator=g)).to(dev)
+    ln_b = (0.1 * torch.randn(kvr, generator=g)).to(dev)
+    cos, sin = (t.to(dev) for t in rope_tables_t(L, rope))
+    att = _C._fused_attend_ln(x, in_w, B, L, d, H, hd, nope, kvr, ln_w, ln_b, 1e-5, up_w, cos, sin, hd ** -0.5)
+    assert att is not None, "the geometry has the fused kernels"
+    projected = _C.linear(x, in_w)
+    ref = _C._fused_attend(projected, B, L, d, H, hd, nope, kvr, ln_w, ln_b, 1e-5, up_w, cos, sin, hd ** -0.5)
+    assert torch.equal(att, ref)
