@@ -414,7 +414,9 @@ void mla_attend_kernel(MlaAttendArgs p) {
     constexpr int OT = HD / 16;
     static_assert(HD <= KV && KV == 64 && HD % 32 == 0 && UPW % 16 == 0 && NOPE % 4 == 0 && HALF % 4 == 0,
                   "geometry");
-    __shared__ __attribute__((aligned(16))) u16 xq_s[LMAX * XP];  // LN(kv_latent); later q (pitch KP)
+    // LN(kv_latent), then q (pitch KP); the LNIN form keeps only q here (its
+    // kv_up operands go from memory into registers).
+    __shared__ __attribute__((aligned(16))) u16 xq_s[LMAX * (LNIN ? KP : XP)];
     __shared__ __attribute__((aligned(16))) u16 wu_s[UPW * XP];
     __shared__ __attribute__((aligned(16))) u16 k_s[LMAX * KP];
     __shared__ __attribute__((aligned(16))) u16 vt_s[HD * VP];
@@ -462,16 +464,21 @@ void mla_attend_kernel(MlaAttendArgs p) {
     static_assert((LMAX * QN) % THREADS == 0, "q units must split evenly");
     constexpr int NI = LMAX * QN / THREADS;
     const int lr = tid >> 4, lc = tid & 15;
-    constexpr int LATI = LMAX * (KV / 8) / THREADS;  // LNIN: 16-byte units of the bf16 latent rows per thread
-    static_assert(!LNIN || (LMAX * (KV / 8)) % THREADS == 0, "latent units must split evenly");
+    // LNIN: wave w computes kv_up for the row tiles w + NW j, and loads their
+    // A fragments (row 16 (w + NW j) + l, k = 32 ks + 8 g) of the normalised
+    // latent straight into registers.
+    constexpr int RPW = LMAX / 16 / NW;
+    static_assert(!LNIN || (LMAX / 16) % NW == 0, "kv_up row tiles must split evenly over the waves");
     float4 xs[LNIN ? 1 : PASSES];
-    uint4 lat[LNIN ? LATI : 1];
+    uint4 afr[LNIN ? RPW : 1][KV / 32];
     if constexpr (LNIN) {
 #pragma unroll
-        for (int it = 0; it < LATI; ++it) {
-            const int u = tid + it * THREADS;
-            const int row = u / (KV / 8), rc = row < L ? row : L - 1;
-            lat[it] = *reinterpret_cast<const uint4*>(p.latent + (b * L + rc) * static_cast<int64_t>(KV) + 8 * (u % (KV / 8)));
+        for (int j = 0; j < RPW; ++j) {
+            const int row = 16 * (wave + NW * j) + li, rc = row < L ? row : L - 1;
+#pragma unroll
+            for (int ks = 0; ks < KV / 32; ++ks) {
+                afr[j][ks] = *reinterpret_cast<const uint4*>(p.latent + (b * L + rc) * static_cast<int64_t>(KV) + 32 * ks + 8 * g);
+            }
         }
     } else {
 #pragma unroll
@@ -511,14 +518,7 @@ void mla_attend_kernel(MlaAttendArgs p) {
         const int row = u / QN, rc = row < L ? row : L - 1;
         qn[it] = *reinterpret_cast<const float4*>(rows + rc * p.proj_ts + p.q_off + h * HD + 4 * (u % QN));
     }
-    if constexpr (LNIN) {
-#pragma unroll
-        for (int it = 0; it < LATI; ++it) {
-            const int u = tid + it * THREADS;
-            const int row = u / (KV / 8);
-            *reinterpret_cast<uint4*>(xq_s + row * XP + 8 * (u % (KV / 8))) = row < L ? lat[it] : uint4{0u, 0u, 0u, 0u};
-        }
-    } else {
+    if constexpr (!LNIN) {
         const float4 wv = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
         const float4 bv = p.ln_b ? *reinterpret_cast<const float4*>(p.ln_b + 4 * lc) : make_float4(0.f, 0.f, 0.f, 0.f);
 
@@ -610,12 +610,18 @@ void mla_attend_kernel(MlaAttendArgs p) {
     {
         constexpr int RT = LMAX / 16, CT = UPW / 16;
         for (int tix = wave; tix < RT * CT; tix += NW) {
-            const int rt = tix / CT, ct = tix % CT;
+            // LNIN: tile (w + NW j, ct) for j, ct in order; otherwise tiles w, w + NW, ... in row-major order.
+            const int rt = LNIN ? wave + NW * (tix / (NW * CT)) : tix / CT;
+            const int ct = LNIN ? (tix / NW) % CT : tix % CT;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KV / 32; ++ks) {
-                const bf16x8 a = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const uint4*>(xq_s + (16 * rt + li) * XP + 32 * ks + 8 * g));
+                bf16x8 a;
+                if constexpr (LNIN) {  // rows past L are zero, as the LayerNorm form stores them
+                    a = __builtin_bit_cast(bf16x8, 16 * rt + li < L ? afr[tix / (NW * CT)][ks] : uint4{0u, 0u, 0u, 0u});
+                } else {
+                    a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xq_s + (16 * rt + li) * XP + 32 * ks + 8 * g));
+                }
                 const bf16x8 bw = __builtin_bit_cast(
                     bf16x8, *reinterpret_cast<const uint4*>(wu_s + (16 * ct + li) * XP + 32 * ks + 8 * g));
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bw, acc, 0, 0, 0);
