@@ -855,6 +855,7 @@ void scan_fused_kernel(ScanArgs a) {
     constexpr int NP = N + 4, WP = C + 4;
     constexpr int NPAIR = CT * (CT + 1) / 2;
     constexpr int RM = N / 2;  // rotary angles at most
+    constexpr bool kEarlyGate = DT == 2;
     static_assert(NTH % N == 0, "a thread keeps one q/k column across the chunk");
     __shared__ __attribute__((aligned(16))) float q_sh[C * NP];
     __shared__ __attribute__((aligned(16))) float k_sh[C * NP];
@@ -926,6 +927,29 @@ void scan_fused_kernel(ScanArgs a) {
         const int col = 16 * wave + li, n_own = tid % N;
         const int Lc = last ? static_cast<int>(L - c0) : C;
         const int par = static_cast<int>((c0 / C) & 1);
+        // Output gates of this lane's (token, column) pairs from z alone:
+        // silu(z) in double (or z itself for an explicit gate). Two-wave blocks
+        // form them in the phases where the wave would otherwise wait (wave 0
+        // beside the coefficient wave in b, wave 1 beside the angle sums in c);
+        // other blocks just before the outputs. The values are held where they
+        // are formed: left to itself the compiler sinks each gate into the
+        // predicated store of its output (the last chunk's stores are guarded),
+        // where the fp64 chains run one after another.
+        double gz[CT][4];
+        auto gates = [&]() {
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const double z = static_cast<double>(zx[tt][v]);
+                    const double sz = z / (1.0 + exp_d(-z));
+                    gz[tt][v] = a.gate_logits ? sz : z;
+                }
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(gz[tt][v]));
+        };
         // a. Every global load of the chunk issued before the first wait
         //    (tokens past the end read the last token; they carry no weight).
         //    Offsets are 32-bit from the chunk's first row (checked at launch).
@@ -1089,6 +1113,9 @@ void scan_fused_kernel(ScanArgs a) {
                 }
             }
         }
+        if constexpr (kEarlyGate) {
+            if (wave == 0) gates();  // wave 1 runs the coefficients and decay weights meanwhile
+        }
         __syncthreads();
         // c. q and k (all values read before any is written back); the
         //    running angle sums into cum_s; the decay weights.
@@ -1123,6 +1150,9 @@ void scan_fused_kernel(ScanArgs a) {
                     cum_s[(t0 + i) * RM + tid] = static_cast<float>(running);
                 }
             }
+        }
+        if constexpr (kEarlyGate) {
+            if (wave == 1) gates();  // wave 0 runs the angle sums meanwhile
         }
         __syncthreads();
         // d. Rotation of the (2r, 2r + 1) pairs.
@@ -1181,26 +1211,10 @@ void scan_fused_kernel(ScanArgs a) {
         }
         if (tid < N) kp_s[par ^ 1][tid] = k_sh[(C - 1) * NP + tid];
         __syncthreads();
-        // f. This wave's output columns. The gate factors depend on z only and
-        //    are formed first, branch-free, so that their fp64 work can issue
-        //    while the matrix cores run the products below.
+        // f. This wave's output columns (gates formed above for two-wave
+        //    blocks, here otherwise).
         {
-            double gz[CT][4];
-#pragma unroll
-            for (int tt = 0; tt < CT; ++tt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const double z = static_cast<double>(zx[tt][v]);
-                    const double sz = z / (1.0 + exp_d(-z));
-                    gz[tt][v] = a.gate_logits ? sz : z;
-                }
-            // Held here: left to itself the compiler sinks each gate into the
-            // predicated store of its output (the last chunk's stores are
-            // guarded), where the eight fp64 chains run one after another.
-#pragma unroll
-            for (int tt = 0; tt < CT; ++tt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(gz[tt][v]));
+            if constexpr (!kEarlyGate) gates();
             int p0 = 0;  // index of pair (tt, 0)
 #pragma unroll
             for (int tt = 0; tt < CT; ++tt) {
