@@ -804,7 +804,8 @@ mlk_status mlk_mhc_combine(const float* streams, int64_t tokens, int64_t n, int6
                            int64_t token_stride, const float* res, const float* post, const float* out,
                            float* new_streams, float* collapsed, mlk_stream_t stream) {
     MLK_CHECK(n > 0 && d > 0, "streams must be non-empty");
-    MLK_CHECK(new_streams != nullptr || collapsed != nullptr, "mhc_combine needs an output");
+    MLK_CHECK(new_streams != nullptr || collapsed != nullptr || tokens == 0, "mhc_combine needs an output");
+    if (tokens == 0) return MLK_OK;
     return launch_combine(streams, tokens, n, d, stream_stride, token_stride, res, post, out, new_streams, collapsed,
                           stream);
 }
