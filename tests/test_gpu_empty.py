@@ -74,3 +74,33 @@ def test_mhc_combine_prepare_and_collapse_empty(dev):
     new, agg, pre, post2, res2 = _C.mhc_combine_prepare(streams, res, post, out, nw, 1e-5, pw, pb, qb, rb, *a, 20)
     assert new.shape == (0, 3, n, d) and agg.shape == (0, 3, d) and res2.shape == (0, 3, n, n)
     assert _C.mhc_combine_collapse(streams, res, post, out).shape[0] == 0
+
+
+def test_mamba3_step_empty(dev):
+    from montlok import _C
+
+    N, G, H, D, R = 16, 1, 2, 16, 4
+    W = 2 * H * D + 2 * G * N + 3 * H + R
+    ones = lambda *s: torch.ones(*s, device=dev)  # noqa: E731
+    state = _C.new_mamba3_state(0, H, N, D, R, dev)
+    out = _C.mamba3_siso_step(torch.empty(0, W, device=dev), state, ones(H, N), ones(H, N), ones(N), ones(N), ones(H),
+                              ones(H), N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    assert out.shape[0] == 0
+
+
+@pytest.mark.parametrize("hd,nope,bf16", [(32, 16, True), (32, 16, False), (64, 32, True)])
+def test_mla_forward_empty(dev, hd, nope, bf16):
+    from montlok import _C
+    from test_gpu_mla import rope_tables_t
+
+    H, kvr, L = 4, 64, 8
+    d, rope = H * hd, hd - nope
+    dt = torch.bfloat16 if bf16 else torch.float32
+    x = torch.empty(0, L, d, device=dev)
+    in_w = torch.randn(d + kvr + rope, d, device=dev).to(dt)
+    up_w = torch.randn(H * (nope + hd), kvr, device=dev).to(dt)
+    o_w = torch.randn(d, d, device=dev).to(dt)
+    cos, sin = (t.to(dev) for t in rope_tables_t(L, rope))
+    out = _C.mla_forward(x, in_w, x.new_empty(0), torch.ones(kvr, device=dev), None, 1e-5, up_w, o_w, cos, sin, H, hd,
+                         nope, kvr, L, True, hd ** -0.5)
+    assert out.shape == (0, L, d)
