@@ -41,6 +41,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16;
 
 constexpr int kThreads = 512;                  // 8 waves
@@ -604,6 +605,104 @@ void launch_small_norm(const LinearArgs& p, int64_t tiles, hipStream_t stream) {
     }
 }
 
+// bf16 weights with K <= 256 on the 32 x 32 x 16 matrix cores: each wave owns
+// 32 rows (256 per block), holds their bf16 x fragments for all of K, and
+// each W fragment read from LDS (32 columns x 16 k) feeds a 32-row product,
+// half the LDS traffic per row of the 16 x 16 x 32 form. Operands transposed
+// as in the tiled form (W as A, x as B): lane (h, l) of the accumulator holds
+// row l, columns 8j + 4h .. + 3 (j = 0..3) of a 32-column tile. W chunks of 64
+// columns are staged and double-buffered as in the other forms.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void linear_t32_kernel(LinearArgs p) {
+    using T = u16;
+    constexpr int KC = WTraits<true>::kKChunk;  // 256: all of K
+    constexpr int kPitch = WTraits<true>::kPitch;
+    constexpr int kSteps = KC / 16;
+    __shared__ __attribute__((aligned(16))) T w_lds[2][kColsPerChunk * kPitch];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * (2 * kRowsPerBlock) + 32 * wave;
+    const int64_t n_chunks = (p.N + kColsPerChunk - 1) / kColsPerChunk;
+    const int64_t my_chunks = (n_chunks - blockIdx.y + gridDim.y - 1) / gridDim.y;
+    if (my_chunks <= 0) return;
+    const int kspan = static_cast<int>((p.K + 31) / 32 * 32);
+    const bool vec_out = (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 &&
+                         (p.residual == nullptr ||
+                          ((reinterpret_cast<uintptr_t>(p.residual) & 15) == 0 && p.res_stride % 4 == 0));
+    auto n0_of = [&](int64_t c) { return (blockIdx.y + c * gridDim.y) * kColsPerChunk; };
+
+    WStage<true, VEC> stage;
+    stage.fetch(p, n0_of(0), 0, kspan);
+    // x fragments: step s holds row r32's k = 16 s + 8 h .. + 7 (zero past K or past the rows).
+    bf16x8 xf[kSteps];
+    {
+        const int64_t row = row0 + r32;
+        const bool live_row = row < p.rows;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            float v[8];
+            load_x8<VEC>(p, row, 16 * s + 8 * h, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xf[s][j] = static_cast<__bf16>(live_row ? v[j] : 0.0f);
+        }
+    }
+    stage.store(p, n0_of(0), w_lds[0], kspan);
+    __syncthreads();
+
+    for (int64_t c = 0; c < my_chunks; ++c) {
+        const int64_t n0 = n0_of(c);
+        const bool more = c + 1 < my_chunks;
+        if (more) stage.fetch(p, n0_of(c + 1), 0, kspan);
+        const T* buf = w_lds[c & 1];
+        f32x16 acc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[t][v] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            if (16 * s < kspan) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const bf16x8 wv = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4*>(buf + (32 * t + r32) * kPitch + 16 * s + 8 * h));
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv, xf[s], acc[t], 0, 0, 0);
+                }
+            }
+        }
+        const int64_t row = row0 + r32;
+        if (row < p.rows) {
+            float* orow = p.out + row * p.out_stride;
+            const float* rrow = p.residual != nullptr ? p.residual + row * p.res_stride : nullptr;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t col = n0 + 32 * t + 8 * j + 4 * h;
+                    f32x4 y = {acc[t][4 * j], acc[t][4 * j + 1], acc[t][4 * j + 2], acc[t][4 * j + 3]};
+                    if (p.bias != nullptr) {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) y[u] += p.bias[col + u < p.N ? col + u : p.N - 1];
+                    }
+                    if (col + 4 <= p.N && vec_out) {
+                        if (rrow != nullptr) y = *reinterpret_cast<const f32x4*>(rrow + col) + y;
+                        *reinterpret_cast<f32x4*>(orow + col) = y;
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            if (col + u < p.N) orow[col + u] = rrow != nullptr ? rrow[col + u] + y[u] : y[u];
+                        }
+                    }
+                }
+        }
+        if (more) stage.store(p, n0_of(c + 1), w_lds[(c + 1) & 1], kspan);
+        __syncthreads();
+    }
+}
+
 // Shapes too small to give the 128-row blocks one per CU (256 CUs), with K
 // held in at most eight 32-wide steps.
 bool small_shape(int64_t rows, int64_t K, int64_t N) {
@@ -627,6 +726,21 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
             launch_small<BF16W, 8>(p, tiles, stream);
         }
         return;
+    }
+    // bf16 weights with K within one chunk and a wide output (12 or more
+    // 64-column chunks): the 32 x 32 x 16 form, 256 rows per block (262144 x
+    // 256 -> 1192: 577 -> 513 us). Narrower outputs keep the 16 x 16 x 32
+    // form, whose smaller blocks give more parallelism (32768 x 256 -> 336:
+    // 28 us against 42 us; 262144 x 40 -> 256: 90 against 129 us).
+    if constexpr (BF16W) {
+        if (p.K <= KC && n_chunks >= 12) {
+            const int64_t row_blocks32 = ceil_div(rows, 2 * kRowsPerBlock);
+            int64_t gy32 = 1;
+            while (gy32 < n_chunks && row_blocks32 * gy32 < 512) ++gy32;
+            hipLaunchKernelGGL((linear_t32_kernel<VEC>), dim3(static_cast<unsigned>(row_blocks32), static_cast<unsigned>(gy32)),
+                               dim3(kThreads), 0, stream, p);
+            return;
+        }
     }
     // gy splits N only while there are fewer than ~512 blocks (two per CU).
     // Two row tiles per wave (half the LDS reads of W per row) measured

@@ -38,7 +38,9 @@ SHAPES = [(2048, 64, 304, False),    # RMSNorm->Mamba-3 block in_proj
           (64, 512, 1192, False),    # full-stack Mamba in_proj width
           (300, 96, 70, True),       # one wave per tile: ragged rows and N, K past the last 32-wide step
           (50, 200, 33, True),       # ... K = 200 (eight steps, the last two partly or wholly past K)
-          (16, 8, 16, False)]        # ... a single 8-wide k segment
+          (16, 8, 16, False),        # ... a single 8-wide k segment
+          (9000, 256, 1192, True),   # bf16: the 32x32x16 form (wide output), ragged row block
+          (5000, 96, 800, False)]    # ... K short of the chunk, N ragged
 
 
 @pytest.mark.parametrize("M,K,N,with_bias", SHAPES)
