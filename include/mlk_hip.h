@@ -88,11 +88,11 @@ mlk_status mlk_add_rms_norm(const float* left, const float* right, int64_t rows,
 mlk_status mlk_layer_norm(const float* x, int64_t rows, int64_t dim, int64_t row_stride, const float* weight,
                           const float* bias, double eps, float* out, mlk_stream_t stream);
 
-/* layer_norm as mlk_layer_norm computes it, each float result then rounded
- * to bf16 (nearest even) into out [rows, dim]: the normalised MLA latent in
- * the form the matrix cores take (mlk_mla_attend_normed). Built for 16-byte
- * aligned rows of 4 * 2^k floats (k <= 6); MLK_ERR_UNSUPPORTED otherwise.
- * No reference operator of its own. */
+/* layer_norm as mlk_layer_norm computes it (montlok.cpp:1057-1082), each
+ * float result then rounded to bf16 (nearest even) into out [rows, dim]: the
+ * kv_norm of mla_forward (montlok.cpp:1200) in the form the matrix cores take
+ * for its kv_up (:1201), as mlk_mla_attend_normed reads it. Built for 16-byte
+ * aligned rows of 4 * 2^k floats (k <= 6); MLK_ERR_UNSUPPORTED otherwise. */
 mlk_status mlk_layer_norm_bf16(const float* x, int64_t rows, int64_t dim, int64_t row_stride, const float* weight,
                                const float* bias, double eps, void* out, mlk_stream_t stream);
 
@@ -187,11 +187,11 @@ mlk_status mlk_mla_attend(const float* projected, int64_t batch, int64_t length,
                           const float* sine, double scale, float* out, mlk_stream_t stream);
 
 
-/* mlk_mla_attend with the latent already normalised: latent_normed holds
- * bf16 rows [B * L, kv_rank] (mlk_layer_norm_bf16 of the latent columns) and
- * the block skips its LayerNorm, which otherwise every head's block repeats;
- * everything else as mlk_mla_attend, and the same result bit for bit. No
- * reference operator of its own. */
+/* mlk_mla_attend with the latent already normalised (the part of mla_forward
+ * after its kv_norm, montlok.cpp:1201-1209): latent_normed holds bf16 rows
+ * [B * L, kv_rank] (mlk_layer_norm_bf16 of the latent columns) and the block
+ * skips its LayerNorm, which otherwise every head's block repeats; everything
+ * else as mlk_mla_attend, and the same result bit for bit. */
 mlk_status mlk_mla_attend_normed(const float* projected, int64_t batch, int64_t length, int64_t proj_token_stride,
                                  int64_t q_offset, int64_t k_rope_offset, int64_t heads, int64_t head_dim,
                                  int64_t nope_dim, int64_t kv_rank, const void* latent_normed,
