@@ -961,9 +961,9 @@ def main() -> int:
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU only: every GPU box of this build has one GPU (asked for --gpus "
-              f"{args.gpus}, WORLD_SIZE={world}). The workloads shard by independent windows/tokens/streams; "
-              f"see DESIGN.md for how the path would shard.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}). The workloads "
+              f"shard by independent windows, tokens and streams, one share per GPU, with no exchange between "
+              f"GPUs inside a step.", file=sys.stderr)
         return 2
     line = WORKLOADS[args.workload](args.steps, args.warmup, cpu=not args.no_cpu)
     print(json.dumps(line))

@@ -10,8 +10,8 @@ Two CPU implementations behind one numpy-level API:
                    checkout was available when ``oracle/Makefile`` ran.
 
 Only tests, ``__graft_entry__.smoke()`` and the cpu_baseline leg of
-``bench.py`` may import this package, and only as the checker or the timed
-baseline. The product path never routes through it.
+``bench.py`` may import this package, and only to check results or as the
+timed CPU baseline. The product path never routes through it.
 """
 
 from __future__ import annotations
