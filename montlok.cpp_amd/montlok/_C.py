@@ -809,7 +809,7 @@ def _mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_n
 
 
 def build_info() -> dict:
-    """Kernel variant and device of this build (replaces montlok.cpp:1417-1455)."""
+    """Kernel variant and device of this library (replaces montlok.cpp:1417-1455)."""
     lib = _load()
     buf = C.create_string_buffer(1024)
     _call("mlk_build_info", buf, len(buf))
@@ -860,7 +860,7 @@ def active_isa() -> str:
 
 def set_isa(name: str, force: bool = False) -> str:
     if name not in ("gfx950", "auto"):
-        raise RuntimeError(f"unknown kernel variant {name!r}: this build has gfx950 only")
+        raise RuntimeError(f"unknown kernel variant {name!r}: this library has gfx950 only")
     return "gfx950"
 
 

@@ -3,7 +3,7 @@
 The reference enables its CPU kernels with ``MONTLOK_CPP=1`` and per-family
 switches (``MONTLOK_CPP_LAYERS``, ``MONTLOK_CPP_MHC``; python/montlok/rdt/
 layers.py:32-39, mhc.py:62-69, mla.py:86-104) and falls back to the upstream
-PyTorch modules otherwise. This build ships the GPU kernels only: outside the
+PyTorch modules otherwise. This package ships the GPU kernels only: outside the
 conditions below a module raises instead of computing something else.
 """
 
@@ -24,7 +24,7 @@ def require_gpu_inference(module: str, x: torch.Tensor, family: str | None = Non
     """Raise unless ``x`` can take the GPU path: kernels enabled, fp32 on the ROCm device, no autograd."""
     if not backend_enabled(family):
         switch = f"MONTLOK_CPP=1{'' if family is None else f' and {family}!=0'}"
-        raise RuntimeError(f"{module}: the GPU kernels are switched off ({switch} enables them); this build has "
+        raise RuntimeError(f"{module}: the GPU kernels are switched off ({switch} enables them); this package has "
                            f"no other forward")
     if x.device.type != "cuda":
         raise RuntimeError(f"{module}: input must be on the ROCm device, got {x.device}")
