@@ -1050,33 +1050,64 @@ void scan_fused_kernel(ScanArgs a) {
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             }
-            const int wl = ct;
-            if (wl >= 0 && wl < C + 2) {
+            // Walkers: columns s < C, then Din (column kDin) and Wp (kWp), both
+            // with s = 0. Lane w < C + 2 walks t = s + 1 .. s + 16 of walker
+            // w; a walk longer than 16 steps (s < C - 17, and Din, Wp) has a
+            // second lane, C + 2 + j, for t = s + 17 .. C - 1. That lane first
+            // runs 16 multiply-only steps to form the same sequential
+            // products the first lane holds at t = s + 16, so every weight is
+            // bit-identical to one lane walking the whole column, while the
+            // wave issues 16 full steps instead of 31. Four-wave blocks keep
+            // one lane per walker (32 full steps): the split's registers cost
+            // them more than the shorter walk saves.
+            constexpr bool kSplit = DT <= 2;
+            constexpr int kFull = kSplit ? 16 : 32;  // full steps per lane (whole batches of 8)
+            constexpr int kLong = C - 17;  // columns whose walk exceeds 16 steps
+            static_assert(C + 2 + kLong + 2 <= 64, "the walkers' lanes must fit one wave");
+            const int hf = kSplit && ct >= C + 2 ? 1 : 0;
+            const int j2 = ct - (C + 2);
+            const int wl = hf == 0 ? ct : (j2 < kLong ? j2 : C + (j2 - kLong));
+            if (ct >= 0 && (hf == 0 ? ct < C + 2 : j2 < kLong + 2)) {
                 const int s = wl < C ? wl : 0;
                 const double b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
                 const double gam = wl < C ? static_cast<double>(coef[2][s]) : (wl == C ? static_cast<double>(coef[0][0]) : b0);
                 const double bet = wl + 1 < C ? static_cast<double>(coef[1][wl + 1]) : 0.0;
                 const int colw = wl < C ? wl : (wl == C ? kDin : kWp);
-                w_s[s * WP + colw] = static_cast<float>(gam * 1.0);  // t = s
-                // Step k handles t = s + 1 + k; alpha of t is read from a
-                // clamped slot. Steps with t >= C (and the one step past
-                // k = C - 2 that rounds the walk up to whole batches of 8) store
-                // into the sink row C, so no step is predicated. Each group of 4
-                // steps runs the two product chains first, then the 4
-                // independent weights, then the 4 stores.
+                if (hf == 0) w_s[s * WP + colw] = static_cast<float>(gam * 1.0);  // t = s
+                // Step k handles t = s + 1 + k with alpha from a clamped slot;
+                // steps with t >= C store into the sink row C, so no step is
+                // predicated.
+                double dd = 1.0, e = 1.0;
+                if constexpr (kSplit) {
+                    float al[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) al[k] = coef[0][min(s + 1 + k, C - 1)];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) {
+                        const double at = al[k];
+                        dd *= at;
+                        if (k > 0) e *= at;
+                    }
+                }
+                if (hf == 0) {  // (the first lane walks from t = s + 1)
+                    dd = 1.0;
+                    e = 1.0;
+                }
+                const int kb = 16 * hf;
                 float nx[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + i, C - 1)];
-                double dd = 1.0, e = 1.0;
+                for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + kb + i, C - 1)];
 #pragma unroll 1
-                for (int k0 = 0; k0 < C - 1; k0 += 8) {
+                for (int k0 = 0; k0 < kFull; k0 += 8) {
                     float al[8];
 #pragma unroll
                     for (int i = 0; i < 8; ++i) al[i] = nx[i];
-                    if (k0 + 8 < C - 1) {
+                    if (k0 + 8 < kFull) {
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + k0 + 8 + i, C - 1)];
+                        for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + kb + k0 + 8 + i, C - 1)];
                     }
+                    // Each group of 4 steps runs the two product chains first,
+                    // then the 4 independent weights, then the 4 stores.
 #pragma unroll
                     for (int i0 = 0; i0 < 8; i0 += 4) {
                         double ddv[4], ev[4];
@@ -1084,7 +1115,7 @@ void scan_fused_kernel(ScanArgs a) {
                         for (int i = 0; i < 4; ++i) {
                             const double at = al[i0 + i];
                             dd *= at;
-                            if (k0 + i0 + i > 0) e *= at;
+                            if (kb + k0 + i0 + i > 0) e *= at;
                             ddv[i] = dd;
                             ev[i] = e;
                         }
@@ -1093,7 +1124,7 @@ void scan_fused_kernel(ScanArgs a) {
                         for (int i = 0; i < 4; ++i) wv[i] = static_cast<float>(fma(bet, ev[i], gam * ddv[i]));
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const int t = s + 1 + k0 + i0 + i;
+                            const int t = s + 1 + kb + k0 + i0 + i;
                             w_s[(t < C ? t : C) * WP + colw] = wv[i];
                         }
                     }
