@@ -1,21 +1,31 @@
 #!/usr/bin/env python3
 """Throughput of the RDT4quant fused forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload mhc]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload block]
 
-Default workload: the mHC residual mix alone, fp32, n = 4 streams, d = 128,
-8192 tokens (64 windows of 128 tokens), 20 Sinkhorn iterations. One step is
-one hyper-connection over one batch: mhc_prepare (coefficients + aggregate),
-the wrapped layer as the identity (out = agg), mhc_combine (new streams).
-Inputs are resident in HBM before timing; the step rotates over enough
-independent input/output sets (more than the 256 MB Infinity Cache) that each
-step reads cold data.
+Default workload (the metric's configuration): the RMSNorm -> Mamba-3 block
+forward, fp32, 64 windows x 32 tokens, d_model 64, 4 heads of 32, d_state 16,
+expand 2, GroupedRMSNorm with 8 groups: one step is
+x + out_proj(mamba3(in_proj(GroupedRMSNorm(x)))) over the 64 windows, and the
+value is windows/s. Other workloads: ``mhc`` (the residual mix alone, 8192
+tokens, tokens/s), ``mla`` (causal MLA, 256 x 128 tokens, windows/s),
+``decode`` (65536 streams x 2 Mamba-3 blocks + head, stream-steps/s),
+``stack`` (the 4-layer hybrid stack, 1024 x 256 tokens, windows/s).
 
-Prints one JSON line: whole-job throughput (windows/s), the roofline of the
-dominant kernel (per-launch average from HIP events recorded on the kernels'
-stream inside the timed region) and the CPU baseline (the reference's CPU
-kernels compiled from its sources into oracle/_ref, timed on this host on a
-bounded sample, or the oracle port when that library is absent).
+Timing: W untimed steps (replays of one-step HIP graphs), then exactly K
+steps as one replay of a HIP graph that holds the K steps in order, between
+two HIP events, synchronized on both sides; ms_per_step is that region's
+time / K. Further replays of the same graph (30, or as many as fit in 10 s)
+give the median and spread of the per-step time. Inputs are resident in HBM
+before timing.
+
+Prints one JSON line: whole-job throughput, the roofline of the dominant
+kernel (per-launch average from HIP events over graph replays of that kernel
+on the stream it runs on) and the CPU baseline: the reference's CPU kernels
+compiled from its sources into oracle/_ref (the oracle port where that
+library is absent) with torch CPU for GEMMs and SDPA, timed on this host with
+every core and with one thread, warm-up 5 then the median of at least 30
+steps, FTZ/DAZ on.
 """
 
 from __future__ import annotations
@@ -36,7 +46,7 @@ for p in (ROOT, ROOT / "montlok.cpp_amd"):
 HBM_PEAK_GBS = 8000.0
 METRIC = "windows/sec for the RDT4quant block fwd at 1 GPU; % HBM or MFMA roofline"
 
-# mHC residual mix, n = 4, d = 128, 8192 tokens (64 windows x 128 tokens).
+# mHC residual mix alone, n = 4, d = 128, 8192 tokens (stored as 64 x 128), 20 Sinkhorn iterations.
 MHC = dict(n=4, d=128, windows=64, seq=128, iters=20)
 
 
@@ -55,10 +65,11 @@ def mhc_bytes(n: int, d: int, T: int) -> tuple[int, int]:
 
 
 def cpu_baseline_mhc(cfg: dict, budget_s: float = 12.0) -> dict:
-    """The reference's own CPU kernels (oracle/_ref) on the same workload."""
+    """The reference's own CPU kernels (oracle/_ref) on the same workload (the oracle port where that library
+    is absent)."""
     import numpy as np
 
-    from oracle import Oracle, Reference, host_isa, reference_available
+    from oracle import Oracle, Reference, reference_available
 
     n, d, T = cfg["n"], cfg["d"], cfg["windows"] * cfg["seq"]
     rng = np.random.default_rng(0)
@@ -67,33 +78,23 @@ def cpu_baseline_mhc(cfg: dict, budget_s: float = 12.0) -> dict:
     pw = (rng.standard_normal((2 * n + n * n, d)) / np.sqrt(d)).astype(np.float64)
     pb, qb = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
     rb = rng.standard_normal((n, n)).astype(np.float32)
-    cores = len(os.sched_getaffinity(0))
-    if reference_available():
-        lib, kind = Reference(), "reference"
-        lib.set_threads(cores)
-        threads = cores
-        variant = lib.variant
-    else:
-        lib, kind = Oracle(), "port"
-        threads = 1
-        variant = "oracle"
+    ref = reference_available()
+    lib = Reference() if ref else Oracle()
 
-    def step():
-        agg, pre, post, res = lib.mhc_prepare(s, nw, 1e-5, pw, pb, qb, rb, 0.7, 0.7, 0.7, cfg["iters"])
-        lib.mhc_combine(s, res, post, agg)
+    def make_step(threads):
+        if ref:
+            lib.set_threads(threads)
 
-    step()
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        step()
-        reps += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= budget_s or reps >= 100000:
-            break
-    windows_per_s = reps * cfg["windows"] / elapsed
-    return {"value": windows_per_s, "unit": "windows/s", "cores": threads, "kind": kind,
-            "sample": f"{reps} full steps (prepare + combine, {T} tokens each) in {elapsed:.1f} s, "
-                      f"{variant} build, {threads} OpenMP threads of {cores} host cores"}
+        def step():
+            agg, pre, post, res = lib.mhc_prepare(s, nw, 1e-5, pw, pb, qb, rb, 0.7, 0.7, 0.7, cfg["iters"])
+            lib.mhc_combine(s, res, post, agg)
+        return step
+
+    line = _cpu_legs(make_step, T, "tokens/s", "reference" if ref else "port",
+                     f"full steps (prepare + combine, {T} tokens each) in the "
+                     f"{'reference ' + lib.variant if ref else 'oracle'} build, OpenMP threads = torch threads",
+                     budget_s)
+    return line
 
 
 def _graph(fn_list):
@@ -127,6 +128,52 @@ def _time_graph(g, replays: int) -> float:
     stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / replays
+
+
+def _gpu_steps(step_fns, steps: int, warmup: int, budget_s: float = 10.0) -> dict:
+    """Times exactly `steps` steps; step i runs step_fns[i % len(step_fns)].
+
+    The warm-up runs `warmup` steps as replays of one-step graphs. The `steps` steps are then captured, in
+    order, into one HIP graph, and the timed region is one replay of it between two HIP events, synchronized
+    on both sides: no host work between the steps. ms_per_step is that region's time / steps. Further
+    replays of the same graph (30, or as many as fit in `budget_s`, at least 3) give the median and the
+    spread of the per-step time."""
+    import statistics
+
+    import torch
+
+    n = len(step_fns)
+    singles = [_graph([fn]) for fn in step_fns]
+    for i in range(warmup):
+        singles[i % n].replay()
+    torch.cuda.synchronize()
+    g = _graph([step_fns[i % n] for i in range(steps)])
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    g.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+
+    reps = 30 if 30 * total_ms * 1e-3 <= budget_s else max(3, int(budget_s / max(total_ms * 1e-3, 1e-9)))
+    per = []
+    for _ in range(reps):
+        start.record(stream)
+        g.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        per.append(start.elapsed_time(stop) / steps)
+    per.sort()
+    return {"steps": steps, "ms_per_step": total_ms / steps, "timed_region_ms": total_ms,
+            "median_ms_per_step": statistics.median(per), "p10_ms_per_step": per[int(0.1 * (reps - 1))],
+            "p90_ms_per_step": per[int(0.9 * (reps - 1))], "median_replays": reps}
+
+
+def _timing_fields(t: dict) -> dict:
+    return {k: t[k] for k in ("timed_region_ms", "median_ms_per_step", "p10_ms_per_step", "p90_ms_per_step",
+                              "median_replays")}
 
 
 MFMA_PEAK_TFS = {"bf16": 2500.0, "f32": 157.3}
@@ -177,32 +224,55 @@ def _base_line(value, unit, steps, warmup, ms, dtype, data, config) -> dict:
             "data": data, "config": config}
 
 
-def _time_steps(step_fns, steps: int, warmup: int, per_graph: int):
-    """Captures `per_graph` steps in one graph; returns (steps actually timed, ms per step)."""
-    g = _graph(step_fns * per_graph if len(step_fns) == 1 else step_fns)
-    replays = max(1, steps // per_graph)
-    for _ in range(max(1, warmup // per_graph)):
-        g.replay()
-    return replays * per_graph, _time_graph(g, replays) / per_graph
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
-def _torch_cpu_threads() -> int:
+def _cpu_median(fn, budget_s: float, warmup: int = 5, min_samples: int = 30) -> tuple[float, int, float]:
+    """The reference harness's procedure (tools/rdt/bench_montlok_kernel.py:90-107): `warmup` untimed calls,
+    then timed calls until there are `min_samples` of them and `budget_s` has passed (at most 2 x budget_s);
+    returns (median seconds per call, samples, seconds spent)."""
+    import statistics
+
+    for _ in range(warmup):
+        fn()
+    samples, t_all = [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        samples.append(time.perf_counter() - t0)
+        spent = time.perf_counter() - t_all
+        if (len(samples) >= min_samples and spent >= budget_s) or spent >= 2 * budget_s or len(samples) >= 100000:
+            return statistics.median(samples), len(samples), spent
+
+
+def _cpu_legs(make_step, units: float, unit: str, kind: str, sample: str, budget_s: float) -> dict:
+    """Times `make_step(threads)` with every host core and with one thread, FTZ/DAZ on (torch's flag, as the
+    reference harness sets it, bench_montlok_kernel.py:264-265; the reference recurrence sets its own guard,
+    montlok_kernel.h:439). `units` windows (or streams) per step."""
     import torch
 
     cores = len(os.sched_getaffinity(0))
+    torch.set_flush_denormal(True)
+    legs = {}
+    for threads in (cores, 1):
+        torch.set_num_threads(threads)
+        med, n, spent = _cpu_median(make_step(threads), budget_s / 2)
+        legs[threads] = (units / med, n, spent, med)
     torch.set_num_threads(cores)
-    return cores
-
-
-def _timed_loop(fn, budget_s: float, cap: int = 100000) -> tuple[int, float]:
-    fn()
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        fn()
-        reps += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= budget_s or reps >= cap:
-            return reps, elapsed
+    value, n, spent, med = legs[cores]
+    return {"value": value, "unit": unit, "cores": cores, "kind": kind,
+            "sample": f"{sample}; median of {n} steps after 5 warm-up ({med * 1e3:.3f} ms per step, {spent:.1f} s), "
+                      f"FTZ/DAZ on",
+            "one_thread_value": legs[1][0],
+            "one_thread_sample": f"median of {legs[1][1]} steps after 5 warm-up ({legs[1][3] * 1e3:.3f} ms per step)",
+            "cpu_model": _cpu_model(), "torch_threads": cores}
 
 
 # ---------------------------------------------------------------- workloads
@@ -252,35 +322,30 @@ def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
                 raise RuntimeError(lib.mlk_last_error().decode())
         return run
 
-    # Correctness guard on the timed configuration before timing: eager run,
-    # then the captured graph, bit-identical.
-    prepare(0)()
-    combine(0)()
+    def step(i):
+        p, c = prepare(i), combine(i)
+
+        def run():
+            p()
+            c()
+        return run
+
+    # Correctness guard on the timed configuration before timing: eager run, then the graphs, bit-identical.
+    step(0)()
     torch.cuda.synchronize()
     eager = outs[0].clone()
     assert torch.isfinite(eager).all().item()
-    step_graph = _graph([f for i in range(sets) for f in (prepare(i), combine(i))])
-    prep_graph = _graph([prepare(i) for i in range(sets)])
-    comb_graph = _graph([combine(i) for i in range(sets)])
-    step_graph.replay()
-    torch.cuda.synchronize()
+    t = _gpu_steps([step(i) for i in range(sets)], steps, warmup)
     assert torch.equal(outs[0], eager), "graph replay differs from the eager step"
-
-    replays = max(1, steps // sets)
-    steps = replays * sets
-    for _ in range(max(1, warmup // sets)):
-        step_graph.replay()
-    # Timed region: `steps` steps (graph replays of 16 steps each) between two
-    # synchronisations.
-    ms_per_step = _time_graph(step_graph, replays) / sets
-    prep_ms = _time_graph(prep_graph, replays) / sets
-    comb_ms = _time_graph(comb_graph, replays) / sets
+    ms_per_step = t["ms_per_step"]
+    # Per-kernel launch times: 16 launches of one kernel over the 16 sets in one graph, replayed.
+    replays = max(4, steps // sets)
+    prep_ms = _time_graph(_graph([prepare(i) for i in range(sets)]), replays) / sets
+    comb_ms = _time_graph(_graph([combine(i) for i in range(sets)]), replays) / sets
     # Warm-cache rate: one input set over and over (Infinity-Cache resident).
-    warm_graph = _graph([f for _ in range(sets) for f in (prepare(0), combine(0))])
-    warm_ms = _time_graph(warm_graph, replays) / sets
+    warm_ms = _time_graph(_graph([f for _ in range(sets) for f in (prepare(0), combine(0))]), replays) / sets
 
     prep_bytes, comb_bytes = mhc_bytes(n, d, T)
-    windows_per_s = W / (ms_per_step * 1e-3)
     kernels = {"mhc_prepare": (prep_ms, prep_bytes), "mhc_combine": (comb_ms, comb_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0])
     dom_ms, dom_bytes = kernels[dom]
@@ -289,36 +354,24 @@ def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
     tfile = ROOT / "profiles" / "mhc_n4_d128_t8192_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get(dom)
-    line = {
-        "metric": METRIC,
-        "value": windows_per_s,
-        "unit": "windows/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32 (f64 accumulate)",
-        "data": "synthetic (seeded N(0,1) streams, random-init mHC weights)",
-        "config": {"workload": "mhc_residual_mix", "n_streams": n, "d_model": d, "tokens": T, "windows": W,
-                   "seq_len": L, "sinkhorn_iters": iters, "step": "mhc_prepare + identity fn + mhc_combine",
-                   "launch": "HIP graph of 16 steps over 16 independent input sets, replayed",
-                   "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "algorithmic_bytes": dom_bytes,
-                     "launch_ms": dom_ms},
-        "kernels": {k: {"launch_ms": v[0], "algorithmic_bytes": v[1],
-                        "achieved_GBs": v[1] / (v[0] * 1e-3) / 1e9} for k, v in kernels.items()},
-        "step_roofline_frac": (prep_bytes + comb_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "tokens_per_s": T / (ms_per_step * 1e-3),
-        "stream_steps_per_s": n * T / (ms_per_step * 1e-3),
-        "warm_cache_windows_per_s": W / (warm_ms * 1e-3),
-    }
+    line = _base_line(T / (ms_per_step * 1e-3), "tokens/s", t["steps"], warmup, ms_per_step, "f32 (f64 accumulate)",
+                      "synthetic (seeded N(0,1) streams, random-init mHC weights)",
+                      {"workload": "mhc_residual_mix", "n_streams": n, "d_model": d, "tokens": T,
+                       "sinkhorn_iters": iters, "step": "mhc_prepare + identity fn + mhc_combine",
+                       "launch": "the K steps in one HIP graph, rotating over 16 independent input sets (cold HBM)",
+                       "parallelism": "single GPU"})
+    line["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "algorithmic_bytes": dom_bytes,
+                        "launch_ms": dom_ms}
+    line["kernels"] = {k: {"launch_ms": v[0], "algorithmic_bytes": v[1], "achieved_GBs": v[1] / (v[0] * 1e-3) / 1e9}
+                       for k, v in kernels.items()}
+    line.update(_timing_fields(t))
+    line["step_roofline_frac"] = (prep_bytes + comb_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
+    line["stream_steps_per_s"] = n * T / (ms_per_step * 1e-3)
+    line["warm_cache_tokens_per_s"] = T / (warm_ms * 1e-3)
     if cpu:
         line["cpu_baseline"] = cpu_baseline_mhc(cfg)
-        line["cpu_baseline"]["gpu_over_cpu"] = windows_per_s / line["cpu_baseline"]["value"]
+        line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
     return line
 
 
@@ -359,35 +412,35 @@ def _mamba_weights(g, d_model: int, geo: dict, dev, dtype=None):
 MAMBA_PARAM_KEYS = ("b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")
 
 
-def cpu_baseline_block(cfg: dict, x_cpu, norm_w, weights: dict, geo: dict, budget_s: float = 10.0) -> dict:
+def cpu_baseline_block(cfg: dict, x_cpu, norm_w, weights: dict, geo: dict, budget_s: float = 12.0) -> dict:
     """Reference CPU kernels (oracle/_ref) for the norm and the mixer, torch CPU for the two GEMMs and the
     residual add, as the reference itself calls oneDNN / at::linear (montlok.cpp:67-91)."""
     import torch
 
     from oracle import Oracle, Reference, reference_available
 
-    cores = _torch_cpu_threads()
-    lib = Reference() if reference_available() else Oracle()
-    kind = "reference" if isinstance(lib, Reference) else "port"
-    if kind == "reference":
-        lib.set_threads(cores)
+    ref = reference_available()
+    lib = Reference() if ref else Oracle()
     w = {k: v.cpu() for k, v in weights.items()}
     x = x_cpu.numpy()
     nw = norm_w.cpu().numpy()
     p = [w[k].numpy() for k in MAMBA_PARAM_KEYS]
     N, G, H, D, R = geo["N"], geo["G"], geo["H"], geo["D"], geo["R"]
 
-    def step():
-        h = torch.from_numpy(lib.rms_norm(x, nw, 1e-5, cfg["norm_groups"]))
-        proj = torch.nn.functional.linear(h, w["in_w"]).numpy()
-        y = lib.mamba3_siso_forward(proj, N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4)
-        return x_cpu + torch.nn.functional.linear(torch.from_numpy(y), w["out_w"])
+    def make_step(threads):
+        if ref:
+            lib.set_threads(threads)
 
-    reps, elapsed = _timed_loop(step, budget_s)
-    return {"value": reps * cfg["windows"] / elapsed, "unit": "windows/s", "cores": cores, "kind": kind,
-            "sample": f"{reps} full steps ({cfg['windows']} windows x {cfg['seq']} tokens) in {elapsed:.1f} s; "
-                      f"norm + mixer in the {'reference ' + lib.variant if kind == 'reference' else 'oracle'} "
-                      f"build, GEMMs in torch CPU, {cores} threads"}
+        def step():
+            h = torch.from_numpy(lib.rms_norm(x, nw, 1e-5, cfg["norm_groups"]))
+            proj = torch.nn.functional.linear(h, w["in_w"]).numpy()
+            y = lib.mamba3_siso_forward(proj, N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4)
+            return x_cpu + torch.nn.functional.linear(torch.from_numpy(y), w["out_w"])
+        return step
+
+    return _cpu_legs(make_step, cfg["windows"], "windows/s", "reference" if ref else "port",
+                     f"full steps ({cfg['windows']} windows x {cfg['seq']} tokens); norm + mixer in the "
+                     f"{'reference ' + lib.variant if ref else 'oracle'} build, GEMMs in torch CPU", budget_s)
 
 
 def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
@@ -409,52 +462,55 @@ def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
     mp = [wts[k] for k in MAMBA_PARAM_KEYS]
     consts = (N, G, H, D, R, 1e-5, 1e-5, 1e-4)
     res = [None]
+    block_args = (norm_w, 1e-5, cfg["norm_groups"], wts["in_w"], wts["out_w"], *mp, *consts)
 
     def step():
-        # GroupedRMSNorm + in_proj in one launch, the scan, out_proj + residual in one launch:
-        # bit-identical to rms_norm -> mamba3_siso_layer -> x + y.
-        proj = _C.rms_norm_linear(x, norm_w, 1e-5, cfg["norm_groups"], wts["in_w"])
-        y = _C.mamba3_siso_forward(proj, None, *mp, *consts)
-        res[0] = _C.linear_residual(y, wts["out_w"], None, x)
+        res[0] = _C.mamba3_block(x, *block_args)
 
     step()
     torch.cuda.synchronize()
     eager = res[0].clone()
     unfused = x + _C.mamba3_siso_layer(_C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"]), wts["in_w"], wts["out_w"],
                                        *mp, *consts)
-    assert torch.equal(eager, unfused), "fused block step differs from the separate operators"
-    steps, ms = _time_steps([step], steps, warmup, per_graph=16)
+    assert torch.equal(eager, unfused), "block step differs from the separate operators"
+    t = _gpu_steps([step], steps, warmup)
     assert torch.equal(res[0], eager), "graph replay differs from the eager step"
+    ms = t["ms_per_step"]
 
-    h = _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"])
-    proj = _C.linear(h, wts["in_w"])
-    y = _C.mamba3_siso_forward(proj, None, *mp, *consts)
     f = 4
-    ops = {
-        "rms_norm_in_proj": dict(fn=lambda: _C.rms_norm_linear(x, norm_w, 1e-5, cfg["norm_groups"], wts["in_w"]),
-                                 bytes=(T * d + d + W * d + T * W) * f, flops=2 * T * d * W),
-        "mamba3_siso_forward": dict(fn=lambda: _C.mamba3_siso_forward(proj, None, *mp, *consts),
-                                    bytes=(T * W + T * d_inner) * f, flops=7 * T * H * N * D),
-        "out_proj_residual": dict(fn=lambda: _C.linear_residual(y, wts["out_w"], None, x),
-                                  bytes=(T * d_inner + d * d_inner + 2 * T * d) * f, flops=2 * T * d_inner * d),
-    }
-    table = _kernel_table(ops, _op_times(ops, max(4, steps // 16)), "f32")
-    dom = max(table, key=lambda k: table[k]["launch_ms"])
     total_bytes = (2 * T * d + W * d + d * d_inner) * f + d * f
     total_flops = 2 * T * d * W + 7 * T * H * N * D + 2 * T * d_inner * d
-    line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms, "f32",
+    launches = _C.mamba3_block_launches(x, *block_args)
+    if len(launches) == 1:
+        ops = {launches[0]: dict(fn=step, bytes=total_bytes, flops=total_flops)}
+    else:
+        h = _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"])
+        proj = _C.linear(h, wts["in_w"])
+        y = _C.mamba3_siso_forward(proj, None, *mp, *consts)
+        ops = {
+            "rms_norm_in_proj": dict(fn=lambda: _C.rms_norm_linear(x, norm_w, 1e-5, cfg["norm_groups"], wts["in_w"]),
+                                     bytes=(T * d + d + W * d + T * W) * f, flops=2 * T * d * W),
+            "mamba3_siso_forward": dict(fn=lambda: _C.mamba3_siso_forward(proj, None, *mp, *consts),
+                                        bytes=(T * W + T * d_inner) * f, flops=7 * T * H * N * D),
+            "out_proj_residual": dict(fn=lambda: _C.linear_residual(y, wts["out_w"], None, x),
+                                      bytes=(T * d_inner + d * d_inner + 2 * T * d) * f, flops=2 * T * d_inner * d),
+        }
+    table = _kernel_table(ops, _op_times(ops, max(8, steps)), "f32")
+    dom = max(table, key=lambda k: table[k]["launch_ms"])
+    line = _base_line(B / (ms * 1e-3), "windows/s", t["steps"], warmup, ms, "f32",
                       "synthetic (seeded N(0,1) inputs, Kaiming-uniform weights, dt bias per mamba3.py:128-130)",
                       {"workload": "rmsnorm_mamba3_block", "windows": B, "seq_len": L, "d_model": d, "heads": H,
                        "d_state": N, "headdim": D, "rope_angles": R, "expand": cfg["expand"],
                        "norm_groups": cfg["norm_groups"], "step": "x + out_proj(mamba3(in_proj(GroupedRMSNorm(x))))",
-                       "launches": "rms_norm_linear (GroupedRMSNorm + in_proj), mamba3_siso_forward, "
-                                   "linear_residual (out_proj + x)",
-                       "launch": "HIP graph of 16 steps, replayed", "parallelism": "single GPU"})
+                       "launches": ", ".join(launches), "launch": "the K steps in one HIP graph",
+                       "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32")
     line["kernels"] = table
+    line.update(_timing_fields(t))
     line["step_algorithmic_bytes"] = total_bytes
     line["step_algorithmic_flops"] = total_flops
     line["step_hbm_frac"] = total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+    line["step_fp32_frac"] = total_flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFS["f32"]
     line["tokens_per_s"] = T / (ms * 1e-3)
     if cpu:
         line["cpu_baseline"] = cpu_baseline_block(cfg, x_cpu, norm_w, wts, geo)
@@ -481,7 +537,7 @@ def rope_tables(length: int, rope_dim: int, theta: float):
     return emb.cos(), emb.sin()
 
 
-def cpu_baseline_mla(cfg: dict, x_cpu, w: dict, cos, sin, budget_s: float = 10.0, windows: int = 16) -> dict:
+def cpu_baseline_mla(cfg: dict, x_cpu, w: dict, cos, sin, budget_s: float = 12.0, windows: int = 16) -> dict:
     """torch CPU for the GEMMs and SDPA (the reference calls oneDNN and at::scaled_dot_product_attention,
     montlok.cpp:1187-1210), reference CPU kernels for the latent LayerNorm and the rotary step."""
     import torch
@@ -489,11 +545,8 @@ def cpu_baseline_mla(cfg: dict, x_cpu, w: dict, cos, sin, budget_s: float = 10.0
 
     from oracle import Oracle, Reference, reference_available
 
-    cores = _torch_cpu_threads()
-    lib = Reference() if reference_available() else Oracle()
-    kind = "reference" if isinstance(lib, Reference) else "port"
-    if kind == "reference":
-        lib.set_threads(cores)
+    ref = reference_available()
+    lib = Reference() if ref else Oracle()
     H, hd, r, kvr = cfg["heads"], cfg["head_dim"], cfg["rope"], cfg["kv_rank"]
     nope = hd - r
     x = x_cpu[:windows].contiguous()
@@ -502,23 +555,28 @@ def cpu_baseline_mla(cfg: dict, x_cpu, w: dict, cos, sin, budget_s: float = 10.0
     cosn, sinn = cos.numpy(), sin.numpy()
     scale = 1.0 / hd ** 0.5
 
-    def step():
-        projected = F.linear(x, wf["in_w"])
-        q = projected[..., :d].reshape(B, L, H, hd).numpy()
-        kv_lat = projected[..., d:d + kvr].contiguous().numpy()
-        k_rope = projected[..., d + kvr:].contiguous().numpy()
-        kvn = torch.from_numpy(lib.layer_norm(kv_lat, wf["ln_w"].numpy(), wf["ln_b"].numpy(), 1e-5))
-        kv = F.linear(kvn, wf["kv_up"]).reshape(B, L, H, nope + hd)
-        q, k = lib.mla_rope(q, kv.numpy(), k_rope, cosn, sinn, nope)
-        att = F.scaled_dot_product_attention(torch.from_numpy(q).transpose(1, 2), torch.from_numpy(k).transpose(1, 2),
-                                             kv[..., nope:].transpose(1, 2), is_causal=True, scale=scale)
-        return F.linear(att.transpose(1, 2).reshape(B, L, d), wf["o"])
+    def make_step(threads):
+        if ref:
+            lib.set_threads(threads)
 
-    reps, elapsed = _timed_loop(step, budget_s)
-    return {"value": reps * windows / elapsed, "unit": "windows/s", "cores": cores, "kind": kind,
-            "sample": f"{reps} steps over {windows} of the {cfg['windows']} windows in {elapsed:.1f} s (rate scales "
-                      f"per window); LayerNorm + RoPE in the {'reference ' + lib.variant if kind == 'reference' else 'oracle'} "
-                      f"build, GEMMs and SDPA in torch CPU (fp32, bf16 weights upcast), {cores} threads"}
+        def step():
+            projected = F.linear(x, wf["in_w"])
+            q = projected[..., :d].reshape(B, L, H, hd).numpy()
+            kv_lat = projected[..., d:d + kvr].contiguous().numpy()
+            k_rope = projected[..., d + kvr:].contiguous().numpy()
+            kvn = torch.from_numpy(lib.layer_norm(kv_lat, wf["ln_w"].numpy(), wf["ln_b"].numpy(), 1e-5))
+            kv = F.linear(kvn, wf["kv_up"]).reshape(B, L, H, nope + hd)
+            q, k = lib.mla_rope(q, kv.numpy(), k_rope, cosn, sinn, nope)
+            att = F.scaled_dot_product_attention(torch.from_numpy(q).transpose(1, 2),
+                                                 torch.from_numpy(k).transpose(1, 2), kv[..., nope:].transpose(1, 2),
+                                                 is_causal=True, scale=scale)
+            return F.linear(att.transpose(1, 2).reshape(B, L, d), wf["o"])
+        return step
+
+    return _cpu_legs(make_step, windows, "windows/s", "reference" if ref else "port",
+                     f"steps over {windows} of the {cfg['windows']} windows (the rate scales per window); LayerNorm "
+                     f"+ RoPE in the {'reference ' + lib.variant if ref else 'oracle'} build, GEMMs and SDPA in "
+                     f"torch CPU (fp32, bf16 weights upcast)", budget_s)
 
 
 def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
@@ -556,8 +614,9 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
     torch.cuda.synchronize()
     eager = outs[0].clone()
     assert torch.isfinite(eager).all().item()
-    steps, ms = _time_steps([step(i) for i in range(sets)], steps, warmup, per_graph=sets)
+    t = _gpu_steps([step(i) for i in range(sets)], steps, warmup)
     assert torch.equal(outs[0], eager), "graph replay differs from the eager step"
+    steps, ms = t["steps"], t["ms_per_step"]
 
     x = xs[0]
     projected = _C.linear(x, w["in_w"]).view(T, d + kvr + r)
@@ -588,10 +647,11 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
                        "head_dim": hd, "rope_dim": r, "kv_rank": kvr, "rope_theta": cfg["theta"],
                        "step": "mla_forward: in_proj GEMM, latent LayerNorm (once per row, bf16), fused kv_up + RoPE + "
                                "causal attention, o_proj GEMM",
-                       "launch": f"HIP graph of {sets} steps over {sets} input sets, replayed",
+                       "launch": f"the K steps in one HIP graph, rotating over {sets} input sets",
                        "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")
     line["kernels"] = table
+    line.update(_timing_fields(t))
     line["step_algorithmic_bytes"] = total_bytes
     line["step_algorithmic_flops"] = total_flops
     line["step_hbm_frac"] = total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
@@ -615,16 +675,18 @@ def _decode_state_bytes(S: int, geo: dict) -> int:
     return S * H * ((N * D + N + D) * 4 + max(R, 1) * 8)
 
 
-def cpu_baseline_decode(cfg: dict, geo: dict, weights: list, norms: list, head, states: list, x_cpu,
-                        budget_s: float = 10.0, streams: int = 1024) -> dict:
-    """No reference step operator exists: the oracle's step restatement (one thread) for the mixer, the
+def cpu_baseline_decode(cfg: dict, geo: dict, stack, states: list, x_cpu, budget_s: float = 12.0,
+                        streams: int = 1024) -> dict:
+    """No reference step operator exists: the oracle's step restatement for the mixer, run over the streams by
+    one Python thread per core (ctypes releases the interpreter lock, so the C calls run in parallel), the
     reference CPU RMSNorm and torch CPU GEMMs, on the first `streams` streams."""
+    import concurrent.futures as cf
+
     import numpy as np
     import torch
 
     from oracle import Oracle, Reference, reference_available
 
-    cores = _torch_cpu_threads()
     orc = Oracle()
     ref = Reference() if reference_available() else orc
     N, G, H, D, R = geo["N"], geo["G"], geo["H"], geo["D"], geo["R"]
@@ -632,27 +694,42 @@ def cpu_baseline_decode(cfg: dict, geo: dict, weights: list, norms: list, head, 
     st = [{"ssm": s["ssm"][:streams].cpu().numpy().copy(), "k_prev": s["k"][:streams].cpu().numpy().copy(),
            "v_prev": s["v"][:streams].cpu().numpy().copy(), "angle": s["angle"][:streams].cpu().numpy().copy(),
            "started": 1} for s in states]
-    ws = [{k: v.cpu() for k, v in w.items()} for w in weights]
-    nws = [n.cpu().numpy() for n in norms]
-    hw, hb, fw = (t.cpu() for t in head)
+    f32 = lambda t: t.detach().float().cpu()  # noqa: E731
+    layers = [dict(norm=f32(b.norm.weight).numpy(), in_w=f32(b.mamba.in_proj.weight), out_w=f32(b.mamba.out_proj.weight),
+                   p=[f32(t).numpy() for t in b.mamba._mixer_args()]) for b in stack.layers]
+    fw, hw, hb = (f32(t) for t in (stack.final_norm.weight, stack.head.weight, stack.head.bias))
 
-    def step():
-        hcur = x
-        for layer in range(cfg["layers"]):
-            w = ws[layer]
-            nrm = ref.rms_norm(hcur.numpy(), nws[layer], 1e-5, cfg["norm_groups"])
-            proj = torch.nn.functional.linear(torch.from_numpy(nrm), w["in_w"]).numpy()
-            p = [w[k].numpy() for k in MAMBA_PARAM_KEYS]
-            y = orc.mamba3_step(proj, st[layer], N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4)
-            hcur = hcur + torch.nn.functional.linear(torch.from_numpy(np.ascontiguousarray(y)), w["out_w"])
-        fin = torch.from_numpy(ref.rms_norm(hcur.numpy(), fw.numpy(), 1e-5, 1))
-        return torch.nn.functional.linear(fin, hw, hb)
+    def make_step(threads):
+        if isinstance(ref, Reference):
+            ref.set_threads(threads)
+        pool = cf.ThreadPoolExecutor(threads) if threads > 1 else None
+        cuts = np.linspace(0, streams, threads + 1).astype(int)
 
-    reps, elapsed = _timed_loop(step, budget_s)
-    return {"value": reps * streams / elapsed, "unit": "stream-steps/s", "cores": cores, "kind": "port",
-            "sample": f"{reps} steps of {streams} of the {cfg['streams']} streams in {elapsed:.1f} s (rate scales "
-                      f"per stream); mixer step in the oracle's C restatement (1 thread, no reference step op "
-                      f"exists), RMSNorm in the reference build, GEMMs in torch CPU ({cores} threads)"}
+        def mixer(proj, state, p):
+            def part(i):
+                a, b = cuts[i], cuts[i + 1]
+                sub = {k: (v[a:b] if isinstance(v, np.ndarray) else v) for k, v in state.items()}
+                return orc.mamba3_step(proj[a:b], sub, N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4)
+            if pool is None:
+                return part(0)
+            return np.concatenate(list(pool.map(part, range(threads))))
+
+        def step():
+            hcur = x
+            for lw, s_l in zip(layers, st):
+                nrm = ref.rms_norm(hcur.numpy(), lw["norm"], 1e-5, cfg["norm_groups"])
+                proj = torch.nn.functional.linear(torch.from_numpy(nrm), lw["in_w"]).numpy()
+                y = mixer(proj, s_l, lw["p"])
+                hcur = hcur + torch.nn.functional.linear(torch.from_numpy(y), lw["out_w"])
+            fin = torch.from_numpy(ref.rms_norm(hcur.numpy(), fw.numpy(), 1e-5, 1))
+            return torch.nn.functional.linear(fin, hw, hb)
+        return step
+
+    return _cpu_legs(make_step, streams, "stream-steps/s", "port",
+                     f"steps of {streams} of the {cfg['streams']} streams (the rate scales per stream); mixer step in "
+                     f"the oracle's C restatement (no reference step operator exists), one thread per core over the "
+                     f"streams; RMSNorm in the {'reference' if isinstance(ref, Reference) else 'oracle'} build; GEMMs "
+                     f"in torch CPU", budget_s)
 
 
 def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
@@ -661,6 +738,7 @@ def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
     import torch
 
     from montlok import _C
+    from montlok.rdt.block import DecodeStackHIP
 
     cfg = DECODE
     S, d = cfg["streams"], cfg["d_model"]
@@ -670,58 +748,58 @@ def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
     g = torch.Generator(device="cpu").manual_seed(0)
     x_cpu = torch.randn(S, d, generator=g)
     x = x_cpu.to(dev)
-    weights = [_mamba_weights(g, d, geo, dev) for _ in range(cfg["layers"])]
-    norms = [torch.ones(d, device=dev) for _ in range(cfg["layers"])]
-    bound = 1 / math.sqrt(d)
-    head = ((torch.rand(1, d, generator=g) * 2 - 1).mul(bound).to(dev), (torch.rand(1, generator=g) * 2 - 1).mul(
-        bound).to(dev), torch.ones(d, device=dev))
-    states = []
-    for _ in range(cfg["layers"]):
-        st = _C.new_mamba3_state(S, H, N, D, R, dev)
+    stack = DecodeStackHIP(d_model=d, n_layers=cfg["layers"], d_state=N, expand=cfg["expand"], headdim=D,
+                           num_groups=cfg["norm_groups"]).eval()
+    with torch.no_grad():
+        for block in stack.layers:
+            w = _mamba_weights(g, d, geo, "cpu")
+            m = block.mamba
+            m.in_proj.weight.copy_(w["in_w"])
+            m.out_proj.weight.copy_(w["out_w"])
+            m.dt_bias.copy_(w["dt_bias"])
+        bound = 1 / math.sqrt(d)
+        stack.head.weight.copy_((torch.rand(1, d, generator=g) * 2 - 1) * bound)
+        stack.head.bias.copy_((torch.rand(1, generator=g) * 2 - 1) * bound)
+    stack = stack.to(dev)
+    states = stack.new_state(S, dev)
+    for st in states:
         st["ssm"].normal_(0.0, 0.1)
         st["k"].normal_(0.0, 0.1)
         st["v"].normal_(0.0, 0.1)
         st["angle"].uniform_(0.0, 2 * math.pi)
         st["started"] = True
-        states.append(st)
     states_cpu = [{k: (v.cpu() if torch.is_tensor(v) else v) for k, v in st.items()} for st in states]
-    consts = (N, G, H, D, R, 1e-5, 1e-5, 1e-4)
     result = {}
 
     def step():
-        h = x
-        for layer in range(cfg["layers"]):
-            w = weights[layer]
-            nrm = _C.rms_norm(h, norms[layer], 1e-5, cfg["norm_groups"])
-            proj = _C.linear(nrm, w["in_w"])
-            y = _C.mamba3_siso_step(proj, states[layer], *(w[k] for k in MAMBA_PARAM_KEYS), *consts)
-            h = h + _C.linear(y, w["out_w"])
-        result["out"] = _C.linear(_C.rms_norm(h, head[2], 1e-5, 1), head[0], head[1])
+        result["out"] = stack.step(x, states)
 
-    # One eager step checks the graph path and leaves the state one bar further; the CPU leg starts from
-    # the initial state copied above.
-    step()
-    torch.cuda.synchronize()
-    assert torch.isfinite(result["out"]).all().item()
-    steps, ms = _time_steps([step], steps, warmup, per_graph=1)
+    # One eager step checks the path and leaves the state one bar further; the CPU leg starts from the
+    # initial state copied above.
+    with torch.no_grad():
+        step()
+        torch.cuda.synchronize()
+        assert torch.isfinite(result["out"]).all().item()
+        t = _gpu_steps([step], steps, warmup)
+    steps, ms = t["steps"], t["ms_per_step"]
 
-    w = weights[0]
-    nrm = _C.rms_norm(x, norms[0], 1e-5, cfg["norm_groups"])
-    proj = _C.linear(nrm, w["in_w"])
-    y = _C.mamba3_siso_step(proj, states[0], *(w[k] for k in MAMBA_PARAM_KEYS), *consts)
-    o = _C.linear(y, w["out_w"])
+    blk = stack.layers[0]
+    m = blk.mamba
+    mp = m._mixer_args()
+    consts = m._geometry()
+    proj = _C.rms_norm_linear(x, blk.norm.weight, 1e-5, cfg["norm_groups"], m.in_proj.weight)
+    y = _C.mamba3_siso_step(proj, states[0], *mp, *consts)
     f = 4
     state_bytes = _decode_state_bytes(S, geo)
     ops = {
-        "rms_norm": dict(fn=lambda: _C.rms_norm(x, norms[0], 1e-5, cfg["norm_groups"]), bytes=2 * S * d * f),
-        "in_proj": dict(fn=lambda: _C.linear(nrm, w["in_w"]), bytes=(S * d + W * d + S * W) * f, flops=2 * S * d * W,
-                        precision="f32"),
-        "mamba3_siso_step": dict(fn=lambda: _C.mamba3_siso_step(proj, states[0], *(w[k] for k in MAMBA_PARAM_KEYS),
-                                                                *consts),
+        "rms_norm_in_proj": dict(fn=lambda: _C.rms_norm_linear(x, blk.norm.weight, 1e-5, cfg["norm_groups"],
+                                                               m.in_proj.weight),
+                                 bytes=(S * d + W * d + S * W) * f, flops=2 * S * d * W, precision="f32"),
+        "mamba3_siso_step": dict(fn=lambda: _C.mamba3_siso_step(proj, states[0], *mp, *consts),
                                  bytes=2 * state_bytes + (S * W + S * d_inner) * f),
-        "out_proj": dict(fn=lambda: _C.linear(y, w["out_w"]), bytes=(S * d_inner + d * d_inner + S * d) * f,
-                         flops=2 * S * d_inner * d, precision="f32"),
-        "residual_add": dict(fn=lambda: x + o, bytes=3 * S * d * f),
+        "out_proj_residual": dict(fn=lambda: _C.linear_residual(y, m.out_proj.weight, None, x),
+                                  bytes=(S * d_inner + d * d_inner + 2 * S * d) * f, flops=2 * S * d_inner * d,
+                                  precision="f32"),
     }
     table = _kernel_table(ops, _op_times(ops, max(4, steps // 4), reps=2), "f32")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
@@ -731,15 +809,16 @@ def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
                       {"workload": "streaming_decode", "streams": S, "layers": cfg["layers"], "d_model": d,
                        "d_state": N, "heads": H, "headdim": D, "rope_angles": R, "norm_groups": cfg["norm_groups"],
                        "step": "2 x [x + out_proj(mamba3_step(in_proj(GroupedRMSNorm(x))))], RMSNorm, Linear(128->1)",
-                       "launch": "HIP graph of one step, replayed (state carried in place)",
+                       "launch": "the K steps in one HIP graph (state carried in place)",
                        "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32")
     line["kernels"] = table
+    line.update(_timing_fields(t))
     line["step_algorithmic_bytes"] = total_bytes
     line["step_hbm_frac"] = total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
     line["state_bytes_per_layer"] = state_bytes
     if cpu:
-        line["cpu_baseline"] = cpu_baseline_decode(cfg, geo, weights, norms, head, states_cpu, x_cpu)
+        line["cpu_baseline"] = cpu_baseline_decode(cfg, geo, stack, states_cpu, x_cpu)
         line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
     return line
 
@@ -784,11 +863,8 @@ def cpu_baseline_stack(cfg: dict, stack, feats_cpu, budget_s: float = 12.0, wind
     from montlok.rdt.mla import rope_tables
     from oracle import Oracle, Reference, reference_available
 
-    cores = _torch_cpu_threads()
     lib = Reference() if reference_available() else Oracle()
     kind = "reference" if isinstance(lib, Reference) else "port"
-    if kind == "reference":
-        lib.set_threads(cores)
     x = feats_cpu[:windows].contiguous()
     B, L, _ = x.shape
     f32 = lambda t: t.detach().float().cpu()  # noqa: E731
@@ -848,12 +924,15 @@ def cpu_baseline_stack(cfg: dict, stack, feats_cpu, budget_s: float = 12.0, wind
             out = mamba(mix[i], agg) if i % 2 == 0 else attn(mix[i], agg)
         return lib.mhc_combine(streams, res, post, out, collapse=True, materialize=False)
 
-    reps, elapsed = _timed_loop(step, budget_s, cap=1000)
-    return {"value": reps * windows / elapsed, "unit": "windows/s", "cores": cores, "kind": kind,
-            "sample": f"{reps} steps over {windows} of the {cfg['windows']} windows in {elapsed:.1f} s (rate scales "
-                      f"per window); mHC, norms, Mamba-3 mixer and RoPE in the "
-                      f"{'reference ' + lib.variant if kind == 'reference' else 'oracle'} build, GEMMs and SDPA in "
-                      f"torch CPU (fp32, bf16 weights upcast), {cores} threads"}
+    def make_step(threads):
+        if kind == "reference":
+            lib.set_threads(threads)
+        return step
+
+    return _cpu_legs(make_step, windows, "windows/s", kind,
+                     f"steps over {windows} of the {cfg['windows']} windows (the rate scales per window); mHC, norms, "
+                     f"Mamba-3 mixer and RoPE in the {'reference ' + lib.variant if kind == 'reference' else 'oracle'} "
+                     f"build, GEMMs and SDPA in torch CPU (fp32, bf16 weights upcast)", budget_s)
 
 
 def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
@@ -882,8 +961,9 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
         torch.cuda.synchronize()
         eager = result["out"].clone()
         assert torch.isfinite(eager).all().item()
-        steps, ms = _time_steps([step], max(steps // 10, 4), max(warmup // 10, 2), per_graph=1)
+        t = _gpu_steps([step], steps, warmup)
         assert torch.equal(result["out"], eager), "graph replay differs from the eager step"
+        steps, ms = t["steps"], t["ms_per_step"]
 
         # Per-operator launches on the tensors of one eager pass.
         c = _C
@@ -898,7 +978,6 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
         y = m0.forward_projected(proj)
         W, di = m0.in_proj.weight.shape[0], m0.d_inner
         f, h2 = 4, 2
-        mhc_tok = lambda: T * (n * d * f + d * f + 2 * n * f + n * n * f)  # noqa: E731
         ops = {
             "feature_proj": dict(fn=lambda: c.linear(feats, stack.feature_proj.weight, stack.feature_proj.bias),
                                  bytes=T * (cfg["features"] + d) * f, flops=2 * T * cfg["features"] * d),
@@ -906,7 +985,10 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
                                           bytes=T * (2 * d + 2 * n + n * n) * f),
             "mhc_combine_prepare": dict(fn=lambda: hc1._combine_prepare(streams1, prep1, out1, stack.hcs[2],
                                                                         output_norm=stack.norms[2]),
-                                        bytes=T * (n * d + n * n + n + d) * f + T * n * d * f + mhc_tok()),
+                                        # reads: old streams, res, post, the layer output; writes: the new
+                                        # streams (never read back) and the next agg, pre, post, res
+                                        bytes=T * (n * d + n * n + n + d) * f + T * n * d * f +
+                                        T * (d + 2 * n + n * n) * f),
             "mhc_combine_collapse": dict(fn=lambda: hc1._combine_collapse(streams1, prep1, out1),
                                          bytes=T * (n * d + n * n + n + 2 * d) * f),
             "mamba_in_proj": dict(fn=lambda: c.linear(agg, m0.in_proj.weight), bytes=T * (d + W) * f + W * d * h2,
@@ -927,7 +1009,7 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
                                                                    ops["mamba3_siso_forward"]["flops"] +
                                                                    ops["mamba_out_proj"]["flops"]) + \
         2 * ops["mla_forward"]["flops"]
-    line = _base_line(B / (ms * 1e-3), "windows/s", steps, max(warmup // 10, 2), ms,
+    line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms,
                       "bf16 weights, f32 activations/state/accumulate",
                       "synthetic (seeded N(0,1) features clipped to [-8,8], N(0,0.02) bf16 weights)",
                       {"workload": "rdt4quant_stack_4_layers", "windows": B, "seq_len": L, "features": cfg["features"],
@@ -936,9 +1018,10 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
                                 f"{m0.num_rope_angles} rotary angles",
                        "mla": f"{cfg['heads']} heads of {cfg['head_dim']}, rope {cfg['rope']}, kv rank {cfg['kv_rank']}",
                        "step": "Linear(40->256), 4 x mHC[fn = mixer(RMSNorm(agg))] alternating Mamba-3 / MLA, collapse",
-                       "launch": "HIP graph of one step, replayed", "parallelism": "single GPU"})
+                       "launch": "the K steps in one HIP graph", "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")
     line["kernels"] = table
+    line.update(_timing_fields(t))
     line["step_flops"] = flops
     line["step_achieved_TFs"] = flops / (ms * 1e-3) / 1e12
     line["tokens_per_s"] = T / (ms * 1e-3)
@@ -956,7 +1039,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="mhc", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="block", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -509,6 +509,52 @@ def mamba3_siso_layer(inputs, in_weight, out_weight, b_bias, c_bias, b_norm_w, c
     return linear(output, out_weight)
 
 
+def mamba3_block(inputs, norm_weight, norm_eps, norm_groups, in_weight, out_weight, b_bias, c_bias, b_norm_w,
+                 c_norm_w, dt_bias, skip, d_state, ngroups, nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor):
+    """The RMSNorm -> Mamba-3 residual block, x + mamba3_siso_layer(GroupedRMSNorm(x)) (the Mamba3Layer
+    forward of python/montlok/rdt/reference/Model/layers/mamba3_layer.py:488-498 on the official backend;
+    montlok.cpp:496-519 for the layer). No single counterpart in the reference's op table.
+
+    GroupedRMSNorm + in_proj run as one launch where that form is built, then the fused mixer, then
+    out_proj with the residual added in its epilogue: the result equals rms_norm -> mamba3_siso_layer ->
+    x + y bit for bit."""
+    _require_f32_gpu(inputs, "inputs")
+    _check(inputs.dim() == 3, "inputs must be [B,L,d_model]")
+    projected = rms_norm_linear(inputs, norm_weight, norm_eps, norm_groups, in_weight)
+    y = mamba3_siso_forward(projected, None, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups,
+                            nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor)
+    return linear_residual(y, out_weight, None, inputs)
+
+
+def mamba3_block_launches(inputs, norm_weight, norm_eps, norm_groups, in_weight, *_):
+    """Names of the kernel launches ``mamba3_block`` makes for these arguments, in order."""
+    first = ["rms_norm_linear"] if _fused_norm_linear(inputs, norm_groups, in_weight) else ["rms_norm", "linear"]
+    return first + ["mamba3_siso_forward", "linear_residual"]
+
+
+def _fused_norm_linear(x: torch.Tensor, groups: int, weight: torch.Tensor) -> bool:
+    n, k = weight.shape
+    rows = x.numel() // max(k, 1)
+    gs = k // groups if groups > 0 else 0
+    wsize = weight.element_size()
+    return (gs in (8, 16, 32, 64) and k % 8 == 0 and k <= 256 and (k * wsize) % 16 == 0
+            and -(-rows // 128) * -(-n // 64) < 256)
+
+
+def mamba3_block_step(inputs, state, norm_weight, norm_eps, norm_groups, in_weight, out_weight, b_bias, c_bias,
+                      b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups, nheads, headdim, num_rope_angles, b_eps,
+                      c_eps, a_floor):
+    """One token of ``mamba3_block`` for S streams with carried state: inputs [S, d_model] ->
+    x + out_proj(mamba3_siso_step(in_proj(GroupedRMSNorm(x)))). ``state`` as for mamba3_siso_step, updated
+    in place. Stepping T tokens from a zero state gives mamba3_block over those T tokens."""
+    _require_f32_gpu(inputs, "inputs")
+    _check(inputs.dim() == 2, "inputs must be [S,d_model]")
+    projected = rms_norm_linear(inputs, norm_weight, norm_eps, norm_groups, in_weight)
+    y = mamba3_siso_step(projected, state, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups,
+                         nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor)
+    return linear_residual(y, out_weight, None, inputs)
+
+
 def stage1_forward(inputs, layers, mamba_norm_eps, mamba_norm_groups, ffn_norm_eps, d_state, ngroups, nheads, headdim,
                    num_rope_angles, b_eps, c_eps, a_floor):
     """montlok.cpp:1011-1053. Each layer pack holds 14 tensors: outer norm, Mamba in/out, B/C bias and norm,

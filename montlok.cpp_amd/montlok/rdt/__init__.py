@@ -2,8 +2,21 @@
 
 Importing this package enables the GPU kernels unless ``MONTLOK_CPP`` is
 already set (the reference does the same for its CPU kernels,
-python/montlok/rdt/__init__.py:27); ``MONTLOK_CPP=0`` keeps the pure PyTorch
-path of each module.
+python/montlok/rdt/__init__.py:27).
+
+Switches (README.md:265-280 of the reference), read on every call:
+
+- ``MONTLOK_CPP=0``, ``MONTLOK_CPP_MHC=0``, ``MONTLOK_CPP_LAYERS=0``: the
+  reference runs the upstream PyTorch modules instead; this package has no
+  such forward, so the affected modules raise ``RuntimeError``.
+- ``MONTLOK_CPP_FUSED=0``: Mamba-3 pre-processing as tensor operations, then
+  the recurrence kernel alone (``mamba3.cpp_backend``).
+- ``MONTLOK_CPP_TAIL=0``: the model evaluates every position and takes the
+  last one instead of the last-position tail (``model.tail_enabled``).
+- ``MONTLOK_CPP_NATIVE_STAGE1=0`` / ``MONTLOK_CPP_NATIVE_STAGE2=0``: the
+  stage-1 / stage-2 modules run one by one instead of the one-call
+  ``stage1_forward`` / ``stage2_tail_forward``.
+- ``MONTLOK_CACHE_PARAMETER_PACKS=0``: parameter packs are rebuilt per call.
 """
 
 from __future__ import annotations
@@ -34,6 +47,8 @@ _EXPORTS = {
     "RDT4QuantHIP": "model",
     "MultiAssetRDTCPU": "model",
     "MultiAssetRDTHIP": "model",
+    "Mamba3BlockHIP": "block",
+    "DecodeStackHIP": "block",
     "RDTModelConfig": "model",
     "cpu_linear": "linear",
 }

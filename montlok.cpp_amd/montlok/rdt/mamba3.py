@@ -13,21 +13,48 @@ down to even) / 2 rotary angles. ``forward`` is the fused layer
 carried state (S, k_prev, v_prev and the fp64 rotary phase). No reference
 operator exists for this; stepping T tokens from ``new_state`` gives the
 forward over those T tokens.
+
+Backends (chosen per call from the environment, as mamba3.py:50-54 does):
+
+``MONTLOK_CPP=1`` (the default once ``montlok.rdt`` is imported)
+    the fused layer: in_proj, one kernel from the in_proj rows to the gated
+    output (BCNorm, biases, dt/A/trap, rotary phase, recurrence, silu gate),
+    out_proj.
+``MONTLOK_CPP=1 MONTLOK_CPP_FUSED=0``
+    the reference's debug ladder for isolating a mismatch between the fused
+    pre-processing and the recurrence (mamba3.py:14-16, 226-240): the
+    pre-processing as tensor operations on the device, then only the
+    recurrence kernel (``mamba3_siso_recurrent``). Its fp32 rotary cumsum
+    and libm-free tensor math differ from the fused kernel's fp64 running
+    phase by rounding; the reference's own gate for this pair is
+    2e-5 (1 + max|y|) (tests/rdt/test_rdt_kernels.py:126-128).
+``MONTLOK_CPP`` other than ``1``
+    raises: this package has no PyTorch forward of its own.
 """
 
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 from torch import nn
+from torch.nn import functional as F
 
 from ._gate import backend_enabled, ext, require_gpu_inference
 
 
 def cpp_backend() -> str | None:
-    """``"fused"`` when the GPU kernels are enabled (``MONTLOK_CPP=1``), else ``None`` (mamba3.py:50-54)."""
-    return "fused" if backend_enabled() else None
+    """``"fused"`` or ``"recurrent"`` (``MONTLOK_CPP_FUSED=0``) when the GPU kernels are enabled
+    (``MONTLOK_CPP=1``), else ``None`` (mamba3.py:50-54)."""
+    if not backend_enabled():
+        return None
+    return "recurrent" if os.environ.get("MONTLOK_CPP_FUSED") == "0" else "fused"
+
+
+def heavy_tail_activation(value: torch.Tensor) -> torch.Tensor:
+    """x for x >= 0, 1 / (1 - x) below (mamba3.py:30-33)."""
+    return value.clamp_min(0) + torch.reciprocal(1 - value.clamp_max(0))
 
 
 class BCNorm(nn.Module):
@@ -88,8 +115,50 @@ class Mamba3HIP(nn.Module):
         if inputs.ndim != 3 or inputs.shape[-1] != self.d_model:
             raise ValueError("Mamba3HIP expects [batch, length, d_model]")
         require_gpu_inference(type(self).__name__, inputs)
-        return ext().mamba3_siso_layer(inputs, self.in_proj.weight, self.out_proj.weight, *self._mixer_args(),
-                                       *self._geometry())
+        c = ext()
+        if cpp_backend() == "recurrent":
+            projected = c.linear(inputs, self.in_proj.weight)
+            return c.linear(self._forward_recurrent(projected), self.out_proj.weight)
+        return c.mamba3_siso_layer(inputs, self.in_proj.weight, self.out_proj.weight, *self._mixer_args(),
+                                   *self._geometry())
+
+    def _forward_recurrent(self, projected: torch.Tensor) -> torch.Tensor:
+        """``MONTLOK_CPP_FUSED=0``: the pre-processing as tensor operations, then the recurrence kernel.
+
+        Splits the in_proj row [z | x | B | C | dt | A | trap | angles], BCNorm's B and C per group plus the
+        per-head biases (group h // (H / G)), dt = softplus(dt + dt_bias), adt = -max(heavy_tail(A), A_floor)
+        * dt, the rotary phase cumsum(tanh(angles) * pi * dt) wrapped to [0, 2 pi), and the rotation of the
+        interleaved pairs (2r, 2r + 1) of q and k for r < R (mamba3.py:199-240). Returns [B, L, d_inner]."""
+        B, L, _ = projected.shape
+        H, N, G, D, R = self.nheads, self.d_state, self.num_bc_heads, self.headdim, self.num_rope_angles
+        z, x, b_val, c_val, raw_dt, raw_a, raw_trap, raw_ang = torch.split(
+            projected, [self.d_inner, self.d_inner, N * G, N * G, H, H, H, R], dim=-1)
+
+        def bc(value, norm, bias):
+            v = value.reshape(B, L, G, N)
+            v = v * torch.rsqrt(v.square().mean(dim=-1, keepdim=True) + norm.eps) * norm.weight
+            return (v.unsqueeze(3) + bias.view(1, 1, G, H // G, N)).reshape(B, L, H, N)
+
+        k = bc(b_val, self.B_norm, self.B_bias)
+        q = bc(c_val, self.C_norm, self.C_bias)
+        dt = F.softplus(raw_dt + self.dt_bias)
+        adt = -heavy_tail_activation(raw_a).clamp_min(self.A_floor) * dt
+        if R > 0:
+            phase = torch.cumsum(torch.tanh(raw_ang).unsqueeze(2) * math.pi * dt.unsqueeze(-1), dim=1)
+            phase = phase - 2 * math.pi * torch.floor(phase / (2 * math.pi))
+            cos, sin = torch.cos(phase), torch.sin(phase)
+
+            def rotate(v):
+                pairs = v[..., :2 * R].unflatten(-1, (R, 2))
+                left, right = pairs[..., 0], pairs[..., 1]
+                turned = torch.stack((left * cos - right * sin, left * sin + right * cos), dim=-1).flatten(-2)
+                return torch.cat((turned, v[..., 2 * R:]), dim=-1)
+
+            q, k = rotate(q), rotate(k)
+        gate = F.silu(z).reshape(B, L, H, D)
+        y = ext().mamba3_siso_recurrent(q.contiguous(), k.contiguous(), x.unflatten(-1, (H, D)), gate, adt, dt,
+                                        raw_trap, self.D)
+        return y.reshape(B, L, self.d_inner)
 
     def forward_projected(self, projected: torch.Tensor) -> torch.Tensor:
         """in_proj output [B, L, W] -> out_proj input [B, L, d_inner] (mamba3.py:175-197)."""

@@ -44,11 +44,30 @@ from torch.nn import functional as F
 
 from ._gate import ext, require_gpu_inference
 from .layers import GroupedRMSNormHIP, LayerNormHIP, RMSNormHIP, SwiGLUHIP
-from .mamba3 import Mamba3HIP
+from .mamba3 import Mamba3HIP, cpp_backend
 from .mhc import ManifoldHyperConnectionHIP
 from .mla import MLAHIP
 
 _FAMILY = "MONTLOK_CPP_MODEL"
+
+
+def tail_enabled() -> bool:
+    """The last-position tail path (model.py:47-48); ``MONTLOK_CPP_TAIL=0`` runs the full recurrence over
+    every position and takes the last row instead."""
+    return cpp_backend() is not None and os.environ.get("MONTLOK_CPP_TAIL") != "0"
+
+
+def native_stage1_enabled() -> bool:
+    """Stage 1 as one ``stage1_forward`` call (model.py:51-55); ``MONTLOK_CPP_NATIVE_STAGE1=0`` (or
+    ``MONTLOK_CPP_FUSED=0``) runs its sub-layer modules one by one."""
+    return (os.environ.get("MONTLOK_CPP_NATIVE_STAGE1") != "0" and os.environ.get("MONTLOK_CPP_LAYERS") != "0"
+            and cpp_backend() == "fused")
+
+
+def native_stage2_enabled() -> bool:
+    """The stage-2 tail as one ``stage2_tail_forward`` call (model.py:144-148); ``MONTLOK_CPP_NATIVE_STAGE2=0``
+    runs the stage-2 modules one by one over every position."""
+    return os.environ.get("MONTLOK_CPP_NATIVE_STAGE2") != "0" and os.environ.get("MONTLOK_CPP_LAYERS") != "0"
 
 
 @dataclasses.dataclass
@@ -138,7 +157,12 @@ class Mamba3LayerHIP(nn.Module):
     def forward(self, x: torch.Tensor, attn_mask: torch.Tensor | None = None, **_: Any) -> torch.Tensor:
         if attn_mask is not None:
             raise NotImplementedError("Mamba3LayerHIP: padding masks are not on the GPU path")
-        return x + self.mamba(self.norm(x))
+        if cpp_backend() != "fused":
+            return x + self.mamba(self.norm(x))
+        require_gpu_inference(type(self).__name__, x)
+        m = self.mamba
+        return ext().mamba3_block(x, self.norm.weight, self.norm.eps, self.norm.num_groups, m.in_proj.weight,
+                                  m.out_proj.weight, *m._mixer_args(), *m._geometry())
 
 
 class MambaSubLayerHIP(nn.Module):
@@ -230,6 +254,14 @@ class TwoStageCoreHIP(nn.Module):
                                     mixer.headdim, mixer.num_rope_angles, mixer.B_norm.eps, mixer.C_norm.eps,
                                     mixer.A_floor)
 
+    def run_stage1_modules(self, e0: torch.Tensor) -> torch.Tensor:
+        """Stage 1 sub-layer by sub-layer (``core._run_stage1``, the reference's path without the native
+        stage-1 call)."""
+        x = e0
+        for layer in self.stage1:
+            x = layer(x)
+        return x
+
     def _expand(self, x: torch.Tensor) -> torch.Tensor:
         return x.unsqueeze(-2).expand(-1, -1, self.n_streams, -1).contiguous()
 
@@ -241,7 +273,7 @@ class TwoStageCoreHIP(nn.Module):
         total = int(steps if steps is not None else self.cfg.recurrent_steps)
         if total <= 0:
             raise ValueError("steps must be positive")
-        backbone = self.run_stage1(e0)
+        backbone = self.run_stage1(e0) if native_stage1_enabled() else self.run_stage1_modules(e0)
         streams = self._expand(backbone)
         for _step in range(total):
             for layer in self.stage2:
@@ -335,8 +367,8 @@ class RDT4QuantHIP(nn.Module):
         depth = int(depth)
         if depth <= 0:
             raise ValueError("steps must be positive")
-        backbone = core.run_stage1(embedded)
-        if len(core.stage2) == 1:
+        backbone = core.run_stage1(embedded) if native_stage1_enabled() else core.run_stage1_modules(embedded)
+        if len(core.stage2) == 1 and native_stage2_enabled():
             return core.stage2_tail(backbone, depth)
         streams = core._expand(backbone)
         for _ in range(depth):
@@ -353,8 +385,15 @@ class RDT4QuantHIP(nn.Module):
         last = self.final_norm(hidden[:, -1].contiguous())
         return self._quantiles(ext().linear(last, head.weight, head.bias).reshape(-1, rows, 3))
 
+    def _hidden_for_head(self, embedded: torch.Tensor, depth: int) -> torch.Tensor:
+        """model.py:366-370: the tail path, or (``MONTLOK_CPP_TAIL=0``) the full recurrence's hidden states."""
+        if tail_enabled():
+            return self._hidden_tail(embedded, depth)
+        hidden, _ = self.recurrent(embedded, steps=depth)
+        return hidden
+
     def forward(self, inputs: torch.Tensor, depth: int):
-        hidden = self._hidden_tail(self._embed(inputs), depth)
+        hidden = self._hidden_for_head(self._embed(inputs), depth)
         return self._head(hidden, self.head, self.n_horizons), hidden.detach().float().square().mean().sqrt()
 
 
@@ -382,7 +421,7 @@ class MultiAssetRDTHIP(RDT4QuantHIP):
         period = self.period_embedding.weight[0 if domain == "equity_daily" else 1]
         projected = ext().linear(x, self.stock_projection.weight, self.stock_projection.bias)
         embedded = self.stock_norm(projected + identity[:, None] + period)
-        hidden = self._hidden_tail(embedded, depth)
+        hidden = self._hidden_for_head(embedded, depth)
         return self._head(hidden, self.stock_heads[domain], 3), hidden.detach().float().square().mean().sqrt()
 
 

@@ -152,14 +152,23 @@ def _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, n_last, causal, scale, cos, 
     return oracle.linear(att.reshape(B, n_last, d), p["o"])
 
 
+MLA_GEOMETRIES = {
+    # MLA block: d_model 256, 8 heads of 32 (rope 16, nope 16), kv rank 64, 128 tokens; 16 windows.
+    "block": (16, 128, 256, 8, 32, 16, 64),
+    # Full stack's MLA: d_model 256, 4 heads of 64 (rope 32, nope 32), kv rank 64, 256 tokens; 8 windows.
+    "stack": (8, 256, 256, 4, 64, 32, 64),
+}
+
+
+@pytest.mark.parametrize("geometry", sorted(MLA_GEOMETRIES))
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("n_last", ["full", 1])
-def test_mla_forward_block_geometry(dev, oracle, bf16, n_last):
-    """d_model 256, 8 heads of 32 (rope 16, nope 16), kv rank 64, 128 tokens; 16 windows."""
+def test_mla_forward_block_geometry(dev, oracle, bf16, n_last, geometry):
+    """mla_forward (the fused attend kernels where built) against the oracle chain at each geometry."""
     from montlok import _C
 
     rng = np.random.default_rng(1 + bf16)
-    B, L, d, H, hd, nope, kv_rank = 16, 128, 256, 8, 32, 16, 64
+    B, L, d, H, hd, nope, kv_rank = MLA_GEOMETRIES[geometry]
     n_last = L if n_last == "full" else n_last
     x = rng.standard_normal((B, L, d)).astype(np.float32)
     p = _mla_params(rng, d, H, hd, nope, kv_rank, bf16)
@@ -177,7 +186,8 @@ def test_mla_forward_block_geometry(dev, oracle, bf16, n_last):
                          w(p["o"]), _t(cos, dev), _t(sin, dev), H, hd, nope, kv_rank, n_last, True, scale)
     assert out.shape == (B, n_last, d)
     expect = _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, n_last, True, scale, cos, sin)
-    assert_close(out, expect, tol=BF16_TOL if bf16 else 1e-5, name=f"mla_forward bf16={bf16} n_last={n_last}")
+    assert_close(out, expect, tol=BF16_TOL if bf16 else 1e-5,
+                 name=f"mla_forward {geometry} bf16={bf16} n_last={n_last}")
 
 
 def test_mla_errors(dev):

@@ -1,6 +1,14 @@
 """GPU parity of the hybrid stack (feature projection, 4 mHC residual layers
 alternating Mamba-3 and MLA, collapse) against the same chain of oracle ops:
-fp32 weights within 1e-5, bf16 weights within 2e-2 (normwise)."""
+fp32 weights within 1e-5, bf16 weights within 2e-2 (normwise).
+
+Two geometries: a small one (d_model 64, d_state 16, 2 MLA heads of 32,
+kv rank 32, 2 x 32 tokens), and the full stack's own (d_model 256, d_state 64,
+Mamba-3 8 heads of 64, MLA 4 heads of 64 with RoPE 32 and kv rank 64, n = 4
+streams, 20 Sinkhorn iterations, 40 features; reference/Model/two_stage.py
+:98-116, 402-409 with reference/config.json:27-46) on 2 windows x 256 tokens,
+which takes the same fused kernels as the 1024-window workload (the MLA
+attend form with head_dim 64 / nope 32, the d-256 combine+prepare)."""
 
 from __future__ import annotations
 
@@ -62,14 +70,23 @@ def _oracle_stack(oracle, stack, feats):
     return oracle.mhc_combine(streams, res, post, out, collapse=True, materialize=False)
 
 
+GEOMETRIES = {
+    "small": (dict(d_model=64, d_state=16, mamba_headdim=32, n_heads=2, head_dim=32, rope_head_dim=16,
+                   kv_lora_rank=32), 32),
+    "stack": (dict(d_model=256, d_state=64, mamba_headdim=64, n_heads=4, head_dim=64, rope_head_dim=32,
+                   kv_lora_rank=64), 256),
+}
+
+
+@pytest.mark.parametrize("geometry", sorted(GEOMETRIES))
 @pytest.mark.parametrize("bf16", [False, True])
-def test_hybrid_stack(dev, oracle, bf16):
+def test_hybrid_stack(dev, oracle, bf16, geometry):
     from montlok.rdt.stack import HybridStackHIP
 
-    stack = HybridStackHIP(40, d_model=64, n_layers=4, n_streams=4, d_state=16, mamba_headdim=32, n_heads=2,
-                           head_dim=32, rope_head_dim=16, kv_lora_rank=32).eval()
+    kwargs, L = GEOMETRIES[geometry]
+    stack = HybridStackHIP(40, n_layers=4, n_streams=4, **kwargs).eval()
     _randomise(stack, bf16)
-    feats = np.clip(np.random.default_rng(6).standard_normal((2, 32, 40)), -8, 8).astype(np.float32)
+    feats = np.clip(np.random.default_rng(6).standard_normal((2, L, 40)), -8, 8).astype(np.float32)
     expect = _oracle_stack(oracle, stack, feats)
     stack = stack.to(dev)
     if bf16:
@@ -77,5 +94,5 @@ def test_hybrid_stack(dev, oracle, bf16):
             w.data = w.data.bfloat16()
     with torch.no_grad():
         out = stack(torch.from_numpy(feats).to(dev))
-    assert out.shape == (2, 32, 64)
-    assert_close(out, expect, tol=BF16_TOL if bf16 else 1e-5, name=f"hybrid stack bf16={bf16}")
+    assert out.shape == (2, L, kwargs["d_model"])
+    assert_close(out, expect, tol=BF16_TOL if bf16 else 1e-5, name=f"hybrid stack {geometry} bf16={bf16}")

@@ -203,3 +203,41 @@ def test_model_config_refusals():
     with pytest.raises(RuntimeError, match="ROCm device|switched off"):
         with torch.no_grad():
             m(torch.zeros(1, 4, 7), 1)
+
+
+def test_switch_predicates(monkeypatch):
+    """The reference's MONTLOK_CPP* switches (README.md:265-280) as this package reads them."""
+    from montlok.rdt import mamba3, model
+
+    for name in ("MONTLOK_CPP_FUSED", "MONTLOK_CPP_TAIL", "MONTLOK_CPP_NATIVE_STAGE1", "MONTLOK_CPP_NATIVE_STAGE2",
+                 "MONTLOK_CPP_LAYERS"):
+        monkeypatch.delenv(name, raising=False)
+    monkeypatch.setenv("MONTLOK_CPP", "1")
+    assert mamba3.cpp_backend() == "fused"
+    assert model.tail_enabled() and model.native_stage1_enabled() and model.native_stage2_enabled()
+    monkeypatch.setenv("MONTLOK_CPP_FUSED", "0")
+    assert mamba3.cpp_backend() == "recurrent" and not model.native_stage1_enabled() and model.tail_enabled()
+    monkeypatch.delenv("MONTLOK_CPP_FUSED")
+    monkeypatch.setenv("MONTLOK_CPP_TAIL", "0")
+    assert not model.tail_enabled() and model.native_stage1_enabled()
+    monkeypatch.setenv("MONTLOK_CPP_NATIVE_STAGE2", "0")
+    assert not model.native_stage2_enabled() and model.native_stage1_enabled()
+    monkeypatch.setenv("MONTLOK_CPP_NATIVE_STAGE1", "0")
+    assert not model.native_stage1_enabled()
+    monkeypatch.setenv("MONTLOK_CPP", "0")
+    assert mamba3.cpp_backend() is None and not model.tail_enabled()
+
+
+def test_block_and_decode_stack_contract():
+    """Mamba3BlockHIP carries the upstream Mamba3Layer keys (norm.weight, mamba.*); DecodeStackHIP adds the
+    final norm and the head."""
+    from montlok.rdt import DecodeStackHIP, Mamba3BlockHIP
+
+    b = Mamba3BlockHIP(64, d_state=16, headdim=32, num_groups=8)
+    keys = set(b.state_dict())
+    assert {"norm.weight", "mamba.in_proj.weight", "mamba.out_proj.weight", "mamba.dt_bias", "mamba.D"} <= keys
+    assert b.norm.num_groups == 8 and b.mamba.in_proj.weight.shape == (2 * 128 + 2 * 16 + 3 * 4 + 4, 64)
+    s = DecodeStackHIP(d_model=128, n_layers=2, d_state=64, headdim=64)
+    assert s.head.weight.shape == (1, 128) and len(s.layers) == 2
+    with pytest.raises(ValueError, match="expects"):
+        b(torch.zeros(2, 3, 32))
