@@ -260,6 +260,26 @@ mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, c
                                      int64_t headdim, float* out, void* workspace, size_t workspace_bytes,
                                      mlk_stream_t stream);
 
+/* mlk_mamba3_siso_recurrent without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Same arguments, checks and result (bit for bit) as
+ * mlk_mamba3_siso_recurrent; the (alpha, beta, gamma) coefficients live in a
+ * static device array of MLK_NOALLOC_SCRATCH_BYTES that each GPU holds from
+ * library load to process end, so batch * length * heads may be at most
+ * MLK_NOALLOC_SCRATCH_BYTES / 12 (699,050); larger calls fail with
+ * MLK_ERR_INVALID_ARGUMENT. The entry point calls no allocating routine.
+ * All calls on one GPU share its array: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller. */
+#define MLK_NOALLOC_SCRATCH_BYTES (8u << 20)
+mlk_status mlk_mamba3_siso_recurrent_noalloc(const float* q, const int64_t* q_strides, const float* k,
+                                             const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                                             const float* gate, const int64_t* gate_strides, const float* adt,
+                                             const int64_t* adt_strides, const float* dt, const int64_t* dt_strides,
+                                             const float* trap_logit, const int64_t* trap_strides, const float* skip,
+                                             int64_t batch, int64_t length, int64_t heads, int64_t d_state,
+                                             int64_t headdim, float* out, mlk_stream_t stream);
+
 /* mamba3_siso_forward(projected, gate, B_bias, C_bias, B_norm_w, C_norm_w,
  * dt_bias, D, d_state, ngroups, nheads, headdim, num_rope_angles, b_eps,
  * c_eps, a_floor) -- montlok.cpp:333-492, kernels montlok_kernel.h:463-597

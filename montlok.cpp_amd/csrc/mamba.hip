@@ -42,6 +42,8 @@
 #include <cstring>
 #include <type_traits>
 
+#include <mutex>
+
 #include "mlk_common.h"
 
 namespace mlk {
@@ -1595,22 +1597,22 @@ size_t mlk_mamba3_workspace_bytes(int64_t batch, int64_t length, int64_t nheads,
     return sizeof(float) * static_cast<size_t>(2 * blh * d_state + 3 * blh + blh * rw);
 }
 
-mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, const float* k,
-                                     const int64_t* k_strides, const float* v, const int64_t* v_strides,
-                                     const float* gate, const int64_t* gate_strides, const float* adt,
-                                     const int64_t* adt_strides, const float* dt, const int64_t* dt_strides,
-                                     const float* trap_logit, const int64_t* trap_strides, const float* skip,
-                                     int64_t batch, int64_t length, int64_t heads, int64_t d_state,
-                                     int64_t headdim, float* out, void* workspace, size_t workspace_bytes,
-                                     mlk_stream_t stream) {
-    MLK_CHECK(batch >= 0 && length >= 0 && heads >= 0 && d_state >= 0 && headdim >= 0, "q/k must be [B,L,H,N]");
+}  // extern "C"
+
+namespace mlk {
+namespace {
+
+// mamba3_siso_recurrent with the (alpha, beta, gamma) coefficients in
+// `coef` (3 * B * L * H floats): coef_kernel fills all of it before the
+// recurrence reads it, so nothing in it needs clearing.
+mlk_status siso_recurrent(const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+                          const float* v, const int64_t* v_strides, const float* gate, const int64_t* gate_strides,
+                          const float* adt, const int64_t* adt_strides, const float* dt, const int64_t* dt_strides,
+                          const float* trap_logit, const int64_t* trap_strides, const float* skip, int64_t batch,
+                          int64_t length, int64_t heads, int64_t d_state, int64_t headdim, float* out, float* coef,
+                          hipStream_t stream) {
     const int64_t blh = batch * length * heads;
-    MLK_CHECK(workspace_bytes >= sizeof(float) * static_cast<size_t>(3 * blh), "workspace too small");
-    if (blh == 0 || headdim == 0) return MLK_OK;
-    MLK_CHECK(q && k && v && gate && adt && dt && trap_logit && skip && out && workspace, "null tensor pointer");
-    MLK_CHECK(q_strides && k_strides && v_strides && gate_strides && adt_strides && dt_strides && trap_strides,
-              "null stride array");
-    float* alpha = static_cast<float*>(workspace);
+    float* alpha = coef;
     float* beta = alpha + blh;
     float* gamma = beta + blh;
     auto s3 = [](const int64_t* x) { return Strides3{x[0], x[1], x[2]}; };
@@ -1641,6 +1643,95 @@ mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, c
     a.out = out;
     a.os = {length * heads * headdim, heads * headdim, headdim};
     return launch_rec(a, stream);
+}
+
+// Device memory of mlk_mamba3_siso_recurrent_noalloc: a file-scope array each
+// GPU holds from module load to process end. Host code never uses the
+// array's name as an address (on the host it is only a stand-in for the
+// symbol); it uses the device address hipGetSymbolAddress returns, looked up
+// once per device with that device current.
+constexpr size_t kNoallocScratchBytes = MLK_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+mlk_status scratch_for_current_device(void** ptr) {
+    int device = -1;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) {
+        set_error(std::string("mamba3_siso_recurrent_noalloc: hipGetDevice: ") + hipGetErrorString(err));
+        return MLK_ERR_RUNTIME;
+    }
+    if (device < 0 || device >= kMaxDevices) {
+        set_error("mamba3_siso_recurrent_noalloc: device index beyond the library's table");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* found = nullptr;
+        err = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || found == nullptr) {
+            set_error(std::string("mamba3_siso_recurrent_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(err));
+            return MLK_ERR_RUNTIME;
+        }
+        g_scratch_ptr[device] = found;
+    }
+    *ptr = g_scratch_ptr[device];
+    return MLK_OK;
+}
+
+}  // namespace
+}  // namespace mlk
+
+extern "C" {
+
+mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, const float* k,
+                                     const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                                     const float* gate, const int64_t* gate_strides, const float* adt,
+                                     const int64_t* adt_strides, const float* dt, const int64_t* dt_strides,
+                                     const float* trap_logit, const int64_t* trap_strides, const float* skip,
+                                     int64_t batch, int64_t length, int64_t heads, int64_t d_state,
+                                     int64_t headdim, float* out, void* workspace, size_t workspace_bytes,
+                                     mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 0 && heads >= 0 && d_state >= 0 && headdim >= 0, "q/k must be [B,L,H,N]");
+    const int64_t blh = batch * length * heads;
+    MLK_CHECK(workspace_bytes >= sizeof(float) * static_cast<size_t>(3 * blh), "workspace too small");
+    if (blh == 0 || headdim == 0) return MLK_OK;
+    MLK_CHECK(q && k && v && gate && adt && dt && trap_logit && skip && out && workspace, "null tensor pointer");
+    MLK_CHECK(q_strides && k_strides && v_strides && gate_strides && adt_strides && dt_strides && trap_strides,
+              "null stride array");
+    return siso_recurrent(q, q_strides, k, k_strides, v, v_strides, gate, gate_strides, adt, adt_strides, dt,
+                          dt_strides, trap_logit, trap_strides, skip, batch, length, heads, d_state, headdim, out,
+                          static_cast<float*>(workspace), reinterpret_cast<hipStream_t>(stream));
+}
+
+mlk_status mlk_mamba3_siso_recurrent_noalloc(const float* q, const int64_t* q_strides, const float* k,
+                                             const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                                             const float* gate, const int64_t* gate_strides, const float* adt,
+                                             const int64_t* adt_strides, const float* dt, const int64_t* dt_strides,
+                                             const float* trap_logit, const int64_t* trap_strides, const float* skip,
+                                             int64_t batch, int64_t length, int64_t heads, int64_t d_state,
+                                             int64_t headdim, float* out, mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 0 && heads >= 0 && d_state >= 0 && headdim >= 0, "q/k must be [B,L,H,N]");
+    const int64_t blh = batch * length * heads;
+    if (blh == 0 || headdim == 0) return MLK_OK;
+    if (static_cast<uint64_t>(blh) > kNoallocScratchBytes / (3 * sizeof(float))) {
+        set_error("mamba3_siso_recurrent_noalloc: batch * length * heads = " + std::to_string(blh) +
+                  " exceeds the static scratch (" + std::to_string(kNoallocScratchBytes / (3 * sizeof(float))) +
+                  " at most); use mlk_mamba3_siso_recurrent with a workspace");
+        return MLK_ERR_INVALID_ARGUMENT;
+    }
+    MLK_CHECK(q && k && v && gate && adt && dt && trap_logit && skip && out, "null tensor pointer");
+    MLK_CHECK(q_strides && k_strides && v_strides && gate_strides && adt_strides && dt_strides && trap_strides,
+              "null stride array");
+    void* coef = nullptr;
+    const mlk_status st = scratch_for_current_device(&coef);
+    if (st != MLK_OK) return st;
+    return siso_recurrent(q, q_strides, k, k_strides, v, v_strides, gate, gate_strides, adt, adt_strides, dt,
+                          dt_strides, trap_logit, trap_strides, skip, batch, length, heads, d_state, headdim, out,
+                          static_cast<float*>(coef), reinterpret_cast<hipStream_t>(stream));
 }
 
 mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_t length, int64_t width,

@@ -58,6 +58,7 @@ def _load():
         "mlk_mhc_combine": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp],
         "mlk_math_check": [_vp, _i64, _vp, _vp],
         "mlk_mamba3_siso_recurrent": [_vp, _vp] * 7 + [_vp] + [_i64] * 5 + [_vp, _vp, C.c_size_t, _vp],
+        "mlk_mamba3_siso_recurrent_noalloc": [_vp, _vp] * 7 + [_vp] + [_i64] * 5 + [_vp, _vp],
         "mlk_mamba3_siso_forward": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64] + [_vp] * 6 + [_i64] * 5 +
                                    [_dbl, _dbl, _dbl, _vp, _vp, C.c_size_t, _vp],
         "mlk_mamba3_siso_step": [_vp, _i64, _i64] + [_vp] * 6 + [_i64] * 5 + [_dbl, _dbl, _dbl] + [_vp] * 4 +
@@ -408,6 +409,17 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 
 def mamba3_siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip):
     """montlok.cpp:245-325: gated SSM output [B, L, H, D] (gate = z * sigmoid(z))."""
+    return _siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip, noalloc=False)
+
+
+def mamba3_siso_recurrent_noalloc(q, k, v, gate, adt, dt, trap_logit, skip):
+    """mamba3_siso_recurrent through the entry point that allocates no device memory: the coefficients live
+    in the library's static per-GPU scratch (B * L * H at most 699,050). Same result bit for bit; calls that
+    overlap on one GPU race. No counterpart in the reference."""
+    return _siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip, noalloc=True)
+
+
+def _siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip, noalloc: bool):
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (gate, "gate"), (adt, "adt"), (dt, "dt"),
                     (trap_logit, "trap_logit")):
         _require_f32_gpu(t, name)
@@ -422,10 +434,14 @@ def mamba3_siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip):
         _require_inner_dense(t, name)
     sk = _dense_parameter(skip, H, "skip")
     out = torch.empty((B, L, H, D), dtype=torch.float32, device=q.device)
-    ws = _workspace(4 * 3 * B * L * H, q.device)
-    _call("mlk_mamba3_siso_recurrent", _ptr(q), _strides3(q), _ptr(k), _strides3(k), _ptr(v), _strides3(v),
-          _ptr(gate), _strides3(gate), _ptr(adt), _strides3(adt), _ptr(dt), _strides3(dt), _ptr(trap_logit),
-          _strides3(trap_logit), _ptr(sk), B, L, H, N, D, _ptr(out), _ptr(ws), ws.numel(), _stream())
+    args = (_ptr(q), _strides3(q), _ptr(k), _strides3(k), _ptr(v), _strides3(v), _ptr(gate), _strides3(gate),
+            _ptr(adt), _strides3(adt), _ptr(dt), _strides3(dt), _ptr(trap_logit), _strides3(trap_logit), _ptr(sk),
+            B, L, H, N, D, _ptr(out))
+    if noalloc:
+        _call("mlk_mamba3_siso_recurrent_noalloc", *args, _stream())
+    else:
+        ws = _workspace(4 * 3 * B * L * H, q.device)
+        _call("mlk_mamba3_siso_recurrent", *args, _ptr(ws), ws.numel(), _stream())
     return out
 
 
@@ -914,7 +930,8 @@ def exported_symbols() -> list[str]:
     """Names of the C ABI entry points this module binds."""
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
-            "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent", "mlk_mamba3_siso_forward",
+            "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent",
+            "mlk_mamba3_siso_recurrent_noalloc", "mlk_mamba3_siso_forward",
             "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear",
             "mlk_layer_norm_bf16", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend", "mlk_mla_attend_normed"]
 
