@@ -480,9 +480,18 @@ def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
     f = 4
     total_bytes = (2 * T * d + W * d + d * d_inner) * f + d * f
     total_flops = 2 * T * d * W + 7 * T * H * N * D + 2 * T * d_inner * d
-    launches = _C.mamba3_block_launches(x, *block_args)
-    if len(launches) == 1:
-        ops = {launches[0]: dict(fn=step, bytes=total_bytes, flops=total_flops)}
+    launches = _C.mamba3_block_launches()
+    if launches[0] == "rms_norm_mamba3_forward":
+        y = _C.rms_norm_mamba3_forward(x, norm_w, 1e-5, cfg["norm_groups"], wts["in_w"], *mp, *consts)
+        ops = {
+            # GroupedRMSNorm + in_proj + scan in one kernel: x and the in_proj weight in, y out.
+            "rms_norm_mamba3_forward": dict(fn=lambda: _C.rms_norm_mamba3_forward(x, norm_w, 1e-5, cfg["norm_groups"],
+                                                                                  wts["in_w"], *mp, *consts),
+                                            bytes=(T * d + d + W * d + T * d_inner) * f,
+                                            flops=2 * T * d * W + 7 * T * H * N * D),
+            "out_proj_residual": dict(fn=lambda: _C.linear_residual(y, wts["out_w"], None, x),
+                                      bytes=(T * d_inner + d * d_inner + 2 * T * d) * f, flops=2 * T * d_inner * d),
+        }
     else:
         h = _C.rms_norm(x, norm_w, 1e-5, cfg["norm_groups"])
         proj = _C.linear(h, wts["in_w"])

@@ -296,6 +296,34 @@ mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_
                                    double c_eps, double a_floor, float* out, void* workspace,
                                    size_t workspace_bytes, mlk_stream_t stream);
 
+/* The mixer of the RMSNorm -> Mamba-3 residual block in one launch:
+ *   out = mamba3_siso_forward(in_proj(GroupedRMSNorm(x)))
+ * with the in-kernel silu gate: rms_norm (montlok.cpp:915-938), the in_proj
+ * linear and mamba3_siso_forward (montlok.cpp:333-492) of the Mamba3Layer
+ * forward (reference/Model/layers/mamba3_layer.py:488-498; mamba3_siso_layer,
+ * montlok.cpp:496-519, without its out_proj). No single counterpart in the
+ * reference's op table. x: [B, L, d_model] with batch/token strides (dense
+ * last dim); norm_w [d_model] (norm_groups groups, eps cast through float32);
+ * in_weight [W, d_model] fp32 (in_dtype: mlk_dtype); the mixer's parameters
+ * and geometry as mlk_mamba3_siso_forward; out: [B, L, d_inner] contiguous.
+ * One block per (window, head) computes the in_proj columns its head reads
+ * into LDS and runs the chunked scan from there, so the in_proj rows never
+ * reach memory. The result equals mlk_rms_norm_linear ->
+ * mlk_mamba3_siso_forward bit for bit where mlk_rms_norm_linear takes its
+ * one-wave-per-tile form. Built for d_state 16 with heads of 32, d_model <= 64
+ * in RMSNorm groups of 8, 3 * nheads + num_rope_angles <= 16, one B/C group,
+ * fp32 in_proj weights and 16-byte aligned x rows; MLK_ERR_UNSUPPORTED
+ * otherwise (the caller then runs the two operators). The block is this,
+ * then mlk_linear_residual for out_proj + x. */
+mlk_status mlk_rms_norm_mamba3_forward(const float* x, int64_t batch, int64_t length, int64_t d_model,
+                                       int64_t x_batch_stride, int64_t x_token_stride, const float* norm_w,
+                                       double norm_eps, int64_t norm_groups, const void* in_weight, int32_t in_dtype,
+                                       const float* b_bias, const float* c_bias, const float* b_norm_w,
+                                       const float* c_norm_w, const float* dt_bias, const float* skip,
+                                       int64_t d_state, int64_t ngroups, int64_t nheads, int64_t headdim,
+                                       int64_t num_rope_angles, double b_eps, double c_eps, double a_floor,
+                                       float* out, mlk_stream_t stream);
+
 /* One token of the same layer for `streams` independent sequences with
  * carried state. No reference operator exists (the reference kernel keeps the
  * state inside one call, montlok_kernel.h:257-259); this is the state the

@@ -35,6 +35,7 @@
 // sequential fp32 dot product by rounding only.
 
 #include "mlk_common.h"
+#include "tile_f32.h"
 
 namespace mlk {
 namespace {
@@ -454,68 +455,15 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
     const int64_t n0 = static_cast<int64_t>(blockIdx.x % n_tiles) * 16;
     const int64_t xr = row0 + li < p.rows ? row0 + li : p.rows - 1;
     const int64_t wr = n0 + li < p.N ? n0 + li : p.N - 1;
-    const float* xrow = p.x + xr * p.x_stride;
+    const int K = static_cast<int>(p.K);
     float xv[KS][8];
     bool live[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-        const int k = 32 * s + 8 * group;
-        live[s] = k < p.K;
-        const float* src = xrow + (live[s] ? k : 0);
-        const float4 lo = *reinterpret_cast<const float4*>(src);
-        const float4 hi = *reinterpret_cast<const float4*>(src + 4);
-        xv[s][0] = lo.x; xv[s][1] = lo.y; xv[s][2] = lo.z; xv[s][3] = lo.w;
-        xv[s][4] = hi.x; xv[s][5] = hi.y; xv[s][6] = hi.z; xv[s][7] = hi.w;
-    }
+    tile_load8<KS>(p.x + xr * p.x_stride, K, group, xv, live);
     if constexpr (GS > 0) {
-        static_assert(GS == 8 || GS == 16 || GS == 32 || (GS == 64 && KS % 2 == 0), "RMSNorm group size");
         float nw[KS][8];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const float* src = p.norm_w + (live[s] ? 32 * s + 8 * group : 0);
-            const float4 lo = *reinterpret_cast<const float4*>(src);
-            const float4 hi = *reinterpret_cast<const float4*>(src + 4);
-            nw[s][0] = lo.x; nw[s][1] = lo.y; nw[s][2] = lo.z; nw[s][3] = lo.w;
-            nw[s][4] = hi.x; nw[s][5] = hi.y; nw[s][6] = hi.z; nw[s][7] = hi.w;
-        }
-        double part[KS][2];
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const double a = xv[s][4 * hf], b = xv[s][4 * hf + 1], c = xv[s][4 * hf + 2], d = xv[s][4 * hf + 3];
-                part[s][hf] = (a * a + b * b) + (c * c + d * d);
-            }
-        if constexpr (GS == 64) {
-#pragma unroll
-            for (int s = 0; s < KS; s += 2)
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const double q = part[s][hf] + part[s + 1][hf];
-                    part[s][hf] = q;
-                    part[s + 1][hf] = q;
-                }
-        }
-        if constexpr (GS >= 32) {
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) part[s][hf] += shfl_xor_d(part[s][hf], 32);
-        }
-        if constexpr (GS >= 16) {
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) part[s][hf] += shfl_xor_d(part[s][hf], 16);
-        }
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const double scale = 1.0 / sqrt((part[s][0] + part[s][1]) / static_cast<double>(GS) + p.norm_eps);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                xv[s][j] = static_cast<float>((static_cast<double>(xv[s][j]) * scale) * static_cast<double>(nw[s][j]));
-            }
-        }
+        bool nlive[KS];
+        tile_load8<KS>(p.norm_w, K, group, nw, nlive);
+        tile_rms_norm<KS, GS>(xv, nw, p.norm_eps);
     }
     f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
     if (p.bias != nullptr) {
@@ -545,29 +493,10 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
         }
         y = acc;
     } else {
-        const float* wrow = static_cast<const float*>(p.w) + wr * p.K;
         float wv[KS][8];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const float* src = wrow + (live[s] ? 32 * s + 8 * group : 0);
-            const float4 lo = *reinterpret_cast<const float4*>(src);
-            const float4 hi = *reinterpret_cast<const float4*>(src + 4);
-            wv[s][0] = lo.x; wv[s][1] = lo.y; wv[s][2] = lo.z; wv[s][3] = lo.w;
-            wv[s][4] = hi.x; wv[s][5] = hi.y; wv[s][6] = hi.z; wv[s][7] = hi.w;
-        }
-        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
-        f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(live[s] ? wv[s][j] : 0.0f, live[s] ? xv[s][j] : 0.0f,
-                                                            acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(live[s] ? wv[s][j + 1] : 0.0f,
-                                                            live[s] ? xv[s][j + 1] : 0.0f, acc1, 0, 0, 0);
-            }
-        }
-        y = acc0 + acc1;
+        bool wlive[KS];
+        tile_load8<KS>(static_cast<const float*>(p.w) + wr * p.K, K, group, wv, wlive);
+        y = tile_mfma_f32<KS>(wv, xv, live);
     }
     y += bias;
     const int64_t row = row0 + li;

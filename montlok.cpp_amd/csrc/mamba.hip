@@ -45,6 +45,7 @@
 #include <mutex>
 
 #include "mlk_common.h"
+#include "tile_f32.h"
 
 namespace mlk {
 namespace {
@@ -845,12 +846,42 @@ struct ScanArgs {
     float* out;  // [B, L, H*D] contiguous
 };
 
-// Four waves per SIMD for the four-wave blocks: at d_state 64 the compiler
-// then spills 8 VGPRs, and the kernel is 5% faster than at three waves
-// (1.17 vs 1.23 ms at 1024 x 256 tokens, 8 heads); the others as they fall.
+// The LDS of one (window, head) scan.
 template <int C, int NT, int DT>
-__global__ __launch_bounds__(64 * DT) __attribute__((amdgpu_waves_per_eu(DT == 4 ? 4 : 1)))
-void scan_fused_kernel(ScanArgs a) {
+struct ScanLds {
+    static constexpr int N = 16 * NT, CT = C / 16, NP = N + 4, WP = C + 4, NPAIR = CT * (CT + 1) / 2, RM = N / 2;
+    __attribute__((aligned(16))) float q_sh[C * NP];
+    __attribute__((aligned(16))) float k_sh[C * NP];
+    __attribute__((aligned(16))) float w_s[(C + 1) * WP];  // row C: sink of the walk's steps past the chunk
+    f32x4_t p_s[NPAIR * 64];
+    float ang_s[C * RM];  // angle logits, then tanh(angle) * pi
+    float cum_s[C * RM];  // cumulative angles
+    float raw_s[3][C];    // dt, A, trap logits
+    __attribute__((aligned(16))) float coef[4][C];  // alpha, beta, gamma, dt
+    float sc_s[2][C];     // B and C norm scales
+    float ck_s[C];
+    float kp_s[2][N];
+    float nrm_s[4][N];    // B norm weight, C norm weight, this head's B bias, C bias
+};
+
+// Called by every thread of the block around each chunk of the scan.
+struct NoChunkHooks {
+    __device__ void before(int64_t) const {}
+    __device__ void after(int64_t, bool) const {}
+};
+
+// The scan of one (window, head) by the DT waves of threads tid_base ..
+// tid_base + 64 DT - 1 of the block, with LDS `sh`. TILE = false: the in_proj
+// rows of window b are in global memory at a.proj + b a.sb + t a.st. TILE =
+// true: the rows of the current chunk only are at a.proj + (t - c0) a.st
+// (LDS, refilled by hooks.before; b and a.sb unused). TILE_OUT (TILE unless
+// given) likewise for the outputs: a.out [B, L, d_inner], or the current
+// chunk's rows at a.out + (t - c0) d_inner.
+// Every thread of the block runs the same sequence of barriers, so several
+// heads can share a block.
+template <int C, int NT, int DT, bool TILE, class Hooks, bool TILE_OUT = TILE>
+__device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>& sh, int64_t b, int64_t h,
+                                          int tid_base, const Hooks& hooks) {
     static_assert(C == 32, "the BCNorm step takes one lane per (token, B|C) pair of a 64-lane wave");
     constexpr int N = 16 * NT, D = 16 * DT, NTH = 64 * DT;
     constexpr int CT = C / 16;
@@ -859,40 +890,37 @@ void scan_fused_kernel(ScanArgs a) {
     constexpr int RM = N / 2;  // rotary angles at most
     constexpr bool kEarlyGate = DT == 2;
     static_assert(NTH % N == 0, "a thread keeps one q/k column across the chunk");
-    __shared__ __attribute__((aligned(16))) float q_sh[C * NP];
-    __shared__ __attribute__((aligned(16))) float k_sh[C * NP];
-    __shared__ __attribute__((aligned(16))) float w_s[(C + 1) * WP];  // row C: sink of the walk's steps past the chunk
-    __shared__ f32x4_t p_s[NPAIR * 64];
-    __shared__ float ang_s[C * RM];  // angle logits, then tanh(angle) * pi
-    __shared__ float cum_s[C * RM];  // cumulative angles
-    __shared__ float raw_s[3][C];    // dt, A, trap logits
-    __shared__ __attribute__((aligned(16))) float coef[4][C];  // alpha, beta, gamma, dt
-    __shared__ float sc_s[2][C];     // B and C norm scales
-    __shared__ float ck_s[C];
-    __shared__ float kp_s[2][N];
-    __shared__ float nrm_s[4][N];    // B norm weight, C norm weight, this head's B bias, C bias
+    float* q_sh = sh.q_sh;
+    float* k_sh = sh.k_sh;
+    float* w_s = sh.w_s;
+    f32x4_t* p_s = sh.p_s;
+    float* ang_s = sh.ang_s;
+    float* cum_s = sh.cum_s;
+    auto& raw_s = sh.raw_s;
+    auto& coef = sh.coef;
+    auto& sc_s = sh.sc_s;
+    float* ck_s = sh.ck_s;
+    auto& kp_s = sh.kp_s;
+    auto& nrm_s = sh.nrm_s;
     // Din(t) and Wp(t) live in the padding columns C and C + 1 of the W rows.
     constexpr int kDin = C, kWp = C + 1;
+    static_assert(NPAIR == ScanLds<C, NT, DT>::NPAIR && NP == ScanLds<C, NT, DT>::NP, "LDS layout");
 
     const int64_t H = a.H, L = a.L, G = a.G;
     const int R = static_cast<int>(a.R);
-    // Block -> (window, head) in 32-bit arithmetic (B * H < 2^31, checked at launch).
-    const unsigned Hu = static_cast<unsigned>(a.H), nblk = static_cast<unsigned>(a.B * a.H);
-    unsigned lin = blockIdx.x;
-    if (nblk % 8 == 0) lin = (lin % 8) * (nblk / 8) + lin / 8;
-    const int64_t b = lin / Hu, h = lin % Hu;
+    const unsigned Hu = static_cast<unsigned>(a.H);
     const int64_t d_inner = H * D, GN = G * N;
-    const float* base = a.proj + b * a.sb;
+    const float* base = TILE ? a.proj : a.proj + b * a.sb;
     const float* brow = base + 2 * d_inner + static_cast<int64_t>(static_cast<unsigned>(h) / (Hu / static_cast<unsigned>(a.G))) * N;
     const float* crow = brow + GN;
     const float* mrow = base + 2 * d_inner + 2 * GN + h;  // dt; A at +H, trap at +2H
     const float* arow = base + 2 * d_inner + 2 * GN + 3 * H;
     const float* xrow = base + d_inner + h * D;
-    const float* zrow = a.gate + b * a.gsb + h * D;
-    float* orow = a.out + b * L * d_inner + h * D;
+    const float* zrow = (TILE ? a.gate : a.gate + b * a.gsb) + h * D;
+    float* orow = (TILE_OUT ? a.out : a.out + b * L * d_inner) + h * D;
     const float skip = a.skip[h], dt_bias = a.dt_bias[h];
 
-    for (int i = threadIdx.x; i < N; i += NTH) {
+    for (int i = static_cast<int>(threadIdx.x) - tid_base; i < N; i += NTH) {
         kp_s[0][i] = 0.0f;  // k_p before the first chunk
         nrm_s[0][i] = a.b_norm_w[i];
         nrm_s[1][i] = a.c_norm_w[i];
@@ -922,7 +950,7 @@ void scan_fused_kernel(ScanArgs a) {
         // The thread index is made opaque per chunk so that the per-lane index
         // arithmetic of the phases below is recomputed here (a few integer
         // operations) rather than hoisted out of the loop and held in VGPRs.
-        int tid = threadIdx.x;
+        int tid = static_cast<int>(threadIdx.x) - tid_base;
         asm volatile("" : "+v"(tid));
         const int lane = tid & 63, g = lane >> 4, li = lane & 15;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -960,12 +988,13 @@ void scan_fused_kernel(ScanArgs a) {
             constexpr int MU = (3 * C + NTH - 1) / NTH;
             constexpr int AU = (C * RM + NTH - 1) / NTH;
             const int st32 = static_cast<int>(a.st), gst32 = static_cast<int>(a.gst);
-            const float* bc = brow + c0 * a.st;
-            const float* cc = crow + c0 * a.st;
-            const float* mc = mrow + c0 * a.st;
-            const float* ac = arow + c0 * a.st;
-            const float* xc = xrow + c0 * a.st;
-            const float* zc = zrow + c0 * a.gst;
+            const int64_t cr = TILE ? 0 : c0 * a.st, cg = TILE ? 0 : c0 * a.gst;
+            const float* bc = brow + cr;
+            const float* cc = crow + cr;
+            const float* mc = mrow + cr;
+            const float* ac = arow + cr;
+            const float* xc = xrow + cr;
+            const float* zc = zrow + cg;
             float bx[BU], cx[BU], mx[MU], ax[AU];
 #pragma unroll
             for (int j = 0; j < BU; ++j) {
@@ -1276,7 +1305,7 @@ void scan_fused_kernel(ScanArgs a) {
                         // With an explicit gate gz = z, and the double product of two
                         // floats rounded once is the fp32 product y * gate.
                         const float o = static_cast<float>(static_cast<double>(y) * gz[tt][v]);
-                        if (!last || t < Lc) orow[(c0 + t) * d_inner + col] = o;
+                        if (!last || t < Lc) orow[((TILE_OUT ? 0 : c0) + t) * d_inner + col] = o;
                     }
                 }
                 p0 += tt + 1;
@@ -1314,8 +1343,31 @@ void scan_fused_kernel(ScanArgs a) {
         __syncthreads();
     };
     int64_t c0 = 0;
-    for (; c0 + C < L; c0 += C) chunk(std::false_type{}, c0);
+    for (; c0 + C < L; c0 += C) {
+        hooks.before(c0);
+        chunk(std::false_type{}, c0);
+        hooks.after(c0, false);
+    }
+    hooks.before(c0);
     chunk(std::true_type{}, c0);
+    hooks.after(c0, true);
+}
+
+// One block of DT waves per (window, head). Four waves per SIMD for the
+// four-wave blocks: at d_state 64 the compiler then spills 8 VGPRs, and the
+// kernel is 5% faster than at three waves (1.17 vs 1.23 ms at 1024 x 256
+// tokens, 8 heads); the others as they fall. Blocks are ordered so that the
+// heads of one window run on one XCD and share its L2 copy of the window's
+// B/C rows.
+template <int C, int NT, int DT>
+__global__ __launch_bounds__(64 * DT) __attribute__((amdgpu_waves_per_eu(DT == 4 ? 4 : 1)))
+void scan_fused_kernel(ScanArgs a) {
+    __shared__ ScanLds<C, NT, DT> sh;
+    // Block -> (window, head) in 32-bit arithmetic (B * H < 2^31, checked at launch).
+    const unsigned Hu = static_cast<unsigned>(a.H), nblk = static_cast<unsigned>(a.B * a.H);
+    unsigned lin = blockIdx.x;
+    if (nblk % 8 == 0) lin = (lin % 8) * (nblk / 8) + lin / 8;
+    scan_head<C, NT, DT, false>(a, sh, lin / Hu, lin % Hu, 0, NoChunkHooks{});
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -1345,6 +1397,143 @@ bool launch_scan_fused(const ScanArgs& s, int64_t N, int64_t D, hipStream_t stre
     MLK_FUSED(1, 1) MLK_FUSED(1, 2) MLK_FUSED(1, 4) MLK_FUSED(2, 1) MLK_FUSED(2, 2) MLK_FUSED(2, 4)
     MLK_FUSED(4, 1) MLK_FUSED(4, 2) MLK_FUSED(4, 4)
 #undef MLK_FUSED
+    return false;
+}
+
+// ---------------------------------------------------------------------------
+// The RMSNorm -> Mamba-3 block: GroupedRMSNorm + in_proj + scan in one kernel
+// ---------------------------------------------------------------------------
+//
+// x + out_proj(mixer(in_proj(GroupedRMSNorm(x)))) (the Mamba3Layer forward of
+// reference/Model/layers/mamba3_layer.py:488-498 over mamba3_siso_layer,
+// montlok.cpp:496-519) in two launches: this kernel (the block's mixer,
+// mlk_rms_norm_mamba3_forward), then the out_proj with the residual added in
+// its epilogue (mlk_linear_residual). One block
+// of DT waves per (window, head), so that each head's scan keeps a SIMD to
+// itself, as in scan_fused_kernel. Per 32-token chunk, before the scan, the
+// block computes the in_proj columns its head reads (its z and x columns, the
+// B/C group rows, the dt/A/trap logits and the angles: 7 column tiles at the
+// block workload's geometry, against 19 for the whole row) for the chunk's
+// rows into LDS, laid out as the whole row; each wave normalises its x
+// fragments of the chunk's two 16-row tiles once and computes 16 x 16 tiles
+// with the arithmetic of the one-wave-per-tile linear and its GroupedRMSNorm
+// prologue (tile_f32.h). scan_head then reads the rows from LDS and writes the
+// gated outputs y [B, L, d_inner]. The in_proj rows never reach HBM; the
+// result equals rms_norm_linear -> mamba3_siso_forward bit for bit wherever
+// the former takes its one-wave-per-tile form.
+struct BlockArgs {
+    const float* x;  // [B, L, dm], token rows x_ts floats apart, windows x_bs apart
+    int64_t x_bs, x_ts;
+    int64_t dm, W;
+    const float* norm_w;  // [dm]
+    double norm_eps;
+    const float* in_w;  // [W, dm] fp32
+    ScanArgs s;         // mixer parameters, B, L, G, H, R and the output y (proj and gate are set in the kernel)
+};
+
+template <int NT, int DT, int KSI, int GS, int NCT>
+__global__ __launch_bounds__(64 * DT) __attribute__((amdgpu_waves_per_eu(1)))
+void mamba3_block_scan_kernel(BlockArgs p) {
+    constexpr int C = 32, D = 16 * DT;
+    static_assert(DT == 2, "one wave per 16-row tile of the 32-token chunk");
+    __shared__ ScanLds<C, NT, DT> sh;
+    extern __shared__ __attribute__((aligned(16))) float proj_s[];  // [C, pp]
+
+    const int64_t H = p.s.H, L = p.s.L;
+    // Block -> (window, head), the heads of a window on one XCD (as scan_fused_kernel).
+    const unsigned Hu = static_cast<unsigned>(H), nblk = static_cast<unsigned>(p.s.B * H);
+    unsigned lin = blockIdx.x;
+    if (nblk % 8 == 0) lin = (lin % 8) * (nblk / 8) + lin / 8;
+    const int64_t b = lin / Hu, h = lin % Hu;
+    const int lane = threadIdx.x & 63, li = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int dm = static_cast<int>(p.dm), W = static_cast<int>(p.W);
+    const int DI = static_cast<int>(H) * D;
+    const int pp = (W + 15) / 16 * 16 + 4;
+    const float* xw = p.x + b * p.x_bs;
+
+    ScanArgs a = p.s;
+    a.proj = proj_s;
+    a.sb = 0;
+    a.st = pp;
+    a.gate = proj_s;
+    a.gsb = 0;
+    a.gst = pp;
+    a.gate_logits = 1;
+
+    struct Hooks {
+        const BlockArgs& p;
+        const float* xw;
+        float* proj_s;
+        int64_t L;
+        int li, grp, wave, dm, W, DI, pp, h;
+
+        // This head's column tiles: z (D / 16), x (D / 16), the B/C rows, then
+        // dt/A/trap/angles to the end of the row.
+        __device__ int tile_col(int j) const {
+            constexpr int DTL = D / 16;
+            if (j < DTL) return h * D + 16 * j;
+            if (j < 2 * DTL) return DI + h * D + 16 * (j - DTL);
+            return 2 * DI + 16 * (j - 2 * DTL);
+        }
+
+        // Wave w computes the chunk's 16-row tile w against all of the head's
+        // column tiles. Every load (its x rows, the norm weight, the NCT
+        // weight fragments) is issued before the first product; the tiles
+        // past the head's count repeat its last one and are not stored.
+        // (Staging the weight rows through LDS once per block measured
+        // slower, 15.7 against 12.2 us at 64 x 32 tokens: the staging loads
+        // ran one after another for want of registers.)
+        __device__ void before(int64_t c0) const {
+            const int ncol = 2 * (D / 16) + (W - 2 * DI + 15) / 16;
+            float xv[KSI][8], nw[KSI][8];
+            bool live[KSI], nlive[KSI];
+            const int64_t r = c0 + 16 * wave + li;
+            tile_load8<KSI>(xw + (r < L ? r : L - 1) * p.x_ts, dm, grp, xv, live);
+            tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
+            float wv[NCT][KSI][8];
+            bool wlive[NCT][KSI];
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) {
+                const int n0 = tile_col(j < ncol ? j : ncol - 1);
+                const int wr = n0 + li < W ? n0 + li : W - 1;
+                tile_load8<KSI>(p.in_w + static_cast<int64_t>(wr) * dm, dm, grp, wv[j], wlive[j]);
+            }
+            tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) {
+                tile_f32x4 y = tile_mfma_f32<KSI>(wv[j], xv, live);
+                y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
+                if (j < ncol) *reinterpret_cast<tile_f32x4*>(proj_s + (16 * wave + li) * pp + tile_col(j) + 4 * grp) = y;
+            }
+            __syncthreads();
+        }
+        __device__ void after(int64_t, bool) const {}
+    };
+    const Hooks hooks{p, xw, proj_s, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h)};
+    scan_head<C, NT, DT, true, Hooks, false>(a, sh, b, h, 0, hooks);
+}
+
+// Geometries of the block kernel: (d_state, headdim, the in_proj's 32-wide k
+// steps, the RMSNorm group size); false where none is built. The k steps
+// follow the one-wave-per-tile linear's choice (2 up to K = 64, 4 up to 128,
+// 8 up to 256), so the tiles run the same instructions.
+bool launch_block_scan(const BlockArgs& p, int64_t N, int64_t D, int64_t gs, hipStream_t stream) {
+    const int ksi = p.dm <= 64 ? 2 : (p.dm <= 128 ? 4 : 8);
+    const size_t lds = sizeof(float) * 32 * static_cast<size_t>((p.W + 15) / 16 * 16 + 4);
+    if (lds > 64 * 1024) return false;
+    const dim3 grid(static_cast<unsigned>(p.s.B * p.s.H));
+    // Column tiles a head reads: its z and x columns, the B/C rows, dt/A/trap/angles.
+    const int64_t DI = p.s.H * D;
+    const int64_t ncol = 2 * (D / 16) + (p.W - 2 * DI + 15) / 16;
+#define MLK_BLOCK(NV, DV, KSIV, GSV, NCTV)                                                                       \
+    if (N == NV && D == DV && ksi == KSIV && gs == GSV && ncol <= NCTV) {                                         \
+        hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV>), grid, dim3(4 * DV),    \
+                           lds, stream, p);                                                                       \
+        return true;                                                                                             \
+    }
+    MLK_BLOCK(16, 32, 2, 8, 7)  // d_model up to 64 in groups of 8, d_state 16, heads of 32, 3H + R <= 16
+#undef MLK_BLOCK
     return false;
 }
 
@@ -1930,6 +2119,68 @@ mlk_status mlk_mamba3_siso_step(const float* projected, int64_t streams, int64_t
     if (d_state <= 64) MLK_STEP(64);
     MLK_STEP(128);
 #undef MLK_STEP
+}
+
+mlk_status mlk_rms_norm_mamba3_forward(const float* x, int64_t batch, int64_t length, int64_t d_model,
+                                       int64_t x_batch_stride, int64_t x_token_stride, const float* norm_w,
+                                       double norm_eps, int64_t norm_groups, const void* in_weight, int32_t in_dtype,
+                                       const float* b_bias, const float* c_bias, const float* b_norm_w,
+                                       const float* c_norm_w, const float* dt_bias, const float* skip,
+                                       int64_t d_state, int64_t ngroups, int64_t nheads, int64_t headdim,
+                                       int64_t num_rope_angles, double b_eps, double c_eps, double a_floor,
+                                       float* out, mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 0 && d_model > 0, "inputs must be [B,L,d_model]");
+    MLK_CHECK(norm_groups > 0 && d_model % norm_groups == 0, "groups must divide the normalised dimension");
+    MLK_CHECK(d_state > 0 && ngroups > 0 && nheads > 0 && headdim > 0, "invalid Mamba-3 geometry");
+    MLK_CHECK(nheads % ngroups == 0, "nheads must be divisible by ngroups");
+    MLK_CHECK(num_rope_angles >= 0 && 2 * num_rope_angles <= d_state, "num_rope_angles must fit in d_state");
+    MLK_CHECK(x_token_stride >= d_model, "inputs must be [B,L,d_model] with a dense last dimension");
+    const int64_t width = 2 * nheads * headdim + 2 * ngroups * d_state + 3 * nheads + num_rope_angles;
+    const int64_t gs = d_model / norm_groups;
+    const bool vec = aligned16(x) && x_token_stride % 4 == 0 && x_batch_stride % 4 == 0 && aligned16(norm_w) &&
+                     aligned16(in_weight) && d_model % 8 == 0;
+    const bool built = d_state == 16 && headdim == 32 && gs == 8 && d_model <= 64 &&
+                       sizeof(float) * 32 * static_cast<size_t>((width + 15) / 16 * 16 + 4) <= 64 * 1024;
+    if (!vec || !built || in_dtype != MLK_DTYPE_F32 || ngroups != 1 || scan_mode() != ScanMode::kFused ||
+        batch * nheads >= (int64_t{1} << 31)) {
+        set_error("rms_norm_mamba3_forward: geometry without the fused kernel (use rms_norm_linear, then "
+                  "mamba3_siso_forward)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    if (batch * length == 0) return MLK_OK;
+    MLK_CHECK(x && norm_w && in_weight && b_bias && c_bias && b_norm_w && c_norm_w && dt_bias && skip && out,
+              "null tensor pointer");
+    BlockArgs p{};
+    p.x = x;
+    p.x_bs = x_batch_stride;
+    p.x_ts = x_token_stride;
+    p.dm = d_model;
+    p.W = width;
+    p.norm_w = norm_w;
+    p.norm_eps = static_cast<double>(static_cast<float>(norm_eps));
+    p.in_w = static_cast<const float*>(in_weight);
+    ScanArgs& s = p.s;
+    s.B = batch;
+    s.L = length;
+    s.G = ngroups;
+    s.H = nheads;
+    s.R = num_rope_angles;
+    s.b_bias = b_bias;
+    s.c_bias = c_bias;
+    s.b_norm_w = b_norm_w;
+    s.c_norm_w = c_norm_w;
+    s.b_eps = static_cast<float>(b_eps);
+    s.c_eps = static_cast<float>(c_eps);
+    s.dt_bias = dt_bias;
+    s.a_floor = static_cast<float>(a_floor);
+    s.skip = skip;
+    s.out = out;
+    if (!launch_block_scan(p, d_state, headdim, gs, reinterpret_cast<hipStream_t>(stream))) {
+        set_error("rms_norm_mamba3_forward: geometry without the fused kernel (use rms_norm_linear, then "
+                  "mamba3_siso_forward)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    return launch_status("rms_norm_mamba3_forward");
 }
 
 }  // extern "C"

@@ -59,6 +59,8 @@ def _load():
         "mlk_math_check": [_vp, _i64, _vp, _vp],
         "mlk_mamba3_siso_recurrent": [_vp, _vp] * 7 + [_vp] + [_i64] * 5 + [_vp, _vp, C.c_size_t, _vp],
         "mlk_mamba3_siso_recurrent_noalloc": [_vp, _vp] * 7 + [_vp] + [_i64] * 5 + [_vp, _vp],
+        "mlk_rms_norm_mamba3_forward": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _dbl, _i64, _vp, C.c_int32] +
+                                       [_vp] * 6 + [_i64] * 5 + [_dbl, _dbl, _dbl, _vp, _vp],
         "mlk_mamba3_siso_forward": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64] + [_vp] * 6 + [_i64] * 5 +
                                    [_dbl, _dbl, _dbl, _vp, _vp, C.c_size_t, _vp],
         "mlk_mamba3_siso_step": [_vp, _i64, _i64] + [_vp] * 6 + [_i64] * 5 + [_dbl, _dbl, _dbl] + [_vp] * 4 +
@@ -525,36 +527,70 @@ def mamba3_siso_layer(inputs, in_weight, out_weight, b_bias, c_bias, b_norm_w, c
     return linear(output, out_weight)
 
 
+_BLOCK_PATH = {"last": None}
+
+
+def rms_norm_mamba3_forward(inputs, norm_weight, norm_eps, norm_groups, in_weight, b_bias, c_bias, b_norm_w,
+                            c_norm_w, dt_bias, skip, d_state, ngroups, nheads, headdim, num_rope_angles, b_eps, c_eps,
+                            a_floor):
+    """mamba3_siso_forward(linear(rms_norm(inputs, norm_weight, norm_eps, norm_groups), in_weight)) with the
+    in-kernel gate: [B, L, d_model] -> [B, L, d_inner]. One launch where the fused kernel is built for the
+    geometry (the in_proj rows stay in LDS), else rms_norm_linear then mamba3_siso_forward; the same result
+    bit for bit where rms_norm_linear takes its one-wave-per-tile form. No single counterpart in the
+    reference's op table (montlok.cpp:915-938, 333-492)."""
+    _require_f32_gpu(inputs, "inputs")
+    _check(inputs.dim() == 3, "inputs must be [B,L,d_model]")
+    B, L, dm = inputs.shape
+    _check(norm_groups > 0 and dm % norm_groups == 0, "groups must divide the normalised dimension")
+    nw = _dense_parameter(norm_weight, dm, "weight")
+    w_in = _weight(in_weight)
+    d_inner = nheads * headdim
+    width = 2 * d_inner + 2 * ngroups * d_state + 3 * nheads + num_rope_angles
+    _check(tuple(w_in.shape) == (width, dm), f"in_proj weight must be [{width}, {dm}]")
+    params = _mamba_params(b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, nheads)
+    if inputs.stride(-1) == 1:
+        out = torch.empty((B, L, d_inner), dtype=torch.float32, device=inputs.device)
+        lib = _load()
+        status = lib.mlk_rms_norm_mamba3_forward(_ptr(inputs), B, L, dm, inputs.stride(0), inputs.stride(1),
+                                                 _ptr(nw), float(norm_eps), int(norm_groups), _ptr(w_in),
+                                                 _WEIGHT_DTYPES[w_in.dtype], *(_ptr(t) for t in params), d_state,
+                                                 ngroups, nheads, headdim, num_rope_angles, float(b_eps),
+                                                 float(c_eps), float(a_floor), _ptr(out), _stream())
+        if status == 0:
+            _BLOCK_PATH["mixer"] = ["rms_norm_mamba3_forward"]
+            return out
+        if status != 3:  # anything but MLK_ERR_UNSUPPORTED
+            raise RuntimeError(lib.mlk_last_error().decode())
+    projected = rms_norm_linear(inputs, norm_weight, norm_eps, norm_groups, in_weight)
+    _BLOCK_PATH["mixer"] = ["rms_norm_linear", "mamba3_siso_forward"]
+    return mamba3_siso_forward(projected, None, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups,
+                               nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor)
+
+
 def mamba3_block(inputs, norm_weight, norm_eps, norm_groups, in_weight, out_weight, b_bias, c_bias, b_norm_w,
                  c_norm_w, dt_bias, skip, d_state, ngroups, nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor):
     """The RMSNorm -> Mamba-3 residual block, x + mamba3_siso_layer(GroupedRMSNorm(x)) (the Mamba3Layer
     forward of python/montlok/rdt/reference/Model/layers/mamba3_layer.py:488-498 on the official backend;
     montlok.cpp:496-519 for the layer). No single counterpart in the reference's op table.
 
-    GroupedRMSNorm + in_proj run as one launch where that form is built, then the fused mixer, then
-    out_proj with the residual added in its epilogue: the result equals rms_norm -> mamba3_siso_layer ->
-    x + y bit for bit."""
+    rms_norm_mamba3_forward (one launch where built), then out_proj with the residual added in its
+    epilogue: equal to rms_norm -> mamba3_siso_layer -> x + y bit for bit where the linears take their
+    one-wave-per-tile forms."""
     _require_f32_gpu(inputs, "inputs")
     _check(inputs.dim() == 3, "inputs must be [B,L,d_model]")
-    projected = rms_norm_linear(inputs, norm_weight, norm_eps, norm_groups, in_weight)
-    y = mamba3_siso_forward(projected, None, b_bias, c_bias, b_norm_w, c_norm_w, dt_bias, skip, d_state, ngroups,
-                            nheads, headdim, num_rope_angles, b_eps, c_eps, a_floor)
+    w_out = _weight(out_weight)
+    _check(tuple(w_out.shape) == (inputs.size(-1), nheads * headdim),
+           f"out_proj weight must be [{inputs.size(-1)}, {nheads * headdim}]")
+    y = rms_norm_mamba3_forward(inputs, norm_weight, norm_eps, norm_groups, in_weight, b_bias, c_bias, b_norm_w,
+                                c_norm_w, dt_bias, skip, d_state, ngroups, nheads, headdim, num_rope_angles, b_eps,
+                                c_eps, a_floor)
+    _BLOCK_PATH["last"] = _BLOCK_PATH["mixer"] + ["linear_residual"]
     return linear_residual(y, out_weight, None, inputs)
 
 
-def mamba3_block_launches(inputs, norm_weight, norm_eps, norm_groups, in_weight, *_):
-    """Names of the kernel launches ``mamba3_block`` makes for these arguments, in order."""
-    first = ["rms_norm_linear"] if _fused_norm_linear(inputs, norm_groups, in_weight) else ["rms_norm", "linear"]
-    return first + ["mamba3_siso_forward", "linear_residual"]
-
-
-def _fused_norm_linear(x: torch.Tensor, groups: int, weight: torch.Tensor) -> bool:
-    n, k = weight.shape
-    rows = x.numel() // max(k, 1)
-    gs = k // groups if groups > 0 else 0
-    wsize = weight.element_size()
-    return (gs in (8, 16, 32, 64) and k % 8 == 0 and k <= 256 and (k * wsize) % 16 == 0
-            and -(-rows // 128) * -(-n // 64) < 256)
+def mamba3_block_launches() -> list[str] | None:
+    """The kernel launches the last ``mamba3_block`` call made, in order."""
+    return _BLOCK_PATH["last"]
 
 
 def mamba3_block_step(inputs, state, norm_weight, norm_eps, norm_groups, in_weight, out_weight, b_bias, c_bias,
@@ -931,7 +967,7 @@ def exported_symbols() -> list[str]:
     return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent",
-            "mlk_mamba3_siso_recurrent_noalloc", "mlk_mamba3_siso_forward",
+            "mlk_mamba3_siso_recurrent_noalloc", "mlk_mamba3_siso_forward", "mlk_rms_norm_mamba3_forward",
             "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear",
             "mlk_layer_norm_bf16", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend", "mlk_mla_attend_normed"]
 

@@ -56,26 +56,74 @@ def _oracle_block(oracle, block, x):
     return x + oracle.linear(y, _np(m.out_proj.weight))
 
 
-@pytest.mark.parametrize("B,L", [(64, 32), (3, 45), (1, 1)])
-def test_block_vs_oracle_and_separate_ops(dev, oracle, B, L):
+@pytest.mark.parametrize("dm,H,groups,B,L", [(64, 4, 8, 64, 32),   # the block workload
+                                              (64, 4, 8, 3, 45),    # two chunks, the second partial
+                                              (64, 4, 8, 1, 1),
+                                              (64, 4, 8, 5, 96),    # three full chunks
+                                              (32, 2, 4, 7, 33)])   # d_model 32 in 4 groups of 8, 2 heads
+def test_block_vs_oracle_and_separate_ops(dev, oracle, dm, H, groups, B, L):
+    """The block (the fused norm + in_proj + scan kernel, then out_proj + x) against the oracle chain at 1e-5
+    and against the separate operators bit for bit (they take their one-wave-per-tile linears here)."""
     from montlok import _C
     from montlok.rdt import Mamba3BlockHIP
 
-    g = torch.Generator().manual_seed(B * 100 + L)
-    block = Mamba3BlockHIP(64, d_state=16, expand=2, headdim=32, num_groups=8).eval()
+    g = torch.Generator().manual_seed(B * 100 + L + dm)
+    block = Mamba3BlockHIP(dm, d_state=16, expand=2, headdim=32, num_groups=groups).eval()
+    assert block.mamba.nheads == H
     _init(block, g)
-    x = torch.randn(B, L, 64, generator=g)
+    x = torch.randn(B, L, dm, generator=g)
     expect = _oracle_block(oracle, block, x.numpy())
     block = block.to(dev)
     xd = x.to(dev)
     with torch.no_grad():
         out = block(xd)
+        assert _C.mamba3_block_launches() == ["rms_norm_mamba3_forward", "linear_residual"], "the geometry has the one-launch kernel"
         m = block.mamba
-        separate = xd + _C.mamba3_siso_layer(_C.rms_norm(xd, block.norm.weight, 1e-5, 8), m.in_proj.weight,
+        separate = xd + _C.mamba3_siso_layer(_C.rms_norm(xd, block.norm.weight, 1e-5, groups), m.in_proj.weight,
                                              m.out_proj.weight, *m._mixer_args(), *m._geometry())
-    assert out.shape == (B, L, 64)
+    assert out.shape == (B, L, dm)
     assert_close(out, expect, name=f"block {B}x{L} vs oracle")
     assert_bitwise(out, separate.cpu().numpy(), f"block {B}x{L} vs separate operators")
+
+
+def test_block_many_windows_vs_oracle(dev, oracle):
+    """300 windows x 70 tokens: 1200 (window, head) blocks of the fused mixer kernel (the separate in_proj
+    takes its tiled form here, so only the oracle gate applies)."""
+    from montlok import _C
+    from montlok.rdt import Mamba3BlockHIP
+
+    g = torch.Generator().manual_seed(77)
+    block = Mamba3BlockHIP(64, d_state=16, expand=2, headdim=32, num_groups=8).eval()
+    _init(block, g)
+    x = torch.randn(300, 70, 64, generator=g)
+    expect = _oracle_block(oracle, block, x.numpy())
+    block = block.to(dev)
+    with torch.no_grad():
+        out = block(x.to(dev))
+    assert _C.mamba3_block_launches() == ["rms_norm_mamba3_forward", "linear_residual"]
+    assert_close(out, expect, name="block 300x70 vs oracle")
+
+
+def test_block_strided_input_and_unfused_scan(dev, monkeypatch):
+    """A token-strided input (a column slice of wider rows) and MLK_MAMBA3_SCAN=unfused, which sends the
+    block to the three separate launches with the unfused scan: the same result bit for bit."""
+    from montlok import _C
+    from montlok.rdt import Mamba3BlockHIP
+
+    g = torch.Generator().manual_seed(78)
+    block = Mamba3BlockHIP(64, d_state=16, expand=2, headdim=32, num_groups=8).eval()
+    _init(block, g)
+    block = block.to(dev)
+    wide = torch.randn(7, 40, 96, generator=g).to(dev)
+    x = wide[..., 16:80]  # tokens 96 floats apart, windows 40 x 96 apart, dense rows
+    assert not x.is_contiguous()
+    with torch.no_grad():
+        one = block(x)
+        assert _C.mamba3_block_launches() == ["rms_norm_mamba3_forward", "linear_residual"]
+        monkeypatch.setenv("MLK_MAMBA3_SCAN", "unfused")
+        three = block(x.contiguous())
+        assert _C.mamba3_block_launches() == ["rms_norm_linear", "mamba3_siso_forward", "linear_residual"]
+    assert_bitwise(one, three.cpu().numpy(), "fused mixer vs three launches (unfused scan)")
 
 
 def _started_states(stack, S, g):
