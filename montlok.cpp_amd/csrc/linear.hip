@@ -445,7 +445,7 @@ void linear_tiles_kernel(LinearArgs p) {
 // apart, the two halves in registers), scale = 1 / sqrt(sum / GS + eps),
 // x * scale * w rounded once. The normalised x is bit-identical to the
 // rms_norm operator's output, so the product is that of rms_norm then linear.
-template <bool BF16W, int KS, int GS>
+template <bool BF16W, int KS, int GS, bool ALL_LIVE = false>
 __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
     const int lane = threadIdx.x;
     const int li = lane & 15;
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
         float wv[KS][8];
         bool wlive[KS];
         tile_load8<KS>(static_cast<const float*>(p.w) + wr * p.K, K, group, wv, wlive);
-        y = tile_mfma_f32<KS>(wv, xv, live);
+        y = tile_mfma_f32<KS, ALL_LIVE>(wv, xv, live);
     }
     y += bias;
     const int64_t row = row0 + li;
@@ -518,6 +518,12 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
 
 template <bool BF16W, int KS, int GS = 0>
 void launch_small(const LinearArgs& p, int64_t tiles, hipStream_t stream) {
+    // fp32 weights with K filling all KS steps skip the per-operand selects.
+    if (!BF16W && p.K == 32 * KS) {
+        hipLaunchKernelGGL((linear_small_kernel<BF16W, KS, GS, true>), dim3(static_cast<unsigned>(tiles)), dim3(64),
+                           0, stream, p);
+        return;
+    }
     hipLaunchKernelGGL((linear_small_kernel<BF16W, KS, GS>), dim3(static_cast<unsigned>(tiles)), dim3(64), 0, stream,
                        p);
 }

@@ -1431,8 +1431,11 @@ struct BlockArgs {
     ScanArgs s;         // mixer parameters, B, L, G, H, R and the output y (proj and gate are set in the kernel)
 };
 
-template <int NT, int DT, int KSI, int GS, int NCT>
-__global__ __launch_bounds__(64 * DT) __attribute__((amdgpu_waves_per_eu(1)))
+// HELP: the block has DT more waves, which compute half of the in_proj
+// tiles of the one chunk (L <= 32) and then end; S_BARRIER waits on the
+// surviving waves only, so the scan's barriers are unaffected.
+template <int NT, int DT, int KSI, int GS, int NCT, bool ALL_LIVE, bool HELP>
+__global__ __launch_bounds__(64 * DT * (HELP ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(1)))
 void mamba3_block_scan_kernel(BlockArgs p) {
     constexpr int C = 32, D = 16 * DT;
     static_assert(DT == 2, "one wave per 16-row tile of the 32-token chunk");
@@ -1477,40 +1480,62 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             return 2 * DI + 16 * (j - 2 * DTL);
         }
 
-        // Wave w computes the chunk's 16-row tile w against all of the head's
-        // column tiles. Every load (its x rows, the norm weight, the NCT
-        // weight fragments) is issued before the first product; the tiles
-        // past the head's count repeat its last one and are not stored.
-        // (Staging the weight rows through LDS once per block measured
-        // slower, 15.7 against 12.2 us at 64 x 32 tokens: the staging loads
-        // ran one after another for want of registers.)
+        // Wave w computes the chunk's 16-row tile w % 2 against the head's
+        // column tiles j = w / 2, w / 2 + NW / 2, ... (NW = DT waves, or 2 DT
+        // with the helper waves). Every load (its x rows, the norm weight,
+        // its weight fragments) is issued before the first product and
+        // waited on once; the tiles past the head's count repeat its last
+        // one and are not stored. (Staging the weight rows through LDS once
+        // per block measured slower, 15.7 against 12.2 us at 64 x 32 tokens:
+        // the staging loads ran one after another for want of registers.)
         __device__ void before(int64_t c0) const {
+            constexpr int NW = HELP ? 2 * DT : DT;
+            constexpr int NTW = (NCT + NW / 2 - 1) / (NW / 2);  // column tiles per wave
             const int ncol = 2 * (D / 16) + (W - 2 * DI + 15) / 16;
+            const int rt = wave & 1, j0 = wave >> 1;
             float xv[KSI][8], nw[KSI][8];
             bool live[KSI], nlive[KSI];
-            const int64_t r = c0 + 16 * wave + li;
+            const int64_t r = c0 + 16 * rt + li;
             tile_load8<KSI>(xw + (r < L ? r : L - 1) * p.x_ts, dm, grp, xv, live);
             tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
-            float wv[NCT][KSI][8];
-            bool wlive[NCT][KSI];
+            float wv[NTW][KSI][8];
+            bool wlive[NTW][KSI];
 #pragma unroll
-            for (int j = 0; j < NCT; ++j) {
+            for (int i = 0; i < NTW; ++i) {
+                const int j = j0 + i * (NW / 2);
                 const int n0 = tile_col(j < ncol ? j : ncol - 1);
                 const int wr = n0 + li < W ? n0 + li : W - 1;
-                tile_load8<KSI>(p.in_w + static_cast<int64_t>(wr) * dm, dm, grp, wv[j], wlive[j]);
+                tile_load8<KSI>(p.in_w + static_cast<int64_t>(wr) * dm, dm, grp, wv[i], wlive[i]);
             }
+            // Every loaded value is held here, so all the loads are in flight
+            // together and waited on once: left to itself the compiler issues
+            // the later tiles' loads after the first products (or after the
+            // norm) and waits on each batch in turn.
+#pragma unroll
+            for (int s2 = 0; s2 < KSI; ++s2)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    asm volatile("" : "+v"(xv[s2][k]), "+v"(nw[s2][k]));
+#pragma unroll
+                    for (int i = 0; i < NTW; ++i) asm volatile("" : "+v"(wv[i][s2][k]));
+                }
             tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);
 #pragma unroll
-            for (int j = 0; j < NCT; ++j) {
-                tile_f32x4 y = tile_mfma_f32<KSI>(wv[j], xv, live);
+            for (int i = 0; i < NTW; ++i) {
+                const int j = j0 + i * (NW / 2);
+                tile_f32x4 y = tile_mfma_f32<KSI, ALL_LIVE>(wv[i], xv, live);
                 y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
-                if (j < ncol) *reinterpret_cast<tile_f32x4*>(proj_s + (16 * wave + li) * pp + tile_col(j) + 4 * grp) = y;
+                if (j < ncol) *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + tile_col(j) + 4 * grp) = y;
             }
             __syncthreads();
         }
         __device__ void after(int64_t, bool) const {}
     };
     const Hooks hooks{p, xw, proj_s, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h)};
+    if (HELP && wave >= DT) {
+        hooks.before(0);  // the helpers' share of the chunk's in_proj tiles, then they end
+        return;
+    }
     scan_head<C, NT, DT, true, Hooks, false>(a, sh, b, h, 0, hooks);
 }
 
@@ -1528,8 +1553,20 @@ bool launch_block_scan(const BlockArgs& p, int64_t N, int64_t D, int64_t gs, hip
     const int64_t ncol = 2 * (D / 16) + (p.W - 2 * DI + 15) / 16;
 #define MLK_BLOCK(NV, DV, KSIV, GSV, NCTV)                                                                       \
     if (N == NV && D == DV && ksi == KSIV && gs == GSV && ncol <= NCTV) {                                         \
-        hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV>), grid, dim3(4 * DV),    \
-                           lds, stream, p);                                                                       \
+        const bool all_live = p.dm == 32 * KSIV, help = p.s.L <= 32;                                             \
+        if (all_live && help) {                                                                                  \
+            hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV, true, true>), grid,   \
+                               dim3(8 * DV), lds, stream, p);                                                     \
+        } else if (all_live) {                                                                                   \
+            hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV, true, false>), grid,  \
+                               dim3(4 * DV), lds, stream, p);                                                     \
+        } else if (help) {                                                                                       \
+            hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV, false, true>), grid,  \
+                               dim3(8 * DV), lds, stream, p);                                                     \
+        } else {                                                                                                 \
+            hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV, false, false>), grid, \
+                               dim3(4 * DV), lds, stream, p);                                                     \
+        }                                                                                                        \
         return true;                                                                                             \
     }
     MLK_BLOCK(16, 32, 2, 8, 7)  // d_model up to 64 in groups of 8, d_state 16, heads of 32, 3H + R <= 16

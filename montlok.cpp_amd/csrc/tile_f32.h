@@ -84,20 +84,23 @@ __device__ __forceinline__ void tile_rms_norm(float (&xv)[KS][8], const float (&
 
 // The tile's products with fp32 weights: W as the A operand (so the result is
 // transposed into the lane layout above), the even and odd k of each lane in
-// two accumulation chains, summed at the end.
-template <int KS>
+// two accumulation chains, summed at the end. ALL_LIVE (K = 32 KS, every step
+// live) takes the operands as loaded: the same products, without the select
+// in front of every MFMA, whose VALU -> MFMA operand hazard otherwise halves
+// the issue rate.
+template <int KS, bool ALL_LIVE = false>
 __device__ __forceinline__ tile_f32x4 tile_mfma_f32(const float (&wv)[KS][8], const float (&xv)[KS][8],
                                                    const bool (&live)[KS]) {
     tile_f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
     tile_f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
+        const bool on = ALL_LIVE || live[s];
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(live[s] ? wv[s][j] : 0.0f, live[s] ? xv[s][j] : 0.0f, acc0,
-                                                        0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(live[s] ? wv[s][j + 1] : 0.0f,
-                                                        live[s] ? xv[s][j + 1] : 0.0f, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(on ? wv[s][j] : 0.0f, on ? xv[s][j] : 0.0f, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(on ? wv[s][j + 1] : 0.0f, on ? xv[s][j + 1] : 0.0f, acc1, 0,
+                                                        0, 0);
         }
     }
     return acc0 + acc1;
