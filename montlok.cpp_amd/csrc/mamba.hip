@@ -1438,6 +1438,8 @@ template <int NT, int DT, int KSI, int GS, int NCT, bool ALL_LIVE, bool HELP>
 __global__ __launch_bounds__(64 * DT * (HELP ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(1)))
 void mamba3_block_scan_kernel(BlockArgs p) {
     constexpr int C = 32, D = 16 * DT;
+    constexpr bool STAGE = ALL_LIVE && KSI == 2;  // d_model 64: the weight rows staged in LDS
+    __shared__ __attribute__((aligned(16))) float w_lds[STAGE ? NCT * 16 * 64 : 4];
     static_assert(DT == 2, "one wave per 16-row tile of the 32-token chunk");
     __shared__ ScanLds<C, NT, DT> sh;
     extern __shared__ __attribute__((aligned(16))) float proj_s[];  // [C, pp]
@@ -1468,6 +1470,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
         const BlockArgs& p;
         const float* xw;
         float* proj_s;
+        float* w_lds;
         int64_t L;
         int li, grp, wave, dm, W, DI, pp, h;
 
@@ -1482,12 +1485,17 @@ void mamba3_block_scan_kernel(BlockArgs p) {
 
         // Wave w computes the chunk's 16-row tile w % 2 against the head's
         // column tiles j = w / 2, w / 2 + NW / 2, ... (NW = DT waves, or 2 DT
-        // with the helper waves). Every load (its x rows, the norm weight,
-        // its weight fragments) is issued before the first product and
-        // waited on once; the tiles past the head's count repeat its last
-        // one and are not stored. (Staging the weight rows through LDS once
-        // per block measured slower, 15.7 against 12.2 us at 64 x 32 tokens:
-        // the staging loads ran one after another for want of registers.)
+        // with the helper waves). The tiles past the head's count repeat its
+        // last one and are not stored.
+        //
+        // STAGE (d_model 64): before the first chunk the block copies the
+        // head's weight rows into LDS with direct global-to-LDS loads (each
+        // instruction moves four 256-byte rows; no registers, all in flight
+        // at once, each row read from L2 once per block instead of once per
+        // wave); row r of tile j holds its 16-byte chunk c at slot c ^ r, so
+        // the 16 lanes of a fragment read hit 16 different bank groups.
+        // Otherwise every wave loads its weight fragments into registers,
+        // with all loads issued before the first wait.
         __device__ void before(int64_t c0) const {
             constexpr int NW = HELP ? 2 * DT : DT;
             constexpr int NTW = (NCT + NW / 2 - 1) / (NW / 2);  // column tiles per wave
@@ -1500,25 +1508,55 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
             float wv[NTW][KSI][8];
             bool wlive[NTW][KSI];
-#pragma unroll
-            for (int i = 0; i < NTW; ++i) {
-                const int j = j0 + i * (NW / 2);
-                const int n0 = tile_col(j < ncol ? j : ncol - 1);
-                const int wr = n0 + li < W ? n0 + li : W - 1;
-                tile_load8<KSI>(p.in_w + static_cast<int64_t>(wr) * dm, dm, grp, wv[i], wlive[i]);
-            }
-            // Every loaded value is held here, so all the loads are in flight
-            // together and waited on once: left to itself the compiler issues
-            // the later tiles' loads after the first products (or after the
-            // norm) and waits on each batch in turn.
-#pragma unroll
-            for (int s2 = 0; s2 < KSI; ++s2)
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    asm volatile("" : "+v"(xv[s2][k]), "+v"(nw[s2][k]));
-#pragma unroll
-                    for (int i = 0; i < NTW; ++i) asm volatile("" : "+v"(wv[i][s2][k]));
+            if constexpr (STAGE) {
+                static_assert(KSI == 2 && ALL_LIVE, "staging takes d_model 64 rows: 16 chunks of 16 bytes");
+                if (c0 == 0) {
+                    const int lane = threadIdx.x & 63;
+                    const int rq = lane >> 4, slot = lane & 15;
+#pragma unroll 1
+                    for (int u = wave; u < 4 * NCT; u += NW) {  // quarter-tile u: tile u / 4, rows 4 (u % 4) ..
+                        const int j = u >> 2, row = 4 * (u & 3) + rq;
+                        const int n = tile_col(j < ncol ? j : ncol - 1) + row;
+                        const float* src = p.in_w + static_cast<int64_t>(n < W ? n : W - 1) * 64 + 4 * (slot ^ row);
+                        __builtin_amdgcn_global_load_lds(
+                            (const __attribute__((address_space(1))) void*)src,
+                            (__attribute__((address_space(3))) void*)(w_lds + u * 256), 16, 0, 0);
+                    }
+                    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the LDS copies have landed
+                    __syncthreads();
                 }
+#pragma unroll
+                for (int i = 0; i < NTW; ++i) {
+                    const int j = j0 + i * (NW / 2);
+                    const float* rowp = w_lds + ((j < NCT ? j : NCT - 1) * 16 + li) * 64;
+#pragma unroll
+                    for (int s2 = 0; s2 < KSI; ++s2) {
+                        const int cc = 8 * s2 + 2 * grp;
+                        const float4 lo = *reinterpret_cast<const float4*>(rowp + 4 * (cc ^ li));
+                        const float4 hi = *reinterpret_cast<const float4*>(rowp + 4 * ((cc + 1) ^ li));
+                        wv[i][s2][0] = lo.x; wv[i][s2][1] = lo.y; wv[i][s2][2] = lo.z; wv[i][s2][3] = lo.w;
+                        wv[i][s2][4] = hi.x; wv[i][s2][5] = hi.y; wv[i][s2][6] = hi.z; wv[i][s2][7] = hi.w;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < NTW; ++i) {
+                    const int j = j0 + i * (NW / 2);
+                    const int n0 = tile_col(j < ncol ? j : ncol - 1);
+                    const int wr = n0 + li < W ? n0 + li : W - 1;
+                    tile_load8<KSI>(p.in_w + static_cast<int64_t>(wr) * dm, dm, grp, wv[i], wlive[i]);
+                }
+                // Every loaded value is held here, so all the loads are in
+                // flight together and waited on once: left to itself the
+                // compiler issues the later tiles' loads after the first
+                // products (or after the norm) and waits on each batch in turn.
+#pragma unroll
+                for (int s2 = 0; s2 < KSI; ++s2)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+#pragma unroll
+                        for (int i = 0; i < NTW; ++i) asm volatile("" : "+v"(wv[i][s2][k]));
+            }
             tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);
 #pragma unroll
             for (int i = 0; i < NTW; ++i) {
@@ -1531,7 +1569,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
         }
         __device__ void after(int64_t, bool) const {}
     };
-    const Hooks hooks{p, xw, proj_s, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h)};
+    const Hooks hooks{p, xw, proj_s, w_lds, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h)};
     if (HELP && wave >= DT) {
         hooks.before(0);  // the helpers' share of the chunk's in_proj tiles, then they end
         return;
