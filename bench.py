@@ -181,13 +181,16 @@ RIDGE = {k: v * 1e3 / HBM_PEAK_GBS for k, v in MFMA_PEAK_TFS.items()}  # flop pe
 
 
 def _op_times(ops: dict, replays: int, reps: int = 8) -> dict:
-    """Per-op milliseconds per launch: each op captured `reps` times in its own graph and replayed."""
+    """Per-op milliseconds per launch: each op captured `reps` times in its own graph and replayed. An op
+    given as a list of closures ("fns", one per input set) rotates over them, so its inputs are as cold as
+    in the timed steps."""
     times = {}
     for name, op in ops.items():
-        g = _graph([op["fn"]] * reps)
+        fns = op.get("fns") or [op["fn"]]
+        g = _graph([fns[i % len(fns)] for i in range(max(reps, len(fns)))])
         for _ in range(2):
             g.replay()
-        times[name] = _time_graph(g, replays) / reps
+        times[name] = _time_graph(g, replays) / max(reps, len(fns))
     return times
 
 
@@ -216,6 +219,15 @@ def _roofline(name: str, entry: dict, op: dict, precision: str, traffic=None) ->
     return {"bound": "hbm", "kernel": name, "achieved": entry["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": entry["hbm_frac"], "traffic": traffic, "algorithmic_bytes": op["bytes"],
             "launch_ms": entry["launch_ms"]}
+
+
+def _traffic(tag: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary profiles/<tag>_traffic.json
+    (FETCH_SIZE and WRITE_SIZE passes of rocprofv3 over this workload, scaled by a plain copy's), or None."""
+    path = ROOT / "profiles" / f"{tag}_traffic.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text()).get(kernel)
 
 
 def _base_line(value, unit, steps, warmup, ms, dtype, data, config) -> dict:
@@ -342,18 +354,13 @@ def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
     replays = max(4, steps // sets)
     prep_ms = _time_graph(_graph([prepare(i) for i in range(sets)]), replays) / sets
     comb_ms = _time_graph(_graph([combine(i) for i in range(sets)]), replays) / sets
-    # Warm-cache rate: one input set over and over (Infinity-Cache resident).
-    warm_ms = _time_graph(_graph([f for _ in range(sets) for f in (prepare(0), combine(0))]), replays) / sets
 
     prep_bytes, comb_bytes = mhc_bytes(n, d, T)
     kernels = {"mhc_prepare": (prep_ms, prep_bytes), "mhc_combine": (comb_ms, comb_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0])
     dom_ms, dom_bytes = kernels[dom]
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    traffic = None
-    tfile = ROOT / "profiles" / "mhc_n4_d128_t8192_traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get(dom)
+    traffic = _traffic("mhc_n4_d128_t8192", dom)
     line = _base_line(T / (ms_per_step * 1e-3), "tokens/s", t["steps"], warmup, ms_per_step, "f32 (f64 accumulate)",
                       "synthetic (seeded N(0,1) streams, random-init mHC weights)",
                       {"workload": "mhc_residual_mix", "n_streams": n, "d_model": d, "tokens": T,
@@ -368,7 +375,6 @@ def bench_mhc(steps: int, warmup: int, cpu: bool) -> dict:
     line.update(_timing_fields(t))
     line["step_roofline_frac"] = (prep_bytes + comb_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
     line["stream_steps_per_s"] = n * T / (ms_per_step * 1e-3)
-    line["warm_cache_tokens_per_s"] = T / (warm_ms * 1e-3)
     if cpu:
         line["cpu_baseline"] = cpu_baseline_mhc(cfg)
         line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
@@ -513,7 +519,7 @@ def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
                        "norm_groups": cfg["norm_groups"], "step": "x + out_proj(mamba3(in_proj(GroupedRMSNorm(x))))",
                        "launches": ", ".join(launches), "launch": "the K steps in one HIP graph",
                        "parallelism": "single GPU"})
-    line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32")
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32", _traffic("mamba3_block_b64_l32_d64", dom))
     line["kernels"] = table
     line.update(_timing_fields(t))
     line["step_algorithmic_bytes"] = total_bytes
@@ -627,24 +633,28 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
     assert torch.equal(outs[0], eager), "graph replay differs from the eager step"
     steps, ms = t["steps"], t["ms_per_step"]
 
-    x = xs[0]
-    projected = _C.linear(x, w["in_w"]).view(T, d + kvr + r)
-    latent = _C._latent_normed(projected, d, kvr, w["ln_w"], w["ln_b"], 1e-5)
-    att = _C._attend_normed(projected, latent, B, L, d, H, hd, nope, kvr, w["kv_up"], cos, sin, scale).view(B, L, d)
+    # Per-kernel launches on each input set's intermediates, rotating over the sets as the steps do.
+    projs = [_C.linear(xs[i], w["in_w"]).view(T, d + kvr + r) for i in range(sets)]
+    lats = [_C._latent_normed(projs[i], d, kvr, w["ln_w"], w["ln_b"], 1e-5) for i in range(sets)]
+    atts = [_C._attend_normed(projs[i], lats[i], B, L, d, H, hd, nope, kvr, w["kv_up"], cos, sin, scale).view(B, L, d)
+            for i in range(sets)]
     f, h2 = 4, 2
     pairs = B * H * L * (L + 1) // 2
     ops = {
-        "in_proj": dict(fn=lambda: _C.linear(x, w["in_w"]), bytes=T * d * f + (d + kvr + r) * d * h2 + T * (d + kvr + r) * f,
+        "in_proj": dict(fns=[lambda i=i: _C.linear(xs[i], w["in_w"]) for i in range(sets)],
+                        bytes=T * d * f + (d + kvr + r) * d * h2 + T * (d + kvr + r) * f,
                         flops=2 * T * d * (d + kvr + r)),
         # The latent's LayerNorm once per row, to bf16.
-        "latent_layer_norm": dict(fn=lambda: _C._latent_normed(projected, d, kvr, w["ln_w"], w["ln_b"], 1e-5),
+        "latent_layer_norm": dict(fns=[lambda i=i: _C._latent_normed(projs[i], d, kvr, w["ln_w"], w["ln_b"], 1e-5)
+                                       for i in range(sets)],
                                   bytes=T * kvr * (f + h2) + 2 * kvr * f),
         # kv_up + RoPE + causal attention in one kernel: q, the normalised latent and k_rope in, attention out.
-        "mla_attend": dict(fn=lambda: _C._attend_normed(projected, latent, B, L, d, H, hd, nope, kvr, w["kv_up"], cos,
-                                                        sin, scale),
+        "mla_attend": dict(fns=[lambda i=i: _C._attend_normed(projs[i], lats[i], B, L, d, H, hd, nope, kvr, w["kv_up"],
+                                                              cos, sin, scale) for i in range(sets)],
                            bytes=T * (d + r) * f + T * kvr * h2 + H * (nope + hd) * kvr * h2 + T * d * f,
                            flops=2 * T * kvr * H * (nope + hd) + 4 * pairs * hd),
-        "o_proj": dict(fn=lambda: _C.linear(att, w["o"]), bytes=2 * T * d * f + d * d * h2, flops=2 * T * d * d),
+        "o_proj": dict(fns=[lambda i=i: _C.linear(atts[i], w["o"]) for i in range(sets)],
+                       bytes=2 * T * d * f + d * d * h2, flops=2 * T * d * d),
     }
     table = _kernel_table(ops, _op_times(ops, max(4, steps // 8)), "bf16")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
@@ -658,7 +668,7 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
                                "causal attention, o_proj GEMM",
                        "launch": f"the K steps in one HIP graph, rotating over {sets} input sets",
                        "parallelism": "single GPU"})
-    line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16", _traffic("mla_b256_l128_d256_h8", dom))
     line["kernels"] = table
     line.update(_timing_fields(t))
     line["step_algorithmic_bytes"] = total_bytes
@@ -820,7 +830,7 @@ def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
                        "step": "2 x [x + out_proj(mamba3_step(in_proj(GroupedRMSNorm(x))))], RMSNorm, Linear(128->1)",
                        "launch": "the K steps in one HIP graph (state carried in place)",
                        "parallelism": "single GPU"})
-    line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32")
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "f32", _traffic("decode_s65536_2layers_d128_n64", dom))
     line["kernels"] = table
     line.update(_timing_fields(t))
     line["step_algorithmic_bytes"] = total_bytes
@@ -1028,7 +1038,7 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
                        "mla": f"{cfg['heads']} heads of {cfg['head_dim']}, rope {cfg['rope']}, kv rank {cfg['kv_rank']}",
                        "step": "Linear(40->256), 4 x mHC[fn = mixer(RMSNorm(agg))] alternating Mamba-3 / MLA, collapse",
                        "launch": "the K steps in one HIP graph", "parallelism": "single GPU"})
-    line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16")
+    line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16", _traffic("hybrid_stack_b1024_l256_d256", dom))
     line["kernels"] = table
     line.update(_timing_fields(t))
     line["step_flops"] = flops
