@@ -696,11 +696,8 @@ def _decode_state_bytes(S: int, geo: dict) -> int:
 
 def cpu_baseline_decode(cfg: dict, geo: dict, stack, states: list, x_cpu, budget_s: float = 12.0,
                         streams: int = 1024) -> dict:
-    """No reference step operator exists: the oracle's step restatement for the mixer, run over the streams by
-    one Python thread per core (ctypes releases the interpreter lock, so the C calls run in parallel), the
-    reference CPU RMSNorm and torch CPU GEMMs, on the first `streams` streams."""
-    import concurrent.futures as cf
-
+    """No reference step operator exists: the oracle's step restatement for the mixer, its streams split over
+    OpenMP threads, the reference CPU RMSNorm and torch CPU GEMMs, on the first `streams` streams."""
     import numpy as np
     import torch
 
@@ -721,17 +718,9 @@ def cpu_baseline_decode(cfg: dict, geo: dict, stack, states: list, x_cpu, budget
     def make_step(threads):
         if isinstance(ref, Reference):
             ref.set_threads(threads)
-        pool = cf.ThreadPoolExecutor(threads) if threads > 1 else None
-        cuts = np.linspace(0, streams, threads + 1).astype(int)
 
         def mixer(proj, state, p):
-            def part(i):
-                a, b = cuts[i], cuts[i + 1]
-                sub = {k: (v[a:b] if isinstance(v, np.ndarray) else v) for k, v in state.items()}
-                return orc.mamba3_step(proj[a:b], sub, N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4)
-            if pool is None:
-                return part(0)
-            return np.concatenate(list(pool.map(part, range(threads))))
+            return orc.mamba3_step(proj, state, N, G, H, D, R, *p[:4], 1e-5, 1e-5, p[4], p[5], 1e-4, threads=threads)
 
         def step():
             hcur = x
@@ -746,8 +735,8 @@ def cpu_baseline_decode(cfg: dict, geo: dict, stack, states: list, x_cpu, budget
 
     return _cpu_legs(make_step, streams, "stream-steps/s", "port",
                      f"steps of {streams} of the {cfg['streams']} streams (the rate scales per stream); mixer step in "
-                     f"the oracle's C restatement (no reference step operator exists), one thread per core over the "
-                     f"streams; RMSNorm in the {'reference' if isinstance(ref, Reference) else 'oracle'} build; GEMMs "
+                     f"the oracle's C restatement (no reference step operator exists), the streams split over OpenMP "
+                     f"threads; RMSNorm in the {'reference' if isinstance(ref, Reference) else 'oracle'} build; GEMMs "
                      f"in torch CPU", budget_s)
 
 

@@ -190,6 +190,7 @@ class Oracle(_Lib):
         L.orc_mamba3_step.argtypes = [_i64, _f32p, _i64] + [_i64] * 5 + [_f32p] * 4 + [_dbl, _dbl, _f32p, _f32p,
                                                                                       _dbl, _f32p, _f32p, _f32p,
                                                                                       _f64p, C.c_int, _f32p]
+        L.orc_mamba3_step_threads.argtypes = [C.c_int] + L.orc_mamba3_step.argtypes
         L.orc_mhc_combine.argtypes = [_f32p, _i64, _i64, _f32p, _f32p, _f32p, _i64, _i64, _i64, _f32p, _f32p]
         L.orc_mla_rope.argtypes = [_f32p, _i64, _i64, _f32p, _f32p, _i64, _f32p, _f32p, _f32p] + [_i64] * 5
         L.orc_linear.argtypes = [_f32p, _i64, _f32p, _f32p, _i64, _i64, _i64, _f32p]
@@ -217,15 +218,18 @@ class Oracle(_Lib):
         return out
 
     def mamba3_step(self, proj, state, N, G, H, D, R, b_bias, c_bias, b_norm_w, c_norm_w, b_eps, c_eps, dt_bias,
-                    skip, a_floor):
-        """One token for S streams; `state` = dict(ssm, k_prev, v_prev, angle, started) updated in place."""
+                    skip, a_floor, threads=1):
+        """One token for S streams; `state` = dict(ssm, k_prev, v_prev, angle, started) updated in place.
+        threads > 1 splits the streams over that many OpenMP threads (same result)."""
         proj = _f32(proj)
         S, W = proj.shape
         out = np.empty((S, H * D), np.float32)
         for key, dtype in (("ssm", np.float32), ("k_prev", np.float32), ("v_prev", np.float32),
                            ("angle", np.float64)):
             assert state[key].dtype == dtype and state[key].flags.c_contiguous, key
-        self.lib.orc_mamba3_step(S, _ptr(proj), W, N, G, H, D, R, _ptr(_f32(b_bias)), _ptr(_f32(c_bias)),
+        fn = self.lib.orc_mamba3_step if threads <= 1 else \
+            (lambda *a: self.lib.orc_mamba3_step_threads(int(threads), *a))
+        fn(S, _ptr(proj), W, N, G, H, D, R, _ptr(_f32(b_bias)), _ptr(_f32(c_bias)),
                                  _ptr(_f32(b_norm_w)), _ptr(_f32(c_norm_w)), b_eps, c_eps, _ptr(_f32(dt_bias)),
                                  _ptr(_f32(skip)), a_floor, _ptr(state["ssm"]), _ptr(state["k_prev"]),
                                  _ptr(state["v_prev"]), _ptr(state["angle"], _f64p), int(state["started"]),

@@ -520,6 +520,27 @@ void orc_mamba3_step(int64_t S, const float* proj, int64_t proj_ss, int64_t N, i
     free(qk);
 }
 
+/* orc_mamba3_step over `threads` contiguous ranges of the streams at once.
+ * The streams are independent, so the result equals one call over all of
+ * them; the split only serves the CPU baseline's multi-core timing. */
+void orc_mamba3_step_threads(int threads, int64_t S, const float* proj, int64_t proj_ss, int64_t N, int64_t G,
+                             int64_t H, int64_t D, int64_t R, const float* b_bias, const float* c_bias,
+                             const float* b_norm_w, const float* c_norm_w, double b_eps, double c_eps,
+                             const float* dt_bias, const float* skip, double a_floor, float* ssm, float* k_prev,
+                             float* v_prev, double* angle, int started, float* out) {
+    const int64_t Rw = R > 0 ? R : 1;
+    if (threads < 1) threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(static, 1)
+    for (int t = 0; t < threads; ++t) {
+        const int64_t a = S * t / threads, b = S * (t + 1) / threads;
+        if (b > a) {
+            orc_mamba3_step(b - a, proj + a * proj_ss, proj_ss, N, G, H, D, R, b_bias, c_bias, b_norm_w, c_norm_w,
+                            b_eps, c_eps, dt_bias, skip, a_floor, ssm + a * H * N * D, k_prev + a * H * N,
+                            v_prev + a * H * D, angle + a * H * Rw, started, out + a * H * D);
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* mHC read side: montlok_mhc.h:23-322, op montlok.cpp:659-691               */
 /* ------------------------------------------------------------------------ */

@@ -333,6 +333,33 @@ def test_mamba_step_sequence_identity(oracle):
             assert_bitwise(y, seq[:, t], f"step {t}")
 
 
+def test_mamba_step_threads_equal_one_call(oracle):
+    """The streams split over OpenMP threads (the CPU baseline's form) give the one-call result and states."""
+    rng = np.random.default_rng(5)
+    N, G, H, D, R = 16, 1, 4, 16, 4
+    S = 37
+    W = 2 * H * D + 2 * G * N + 3 * H + R
+    bb, cb = (1 + 0.3 * rng.standard_normal((2, H, N))).astype(np.float32)
+    bw, cw = (rng.random((2, N)) + 0.5).astype(np.float32)
+    dtb = (rng.standard_normal(H) - 2).astype(np.float32)
+    skip = rng.standard_normal(H).astype(np.float32)
+    args = (N, G, H, D, R, bb, cb, bw, cw, 1e-5, 1e-5, dtb, skip, 1e-4)
+    start = dict(ssm=rng.standard_normal((S, H, N, D)).astype(np.float32) * 0.1,
+                 k_prev=rng.standard_normal((S, H, N)).astype(np.float32),
+                 v_prev=rng.standard_normal((S, H, D)).astype(np.float32),
+                 angle=rng.random((S, H, R)) * 6.0, started=1)
+    one = {k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in start.items()}
+    many = {k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in start.items()}
+    for t in range(3):
+        proj = rng.standard_normal((S, W)).astype(np.float32)
+        y1 = oracle.mamba3_step(proj, one, *args)
+        y8 = oracle.mamba3_step(proj, many, *args, threads=8)
+        assert_bitwise(y8, y1, f"threaded step {t}")
+    for key in ("ssm", "k_prev", "v_prev"):
+        assert_bitwise(many[key], one[key], key)
+    assert np.array_equal(many["angle"], one["angle"])
+
+
 def _mhc_params(rng, n, d, alpha=0.7):
     nw = (rng.random(d) + 0.5).astype(np.float32)
     pw = (rng.standard_normal((2 * n + n * n, d)) * 4 / np.sqrt(d)).astype(np.float32).astype(np.float64)
