@@ -627,8 +627,12 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
 
     step(0)()
     torch.cuda.synchronize()
+    launches = _C.mla_forward_launches()
     eager = outs[0].clone()
     assert torch.isfinite(eager).all().item()
+    separate = _C._mla_forward(xs[0], w["in_w"], empty, w["ln_w"], w["ln_b"], 1e-5, w["kv_up"], w["o"], cos, sin, H,
+                               hd, nope, kvr, L, True, scale, allow_fused=True, allow_window=False)
+    assert torch.equal(eager, separate), "the step must equal the four-launch path bit for bit"
     t = _gpu_steps([step(i) for i in range(sets)], steps, warmup)
     assert torch.equal(outs[0], eager), "graph replay differs from the eager step"
     steps, ms = t["steps"], t["ms_per_step"]
@@ -640,7 +644,8 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
             for i in range(sets)]
     f, h2 = 4, 2
     pairs = B * H * L * (L + 1) // 2
-    ops = {
+    total_bytes = 2 * T * d * f + ((d + kvr + r) * d + H * (nope + hd) * kvr + d * d) * h2
+    separate_ops = {
         "in_proj": dict(fns=[lambda i=i: _C.linear(xs[i], w["in_w"]) for i in range(sets)],
                         bytes=T * d * f + (d + kvr + r) * d * h2 + T * (d + kvr + r) * f,
                         flops=2 * T * d * (d + kvr + r)),
@@ -656,20 +661,27 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
         "o_proj": dict(fns=[lambda i=i: _C.linear(atts[i], w["o"]) for i in range(sets)],
                        bytes=2 * T * d * f + d * d * h2, flops=2 * T * d * d),
     }
+    total_flops = sum(op.get("flops", 0) for op in separate_ops.values())
+    if launches == ["mla_forward"]:
+        # The whole forward in one kernel: x in, the output projection out, the bf16 weights once.
+        ops = {"mla_forward": dict(fns=[step(i) for i in range(sets)], bytes=total_bytes, flops=total_flops)}
+    else:
+        ops = separate_ops
     table = _kernel_table(ops, _op_times(ops, max(4, steps // 8)), "bf16")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
-    total_bytes = 2 * T * d * f + ((d + kvr + r) * d + H * (nope + hd) * kvr + d * d) * h2
-    total_flops = sum(op.get("flops", 0) for op in ops.values())
     line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms, "bf16 weights, f32 activations/accumulate",
                       "synthetic (seeded N(0,1) inputs, N(0,0.02) bf16 weights)",
                       {"workload": "mla_causal_fwd", "windows": B, "seq_len": L, "d_model": d, "heads": H,
                        "head_dim": hd, "rope_dim": r, "kv_rank": kvr, "rope_theta": cfg["theta"],
-                       "step": "mla_forward: in_proj GEMM, latent LayerNorm (once per row, bf16), fused kv_up + RoPE + "
-                               "causal attention, o_proj GEMM",
+                       "step": "mla_forward: in_proj, latent LayerNorm, kv_up, RoPE, causal attention, o_proj",
+                       "launches": ", ".join(launches),
                        "launch": f"the K steps in one HIP graph, rotating over {sets} input sets",
                        "parallelism": "single GPU"})
     line["roofline"] = _roofline(dom, table[dom], ops[dom], "bf16", _traffic("mla_b256_l128_d256_h8", dom))
     line["kernels"] = table
+    if ops is not separate_ops:  # the four-launch path the kernel replaces, for comparison
+        line["separate_path_kernels"] = _kernel_table(separate_ops, _op_times(separate_ops, max(4, steps // 8)),
+                                                      "bf16")
     line.update(_timing_fields(t))
     line["step_algorithmic_bytes"] = total_bytes
     line["step_algorithmic_flops"] = total_flops

@@ -198,6 +198,27 @@ mlk_status mlk_mla_attend_normed(const float* projected, int64_t batch, int64_t 
                                  const void* kv_up_weight, const float* cosine, const float* sine, double scale,
                                  float* out, mlk_stream_t stream);
 
+/* mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias,
+ * kv_norm_eps, kv_up_weight, out_weight, cos, sin, n_heads, head_dim,
+ * nope_dim, kv_lora_rank, n_last = L, causal = true, scale) --
+ * montlok.cpp:1159-1211, every causal query: in_proj, kv_norm, kv_up, RoPE,
+ * top-left causal attention and the output projection in one launch, one
+ * block per window, so neither the projection nor the attention output goes
+ * through HBM. x: rows of d_model floats, x_token_stride apart within a
+ * window and x_batch_stride apart between windows; in_proj_weight [d_model +
+ * kv_rank + rope, d_model], kv_up_weight [heads (nope + head_dim), kv_rank]
+ * and out_weight [d_model, d_model], all bf16 (weight_dtype MLK_DTYPE_BF16);
+ * cos/sin [L, rope]; out [B, L, d_model] contiguous. The result equals the
+ * separate path (linear, mlk_layer_norm_bf16, mlk_mla_attend_normed, linear)
+ * bit for bit. Built for 8 heads of 32 (nope 16, rope 16), kv_rank 64,
+ * L <= 128, 16-byte aligned operands; MLK_ERR_UNSUPPORTED otherwise. */
+mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_t d_model, int64_t x_batch_stride,
+                           int64_t x_token_stride, const void* in_proj_weight, const float* kv_norm_w,
+                           const float* kv_norm_b, double kv_norm_eps, const void* kv_up_weight,
+                           const void* out_weight, const float* cosine, const float* sine, int64_t heads,
+                           int64_t head_dim, int64_t nope_dim, int64_t kv_rank, int32_t weight_dtype, double scale,
+                           float* out, mlk_stream_t stream);
+
 /* ----------------------------------------------------------------- mHC -- */
 
 /* mhc_prepare(streams, norm_w, eps, proj_w, pre_bias, post_bias, res_bias,

@@ -783,6 +783,465 @@ void mla_attend_kernel(MlaAttendArgs p) {
     }
 }
 
+// ------------------------------------------------- whole MLA forward per window
+
+// mla_forward (montlok.cpp:1159-1211) for every causal query, one block of 8
+// waves per window, so that neither the in_proj output nor the attention
+// output goes through HBM: x is read once and the o_proj result written once.
+//   in_proj  x (rounded to bf16) in LDS; wave w holds the W fragments of its
+//            column tiles in registers (q nope and q rope of head w, plus
+//            latent tile w for w < 4 or the k_rope tile for w = 4) and runs
+//            them over the 8 row tiles: per (tile, row tile) the 8 k steps of
+//            linear_tiles_kernel's chain, so the columns equal the separate
+//            linear's bit for bit. Epilogue: q rounded to bf16 (its rope lanes
+//            rotated in fp64 first, the pair partner 32 lanes away), the
+//            latent kept in fp32, k_rope rotated.
+//   kv_norm  the LayerNorm of mla_attend_kernel (16 lanes per row, fp64),
+//            into bf16.
+//   heads    two at a time, four waves each: this head's kv_up rows, kv_up,
+//            k = cat(k_nope, rope(k_rope)), causal attention, all as
+//            mla_attend_kernel computes them; the normalised output rounded to
+//            bf16 (the o_proj's operand) over the head's q columns.
+//   o_proj   wave w: output tiles 2w, 2w + 1, W fragments in registers, the
+//            attention output from LDS, the linear's chain again.
+// The x / q / attention tile is [128 rows x 256] bf16 with 16-byte units
+// XOR-swizzled by the row (unit u of row r at u ^ (r mod 8)), so the MFMA
+// fragment reads (16 rows, one unit each per lane group) are conflict-free.
+struct MlaWindowArgs {
+    const float* x;  // [B, L, D], tokens x_ts apart, windows x_bs apart
+    int64_t x_bs, x_ts;
+    const u16* w_in;  // [D + KV + ROPE, D] bf16: q, kv_down, k_rope rows
+    const float* ln_w;
+    const float* ln_b;  // may be null
+    double ln_eps;
+    const u16* w_up;   // [H (NOPE + HD), KV] bf16
+    const u16* w_out;  // [D, D] bf16
+    const float* cosine;  // [L, ROPE]
+    const float* sine;
+    float* out;  // [B, L, D] contiguous
+    int64_t length;
+    float scale_log2;
+};
+
+template <int H>
+__global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
+    constexpr int HD = 32, NOPE = 16, ROPE = 16, KV = 64;  // rope pairs (i, i + 8): 32 lanes apart
+    constexpr int D = H * HD;
+    constexpr int LMAX = 128, RT = LMAX / 16;
+    constexpr int UPW = NOPE + HD;  // kv_up rows of one head
+    constexpr int LP = KV + 8;      // latent pitch in bf16 elements (+16 bytes)
+    constexpr int SLOT = 2 * LMAX * HD;  // one head's k [keys, HD] and v^T [HD, keys], bf16, swizzled
+    constexpr int HG = 4;                // heads at a time, two waves each
+    static_assert(H == 8, "the wave -> column tile map assumes 8 heads on 8 waves");
+    static_assert(LMAX * KV * 4 <= HG * SLOT * 2, "the fp32 latent must fit the head slots it precedes");
+    __shared__ __attribute__((aligned(16))) u16 xq_s[LMAX * D];
+    __shared__ __attribute__((aligned(16))) u16 lat_s[LMAX * LP];
+    __shared__ __attribute__((aligned(16))) u16 kr_s[LMAX * ROPE];
+    __shared__ __attribute__((aligned(16))) u16 head_s[HG * SLOT];
+    float* lat_f = reinterpret_cast<float*>(head_s);  // [LMAX, KV], until the LayerNorm has run
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int L = static_cast<int>(p.length);
+    const int64_t b = blockIdx.x;
+    const float* xw = p.x + b * p.x_bs;
+    // element (row, col) of the swizzled [LMAX, D] tile
+    auto sw = [](int row, int col) { return row * D + ((((col >> 3) ^ (row & 7))) << 3) + (col & 7); };
+    // rotate_half of one pair: x1 c - x2 s on the first half, x2 c + x1 s on the second (x the own value,
+    // the partner 32 lanes away), as rope_kernel: two fp64 products, their sum rounded to fp64, then to fp32.
+    // The product of two floats is exact in fp64, so round(own c + (+-m)) is one fma with the same result,
+    // and the sign of m a select.
+    auto rot = [](float own, float other, float c, float s, bool first) -> u16 {
+        const double m = __dmul_rn(static_cast<double>(other), static_cast<double>(s));
+        return AttnElem<true>::from(
+            static_cast<float>(__fma_rn(static_cast<double>(own), static_cast<double>(c), first ? -m : m)));
+    };
+
+    // 1. Loads: x rows (rows past L read row L - 1 and are zeroed) and the W
+    // fragments of this wave's in_proj tiles; everything else waits until
+    // the W fragments are dead, so the registers hold.
+    // x goes in two halves of K (k < D / 2, then the rest), each followed by the W fragments of its k
+    // steps, so the first half's products start while the second half is still arriving.
+    constexpr int XU = LMAX * (D / 8) / 512;  // 8-float units per thread, XU / 2 per half
+    constexpr int SH = D / 64;                // k steps per half
+    float4 xa[XU], xb[XU];
+    auto xunit = [&](int j, int& row, int& c8) {  // unit j: half j / (XU / 2), 16 rows of 16 units per pass
+        const int hf = j / (XU / 2), u = tid + 512 * (j % (XU / 2));
+        row = u / (D / 16);
+        c8 = hf * (D / 2) + (u % (D / 16)) * 8;
+    };
+    const int tiles[3] = {2 * wave, 2 * wave + 1, 2 * H + (wave < 5 ? wave : 4)};
+    uint4 wf[3][D / 32];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+        for (int j = hf * (XU / 2); j < (hf + 1) * (XU / 2); ++j) {
+            int row, c8;
+            xunit(j, row, c8);
+            const float* src = xw + (row < L ? row : L - 1) * p.x_ts + c8;
+            xa[j] = *reinterpret_cast<const float4*>(src);
+            xb[j] = *reinterpret_cast<const float4*>(src + 4);
+        }
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+            for (int s = hf * SH; s < (hf + 1) * SH; ++s)
+                wf[t][s] = *reinterpret_cast<const uint4*>(p.w_in + (16 * tiles[t] + li) * D + 32 * s + 8 * g);
+    }
+    // cos/sin of every row into LDS (the latent buffer's space, free until the LayerNorm): thread t takes
+    // float4 t % 4 of row t / 4 of both tables.
+    float* cs_s = reinterpret_cast<float*>(lat_s);  // [LMAX, ROPE] cos, then [LMAX, ROPE] sin
+    static_assert(2 * LMAX * ROPE * 4 <= LMAX * LP * 2 && LMAX * ROPE / 4 == 512, "rope tables in the latent space");
+    const int crow = tid >> 2, ccol = 4 * (tid & 3), crc = crow < L ? crow : L - 1;
+    const float4 cv = *reinterpret_cast<const float4*>(p.cosine + crc * ROPE + ccol);
+    const float4 sv = *reinterpret_cast<const float4*>(p.sine + crc * ROPE + ccol);
+    *reinterpret_cast<float4*>(cs_s + crow * ROPE + ccol) = cv;
+    *reinterpret_cast<float4*>(cs_s + LMAX * ROPE + crow * ROPE + ccol) = sv;
+
+    // 2. in_proj: per (tile, row tile) the linear's chain over the 8 k steps, the first half's steps
+    // before the second half is stored.
+    f32x4 acc[3][RT];
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+        for (int m = 0; m < RT; ++m) acc[t][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+        for (int j = hf * (XU / 2); j < (hf + 1) * (XU / 2); ++j) {
+            int row, c8;
+            xunit(j, row, c8);
+            const bool live = row < L;
+            const float v[8] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w};
+            bf16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = static_cast<__bf16>(live ? v[e] : 0.0f);
+            *reinterpret_cast<bf16x8*>(xq_s + sw(row, c8)) = o;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < RT; ++m) {
+#pragma unroll
+            for (int s = hf * SH; s < (hf + 1) * SH; ++s) {
+                const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * m + li, 32 * s + 8 * g));
+#pragma unroll
+                for (int t = 0; t < 3; ++t)
+                    acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[t][s]), xf,
+                                                                        acc[t][m], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();  // every wave is done with x
+
+    // 3. Epilogue: lane (g, li) of row tile m holds row 16 m + li, columns
+    // 4g .. 4g + 3 of each tile (+ 0.0f: the linear adds its zero bias).
+    const bool first_half = g < 2;  // rope indices 0..7 pair with 8..15, 32 lanes away
+#pragma unroll
+    for (int m = 0; m < RT; ++m) {
+        const int row = 16 * m + li;
+        const bool live = row < L;
+        const f32x4 yn = acc[0][m] + f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 yr = acc[1][m] + f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 y3 = acc[2][m] + f32x4{0.f, 0.f, 0.f, 0.f};
+        const float4 cs = *reinterpret_cast<const float4*>(cs_s + row * ROPE + 4 * g);
+        const float4 sn = *reinterpret_cast<const float4*>(cs_s + LMAX * ROPE + row * ROPE + 4 * g);
+        const float c4[4] = {cs.x, cs.y, cs.z, cs.w};
+        const float s4[4] = {sn.x, sn.y, sn.z, sn.w};
+
+        u16 qn[4], qr[4], kr[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const u16 en = AttnElem<true>::from(yn[v]);
+            const u16 er = rot(yr[v], __shfl_xor(yr[v], 32), c4[v], s4[v], first_half);
+            qn[v] = live ? en : u16(0);
+            qr[v] = live ? er : u16(0);
+        }
+        if (wave == 4) {  // the k_rope tile (wave is uniform: a scalar branch)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const u16 ek = rot(y3[v], __shfl_xor(y3[v], 32), c4[v], s4[v], first_half);
+                kr[v] = live ? ek : u16(0);
+            }
+        }
+        auto pack = [](const u16 (&e)[4]) {
+            return make_uint2(static_cast<uint32_t>(e[0]) | (static_cast<uint32_t>(e[1]) << 16),
+                              static_cast<uint32_t>(e[2]) | (static_cast<uint32_t>(e[3]) << 16));
+        };
+        *reinterpret_cast<uint2*>(xq_s + sw(row, HD * wave + 4 * g)) = pack(qn);
+        *reinterpret_cast<uint2*>(xq_s + sw(row, HD * wave + NOPE + 4 * g)) = pack(qr);
+        if (wave < 4) {
+            *reinterpret_cast<f32x4*>(lat_f + row * KV + 16 * wave + 4 * g) = y3;
+        } else if (wave == 4) {
+            *reinterpret_cast<uint2*>(kr_s + row * ROPE + 4 * g) = pack(kr);
+        }
+    }
+    __syncthreads();
+    const int lr = tid >> 4, lc = tid & 15;
+    const float4 lnw = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
+    // A missing bias reads the weight and masks it to +0.0 bit-wise: a select here would become a branch
+    // around the load, and the branch a wait for every load in flight.
+    const bool has_b = p.ln_b != nullptr;
+    const float4 lnb_raw = *reinterpret_cast<const float4*>((has_b ? p.ln_b : p.ln_w) + 4 * lc);
+    const uint32_t bmask = has_b ? 0xffffffffu : 0u;
+    const float4 lnb = make_float4(__uint_as_float(__float_as_uint(lnb_raw.x) & bmask),
+                                   __uint_as_float(__float_as_uint(lnb_raw.y) & bmask),
+                                   __uint_as_float(__float_as_uint(lnb_raw.z) & bmask),
+                                   __uint_as_float(__float_as_uint(lnb_raw.w) & bmask));
+    const int grp = wave >> 1;  // head group: heads grp, grp + HG
+    const int wg = wave & 1;
+    // The kv_up B fragments of the group's first head (lane (g, li): W_up row 16 ct + li, k = 32 ks + 8g ..),
+    // in flight during the LayerNorm.
+    constexpr int CT = UPW / 16;
+    uint4 wu[CT][KV / 32];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int ks = 0; ks < KV / 32; ++ks)
+            wu[ct][ks] = *reinterpret_cast<const uint4*>(p.w_up + (grp * UPW + 16 * ct + li) * KV + 32 * ks + 8 * g);
+
+    // 4. kv_norm: LayerNorm of the latent rows into bf16, the arithmetic of
+    // mla_attend_kernel's (16 lanes per row, 4 columns each, fp64 sums).
+    {
+        constexpr int PASSES = LMAX / 32;
+        const double inv_dim = 1.0 / static_cast<double>(KV);
+        float4 xs[PASSES];
+        double mean[PASSES], sumsq[PASSES];
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            xs[ps] = *reinterpret_cast<const float4*>(lat_f + (32 * ps + lr) * KV + 4 * lc);
+            const float4 x = xs[ps];
+            mean[ps] = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
+                       (static_cast<double>(x.z) + static_cast<double>(x.w));
+        }
+        auto row_sums = [](double (&v)[PASSES]) {
+#pragma unroll
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<8>(v[ps]);
+#pragma unroll
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<4>(v[ps]);
+#pragma unroll
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<2>(v[ps]);
+#pragma unroll
+            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<1>(v[ps]);
+        };
+        row_sums(mean);
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const float4 x = xs[ps];
+            mean[ps] *= inv_dim;
+            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
+            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
+            sumsq[ps] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+        }
+        row_sums(sumsq);
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int row = 32 * ps + lr;
+            const float4 x = xs[ps];
+            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
+            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
+            const double rstd = 1.0 / sqrt(fma(sumsq[ps], inv_dim, p.ln_eps));
+            const bool active = row < L;
+            const u16 o0 = active ? AttnElem<true>::from(static_cast<float>((a0 * rstd) * lnw.x + static_cast<double>(lnb.x))) : u16(0);
+            const u16 o1 = active ? AttnElem<true>::from(static_cast<float>((a1 * rstd) * lnw.y + static_cast<double>(lnb.y))) : u16(0);
+            const u16 o2 = active ? AttnElem<true>::from(static_cast<float>((a2 * rstd) * lnw.z + static_cast<double>(lnb.z))) : u16(0);
+            const u16 o3 = active ? AttnElem<true>::from(static_cast<float>((a3 * rstd) * lnw.w + static_cast<double>(lnb.w))) : u16(0);
+            *reinterpret_cast<uint2*>(lat_s + row * LP + 4 * lc) =
+                make_uint2(static_cast<uint32_t>(o0) | (static_cast<uint32_t>(o1) << 16),
+                           static_cast<uint32_t>(o2) | (static_cast<uint32_t>(o3) << 16));
+        }
+    }
+    __syncthreads();  // the fp32 latent is dead: the head slots take its place
+
+    // 5. Heads, HG at a time, two waves each: group grp takes heads grp and grp + HG. Slot layouts
+    // (16-byte units swizzled so the MFMA operand reads are conflict-free):
+    //   k   [key][HD]   unit u of key r at u ^ ((r >> 1) & 3)
+    //   v^T [HD][key]   unit u of dim d at u ^ (d & 7)
+    u16* k_s = head_s + grp * SLOT;
+    u16* vt_s = k_s + LMAX * HD;
+    auto k_at = [](int key, int dim) { return key * HD + ((((dim >> 3) ^ ((key >> 1) & 3))) << 3) + (dim & 7); };
+    auto v_at = [](int dim, int key) { return dim * LMAX + ((((key >> 3) ^ (dim & 7))) << 3) + (key & 7); };
+    {  // the rotated k_rope, the same for every head, into the k rows (dims NOPE .. HD - 1) of every slot:
+       // thread t copies row t % 128 into slot t / 128
+        const int row = tid & (LMAX - 1);
+        static_assert(512 == HG * LMAX, "one row of one slot per thread");
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+            *reinterpret_cast<uint4*>(head_s + (tid / LMAX) * SLOT + k_at(row, NOPE + 8 * hf)) =
+                *reinterpret_cast<const uint4*>(kr_s + row * ROPE + 8 * hf);
+    }
+    uint4 wo[2][D / 32];  // o_proj fragments, fetched during the last round (the loop is unrolled, so
+                          // their addresses are not held across it)
+#pragma unroll
+    for (int r = 0; r < H / HG; ++r) {
+        const int h = r * HG + grp;
+        // kv = LN(latent) . W_up^T for this head (row tiles wg, wg + 2, ...): k_nope into k_s, v^T into vt_s.
+#pragma unroll
+        for (int j = 0; j < RT / 2; ++j) {
+            const int rt = 2 * j + wg;
+            bf16x8 la[KV / 32];
+#pragma unroll
+            for (int ks = 0; ks < KV / 32; ++ks)
+                la[ks] = *reinterpret_cast<const bf16x8*>(lat_s + (16 * rt + li) * LP + 32 * ks + 8 * g);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KV / 32; ++ks)
+                    a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(la[ks], __builtin_bit_cast(bf16x8, wu[ct][ks]), a, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = 16 * rt + 4 * g + v;
+                    const u16 e = AttnElem<true>::from(a[v]);
+                    if (ct == 0) {
+                        k_s[k_at(row, li)] = e;
+                    } else {
+                        vt_s[v_at(16 * (ct - 1) + li, row)] = e;
+                    }
+                }
+            }
+        }
+        if (r + 1 < H / HG) {  // the next head's fragments
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int ks = 0; ks < KV / 32; ++ks)
+                    wu[ct][ks] = *reinterpret_cast<const uint4*>(p.w_up + ((h + HG) * UPW + 16 * ct + li) * KV +
+                                                                 32 * ks + 8 * g);
+        }
+        __syncthreads();
+        if (r + 1 == H / HG) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int s = 0; s < D / 32; ++s)
+                    wo[t][s] = *reinterpret_cast<const uint4*>(p.w_out + (16 * (2 * wave + t) + li) * D + 32 * s + 8 * g);
+        }
+        // Causal attention (top-left) of head h: query tiles (wg, 7 - wg) and (wg + 2, 5 - wg).
+        constexpr int TQ = 4;
+        const int qt[TQ] = {wg, 7 - wg, wg + 2, 5 - wg};
+        bf16x8 qb[TQ];
+        float m_run[TQ], l_run[TQ];
+        f32x4 o[TQ][HD / 16];
+#pragma unroll
+        for (int i = 0; i < TQ; ++i) {
+            qb[i] = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * qt[i] + li, HD * h + 8 * g));
+            m_run[i] = -INFINITY;
+            l_run[i] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < HD / 16; ++t) o[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        for (int kbase = 0; kbase < L; kbase += kKeysPerChunk) {
+#pragma unroll
+            for (int i = 0; i < TQ; ++i) {
+                const int q0 = 16 * qt[i];
+                if (q0 >= L || kbase > q0 + 15) continue;
+                f32x4 sc[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_s + k_at(kbase + 16 * t + li, 8 * g));
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[i], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
+                const int qpos = q0 + li;
+                float mx = -INFINITY;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int key = kbase + 16 * t + 4 * g + v;
+                        const float xv = (key < L && key <= qpos) ? sc[t][v] * p.scale_log2 : -INFINITY;
+                        sc[t][v] = xv;
+                        mx = fmaxf(mx, xv);
+                    }
+                }
+                mx = xor_max(mx, 16);
+                mx = xor_max(mx, 32);
+                const float m_new = fmaxf(m_run[i], mx);
+                const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+                const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
+                m_run[i] = m_new;
+                float psum = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
+                        sc[t][v] = e;
+                        psum += e;
+                    }
+                }
+                l_run[i] = l_run[i] * corr + psum;
+#pragma unroll
+                for (int t = 0; t < HD / 16; ++t) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) o[i][t][v] *= corr;
+                }
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    bf16x8 pb;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        pb[v] = static_cast<__bf16>(sc[2 * half][v]);
+                        pb[4 + v] = static_cast<__bf16>(sc[2 * half + 1][v]);
+                    }
+#pragma unroll
+                    for (int t = 0; t < HD / 16; ++t) {
+                        const int dim = 16 * t + li, key0 = kbase + 32 * half + 4 * g;
+                        const uint2 lo = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0));
+                        const uint2 hi = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0 + 16));
+                        const uint4 raw = {lo.x, lo.y, hi.x, hi.y};
+                        o[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, raw), pb, o[i][t],
+                                                                           0, 0, 0);
+                    }
+                }
+            }
+        }
+        // Normalised output, rounded to bf16 as the o_proj takes it, over this head's q columns.
+#pragma unroll
+        for (int i = 0; i < TQ; ++i) {
+            const int qi = 16 * qt[i] + li;
+            float l = xor_sum(l_run[i], 16);
+            l = xor_sum(l, 32);
+            if (qi >= L) continue;
+            const float inv = 1.0f / l;
+#pragma unroll
+            for (int t = 0; t < HD / 16; ++t) {
+                u16 e[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) e[v] = AttnElem<true>::from(o[i][t][v] * inv);
+                *reinterpret_cast<uint2*>(xq_s + sw(qi, HD * h + 16 * t + 4 * g)) =
+                    make_uint2(static_cast<uint32_t>(e[0]) | (static_cast<uint32_t>(e[1]) << 16),
+                               static_cast<uint32_t>(e[2]) | (static_cast<uint32_t>(e[3]) << 16));
+            }
+        }
+        __syncthreads();
+    }
+
+    // 6. o_proj: wave w computes output columns 32 w .. 32 w + 31 of every row.
+    float* orow0 = p.out + b * static_cast<int64_t>(L) * D;
+#pragma unroll
+    for (int m = 0; m < RT; ++m) {
+        f32x4 y[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int s = 0; s < D / 32; ++s) {
+            const bf16x8 af = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * m + li, 32 * s + 8 * g));
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                y[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wo[t][s]), af, y[t], 0, 0, 0);
+        }
+        const int row = 16 * m + li;
+        if (row < L) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                *reinterpret_cast<f32x4*>(orow0 + row * D + HD * wave + 16 * t + 4 * g) =
+                    y[t] + f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+}
+
 }  // namespace
 }  // namespace mlk
 
@@ -927,4 +1386,39 @@ extern "C" mlk_status mlk_mla_attend_normed(const float* projected, int64_t batc
         hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, true>), grid, dim3(512), 0, s, p);
     }
     return launch_status("mla_attend_normed");
+}
+
+extern "C" mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_t d_model,
+                                      int64_t x_batch_stride, int64_t x_token_stride, const void* in_proj_weight,
+                                      const float* kv_norm_w, const float* kv_norm_b, double kv_norm_eps,
+                                      const void* kv_up_weight, const void* out_weight, const float* cosine,
+                                      const float* sine, int64_t heads, int64_t head_dim, int64_t nope_dim,
+                                      int64_t kv_rank, int32_t weight_dtype, double scale, float* out,
+                                      mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 1 && heads > 0 && d_model == heads * head_dim, "invalid MLA geometry");
+    const bool built = weight_dtype == MLK_DTYPE_BF16 && heads == 8 && head_dim == 32 && nope_dim == 16 &&
+                       kv_rank == 64 && length <= 128;
+    if (!built) {
+        set_error("mla_forward: geometry without the per-window kernel (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    if (!aligned16(x) || x_token_stride % 4 != 0 || x_batch_stride % 4 != 0 || !aligned16(cosine) ||
+        !aligned16(sine) || !aligned16(kv_norm_w) || (kv_norm_b != nullptr && !aligned16(kv_norm_b)) ||
+        !aligned16(in_proj_weight) || !aligned16(kv_up_weight) || !aligned16(out_weight) || !aligned16(out)) {
+        set_error("mla_forward: operands must be 16-byte aligned for the per-window kernel (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    MLK_CHECK(x_token_stride >= d_model && (length == 1 || x_batch_stride >= length * x_token_stride),
+              "x strides must cover the rows");
+    if (batch == 0) return MLK_OK;
+    MLK_CHECK(x && in_proj_weight && kv_norm_w && kv_up_weight && out_weight && cosine && sine && out,
+              "null tensor pointer");
+    MLK_CHECK(batch <= 0x7fffffff, "too many windows for one launch");
+    MlaWindowArgs p{x, x_batch_stride, x_token_stride, static_cast<const u16*>(in_proj_weight), kv_norm_w, kv_norm_b,
+                    static_cast<double>(static_cast<float>(kv_norm_eps)), static_cast<const u16*>(kv_up_weight),
+                    static_cast<const u16*>(out_weight), cosine, sine, out, length,
+                    static_cast<float>(scale * 1.4426950408889634)};
+    hipLaunchKernelGGL((mla_window_kernel<8>), dim3(static_cast<unsigned>(batch)), dim3(512), 0,
+                       reinterpret_cast<hipStream_t>(stream), p);
+    return launch_status("mla_forward");
 }

@@ -49,6 +49,8 @@ def _load():
         "mlk_mla_attend_normed": [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _dbl,
                                   _vp, _vp],
         "mlk_mla_rope_qk": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
+        "mlk_mla_forward": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _dbl, _vp, _vp, _vp, _vp, _i64, _i64,
+                            _i64, _i64, C.c_int32, _dbl, _vp, _vp],
         "mlk_mla_attend": [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp,
                            _vp, _dbl, _vp, _vp],
         "mlk_attention": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, C.c_int32,
@@ -863,8 +865,50 @@ def _fused_attend_ln(x, in_proj_weight, batch, length, q_width, n_heads, head_di
                           kv_up_weight, cosine, sine, scale)
 
 
+_MLA_PATH = {"last": None}
+
+
+def mla_forward_launches() -> list[str] | None:
+    """The kernel launches the last ``mla_forward`` call made, in order."""
+    return _MLA_PATH["last"]
+
+
+def _mla_window(x, in_proj_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight, cosine,
+                sine, n_heads, head_dim, nope_dim, kv_lora_rank, scale):
+    """The whole forward for every causal query, one block per window (bf16 weights, 8 heads of 32, rope 16,
+    kv rank 64, L <= 128); None where that kernel is not built for the call."""
+    batch, length, d_model = x.shape
+    ws = [in_proj_weight, kv_up_weight, out_weight]
+    if any(w.dtype != torch.bfloat16 or not w.is_contiguous() for w in ws) or x.stride(-1) != 1:
+        return None
+    rope = head_dim - nope_dim
+    if tuple(cosine.shape) != (length, rope) or not cosine.is_contiguous() or sine.shape != cosine.shape or \
+            not sine.is_contiguous():
+        return None
+    _check(tuple(in_proj_weight.shape) == (d_model + kv_lora_rank + rope, d_model),
+           "in_proj_weight must be [d_model + kv_lora_rank + rope_dim, d_model]")
+    _check(tuple(kv_up_weight.shape) == (n_heads * (nope_dim + head_dim), kv_lora_rank),
+           "kv_up_weight must be [n_heads * (nope_dim + head_dim), kv_lora_rank]")
+    _check(tuple(out_weight.shape) == (d_model, d_model), "out_weight must be [d_model, d_model]")
+    w = _dense_parameter(kv_norm_weight, kv_lora_rank, "kv_norm.weight")
+    b = None if kv_norm_bias is None or kv_norm_bias.numel() == 0 else _dense_parameter(kv_norm_bias, kv_lora_rank,
+                                                                                       "kv_norm.bias")
+    out = torch.empty((batch, length, d_model), dtype=torch.float32, device=x.device)
+    lib = _load()
+    status = lib.mlk_mla_forward(_ptr(x), batch, length, d_model, x.stride(0), x.stride(1), _ptr(in_proj_weight),
+                                 _ptr(w), _ptr(b), float(kv_norm_eps), _ptr(kv_up_weight), _ptr(out_weight),
+                                 _ptr(cosine), _ptr(sine), n_heads, head_dim, nope_dim, kv_lora_rank,
+                                 _WEIGHT_DTYPES[torch.bfloat16], float(scale), _ptr(out), _stream())
+    if status == 3:  # MLK_ERR_UNSUPPORTED
+        return None
+    if status != 0:
+        raise RuntimeError(lib.mlk_last_error().decode())
+    return out
+
+
 def _mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight,
-                 cosine, sine, n_heads, head_dim, nope_dim, kv_lora_rank, n_last, causal, scale, allow_fused):
+                 cosine, sine, n_heads, head_dim, nope_dim, kv_lora_rank, n_last, causal, scale, allow_fused,
+                 allow_window=True):
     _require_f32_gpu(x, "x")
     _check(x.dim() == 3, "x must be [B,L,d_model]")
     batch, length, d_model = x.shape
@@ -873,18 +917,27 @@ def _mla_forward(x, in_proj_weight, q_weight, kv_norm_weight, kv_norm_bias, kv_n
     _check(n_last == 1 or n_last == length, "native MLA supports the final query or the full sequence")
     precision = torch.bfloat16 if _weight(in_proj_weight, "in_proj_weight").dtype == torch.bfloat16 else torch.float32
     full = n_last == length
+    if allow_fused and allow_window and full and causal and precision == torch.bfloat16:
+        out = _mla_window(x, in_proj_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight,
+                          cosine, sine, n_heads, head_dim, nope_dim, kv_lora_rank, scale)
+        if out is not None:
+            _MLA_PATH["last"] = ["mla_forward"]
+            return out
     if allow_fused and full and causal and precision == torch.bfloat16:
         attended = _fused_attend_ln(x, in_proj_weight, batch, length, d_model, n_heads, head_dim, nope_dim,
                                     kv_lora_rank, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, cosine,
                                     sine, scale)
         if attended is not None:
+            _MLA_PATH["last"] = ["linear", "layer_norm_bf16", "mla_attend_normed", "linear"]
             return linear(attended.view(batch, length, d_model), out_weight)
     projected = linear(x, in_proj_weight)
     if allow_fused and full and causal and precision == torch.bfloat16:
         attended = _fused_attend(projected, batch, length, d_model, n_heads, head_dim, nope_dim, kv_lora_rank,
                                  kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, cosine, sine, scale)
         if attended is not None:
+            _MLA_PATH["last"] = ["linear", "mla_attend", "linear"]
             return linear(attended.view(batch, length, d_model), out_weight)
+    _MLA_PATH["last"] = ["separate"]
     q_width = d_model if full else 0
     if full:
         q = projected[..., :q_width]
@@ -969,7 +1022,8 @@ def exported_symbols() -> list[str]:
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent",
             "mlk_mamba3_siso_recurrent_noalloc", "mlk_mamba3_siso_forward", "mlk_rms_norm_mamba3_forward",
             "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear",
-            "mlk_layer_norm_bf16", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend", "mlk_mla_attend_normed"]
+            "mlk_layer_norm_bf16", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend", "mlk_mla_attend_normed",
+            "mlk_mla_forward"]
 
 
 def math_check(x: torch.Tensor) -> dict:

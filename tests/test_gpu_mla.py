@@ -263,3 +263,56 @@ def test_latent_layernorm_once_per_row(dev, B, L, H, hd, nope):
     projected = _C.linear(x, in_w)
     ref = _C._fused_attend(projected, B, L, d, H, hd, nope, kvr, ln_w, ln_b, 1e-5, up_w, cos, sin, hd ** -0.5)
     assert torch.equal(att, ref)
+
+
+@pytest.mark.parametrize("B,L,bias,strided", [(16, 128, True, False),   # MLA block geometry
+                                              (3, 37, True, False), (2, 1, False, False), (5, 64, False, True),
+                                              (1, 127, True, True), (64, 128, True, False), (9, 100, False, False)])
+def test_window_kernel_equals_separate_path(dev, B, L, bias, strided):
+    """With bf16 weights, 8 heads of 32 and L <= 128 the whole mla_forward is one launch, one block per
+    window: the result equals the four-launch path (linear, latent LayerNorm into bf16, fused attention,
+    linear) bit for bit, for ragged lengths, no kv_norm bias and token-strided x."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(B * 1000 + L)
+    H, hd, nope, kvr = 8, 32, 16, 64
+    d, rope = H * hd, hd - nope
+    bf = torch.bfloat16
+    wide = torch.randn(B, L, d + 64 if strided else d, generator=g).to(dev)
+    x = wide[..., 32:32 + d] if strided else wide
+    in_w = (torch.randn(d + kvr + rope, d, generator=g) * 0.05).to(dev, bf)
+    up_w = (torch.randn(H * (nope + hd), kvr, generator=g) * 0.1).to(dev, bf)
+    o_w = (torch.randn(d, d, generator=g) * 0.05).to(dev, bf)
+    ln_w = (1 + 0.1 * torch.randn(kvr, generator=g)).to(dev)
+    ln_b = (0.1 * torch.randn(kvr, generator=g)).to(dev) if bias else None
+    cos, sin = (t.to(dev) for t in rope_tables_t(L, rope))
+    args = (x, in_w, x.new_empty(0), ln_w, ln_b, 1e-5, up_w, o_w, cos, sin, H, hd, nope, kvr, L, True, hd ** -0.5)
+    one = _C._mla_forward(*args, allow_fused=True)
+    assert _C.mla_forward_launches() == ["mla_forward"], "the geometry has the per-window kernel"
+    four = _C._mla_forward(*args, allow_fused=True, allow_window=False)
+    assert _C.mla_forward_launches() == ["linear", "layer_norm_bf16", "mla_attend_normed", "linear"]
+    assert one.shape == (B, L, d)
+    assert_bitwise(one, four.cpu().numpy(), f"per-window MLA {B}x{L} vs four launches")
+
+
+def test_window_kernel_vs_oracle(dev, oracle):
+    """The per-window kernel against the oracle chain at the MLA block geometry (bf16 weights: 2e-2)."""
+    from montlok import _C
+
+    rng = np.random.default_rng(31)
+    B, L, d, H, hd, nope, kv_rank = 8, 128, 256, 8, 32, 16, 64
+    x = rng.standard_normal((B, L, d)).astype(np.float32)
+    p = _mla_params(rng, d, H, hd, nope, kv_rank, True)
+    cos, sin = rope_tables(L, hd - nope)
+    scale = 1.0 / math.sqrt(hd)
+
+    def w(a):
+        return _t(a, dev).to(torch.bfloat16)
+
+    in_w = np.concatenate([p["q"], p["kv_down"], p["k_rope"]])
+    out = _C.mla_forward(_t(x, dev), w(in_w), torch.empty(0, device=dev), _t(p["ln_w"], dev), _t(p["ln_b"], dev),
+                         1e-5, w(p["kv_up"]), w(p["o"]), _t(cos, dev), _t(sin, dev), H, hd, nope, kv_rank, L, True,
+                         scale)
+    assert _C.mla_forward_launches() == ["mla_forward"]
+    expect = _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, L, True, scale, cos, sin)
+    assert_close(out, expect, tol=BF16_TOL, name="per-window mla_forward vs oracle")
