@@ -127,11 +127,13 @@ mlk_status mlk_linear_residual(const float* x, int64_t rows, int64_t in_features
 
 /* rms_norm(x, norm_weight, eps, groups) then linear(., weight, bias) in one
  * launch, without the normalised intermediate: bit-identical to mlk_rms_norm
- * into a buffer followed by mlk_linear on it. Built for the shapes that take
- * the one-wave-per-tile linear (fewer 128-row blocks x 64-column chunks than
- * CUs, in_features <= 256 and a multiple of 8), groups of 8, 16, 32 or 64
- * floats and 16-byte aligned x rows, norm weight and weight rows; other
- * shapes return MLK_ERR_UNSUPPORTED and the caller runs the two operators.
+ * into a buffer followed by mlk_linear on it. Built for groups of 8, 16, 32
+ * or 64 floats and 16-byte aligned x rows, norm weight and weight rows, on
+ * the shapes that take the one-wave-per-tile linear (fewer 128-row blocks x
+ * 64-column chunks than CUs, in_features <= 256 and a multiple of 8) and, for
+ * fp32 weights with in_features 128, on any row count (the row-layout linear
+ * with the norm applied to its loaded fragments); other shapes return
+ * MLK_ERR_UNSUPPORTED and the caller runs the two operators.
  * No single counterpart in the reference's op table: it fuses rms_norm
  * (montlok.cpp:1481) with the in_proj linear that follows it (stage1_forward,
  * montlok.cpp:1030-1034). */

@@ -194,7 +194,11 @@ struct WStage {
 // iteration i+1 is fetched before the MFMAs of iteration i and written to the
 // other LDS buffer after them: one barrier per iteration. When K spans several
 // chunks, A is reloaded (from L2) at the start of each iteration.
-template <bool BF16W, bool VEC, bool MULTIK>
+// GS > 0 (fp32 weights, K = one chunk): the grouped RMSNorm of each row
+// (groups of GS floats) applied to the loaded fragments first, the arithmetic
+// of rms_norm_vec_kernel (tile_rms_norm), so the result equals rms_norm then
+// this kernel bit for bit.
+template <bool BF16W, bool VEC, bool MULTIK, int GS = 0>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void linear_kernel(LinearArgs p) {
     using T = typename WTraits<BF16W>::T;
     constexpr int KC = WTraits<BF16W>::kKChunk;
@@ -225,6 +229,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
     AFrag<BF16W> a_cur;  // reloaded per iteration when K spans several chunks
     stage.fetch(p, n0_of(0), 0, kspan_of(0));
     load_a<BF16W, VEC>(p, my_row, 0, group, kspan_of(0) / 32, a_cur);
+    if constexpr (GS > 0) {
+        static_assert(!BF16W && !MULTIK, "the RMSNorm prologue needs all of K in fp32 fragments");
+        float nw[kSteps][8];
+        bool nlive[kSteps];
+        tile_load8<kSteps>(p.norm_w, static_cast<int>(p.K), group, nw, nlive);
+        tile_rms_norm<kSteps, GS>(a_cur.v, nw, p.norm_eps);
+    }
     stage.store(p, n0_of(0), w_lds[0], kspan_of(0));
     __syncthreads();
 
@@ -768,7 +779,11 @@ extern "C" mlk_status mlk_rms_norm_linear(const float* x, int64_t rows, int64_t 
     const size_t wsize = weight_dtype == MLK_DTYPE_BF16 ? 2 : 4;
     const bool vec = aligned16(x) && x_stride % 4 == 0 && aligned16(weight) && (in_features * wsize) % 16 == 0 &&
                      aligned16(norm_weight);
-    if (!vec || !(gs == 8 || gs == 16 || gs == 32 || gs == 64) || !small_shape(rows, in_features, out_features)) {
+    const bool gs_ok = gs == 8 || gs == 16 || gs == 32 || gs == 64;
+    // Large row counts: the row-layout kernel with the prologue, for fp32 weights and K of one chunk.
+    const bool rows_form = vec && gs_ok && !small_shape(rows, in_features, out_features) &&
+                           weight_dtype == MLK_DTYPE_F32 && in_features == WTraits<false>::kKChunk;
+    if (!vec || !gs_ok || !(small_shape(rows, in_features, out_features) || rows_form)) {
         set_error("rms_norm_linear: shape without the fused form (use rms_norm then linear)");
         return MLK_ERR_UNSUPPORTED;
     }
@@ -776,8 +791,25 @@ extern "C" mlk_status mlk_rms_norm_linear(const float* x, int64_t rows, int64_t 
     MLK_CHECK(x && norm_weight && weight && out, "null tensor pointer");
     LinearArgs p{x, rows, in_features, x_stride, weight, bias, out_features, out, out_stride, nullptr, 0,
                  norm_weight, static_cast<double>(static_cast<float>(eps))};
-    const int64_t tiles = ceil_div(rows, 16) * ceil_div(out_features, 16);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (rows_form) {
+        MLK_CHECK(ceil_div(rows, kRowsPerBlock) <= 0x7fffffff, "too many rows");
+        const int64_t n_chunks = ceil_div(out_features, kColsPerChunk);
+        const int64_t row_blocks = ceil_div(rows, kRowsPerBlock);
+        int64_t gy = 1;
+        while (gy < n_chunks && row_blocks * gy < 512) ++gy;
+        const dim3 grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(gy));
+#define MLK_ROWS_GS(G) hipLaunchKernelGGL((linear_kernel<false, true, false, G>), grid, dim3(kThreads), 0, s, p)
+        switch (gs) {
+            case 8: MLK_ROWS_GS(8); break;
+            case 16: MLK_ROWS_GS(16); break;
+            case 32: MLK_ROWS_GS(32); break;
+            default: MLK_ROWS_GS(64); break;
+        }
+#undef MLK_ROWS_GS
+        return launch_status("rms_norm_linear");
+    }
+    const int64_t tiles = ceil_div(rows, 16) * ceil_div(out_features, 16);
 #define MLK_NORM_GS(G)                                                                             \
     (weight_dtype == MLK_DTYPE_BF16 ? launch_small_norm<true, G>(p, tiles, s) : launch_small_norm<false, G>(p, tiles, s))
     switch (gs) {

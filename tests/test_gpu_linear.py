@@ -221,6 +221,27 @@ def test_rms_norm_linear_equals_the_two_operators(dev, M, K, N, groups, wdt):
     assert torch.equal(fused, separate), f"{M}x{K}->{N} groups {groups} {wdt}"
 
 
+@pytest.mark.parametrize("M,N,groups", [(65536, 668, 8), (40000, 257, 16), (4097, 64, 4), (9000, 100, 2)])
+def test_rms_norm_linear_large_rows(dev, M, N, groups):
+    """fp32 weights with in_features 128 take the row-layout form at any row count (the streaming decode's
+    GroupedRMSNorm + in_proj): one launch, bit for bit against rms_norm then linear."""
+    from montlok import _C
+    from montlok._C import _load
+
+    K = 128
+    g = torch.Generator(device="cpu").manual_seed(M + N + groups)
+    x = (torch.randn(M, K, generator=g) * 3).to(dev)
+    nw = (torch.rand(K, generator=g) + 0.5).to(dev)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dev)
+    b = torch.randn(N, generator=g).to(dev)
+    out = torch.empty(M, N, device=dev)
+    status = _load().mlk_rms_norm_linear(x.data_ptr(), M, K, K, nw.data_ptr(), 1e-5, groups, w.data_ptr(), 0,
+                                         b.data_ptr(), N, out.data_ptr(), N, torch.cuda.current_stream().cuda_stream)
+    assert status == 0, "the shape has the fused form"
+    separate = _C.linear(_C.rms_norm(x, nw, 1e-5, groups), w, b)
+    assert torch.equal(out, separate), f"{M}x{K}->{N} groups {groups}"
+
+
 def test_rms_norm_linear_beyond_the_fused_form(dev):
     """Row counts that fill the chip, and groups of 4 floats, run the two operators."""
     from montlok import _C
