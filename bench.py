@@ -1054,6 +1054,27 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
 WORKLOADS = {"mhc": bench_mhc, "block": bench_block, "mla": bench_mla, "decode": bench_decode, "stack": bench_stack}
 
 
+def copy_bandwidth(mib: int = 1024, reps: int = 10) -> float:
+    """GB/s (bytes read + written) of a plain device-to-device copy of `mib` MiB: the HBM rate a kernel that
+    streams its bytes once can reach on this device, beside the 8 TB/s peak the roofline quotes."""
+    import torch
+
+    x = torch.empty(mib << 18, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        y.copy_(x)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del x, y
+    return 2 * (mib << 20) / (ms * 1e-3) / 1e9
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1069,6 +1090,10 @@ def main() -> int:
               f"GPUs inside a step.", file=sys.stderr)
         return 2
     line = WORKLOADS[args.workload](args.steps, args.warmup, cpu=not args.no_cpu)
+    if line["roofline"]["bound"] == "hbm":
+        copy = copy_bandwidth()
+        line["roofline"]["copy_GBs"] = copy
+        line["roofline"]["frac_of_copy"] = line["roofline"]["achieved"] / copy
     print(json.dumps(line))
     return 0
 
