@@ -833,12 +833,14 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     constexpr int SLOT = 2 * LMAX * HD;  // one head's k [keys, HD] and v^T [HD, keys], bf16, swizzled
     constexpr int HG = 4;                // heads at a time, two waves each
     static_assert(H == 8, "the wave -> column tile map assumes 8 heads on 8 waves");
-    static_assert(LMAX * KV * 4 <= HG * SLOT * 2, "the fp32 latent must fit the head slots it precedes");
     __shared__ __attribute__((aligned(16))) u16 xq_s[LMAX * D];
     __shared__ __attribute__((aligned(16))) u16 lat_s[LMAX * LP];
     __shared__ __attribute__((aligned(16))) u16 kr_s[LMAX * ROPE];
     __shared__ __attribute__((aligned(16))) u16 head_s[HG * SLOT];
-    float* lat_f = reinterpret_cast<float*>(head_s);  // [LMAX, KV], until the LayerNorm has run
+    // [LMAX, KV] fp32 until the LayerNorm has run; 16-byte chunk c of row r at slot c ^ (r % 16), so the
+    // epilogue's stores (16 rows, one chunk) and the LayerNorm's reads (one row, 16 chunks) are conflict-free.
+    float* lat_f = reinterpret_cast<float*>(head_s);
+    auto lat_at = [](int row, int chunk) { return row * KV + 4 * (chunk ^ (row & 15)); };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -854,10 +856,9 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     // the partner 32 lanes away), as rope_kernel: two fp64 products, their sum rounded to fp64, then to fp32.
     // The product of two floats is exact in fp64, so round(own c + (+-m)) is one fma with the same result,
     // and the sign of m a select.
-    auto rot = [](float own, float other, float c, float s, bool first) -> u16 {
-        const double m = __dmul_rn(static_cast<double>(other), static_cast<double>(s));
-        return AttnElem<true>::from(
-            static_cast<float>(__fma_rn(static_cast<double>(own), static_cast<double>(c), first ? -m : m)));
+    auto rot = [](float own, float other, double c, double s, bool first) -> u16 {
+        const double m = __dmul_rn(static_cast<double>(other), s);
+        return AttnElem<true>::from(static_cast<float>(__fma_rn(static_cast<double>(own), c, first ? -m : m)));
     };
 
     // 1. Loads: x rows (rows past L read row L - 1 and are zeroed) and the W
@@ -891,15 +892,25 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
             for (int s = hf * SH; s < (hf + 1) * SH; ++s)
                 wf[t][s] = *reinterpret_cast<const uint4*>(p.w_in + (16 * tiles[t] + li) * D + 32 * s + 8 * g);
     }
-    // cos/sin of every row into LDS (the latent buffer's space, free until the LayerNorm): thread t takes
-    // float4 t % 4 of row t / 4 of both tables.
-    float* cs_s = reinterpret_cast<float*>(lat_s);  // [LMAX, ROPE] cos, then [LMAX, ROPE] sin
-    static_assert(2 * LMAX * ROPE * 4 <= LMAX * LP * 2 && LMAX * ROPE / 4 == 512, "rope tables in the latent space");
+    // cos/sin of every row into LDS as doubles, converted once for all heads (the upper half of the head
+    // slots, free until the heads run; the fp32 latent takes the lower half): thread t takes 4 values of
+    // row t / 4 of both tables. A row of 16 doubles is 8 16-byte slots, pair p of the row at slot
+    // p ^ (row % 8), so the 16 rows a fragment reads land in different banks.
+    double* cs_d = reinterpret_cast<double*>(head_s + HG * SLOT / 2);  // [LMAX, ROPE] cos, then sin
+    auto cs_at = [](int row, int pair) { return row * ROPE + 2 * (pair ^ (row & 7)); };
+    static_assert(2 * LMAX * ROPE * 8 <= HG * SLOT, "rope tables in the upper half of the head slots");
+    static_assert(LMAX * KV * 4 <= HG * SLOT, "the fp32 latent in the lower half");
+    static_assert(LMAX * ROPE / 4 == 512, "one quad of each table per thread");
     const int crow = tid >> 2, ccol = 4 * (tid & 3), crc = crow < L ? crow : L - 1;
     const float4 cv = *reinterpret_cast<const float4*>(p.cosine + crc * ROPE + ccol);
     const float4 sv = *reinterpret_cast<const float4*>(p.sine + crc * ROPE + ccol);
-    *reinterpret_cast<float4*>(cs_s + crow * ROPE + ccol) = cv;
-    *reinterpret_cast<float4*>(cs_s + LMAX * ROPE + crow * ROPE + ccol) = sv;
+    {
+        const int p0 = ccol / 2;  // pairs p0, p0 + 1 of the row
+        *reinterpret_cast<double2*>(cs_d + cs_at(crow, p0)) = make_double2(cv.x, cv.y);
+        *reinterpret_cast<double2*>(cs_d + cs_at(crow, p0 + 1)) = make_double2(cv.z, cv.w);
+        *reinterpret_cast<double2*>(cs_d + LMAX * ROPE + cs_at(crow, p0)) = make_double2(sv.x, sv.y);
+        *reinterpret_cast<double2*>(cs_d + LMAX * ROPE + cs_at(crow, p0 + 1)) = make_double2(sv.z, sv.w);
+    }
 
     // 2. in_proj: per (tile, row tile) the linear's chain over the 8 k steps, the first half's steps
     // before the second half is stored.
@@ -946,10 +957,12 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         const f32x4 yn = acc[0][m] + f32x4{0.f, 0.f, 0.f, 0.f};
         const f32x4 yr = acc[1][m] + f32x4{0.f, 0.f, 0.f, 0.f};
         const f32x4 y3 = acc[2][m] + f32x4{0.f, 0.f, 0.f, 0.f};
-        const float4 cs = *reinterpret_cast<const float4*>(cs_s + row * ROPE + 4 * g);
-        const float4 sn = *reinterpret_cast<const float4*>(cs_s + LMAX * ROPE + row * ROPE + 4 * g);
-        const float c4[4] = {cs.x, cs.y, cs.z, cs.w};
-        const float s4[4] = {sn.x, sn.y, sn.z, sn.w};
+        const double2 c01 = *reinterpret_cast<const double2*>(cs_d + cs_at(row, 2 * g));
+        const double2 c23 = *reinterpret_cast<const double2*>(cs_d + cs_at(row, 2 * g + 1));
+        const double2 s01 = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, 2 * g));
+        const double2 s23 = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, 2 * g + 1));
+        const double c4[4] = {c01.x, c01.y, c23.x, c23.y};
+        const double s4[4] = {s01.x, s01.y, s23.x, s23.y};
 
         u16 qn[4], qr[4], kr[4];
 #pragma unroll
@@ -973,7 +986,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         *reinterpret_cast<uint2*>(xq_s + sw(row, HD * wave + 4 * g)) = pack(qn);
         *reinterpret_cast<uint2*>(xq_s + sw(row, HD * wave + NOPE + 4 * g)) = pack(qr);
         if (wave < 4) {
-            *reinterpret_cast<f32x4*>(lat_f + row * KV + 16 * wave + 4 * g) = y3;
+            *reinterpret_cast<f32x4*>(lat_f + lat_at(row, 4 * wave + g)) = y3;
         } else if (wave == 4) {
             *reinterpret_cast<uint2*>(kr_s + row * ROPE + 4 * g) = pack(kr);
         }
@@ -1011,7 +1024,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         double mean[PASSES], sumsq[PASSES];
 #pragma unroll
         for (int ps = 0; ps < PASSES; ++ps) {
-            xs[ps] = *reinterpret_cast<const float4*>(lat_f + (32 * ps + lr) * KV + 4 * lc);
+            xs[ps] = *reinterpret_cast<const float4*>(lat_f + lat_at(32 * ps + lr, lc));
             const float4 x = xs[ps];
             mean[ps] = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
                        (static_cast<double>(x.z) + static_cast<double>(x.w));
@@ -1119,7 +1132,11 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
                 for (int s = 0; s < D / 32; ++s)
                     wo[t][s] = *reinterpret_cast<const uint4*>(p.w_out + (16 * (2 * wave + t) + li) * D + 32 * s + 8 * g);
         }
-        // Causal attention (top-left) of head h: query tiles (wg, 7 - wg) and (wg + 2, 5 - wg).
+        // Causal attention (top-left) of head h: query tiles (wg, 7 - wg) and (wg + 2, 5 - wg). With L <= 128
+        // the key chunks are known: chunk 0 (keys 0..63) for all four tiles, chunk 1 (keys 64..127, when
+        // L > 64) for tiles 7 - wg and 5 - wg only (the other two end below key 64). Each chunk's tiles run
+        // as straight-line code, so their dependent chains interleave; a tile past L computes and is not
+        // stored. Every step is attn_kernel's (mask, running max, exp2, rescale, P in bf16).
         constexpr int TQ = 4;
         const int qt[TQ] = {wg, 7 - wg, wg + 2, 5 - wg};
         bf16x8 qb[TQ];
@@ -1133,70 +1150,73 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
 #pragma unroll
             for (int t = 0; t < HD / 16; ++t) o[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        for (int kbase = 0; kbase < L; kbase += kKeysPerChunk) {
+        auto chunk = [&](int kbase, int i) {
+            const int q0 = 16 * qt[i];
+            f32x4 sc[4];
 #pragma unroll
-            for (int i = 0; i < TQ; ++i) {
-                const int q0 = 16 * qt[i];
-                if (q0 >= L || kbase > q0 + 15) continue;
-                f32x4 sc[4];
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_s + k_at(kbase + 16 * t + li, 8 * g));
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[i], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            }
+            const int qpos = q0 + li;
+            float mx = -INFINITY;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_s + k_at(kbase + 16 * t + li, 8 * g));
-                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[i], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                }
-                const int qpos = q0 + li;
-                float mx = -INFINITY;
+            for (int t = 0; t < 4; ++t) {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int key = kbase + 16 * t + 4 * g + v;
-                        const float xv = (key < L && key <= qpos) ? sc[t][v] * p.scale_log2 : -INFINITY;
-                        sc[t][v] = xv;
-                        mx = fmaxf(mx, xv);
-                    }
-                }
-                mx = xor_max(mx, 16);
-                mx = xor_max(mx, 32);
-                const float m_new = fmaxf(m_run[i], mx);
-                const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-                const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
-                m_run[i] = m_new;
-                float psum = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
-                        sc[t][v] = e;
-                        psum += e;
-                    }
-                }
-                l_run[i] = l_run[i] * corr + psum;
-#pragma unroll
-                for (int t = 0; t < HD / 16; ++t) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) o[i][t][v] *= corr;
-                }
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    bf16x8 pb;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        pb[v] = static_cast<__bf16>(sc[2 * half][v]);
-                        pb[4 + v] = static_cast<__bf16>(sc[2 * half + 1][v]);
-                    }
-#pragma unroll
-                    for (int t = 0; t < HD / 16; ++t) {
-                        const int dim = 16 * t + li, key0 = kbase + 32 * half + 4 * g;
-                        const uint2 lo = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0));
-                        const uint2 hi = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0 + 16));
-                        const uint4 raw = {lo.x, lo.y, hi.x, hi.y};
-                        o[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, raw), pb, o[i][t],
-                                                                           0, 0, 0);
-                    }
+                for (int v = 0; v < 4; ++v) {
+                    const int key = kbase + 16 * t + 4 * g + v;
+                    const float xv = (key < L && key <= qpos) ? sc[t][v] * p.scale_log2 : -INFINITY;
+                    sc[t][v] = xv;
+                    mx = fmaxf(mx, xv);
                 }
             }
+            mx = xor_max(mx, 16);
+            mx = xor_max(mx, 32);
+            const float m_new = fmaxf(m_run[i], mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
+            m_run[i] = m_new;
+            float psum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
+                    sc[t][v] = e;
+                    psum += e;
+                }
+            }
+            l_run[i] = l_run[i] * corr + psum;
+#pragma unroll
+            for (int t = 0; t < HD / 16; ++t) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) o[i][t][v] *= corr;
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                bf16x8 pb;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    pb[v] = static_cast<__bf16>(sc[2 * half][v]);
+                    pb[4 + v] = static_cast<__bf16>(sc[2 * half + 1][v]);
+                }
+#pragma unroll
+                for (int t = 0; t < HD / 16; ++t) {
+                    const int dim = 16 * t + li, key0 = kbase + 32 * half + 4 * g;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0));
+                    const uint2 hi = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0 + 16));
+                    const uint4 raw = {lo.x, lo.y, hi.x, hi.y};
+                    o[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, raw), pb, o[i][t],
+                                                                       0, 0, 0);
+                }
+            }
+        };
+        static_assert(LMAX == 2 * kKeysPerChunk, "two key chunks");
+#pragma unroll
+        for (int i = 0; i < TQ; ++i) chunk(0, i);
+        if (L > kKeysPerChunk) {
+            chunk(kKeysPerChunk, 1);
+            chunk(kKeysPerChunk, 3);
         }
         // Normalised output, rounded to bf16 as the o_proj takes it, over this head's q columns.
 #pragma unroll
