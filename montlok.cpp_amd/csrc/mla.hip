@@ -150,6 +150,21 @@ __device__ __forceinline__ void load_row8(const float* row, int64_t col, int64_t
 __device__ __forceinline__ float xor_max(float x, int mask) { return fmaxf(x, __shfl_xor(x, mask)); }
 __device__ __forceinline__ float xor_sum(float x, int mask) { return x + __shfl_xor(x, mask); }
 
+// The value of lane l ^ 16 (l ^ 32) through the gfx950 row swaps, VALU
+// operations instead of an LDS permute: permlane16_swap(x, x) leaves rows
+// {0, 0, 2, 2} in its first result and {1, 1, 3, 3} in its second (a row is 16
+// lanes), permlane32_swap(x, x) halves {0, 0} and {1, 1}.
+__device__ __forceinline__ float lane_xor16(float x) {
+    const int b = __float_as_int(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    return __int_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+    const int b = __float_as_int(x);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    return __int_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 template <int HD, bool BF16, bool VEC>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p) {
     using E = AttnElem<BF16>;
@@ -968,14 +983,14 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const u16 en = AttnElem<true>::from(yn[v]);
-            const u16 er = rot(yr[v], __shfl_xor(yr[v], 32), c4[v], s4[v], first_half);
+            const u16 er = rot(yr[v], lane_xor32(yr[v]), c4[v], s4[v], first_half);
             qn[v] = live ? en : u16(0);
             qr[v] = live ? er : u16(0);
         }
         if (wave == 4) {  // the k_rope tile (wave is uniform: a scalar branch)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const u16 ek = rot(y3[v], __shfl_xor(y3[v], 32), c4[v], s4[v], first_half);
+                const u16 ek = rot(y3[v], lane_xor32(y3[v]), c4[v], s4[v], first_half);
                 kr[v] = live ? ek : u16(0);
             }
         }
@@ -1170,8 +1185,8 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
                     mx = fmaxf(mx, xv);
                 }
             }
-            mx = xor_max(mx, 16);
-            mx = xor_max(mx, 32);
+            mx = fmaxf(mx, lane_xor16(mx));
+            mx = fmaxf(mx, lane_xor32(mx));
             const float m_new = fmaxf(m_run[i], mx);
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
@@ -1222,8 +1237,8 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
 #pragma unroll
         for (int i = 0; i < TQ; ++i) {
             const int qi = 16 * qt[i] + li;
-            float l = xor_sum(l_run[i], 16);
-            l = xor_sum(l, 32);
+            float l = l_run[i] + lane_xor16(l_run[i]);
+            l = l + lane_xor32(l);
             if (qi >= L) continue;
             const float inv = 1.0f / l;
 #pragma unroll
