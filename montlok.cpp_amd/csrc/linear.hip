@@ -462,8 +462,13 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
     const int li = lane & 15;
     const int group = lane >> 4;
     const int64_t n_tiles = (p.N + 15) / 16;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x / n_tiles) * 16;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x % n_tiles) * 16;
+    // Tile order: consecutive blocks go to the 8 XCDs in turn, so XCD x takes the x-th eighth of the tiles
+    // (whole row tiles together): a row tile's x rows are fetched into one L2 for all its column tiles, and
+    // rows a producer kernel wrote from the same XCD (the Mamba mixer places windows this way) are L2 hits.
+    unsigned lin = blockIdx.x;
+    if (gridDim.x % 8 == 0) lin = (lin % 8) * (gridDim.x / 8) + lin / 8;
+    const int64_t row0 = static_cast<int64_t>(lin / n_tiles) * 16;
+    const int64_t n0 = static_cast<int64_t>(lin % n_tiles) * 16;
     const int64_t xr = row0 + li < p.rows ? row0 + li : p.rows - 1;
     const int64_t wr = n0 + li < p.N ? n0 + li : p.N - 1;
     const int K = static_cast<int>(p.K);
