@@ -154,14 +154,24 @@ __device__ __forceinline__ void store_f(float* dst, float v) {
     }
 }
 
-template <int D, bool FUSED, bool NTS>
-__global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
+// BC: the streams are a broadcast backbone (stream stride 0). The four
+// stream values of a lane are then one load (the same operations follow on
+// the same values, so the result is the general form's bit for bit), and the
+// partial tiles reuse the projection block's LDS after a barrier, so that at
+// d = 256 three blocks fit a CU (registers and LDS) instead of two.
+template <int D, bool FUSED, bool NTS, bool BC = false>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(BC ? 3 : 1)))
+void mhc_prepare_n4_kernel(PrepareArgs a) {
     constexpr int n = 4;
     constexpr int GW = D / 64;  // groups of 16 k per wave; group g covers k in [16g, 16g + 16)
+    static_assert(!(BC && FUSED), "the fused combine reads full streams");
     __shared__ __attribute__((aligned(16))) double w_lds[(2 * n + n * n) * (D + 2)];
-    __shared__ double part[4][2][4][64];
+    static_assert(!BC || 4 * 2 * 4 * 64 <= (2 * n + n * n) * (D + 2), "partial tiles inside the projection block");
+    __shared__ double part_own[BC ? 1 : 4 * 2 * 4 * 64];
+    double (*part)[2][4][64] = reinterpret_cast<double (*)[2][4][64]>(BC ? w_lds : part_own);
     __shared__ double part_sq[4][64];
-    __shared__ double agg_sq[4][64];
+    __shared__ double agg_sq_own[BC ? 1 : 4 * 64];
+    double (*agg_sq)[64] = reinterpret_cast<double (*)[64]>(BC ? &part_sq[0][0] : agg_sq_own);  // BC: after part_sq's reads
     __shared__ float pre_lds[16][4];
 
     const int wave = threadIdx.x / kWave;
@@ -198,8 +208,14 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
 #pragma unroll
     for (int j = 0; j < GW; ++j) {
         const int k0 = 16 * (wave * GW + j) + 4 * q;
+        if constexpr (BC) {
+            sv[j][0] = *reinterpret_cast<const float4*>(base + k0);
 #pragma unroll
-        for (int i = 0; i < n; ++i) sv[j][i] = *reinterpret_cast<const float4*>(base + i * a.sd + k0);
+            for (int i = 1; i < n; ++i) sv[j][i] = sv[j][0];
+        } else {
+#pragma unroll
+            for (int i = 0; i < n; ++i) sv[j][i] = *reinterpret_cast<const float4*>(base + i * a.sd + k0);
+        }
     }
     if constexpr (FUSED) {
         // The previous residual's write on this lane's k-slice of all n
@@ -321,6 +337,7 @@ __global__ __launch_bounds__(kBlock) void mhc_prepare_n4_kernel(PrepareArgs a) {
         gather_rows(sq, x);
         sq = ((x[0] + x[1]) + x[2]) + x[3];
     }
+    if constexpr (BC) __syncthreads();  // every wave is done with the projection block the tiles overwrite
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         part[wave][0][v][l] = acc0[v];
@@ -778,7 +795,14 @@ mlk_status launch_prepare(const PrepareArgs& a, int64_t n, int64_t d, hipStream_
         if (fused) {                                                                                              \
             MLK_PREP_NTS((DV <= 256 ? DV : 256), true)                                                            \
         } else {                                                                                                  \
-            hipLaunchKernelGGL((mhc_prepare_n4_kernel<DV, false, true>), dim3(blocks), dim3(kBlock), 0, stream, a); \
+            if (a.sd == 0 && (DV == 128 || DV == 256)) {                                                          \
+                hipLaunchKernelGGL((mhc_prepare_n4_kernel<DV, false, true, (DV == 128 || DV == 256)>),            \
+                                   dim3(blocks),                                                                  \
+                                   dim3(kBlock), 0, stream, a);                                                   \
+            } else {                                                                                              \
+                hipLaunchKernelGGL((mhc_prepare_n4_kernel<DV, false, true>), dim3(blocks), dim3(kBlock), 0,       \
+                                   stream, a);                                                                    \
+            }                                                                                                     \
         }                                                                                                         \
         break;
         switch (d) {

@@ -135,6 +135,28 @@ def test_mhc_combine_vs_oracle(dev, oracle, n, d):
     assert_bitwise(got, oracle.mhc_combine(expanded, res, post, out), "broadcast combine")
 
 
+@pytest.mark.parametrize("d,B,L,agg_norm", [(256, 4, 250, True), (256, 3, 17, False), (128, 5, 200, True),
+                                             (128, 2, 9, False), (64, 2, 40, True)])
+def test_broadcast_prepare_equals_materialised(dev, d, B, L, agg_norm):
+    """The prepare of a broadcast backbone ([B, L, d], stream stride 0: the form specialised to one stream
+    load per lane at d 128 and 256) equals the prepare of the materialised expand bit for bit, with and
+    without the output RMSNorm of agg."""
+    from montlok import _C
+
+    n = 4
+    rng = np.random.default_rng(d + B + L)
+    s, nw, pw, pb, qb, rb = _random_mhc(rng, B, L, n, d)
+    p = (_t(nw, dev), 1e-5, _t(pw, dev), _t(pb, dev), _t(qb, dev), _t(rb, dev),
+         *(torch.tensor(v, device=dev) for v in (0.7, 0.6, 0.8)), 20)
+    extra = (0, _t((rng.random(d) + 0.5).astype(np.float32), dev), 1e-6) if agg_norm else ()
+    backbone = _t(s[:, :, 0, :], dev)
+    got = _C.mhc_prepare(backbone, *p, n, *extra[1:]) if agg_norm else _C.mhc_prepare(backbone, *p, n)
+    dense_in = backbone.unsqueeze(-2).expand(-1, -1, n, -1).contiguous()
+    dense = _C.mhc_prepare(dense_in, *p, *extra) if agg_norm else _C.mhc_prepare(dense_in, *p)
+    for name, a, b in zip(("agg", "pre", "post", "res"), got, dense):
+        assert_bitwise(a, b.cpu().numpy(), f"broadcast {name} d{d} {B}x{L}")
+
+
 def test_mhc_combine_prepare_equals_separate_passes(dev):
     """The fused write+read equals combine then prepare bit for bit (montlok_selftest.cpp:606-677)."""
     from montlok import _C
