@@ -1128,8 +1128,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 float nx[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + kb + i, C - 1)];
-#pragma unroll 1
-                for (int k0 = 0; k0 < kFull; k0 += 8) {
+                auto batch = [&](int k0) {  // steps k0 .. k0 + 7, the next batch's alpha values read ahead
                     float al[8];
 #pragma unroll
                     for (int i = 0; i < 8; ++i) al[i] = nx[i];
@@ -1159,6 +1158,15 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                             w_s[(t < C ? t : C) * WP + colw] = wv[i];
                         }
                     }
+                };
+                // The split walk's two batches are straight-line code; the one-lane walk (32 steps) keeps
+                // a loop, whose registers the four-wave blocks cannot spare unrolled.
+                if constexpr (kSplit) {
+                    batch(0);
+                    batch(8);
+                } else {
+#pragma unroll 1
+                    for (int k0 = 0; k0 < kFull; k0 += 8) batch(k0);
                 }
             }
         }
