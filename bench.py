@@ -97,22 +97,42 @@ def cpu_baseline_mhc(cfg: dict, budget_s: float = 12.0) -> dict:
     return line
 
 
-def _graph(fn_list):
-    """Capture the given launch closures, in order, into one HIP graph."""
+def _graph(fn_list, prerun: bool = True):
+    """Capture the given launch closures, in order, into one HIP graph (after one eager run of them on a
+    side stream, unless `prerun` is false: every kernel they launch must then have run once already)."""
     import torch
 
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for fn in fn_list:
-            fn()
-    torch.cuda.current_stream().wait_stream(side)
+    if prerun:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for fn in fn_list:
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for fn in fn_list:
             fn()
     return g
+
+
+def _upload(g) -> None:
+    """hipGraphUpload of an instantiated graph on the current stream, so that its first replay launches the
+    prepared graph (kernel arguments and packets already set up on the device) rather than preparing it
+    inside the timed region. Runs none of the graph's work."""
+    import ctypes
+
+    import torch
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipGraphUpload.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipGraphUpload.restype = ctypes.c_int
+    rc = hip.hipGraphUpload(ctypes.c_void_p(g.raw_cuda_graph_exec()),
+                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    if rc != 0:
+        raise RuntimeError(f"hipGraphUpload failed with HIP error {rc}")
+    torch.cuda.synchronize()
 
 
 def _time_graph(g, replays: int) -> float:
@@ -133,9 +153,11 @@ def _time_graph(g, replays: int) -> float:
 def _gpu_steps(step_fns, steps: int, warmup: int, budget_s: float = 10.0) -> dict:
     """Times exactly `steps` steps; step i runs step_fns[i % len(step_fns)].
 
-    The warm-up runs `warmup` steps as replays of one-step graphs. The `steps` steps are then captured, in
-    order, into one HIP graph, and the timed region is one replay of it between two HIP events, synchronized
-    on both sides: no host work between the steps. ms_per_step is that region's time / steps. Further
+    The `steps` steps are captured, in order, into one HIP graph, and the `warmup` steps before them into
+    another (capture runs nothing; the caller has run every step function once). The warm-up is one replay
+    of the `warmup`-step graph, so the GPU runs the warm-up steps back to back and reaches its working clock,
+    right before the timed region: one replay of the `steps`-step graph between two HIP events, synchronized
+    on both sides, no host work between the steps. ms_per_step is that region's time / steps. Further
     replays of the same graph (30, or as many as fit in `budget_s`, at least 3) give the median and the
     spread of the per-step time."""
     import statistics
@@ -143,11 +165,13 @@ def _gpu_steps(step_fns, steps: int, warmup: int, budget_s: float = 10.0) -> dic
     import torch
 
     n = len(step_fns)
-    singles = [_graph([fn]) for fn in step_fns]
-    for i in range(warmup):
-        singles[i % n].replay()
+    g = _graph([step_fns[(warmup + i) % n] for i in range(steps)], prerun=False)
+    _upload(g)
+    if warmup > 0:
+        wg = _graph([step_fns[i % n] for i in range(warmup)], prerun=False)
+        _upload(wg)
+        wg.replay()
     torch.cuda.synchronize()
-    g = _graph([step_fns[i % n] for i in range(steps)])
     stream = torch.cuda.current_stream()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -1079,7 +1103,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="block", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
