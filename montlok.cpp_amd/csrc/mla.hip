@@ -33,6 +33,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16;
 
 // ------------------------------------------------------------------ rope
@@ -808,14 +810,16 @@ void mla_attend_kernel(MlaAttendArgs p) {
 //            latent tile w for w < 4 or the k_rope tile for w = 4) and runs
 //            them over the 8 row tiles: per (tile, row tile) the 8 k steps of
 //            linear_tiles_kernel's chain, so the columns equal the separate
-//            linear's bit for bit. Epilogue: q rounded to bf16 (its rope lanes
-//            rotated in fp64 first, the pair partner 32 lanes away), the
-//            latent kept in fp32, k_rope rotated.
+//            linear's bit for bit. Epilogue: q rounded to bf16 (its rope dims
+//            rotated in fp64 first; the rope tiles take their W rows in an
+//            order that puts each rotate_half pair in one lane), the latent
+//            kept in fp32, k_rope rotated.
 //   kv_norm  the LayerNorm of mla_attend_kernel (16 lanes per row, fp64),
 //            into bf16.
-//   heads    two at a time, four waves each: this head's kv_up rows, kv_up,
+//   heads    four at a time, two waves each: this head's kv_up rows, kv_up,
 //            k = cat(k_nope, rope(k_rope)), causal attention, all as
-//            mla_attend_kernel computes them; the normalised output rounded to
+//            mla_attend_kernel computes them (only the key tiles at or below
+//            each query tile's diagonal); the normalised output rounded to
 //            bf16 (the o_proj's operand) over the head's q columns.
 //   o_proj   wave w: output tiles 2w, 2w + 1, W fragments in registers, the
 //            attention output from LDS, the linear's chain again.
@@ -840,7 +844,7 @@ struct MlaWindowArgs {
 
 template <int H>
 __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
-    constexpr int HD = 32, NOPE = 16, ROPE = 16, KV = 64;  // rope pairs (i, i + 8): 32 lanes apart
+    constexpr int HD = 32, NOPE = 16, ROPE = 16, KV = 64;  // rope pairs (i, i + 8)
     constexpr int D = H * HD;
     constexpr int LMAX = 128, RT = LMAX / 16;
     constexpr int UPW = NOPE + HD;  // kv_up rows of one head
@@ -867,13 +871,13 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     const float* xw = p.x + b * p.x_bs;
     // element (row, col) of the swizzled [LMAX, D] tile
     auto sw = [](int row, int col) { return row * D + ((((col >> 3) ^ (row & 7))) << 3) + (col & 7); };
-    // rotate_half of one pair: x1 c - x2 s on the first half, x2 c + x1 s on the second (x the own value,
-    // the partner 32 lanes away), as rope_kernel: two fp64 products, their sum rounded to fp64, then to fp32.
-    // The product of two floats is exact in fp64, so round(own c + (+-m)) is one fma with the same result,
-    // and the sign of m a select.
-    auto rot = [](float own, float other, double c, double s, bool first) -> u16 {
-        const double m = __dmul_rn(static_cast<double>(other), s);
-        return AttnElem<true>::from(static_cast<float>(__fma_rn(static_cast<double>(own), c, first ? -m : m)));
+    // The rope tiles (q rope of each head, k_rope) take their W rows in the order rp(c): column 4g + v of
+    // the tile is rope dim 2g, 2g + 8, 2g + 1, 2g + 9 for v = 0..3, so the lane that holds a dim also
+    // holds its rotate_half partner (dim +- 8). Each output element still comes from its own W row and x
+    // row by the same chain of products, so the values are the linear's.
+    auto rp = [](int c) { return 2 * (c >> 2) + ((c >> 1) & 1) + 8 * (c & 1); };
+    auto pack2 = [](float a, float b) -> uint32_t {  // two bf16 (round to nearest even) in one word
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
     };
 
     // 1. Loads: x rows (rows past L read row L - 1 and are zeroed) and the W
@@ -890,6 +894,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         c8 = hf * (D / 2) + (u % (D / 16)) * 8;
     };
     const int tiles[3] = {2 * wave, 2 * wave + 1, 2 * H + (wave < 5 ? wave : 4)};
+    const int wrow[3] = {li, rp(li), wave < 4 ? li : rp(li)};  // W row of lane li in each tile
     uint4 wf[3][D / 32];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -905,7 +910,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         for (int t = 0; t < 3; ++t)
 #pragma unroll
             for (int s = hf * SH; s < (hf + 1) * SH; ++s)
-                wf[t][s] = *reinterpret_cast<const uint4*>(p.w_in + (16 * tiles[t] + li) * D + 32 * s + 8 * g);
+                wf[t][s] = *reinterpret_cast<const uint4*>(p.w_in + (16 * tiles[t] + wrow[t]) * D + 32 * s + 8 * g);
     }
     // cos/sin of every row into LDS as doubles, converted once for all heads (the upper half of the head
     // slots, free until the heads run; the fp32 latent takes the lower half): thread t takes 4 values of
@@ -962,48 +967,46 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     }
     __syncthreads();  // every wave is done with x
 
-    // 3. Epilogue: lane (g, li) of row tile m holds row 16 m + li, columns
-    // 4g .. 4g + 3 of each tile (+ 0.0f: the linear adds its zero bias).
-    const bool first_half = g < 2;  // rope indices 0..7 pair with 8..15, 32 lanes away
+    // 3. Epilogue: lane (g, li) of row tile m holds row 16 m + li, columns 4g .. 4g + 3 of each tile
+    // (rope dims 2g, 2g + 8, 2g + 1, 2g + 9 in the rope tiles): q rounded to bf16, its rope dims rotated
+    // first; the latent kept in fp32 (waves 0..3); k_rope rotated (waves 4..7 hold its tile; wave 4 + i
+    // takes row tiles i and i + 4). rotate_half as rope_kernel: x1 c - x2 s on dims d < 8, x2 c + x1 s on
+    // d + 8, two fp64 products and their sum rounded to fp64, then to fp32; the product of two floats is
+    // exact in fp64, so the sum is one fma with the same result. Two things the separate operators do are
+    // left out, as neither changes a stored output bit: the linear's zero bias, which only turns a -0
+    // into +0 (a zero's sign is lost in the sums, maxima and LayerNorm that follow), and the zeroing of
+    // rows past L (their x rows are zero; no stored query reads them as queries, and as keys they lie past
+    // every stored query's diagonal).
+    auto rope4 = [](const f32x4& y, const double2& ca, const double2& cb, const double2& sa, const double2& sb,
+                    float (&o)[4]) {
+        const double x0 = static_cast<double>(y[0]), x8 = static_cast<double>(y[1]);  // dims 2g, 2g + 8
+        const double x1 = static_cast<double>(y[2]), x9 = static_cast<double>(y[3]);  // dims 2g + 1, 2g + 9
+        o[0] = static_cast<float>(__fma_rn(x0, ca.x, -__dmul_rn(x8, sa.x)));
+        o[1] = static_cast<float>(__fma_rn(x8, cb.x, __dmul_rn(x0, sb.x)));
+        o[2] = static_cast<float>(__fma_rn(x1, ca.y, -__dmul_rn(x9, sa.y)));
+        o[3] = static_cast<float>(__fma_rn(x9, cb.y, __dmul_rn(x1, sb.y)));
+    };
 #pragma unroll
     for (int m = 0; m < RT; ++m) {
         const int row = 16 * m + li;
-        const bool live = row < L;
-        const f32x4 yn = acc[0][m] + f32x4{0.f, 0.f, 0.f, 0.f};
-        const f32x4 yr = acc[1][m] + f32x4{0.f, 0.f, 0.f, 0.f};
-        const f32x4 y3 = acc[2][m] + f32x4{0.f, 0.f, 0.f, 0.f};
-        const double2 c01 = *reinterpret_cast<const double2*>(cs_d + cs_at(row, 2 * g));
-        const double2 c23 = *reinterpret_cast<const double2*>(cs_d + cs_at(row, 2 * g + 1));
-        const double2 s01 = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, 2 * g));
-        const double2 s23 = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, 2 * g + 1));
-        const double c4[4] = {c01.x, c01.y, c23.x, c23.y};
-        const double s4[4] = {s01.x, s01.y, s23.x, s23.y};
-
-        u16 qn[4], qr[4], kr[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const u16 en = AttnElem<true>::from(yn[v]);
-            const u16 er = rot(yr[v], lane_xor32(yr[v]), c4[v], s4[v], first_half);
-            qn[v] = live ? en : u16(0);
-            qr[v] = live ? er : u16(0);
-        }
-        if (wave == 4) {  // the k_rope tile (wave is uniform: a scalar branch)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const u16 ek = rot(y3[v], lane_xor32(y3[v]), c4[v], s4[v], first_half);
-                kr[v] = live ? ek : u16(0);
-            }
-        }
-        auto pack = [](const u16 (&e)[4]) {
-            return make_uint2(static_cast<uint32_t>(e[0]) | (static_cast<uint32_t>(e[1]) << 16),
-                              static_cast<uint32_t>(e[2]) | (static_cast<uint32_t>(e[3]) << 16));
-        };
-        *reinterpret_cast<uint2*>(xq_s + sw(row, HD * wave + 4 * g)) = pack(qn);
-        *reinterpret_cast<uint2*>(xq_s + sw(row, HD * wave + NOPE + 4 * g)) = pack(qr);
+        const f32x4 yn = acc[0][m], yr = acc[1][m], y3 = acc[2][m];
+        const double2 ca = *reinterpret_cast<const double2*>(cs_d + cs_at(row, g));      // cos, dims 2g, 2g + 1
+        const double2 cb = *reinterpret_cast<const double2*>(cs_d + cs_at(row, g + 4));  // dims 2g + 8, 2g + 9
+        const double2 sa = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, g));
+        const double2 sb = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, g + 4));
+        float qr[4];
+        rope4(yr, ca, cb, sa, sb, qr);
+        const int q0 = HD * wave;
+        *reinterpret_cast<uint2*>(xq_s + sw(row, q0 + 4 * g)) = make_uint2(pack2(yn[0], yn[1]), pack2(yn[2], yn[3]));
+        *reinterpret_cast<uint32_t*>(xq_s + sw(row, q0 + NOPE + 2 * g)) = pack2(qr[0], qr[2]);
+        *reinterpret_cast<uint32_t*>(xq_s + sw(row, q0 + NOPE + 2 * g + 8)) = pack2(qr[1], qr[3]);
         if (wave < 4) {
             *reinterpret_cast<f32x4*>(lat_f + lat_at(row, 4 * wave + g)) = y3;
-        } else if (wave == 4) {
-            *reinterpret_cast<uint2*>(kr_s + row * ROPE + 4 * g) = pack(kr);
+        } else if ((m & 3) == wave - 4) {  // uniform per wave: a scalar branch
+            float kr[4];
+            rope4(y3, ca, cb, sa, sb, kr);
+            *reinterpret_cast<uint32_t*>(kr_s + row * ROPE + 2 * g) = pack2(kr[0], kr[2]);
+            *reinterpret_cast<uint32_t*>(kr_s + row * ROPE + 2 * g + 8) = pack2(kr[1], kr[3]);
         }
     }
     __syncthreads();
@@ -1113,21 +1116,21 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
 #pragma unroll
             for (int ks = 0; ks < KV / 32; ++ks)
                 la[ks] = *reinterpret_cast<const bf16x8*>(lat_s + (16 * rt + li) * LP + 32 * ks + 8 * g);
+            // k_nope is formed transposed (W_up rows as the A operand), so that each lane holds four
+            // consecutive dims of one key; v as keys x dims, four consecutive keys of one dim: either way
+            // one 8-byte store per lane. The products and their order over k are the same either way.
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
                 f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < KV / 32; ++ks)
-                    a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(la[ks], __builtin_bit_cast(bf16x8, wu[ct][ks]), a, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int row = 16 * rt + 4 * g + v;
-                    const u16 e = AttnElem<true>::from(a[v]);
-                    if (ct == 0) {
-                        k_s[k_at(row, li)] = e;
-                    } else {
-                        vt_s[v_at(16 * (ct - 1) + li, row)] = e;
-                    }
+                    a = ct == 0 ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wu[ct][ks]), la[ks], a, 0, 0, 0)
+                                : __builtin_amdgcn_mfma_f32_16x16x32_bf16(la[ks], __builtin_bit_cast(bf16x8, wu[ct][ks]), a, 0, 0, 0);
+                const uint2 e = make_uint2(pack2(a[0], a[1]), pack2(a[2], a[3]));
+                if (ct == 0) {
+                    *reinterpret_cast<uint2*>(k_s + k_at(16 * rt + li, 4 * g)) = e;  // key 16 rt + li, dims 4g ..
+                } else {
+                    *reinterpret_cast<uint2*>(vt_s + v_at(16 * (ct - 1) + li, 16 * rt + 4 * g)) = e;  // keys 16 rt + 4g ..
                 }
             }
         }
@@ -1147,109 +1150,129 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
                 for (int s = 0; s < D / 32; ++s)
                     wo[t][s] = *reinterpret_cast<const uint4*>(p.w_out + (16 * (2 * wave + t) + li) * D + 32 * s + 8 * g);
         }
-        // Causal attention (top-left) of head h: query tiles (wg, 7 - wg) and (wg + 2, 5 - wg). With L <= 128
-        // the key chunks are known: chunk 0 (keys 0..63) for all four tiles, chunk 1 (keys 64..127, when
-        // L > 64) for tiles 7 - wg and 5 - wg only (the other two end below key 64). Each chunk's tiles run
-        // as straight-line code, so their dependent chains interleave; a tile past L computes and is not
-        // stored. Every step is attn_kernel's (mask, running max, exp2, rescale, P in bf16).
-        constexpr int TQ = 4;
-        const int qt[TQ] = {wg, 7 - wg, wg + 2, 5 - wg};
-        bf16x8 qb[TQ];
-        float m_run[TQ], l_run[TQ];
-        f32x4 o[TQ][HD / 16];
+        // Causal attention (top-left) of head h: query tiles (wg, 7 - wg, wg + 2, 5 - wg), 16 rows each,
+        // against key chunk 0 (keys 0..63) and, for the tiles past row 63 when L > 64, chunk 1 (keys
+        // 64..127). The wave's tiles are compile-time, so each (chunk, tile) pair runs only the 16-key tiles
+        // at or below its diagonal, masks only the diagonal one, and the four tiles' chunk-0 chains are
+        // straight-line code that interleaves. A key tile above the diagonal is all -inf in attn_kernel's
+        // softmax: it adds nothing to the max, +0 to the sum and zero weights to P, so leaving it out
+        // gives the same bits. Keys past L need no mask of their own: a query row below L sees keys up
+        // to itself only, and rows past L are computed but not stored. The first chunk of a tile starts
+        // from m = -inf, l = 0, o = 0, where attn_kernel's rescale multiplies zeros by zero. Every other
+        // step is attn_kernel's (running max, exp2, rescale, P in bf16).
+        auto attend = [&](auto wg_c) {
+            constexpr int WG = decltype(wg_c)::value;
+            constexpr int TQ = 4;
+            constexpr int QT[TQ] = {WG, 7 - WG, WG + 2, 5 - WG};
+            bf16x8 qb[TQ];
+            float m_run[TQ], l_run[TQ];
+            f32x4 o[TQ][HD / 16];
 #pragma unroll
-        for (int i = 0; i < TQ; ++i) {
-            qb[i] = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * qt[i] + li, HD * h + 8 * g));
-            m_run[i] = -INFINITY;
-            l_run[i] = 0.0f;
+            for (int i = 0; i < TQ; ++i) {
+                qb[i] = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * QT[i] + li, HD * h + 8 * g));
 #pragma unroll
-            for (int t = 0; t < HD / 16; ++t) o[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-        auto chunk = [&](int kbase, int i) {
-            const int q0 = 16 * qt[i];
-            f32x4 sc[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_s + k_at(kbase + 16 * t + li, 8 * g));
-                sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[i], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                for (int t = 0; t < HD / 16; ++t) o[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
-            const int qpos = q0 + li;
-            float mx = -INFINITY;
+            auto chunk = [&](auto kc_c, auto i_c) {
+                constexpr int KC = decltype(kc_c)::value, I = decltype(i_c)::value;
+                constexpr int DIAG = QT[I] - 4 * KC;              // the diagonal key tile (none when >= 4)
+                constexpr int NKT = DIAG + 1 < 4 ? DIAG + 1 : 4;  // key tiles at or below the diagonal
+                constexpr bool FIRST = KC == 0;
+                static_assert(NKT >= 1, "a chunk with no key at or below the diagonal is not run");
+                const int kbase = kKeysPerChunk * KC;
+                f32x4 sc[NKT];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int key = kbase + 16 * t + 4 * g + v;
-                    const float xv = (key < L && key <= qpos) ? sc[t][v] * p.scale_log2 : -INFINITY;
-                    sc[t][v] = xv;
-                    mx = fmaxf(mx, xv);
+                for (int t = 0; t < NKT; ++t) {
+                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(k_s + k_at(kbase + 16 * t + li, 8 * g));
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[I], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 }
-            }
-            mx = fmaxf(mx, lane_xor16(mx));
-            mx = fmaxf(mx, lane_xor32(mx));
-            const float m_new = fmaxf(m_run[i], mx);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
-            m_run[i] = m_new;
-            float psum = 0.0f;
+                float mx = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+                for (int t = 0; t < NKT; ++t) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
-                    sc[t][v] = e;
-                    psum += e;
+                    for (int v = 0; v < 4; ++v) {
+                        float xv = sc[t][v] * p.scale_log2;
+                        if (t == DIAG) xv = 4 * g + v <= li ? xv : -INFINITY;  // key 16 t + 4g + v <= query li
+                        sc[t][v] = xv;
+                        mx = fmaxf(mx, xv);
+                    }
                 }
-            }
-            l_run[i] = l_run[i] * corr + psum;
+                mx = fmaxf(mx, lane_xor16(mx));
+                mx = fmaxf(mx, lane_xor32(mx));
+                const float m_new = FIRST ? mx : fmaxf(m_run[I], mx);
+                const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+                float corr = 0.0f;
+                if constexpr (!FIRST) corr = __builtin_amdgcn_exp2f(m_run[I] - m_use);
+                m_run[I] = m_new;
+                float psum = 0.0f;
 #pragma unroll
-            for (int t = 0; t < HD / 16; ++t) {
+                for (int t = 0; t < NKT; ++t) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) o[i][t][v] *= corr;
-            }
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                bf16x8 pb;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    pb[v] = static_cast<__bf16>(sc[2 * half][v]);
-                    pb[4 + v] = static_cast<__bf16>(sc[2 * half + 1][v]);
+                    for (int v = 0; v < 4; ++v) {
+                        const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
+                        sc[t][v] = e;
+                        psum += e;
+                    }
                 }
+                if constexpr (FIRST) {
+                    l_run[I] = psum;
+                } else {
+                    l_run[I] = l_run[I] * corr + psum;
+#pragma unroll
+                    for (int t = 0; t < HD / 16; ++t) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) o[I][t][v] *= corr;
+                    }
+                }
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    if (2 * half >= NKT) continue;  // P is zero over both key tiles (known at compile time)
+                    const int ta = 2 * half, tb = 2 * half + 1 < NKT ? 2 * half + 1 : ta;
+                    const uint2 pa = make_uint2(pack2(sc[ta][0], sc[ta][1]), pack2(sc[ta][2], sc[ta][3]));
+                    const uint2 pz = 2 * half + 1 < NKT ? make_uint2(pack2(sc[tb][0], sc[tb][1]), pack2(sc[tb][2], sc[tb][3]))
+                                                        : make_uint2(0u, 0u);
+                    const bf16x8 pb = __builtin_bit_cast(bf16x8, uint4{pa.x, pa.y, pz.x, pz.y});
+#pragma unroll
+                    for (int t = 0; t < HD / 16; ++t) {
+                        const int dim = 16 * t + li, key0 = kbase + 32 * half + 4 * g;
+                        const uint2 lo = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0));
+                        const uint2 hi = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0 + 16));
+                        const uint4 raw = {lo.x, lo.y, hi.x, hi.y};
+                        o[I][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, raw), pb, o[I][t],
+                                                                           0, 0, 0);
+                    }
+                }
+            };
+            static_assert(LMAX == 2 * kKeysPerChunk, "two key chunks");
+            using C0 = std::integral_constant<int, 0>;
+            using C1 = std::integral_constant<int, 1>;
+            chunk(C0{}, C0{});
+            chunk(C0{}, C1{});
+            chunk(C0{}, std::integral_constant<int, 2>{});
+            chunk(C0{}, std::integral_constant<int, 3>{});
+            if (L > kKeysPerChunk) {  // tiles 7 - wg and 5 - wg reach past key 63
+                chunk(C1{}, C1{});
+                chunk(C1{}, std::integral_constant<int, 3>{});
+            }
+            // Normalised output, rounded to bf16 as the o_proj takes it, over this head's q columns.
+#pragma unroll
+            for (int i = 0; i < TQ; ++i) {
+                const int qi = 16 * QT[i] + li;
+                float l = l_run[i] + lane_xor16(l_run[i]);
+                l = l + lane_xor32(l);
+                if (qi >= L) continue;
+                const float inv = 1.0f / l;
 #pragma unroll
                 for (int t = 0; t < HD / 16; ++t) {
-                    const int dim = 16 * t + li, key0 = kbase + 32 * half + 4 * g;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0));
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vt_s + v_at(dim, key0 + 16));
-                    const uint4 raw = {lo.x, lo.y, hi.x, hi.y};
-                    o[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, raw), pb, o[i][t],
-                                                                       0, 0, 0);
+                    *reinterpret_cast<uint2*>(xq_s + sw(qi, HD * h + 16 * t + 4 * g)) =
+                        make_uint2(pack2(o[i][t][0] * inv, o[i][t][1] * inv), pack2(o[i][t][2] * inv, o[i][t][3] * inv));
                 }
             }
         };
-        static_assert(LMAX == 2 * kKeysPerChunk, "two key chunks");
-#pragma unroll
-        for (int i = 0; i < TQ; ++i) chunk(0, i);
-        if (L > kKeysPerChunk) {
-            chunk(kKeysPerChunk, 1);
-            chunk(kKeysPerChunk, 3);
-        }
-        // Normalised output, rounded to bf16 as the o_proj takes it, over this head's q columns.
-#pragma unroll
-        for (int i = 0; i < TQ; ++i) {
-            const int qi = 16 * qt[i] + li;
-            float l = l_run[i] + lane_xor16(l_run[i]);
-            l = l + lane_xor32(l);
-            if (qi >= L) continue;
-            const float inv = 1.0f / l;
-#pragma unroll
-            for (int t = 0; t < HD / 16; ++t) {
-                u16 e[4];
-#pragma unroll
-                for (int v = 0; v < 4; ++v) e[v] = AttnElem<true>::from(o[i][t][v] * inv);
-                *reinterpret_cast<uint2*>(xq_s + sw(qi, HD * h + 16 * t + 4 * g)) =
-                    make_uint2(static_cast<uint32_t>(e[0]) | (static_cast<uint32_t>(e[1]) << 16),
-                               static_cast<uint32_t>(e[2]) | (static_cast<uint32_t>(e[3]) << 16));
-            }
+        if (wg == 0) {
+            attend(std::integral_constant<int, 0>{});
+        } else {
+            attend(std::integral_constant<int, 1>{});
         }
         __syncthreads();
     }
