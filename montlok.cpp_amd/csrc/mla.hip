@@ -1010,17 +1010,21 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         }
     }
     __syncthreads();
-    const int lr = tid >> 4, lc = tid & 15;
-    const float4 lnw = *reinterpret_cast<const float4*>(p.ln_w + 4 * lc);
+    // LayerNorm operands: four lanes per row, lane q = lane % 4 holding the row's four-column groups q,
+    // q + 4, q + 8, q + 12; wave w takes rows 16 w .. 16 w + 15.
+    const int lq = lane & 3, lrow = 16 * wave + (lane >> 2);
     // A missing bias reads the weight and masks it to +0.0 bit-wise: a select here would become a branch
     // around the load, and the branch a wait for every load in flight.
     const bool has_b = p.ln_b != nullptr;
-    const float4 lnb_raw = *reinterpret_cast<const float4*>((has_b ? p.ln_b : p.ln_w) + 4 * lc);
     const uint32_t bmask = has_b ? 0xffffffffu : 0u;
-    const float4 lnb = make_float4(__uint_as_float(__float_as_uint(lnb_raw.x) & bmask),
-                                   __uint_as_float(__float_as_uint(lnb_raw.y) & bmask),
-                                   __uint_as_float(__float_as_uint(lnb_raw.z) & bmask),
-                                   __uint_as_float(__float_as_uint(lnb_raw.w) & bmask));
+    float4 lnw[4], lnb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        lnw[i] = *reinterpret_cast<const float4*>(p.ln_w + 4 * (lq + 4 * i));
+        const float4 r = *reinterpret_cast<const float4*>((has_b ? p.ln_b : p.ln_w) + 4 * (lq + 4 * i));
+        lnb[i] = make_float4(__uint_as_float(__float_as_uint(r.x) & bmask), __uint_as_float(__float_as_uint(r.y) & bmask),
+                             __uint_as_float(__float_as_uint(r.z) & bmask), __uint_as_float(__float_as_uint(r.w) & bmask));
+    }
     const int grp = wave >> 1;  // head group: heads grp, grp + HG
     const int wg = wave & 1;
     // The kv_up B fragments of the group's first head (lane (g, li): W_up row 16 ct + li, k = 32 ks + 8g ..),
@@ -1033,55 +1037,46 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         for (int ks = 0; ks < KV / 32; ++ks)
             wu[ct][ks] = *reinterpret_cast<const uint4*>(p.w_up + (grp * UPW + 16 * ct + li) * KV + 32 * ks + 8 * g);
 
-    // 4. kv_norm: LayerNorm of the latent rows into bf16, the arithmetic of
-    // mla_attend_kernel's (16 lanes per row, 4 columns each, fp64 sums).
+    // 4. kv_norm: LayerNorm of the latent rows into bf16 with mla_attend_kernel's arithmetic: per group of
+    // four columns (a + b) + (c + d) in fp64, the row's 16 groups combined by the butterfly xor 8, 4, 2, 1
+    // over the groups. Lane q holds groups q, q + 4, q + 8, q + 12, so the xor-8 and xor-4 levels pair
+    // groups inside the lane (each added in the butterfly's order, the own group first) and xor 2, xor 1
+    // are exchanges inside the quad: every sum is formed exactly as the 16-lane form forms it.
     {
-        constexpr int PASSES = LMAX / 32;
         const double inv_dim = 1.0 / static_cast<double>(KV);
-        float4 xs[PASSES];
-        double mean[PASSES], sumsq[PASSES];
+        float4 xv[4];
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            xs[ps] = *reinterpret_cast<const float4*>(lat_f + lat_at(32 * ps + lr, lc));
-            const float4 x = xs[ps];
-            mean[ps] = (static_cast<double>(x.x) + static_cast<double>(x.y)) +
-                       (static_cast<double>(x.z) + static_cast<double>(x.w));
-        }
-        auto row_sums = [](double (&v)[PASSES]) {
-#pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<8>(v[ps]);
-#pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<4>(v[ps]);
-#pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<2>(v[ps]);
-#pragma unroll
-            for (int ps = 0; ps < PASSES; ++ps) v[ps] += xor_row_d<1>(v[ps]);
+        for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const float4*>(lat_f + lat_at(lrow, lq + 4 * i));
+        auto row_sum = [](const double (&sg)[4]) {  // sg[i]: the sum of group lq + 4 i
+            double u = (sg[0] + sg[2]) + (sg[1] + sg[3]);  // xor 8 (q with q + 8, q + 4 with q + 12), then xor 4
+            u += xor_row_d<2>(u);
+            u += xor_row_d<1>(u);
+            return u;
         };
-        row_sums(mean);
+        double sg[4];
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            const float4 x = xs[ps];
-            mean[ps] *= inv_dim;
-            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
-            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
-            sumsq[ps] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+        for (int i = 0; i < 4; ++i)
+            sg[i] = (static_cast<double>(xv[i].x) + static_cast<double>(xv[i].y)) +
+                    (static_cast<double>(xv[i].z) + static_cast<double>(xv[i].w));
+        const double mean = row_sum(sg) * inv_dim;
+        double ac[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ac[i][0] = static_cast<double>(xv[i].x) - mean;
+            ac[i][1] = static_cast<double>(xv[i].y) - mean;
+            ac[i][2] = static_cast<double>(xv[i].z) - mean;
+            ac[i][3] = static_cast<double>(xv[i].w) - mean;
+            sg[i] = (ac[i][0] * ac[i][0] + ac[i][1] * ac[i][1]) + (ac[i][2] * ac[i][2] + ac[i][3] * ac[i][3]);
         }
-        row_sums(sumsq);
+        const double rstd = 1.0 / sqrt(fma(row_sum(sg), inv_dim, p.ln_eps));
+        const uint32_t live = lrow < L ? 0xffffffffu : 0u;
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            const int row = 32 * ps + lr;
-            const float4 x = xs[ps];
-            const double a0 = static_cast<double>(x.x) - mean[ps], a1 = static_cast<double>(x.y) - mean[ps];
-            const double a2 = static_cast<double>(x.z) - mean[ps], a3 = static_cast<double>(x.w) - mean[ps];
-            const double rstd = 1.0 / sqrt(fma(sumsq[ps], inv_dim, p.ln_eps));
-            const bool active = row < L;
-            const u16 o0 = active ? AttnElem<true>::from(static_cast<float>((a0 * rstd) * lnw.x + static_cast<double>(lnb.x))) : u16(0);
-            const u16 o1 = active ? AttnElem<true>::from(static_cast<float>((a1 * rstd) * lnw.y + static_cast<double>(lnb.y))) : u16(0);
-            const u16 o2 = active ? AttnElem<true>::from(static_cast<float>((a2 * rstd) * lnw.z + static_cast<double>(lnb.z))) : u16(0);
-            const u16 o3 = active ? AttnElem<true>::from(static_cast<float>((a3 * rstd) * lnw.w + static_cast<double>(lnb.w))) : u16(0);
-            *reinterpret_cast<uint2*>(lat_s + row * LP + 4 * lc) =
-                make_uint2(static_cast<uint32_t>(o0) | (static_cast<uint32_t>(o1) << 16),
-                           static_cast<uint32_t>(o2) | (static_cast<uint32_t>(o3) << 16));
+        for (int i = 0; i < 4; ++i) {
+            const float o0 = static_cast<float>((ac[i][0] * rstd) * lnw[i].x + static_cast<double>(lnb[i].x));
+            const float o1 = static_cast<float>((ac[i][1] * rstd) * lnw[i].y + static_cast<double>(lnb[i].y));
+            const float o2 = static_cast<float>((ac[i][2] * rstd) * lnw[i].z + static_cast<double>(lnb[i].z));
+            const float o3 = static_cast<float>((ac[i][3] * rstd) * lnw[i].w + static_cast<double>(lnb[i].w));
+            *reinterpret_cast<uint2*>(lat_s + lrow * LP + 4 * (lq + 4 * i)) = make_uint2(pack2(o0, o1) & live, pack2(o2, o3) & live);
         }
     }
     __syncthreads();  // the fp32 latent is dead: the head slots take its place
