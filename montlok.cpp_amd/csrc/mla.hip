@@ -1272,24 +1272,40 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         __syncthreads();
     }
 
-    // 6. o_proj: wave w computes output columns 32 w .. 32 w + 31 of every row.
+    // 6. o_proj: wave w computes output columns 32 w .. 32 w + 31 of every row, two row tiles at a time:
+    // their 16 attention fragments are read first, then the four accumulation chains (two row tiles x two
+    // column tiles, each the linear's chain over the 8 k steps) run interleaved.
     float* orow0 = p.out + b * static_cast<int64_t>(L) * D;
 #pragma unroll
-    for (int m = 0; m < RT; ++m) {
-        f32x4 y[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    for (int m = 0; m < RT; m += 2) {
+        bf16x8 af[2][D / 32];
 #pragma unroll
-        for (int s = 0; s < D / 32; ++s) {
-            const bf16x8 af = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * m + li, 32 * s + 8 * g));
+        for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-                y[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wo[t][s]), af, y[t], 0, 0, 0);
-        }
-        const int row = 16 * m + li;
-        if (row < L) {
+            for (int s = 0; s < D / 32; ++s)
+                af[mm][s] = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * (m + mm) + li, 32 * s + 8 * g));
+        f32x4 y[2][2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                *reinterpret_cast<f32x4*>(orow0 + row * D + HD * wave + 16 * t + 4 * g) =
-                    y[t] + f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) y[mm][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    y[mm][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wo[t][s]), af[mm][s],
+                                                                       y[mm][t], 0, 0, 0);
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+            const int row = 16 * (m + mm) + li;
+            if (row < L) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    *reinterpret_cast<f32x4*>(orow0 + row * D + HD * wave + 16 * t + 4 * g) =
+                        y[mm][t] + f32x4{0.f, 0.f, 0.f, 0.f};
+                }
             }
         }
     }
