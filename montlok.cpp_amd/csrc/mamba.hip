@@ -828,6 +828,124 @@ __global__ __launch_bounds__(64) void rec_chunk_kernel(RecArgs a) {
 // prep -> rotate -> rec_chunk_kernel sequence bit for bit; q and k never leave
 // LDS. Blocks are ordered so that the heads of one window run on one XCD and
 // share its L2 copy of the window's B/C rows.
+// The step coefficients of token ct < C of a chunk (one lane per token):
+// dt = softplus(dt logit + bias), A = -max(heavy_tail(A logit), floor), then
+// (alpha, beta, gamma) by step_coefficients (zero for tokens past Lc) and dt.
+template <int C>
+__device__ __forceinline__ void token_coefficients(int ct, float dt_logit, float a_logit, float trap_logit,
+                                                   float dt_bias, float a_floor, int Lc, float (&coef)[4][C]) {
+    const float dt = softplus_f(dt_logit + dt_bias);
+    const float am = -fmaxf(heavy_tail_f(a_logit), a_floor);
+    float al, be, ga;
+    step_coefficients(am * dt, dt, trap_logit, &al, &be, &ga);
+    const bool valid = ct < Lc;
+    coef[0][ct] = valid ? al : 0.0f;
+    coef[1][ct] = valid ? be : 0.0f;
+    coef[2][ct] = valid ? ga : 0.0f;
+    coef[3][ct] = dt;
+}
+
+// The decay weights of one chunk into w_s (rows of C + 4; column C holds
+// Din, C + 1 Wp; row C is a sink), walked by lane ct (0 .. 63) of one wave
+// that sees the chunk's coefficients. Lane s < C walks t = s + 1, s + 2, ...
+// (lanes drop out past the chunk end), carrying the products
+// prod_{s<r<=t} alpha_r and prod_{s+1<r<=t} alpha_r in fp64; its alpha values
+// are read 8 steps ahead. W[t][s] for t < s is never read (the G tiles mask
+// it). Lanes C and C + 1 write Din(t) = a_0 prod_{0<r<=t} a_r and
+// Wp(t) = b_0 prod_{0<r<=t} a_r as the weights of a column s = 0 with
+// gamma = a_0 (b_0) and no beta term (b_0 = 0 in the first chunk).
+template <int C, bool kSplit>
+__device__ __forceinline__ void decay_walk(int ct, bool first, const float (&coef)[4][C], float* w_s) {
+    constexpr int WP = C + 4, kDin = C, kWp = C + 1;
+    // Walkers: columns s < C, then Din (column kDin) and Wp (kWp), both
+    // with s = 0. Lane w < C + 2 walks t = s + 1 .. s + 16 of walker
+    // w; a walk longer than 16 steps (s < C - 17, and Din, Wp) has a
+    // second lane, C + 2 + j, for t = s + 17 .. C - 1. That lane first
+    // runs 16 multiply-only steps to form the same sequential
+    // products the first lane holds at t = s + 16, so every weight is
+    // bit-identical to one lane walking the whole column, while the
+    // wave issues 16 full steps instead of 31. Four-wave blocks keep
+    // one lane per walker (32 full steps): the split's registers cost
+    // them more than the shorter walk saves.
+    constexpr int kFull = kSplit ? 16 : 32;  // full steps per lane (whole batches of 8)
+    constexpr int kLong = C - 17;  // columns whose walk exceeds 16 steps
+    static_assert(C + 2 + kLong + 2 <= 64, "the walkers' lanes must fit one wave");
+    const int hf = kSplit && ct >= C + 2 ? 1 : 0;
+    const int j2 = ct - (C + 2);
+    const int wl = hf == 0 ? ct : (j2 < kLong ? j2 : C + (j2 - kLong));
+    if (ct >= 0 && (hf == 0 ? ct < C + 2 : j2 < kLong + 2)) {
+        const int s = wl < C ? wl : 0;
+        const double b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
+        const double gam = wl < C ? static_cast<double>(coef[2][s]) : (wl == C ? static_cast<double>(coef[0][0]) : b0);
+        const double bet = wl + 1 < C ? static_cast<double>(coef[1][wl + 1]) : 0.0;
+        const int colw = wl < C ? wl : (wl == C ? kDin : kWp);
+        if (hf == 0) w_s[s * WP + colw] = static_cast<float>(gam * 1.0);  // t = s
+        // Step k handles t = s + 1 + k with alpha from a clamped slot;
+        // steps with t >= C store into the sink row C, so no step is
+        // predicated.
+        double dd = 1.0, e = 1.0;
+        if constexpr (kSplit) {
+            float al[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) al[k] = coef[0][min(s + 1 + k, C - 1)];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const double at = al[k];
+                dd *= at;
+                if (k > 0) e *= at;
+            }
+        }
+        if (hf == 0) {  // (the first lane walks from t = s + 1)
+            dd = 1.0;
+            e = 1.0;
+        }
+        const int kb = 16 * hf;
+        float nx[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + kb + i, C - 1)];
+        auto batch = [&](int k0) {  // steps k0 .. k0 + 7, the next batch's alpha values read ahead
+            float al[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) al[i] = nx[i];
+            if (k0 + 8 < kFull) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + kb + k0 + 8 + i, C - 1)];
+            }
+            // Each group of 4 steps runs the two product chains first,
+            // then the 4 independent weights, then the 4 stores.
+#pragma unroll
+            for (int i0 = 0; i0 < 8; i0 += 4) {
+                double ddv[4], ev[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const double at = al[i0 + i];
+                    dd *= at;
+                    if (kb + k0 + i0 + i > 0) e *= at;
+                    ddv[i] = dd;
+                    ev[i] = e;
+                }
+                float wv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wv[i] = static_cast<float>(fma(bet, ev[i], gam * ddv[i]));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = s + 1 + kb + k0 + i0 + i;
+                    w_s[(t < C ? t : C) * WP + colw] = wv[i];
+                }
+            }
+        };
+        // The split walk's two batches are straight-line code; the one-lane walk (32 steps) keeps
+        // a loop, whose registers the four-wave blocks cannot spare unrolled.
+        if constexpr (kSplit) {
+            batch(0);
+            batch(8);
+        } else {
+#pragma unroll 1
+            for (int k0 = 0; k0 < kFull; k0 += 8) batch(k0);
+        }
+    }
+}
+
 struct ScanArgs {
     const float* proj;  // [B, L, W] rows: [z | x | B | C | dt | A | trap | angles]
     int64_t sb, st;
@@ -878,11 +996,18 @@ struct NoChunkHooks {
 // given) likewise for the outputs: a.out [B, L, d_inner], or the current
 // chunk's rows at a.out + (t - c0) d_inner.
 // Every thread of the block runs the same sequence of barriers, so several
-// heads can share a block.
-template <int C, int NT, int DT, bool TILE, class Hooks, bool TILE_OUT = TILE>
+// heads can share a block. PREP (TILE, one chunk, two waves): other waves of
+// the block have already formed the chunk's coefficients and tanh(angle) * pi
+// (before the barrier that ends hooks.before) and its decay weights (before
+// the barrier that ends step b): step a skips the dt/A/trap and angle columns,
+// steps a and b run without a barrier between them (the norm scales read the
+// B/C rows where hooks.before left them), and both waves form their gates in
+// step b.
+template <int C, int NT, int DT, bool TILE, class Hooks, bool TILE_OUT = TILE, bool PREP = false>
 __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>& sh, int64_t b, int64_t h,
                                           int tid_base, const Hooks& hooks) {
     static_assert(C == 32, "the BCNorm step takes one lane per (token, B|C) pair of a 64-lane wave");
+    static_assert(!PREP || (TILE && DT == 2), "PREP: the tiled two-wave scan");
     constexpr int N = 16 * NT, D = 16 * DT, NTH = 64 * DT;
     constexpr int CT = C / 16;
     constexpr int NP = N + 4, WP = C + 4;
@@ -1005,11 +1130,12 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
             }
 #pragma unroll
             for (int j = 0; j < MU; ++j) {
+                if constexpr (PREP) break;
                 const int u = tid + NTH * j;
                 const int which = u < 3 * C ? u / C : 0, t = u % C;
                 mx[j] = mc[static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + which * static_cast<int>(H))];
             }
-            if (R > 0) {
+            if (!PREP && R > 0) {
 #pragma unroll
                 for (int j = 0; j < AU; ++j) {
                     const unsigned u = static_cast<unsigned>(tid + NTH * j);
@@ -1035,10 +1161,11 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
             }
 #pragma unroll
             for (int j = 0; j < MU; ++j) {
+                if constexpr (PREP) break;
                 const int u = tid + NTH * j;
                 if (u < 3 * C) raw_s[u / C][u % C] = mx[j];
             }
-            if (R > 0) {
+            if (!PREP && R > 0) {
 #pragma unroll
                 for (int j = 0; j < AU; ++j) {
                     const unsigned u = static_cast<unsigned>(tid + NTH * j);
@@ -1047,130 +1174,33 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 }
             }
         }
-        __syncthreads();
+        if constexpr (!PREP) __syncthreads();
         // b. Norm scales, coefficients, tanh(angle) * pi.
         if (tid < 2 * C) {
             const int t = tid % C;
             const bool isb = tid < C;
-            sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? k_sh : q_sh) + t * NP, isb ? a.b_eps : a.c_eps);
+            if constexpr (PREP) {  // the rows as step a copies them (tokens past the end read the last one)
+                const int tc = t < Lc ? t : Lc - 1;
+                sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? brow : crow) + static_cast<int64_t>(tc) * a.st,
+                                                             isb ? a.b_eps : a.c_eps);
+            } else {
+                sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? k_sh : q_sh) + t * NP, isb ? a.b_eps : a.c_eps);
+            }
         }
         // The coefficient wave (wave 1, or wave 0 when the block has one wave)
-        // goes on to the decay weights. Lane s < C walks t = s + 1, s + 2, ...
-        // (lanes drop out past the chunk end), carrying the products
-        // prod_{s<r<=t} alpha_r and prod_{s+1<r<=t} alpha_r in fp64; its alpha
-        // values are read 8 steps ahead. W[t][s] for t < s is never read (the
-        // G tiles mask it). Lanes C and C + 1 write Din(t) = a_0 prod_{0<r<=t}
-        // a_r and Wp(t) = b_0 prod_{0<r<=t} a_r as the weights of a column s = 0
-        // with gamma = a_0 (b_0) and no beta term. tanh runs on the other waves.
-        {
+        // goes on to the decay weights (decay_walk). tanh runs on the other waves.
+        if constexpr (!PREP) {
             const int ct = NTH >= 128 ? tid - 64 : tid;
-            if (ct >= 0 && ct < C) {
-                const float dt = softplus_f(raw_s[0][ct] + dt_bias);
-                const float am = -fmaxf(heavy_tail_f(raw_s[1][ct]), a.a_floor);
-                float al, be, ga;
-                step_coefficients(am * dt, dt, raw_s[2][ct], &al, &be, &ga);
-                const bool valid = ct < Lc;
-                coef[0][ct] = valid ? al : 0.0f;
-                coef[1][ct] = valid ? be : 0.0f;
-                coef[2][ct] = valid ? ga : 0.0f;
-                coef[3][ct] = dt;
-            }
+            if (ct >= 0 && ct < C) token_coefficients<C>(ct, raw_s[0][ct], raw_s[1][ct], raw_s[2][ct], dt_bias, a.a_floor, Lc, coef);
             if (ct >= 0 && ct < 64) {
                 // The coefficients above were written by other lanes of this wave.
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             }
-            // Walkers: columns s < C, then Din (column kDin) and Wp (kWp), both
-            // with s = 0. Lane w < C + 2 walks t = s + 1 .. s + 16 of walker
-            // w; a walk longer than 16 steps (s < C - 17, and Din, Wp) has a
-            // second lane, C + 2 + j, for t = s + 17 .. C - 1. That lane first
-            // runs 16 multiply-only steps to form the same sequential
-            // products the first lane holds at t = s + 16, so every weight is
-            // bit-identical to one lane walking the whole column, while the
-            // wave issues 16 full steps instead of 31. Four-wave blocks keep
-            // one lane per walker (32 full steps): the split's registers cost
-            // them more than the shorter walk saves.
-            constexpr bool kSplit = DT <= 2;
-            constexpr int kFull = kSplit ? 16 : 32;  // full steps per lane (whole batches of 8)
-            constexpr int kLong = C - 17;  // columns whose walk exceeds 16 steps
-            static_assert(C + 2 + kLong + 2 <= 64, "the walkers' lanes must fit one wave");
-            const int hf = kSplit && ct >= C + 2 ? 1 : 0;
-            const int j2 = ct - (C + 2);
-            const int wl = hf == 0 ? ct : (j2 < kLong ? j2 : C + (j2 - kLong));
-            if (ct >= 0 && (hf == 0 ? ct < C + 2 : j2 < kLong + 2)) {
-                const int s = wl < C ? wl : 0;
-                const double b0 = first ? 0.0 : static_cast<double>(coef[1][0]);
-                const double gam = wl < C ? static_cast<double>(coef[2][s]) : (wl == C ? static_cast<double>(coef[0][0]) : b0);
-                const double bet = wl + 1 < C ? static_cast<double>(coef[1][wl + 1]) : 0.0;
-                const int colw = wl < C ? wl : (wl == C ? kDin : kWp);
-                if (hf == 0) w_s[s * WP + colw] = static_cast<float>(gam * 1.0);  // t = s
-                // Step k handles t = s + 1 + k with alpha from a clamped slot;
-                // steps with t >= C store into the sink row C, so no step is
-                // predicated.
-                double dd = 1.0, e = 1.0;
-                if constexpr (kSplit) {
-                    float al[16];
-#pragma unroll
-                    for (int k = 0; k < 16; ++k) al[k] = coef[0][min(s + 1 + k, C - 1)];
-#pragma unroll
-                    for (int k = 0; k < 16; ++k) {
-                        const double at = al[k];
-                        dd *= at;
-                        if (k > 0) e *= at;
-                    }
-                }
-                if (hf == 0) {  // (the first lane walks from t = s + 1)
-                    dd = 1.0;
-                    e = 1.0;
-                }
-                const int kb = 16 * hf;
-                float nx[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + kb + i, C - 1)];
-                auto batch = [&](int k0) {  // steps k0 .. k0 + 7, the next batch's alpha values read ahead
-                    float al[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) al[i] = nx[i];
-                    if (k0 + 8 < kFull) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) nx[i] = coef[0][min(s + 1 + kb + k0 + 8 + i, C - 1)];
-                    }
-                    // Each group of 4 steps runs the two product chains first,
-                    // then the 4 independent weights, then the 4 stores.
-#pragma unroll
-                    for (int i0 = 0; i0 < 8; i0 += 4) {
-                        double ddv[4], ev[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const double at = al[i0 + i];
-                            dd *= at;
-                            if (kb + k0 + i0 + i > 0) e *= at;
-                            ddv[i] = dd;
-                            ev[i] = e;
-                        }
-                        float wv[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) wv[i] = static_cast<float>(fma(bet, ev[i], gam * ddv[i]));
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int t = s + 1 + kb + k0 + i0 + i;
-                            w_s[(t < C ? t : C) * WP + colw] = wv[i];
-                        }
-                    }
-                };
-                // The split walk's two batches are straight-line code; the one-lane walk (32 steps) keeps
-                // a loop, whose registers the four-wave blocks cannot spare unrolled.
-                if constexpr (kSplit) {
-                    batch(0);
-                    batch(8);
-                } else {
-#pragma unroll 1
-                    for (int k0 = 0; k0 < kFull; k0 += 8) batch(k0);
-                }
-            }
+            decay_walk<C, (DT <= 2)>(ct, first, coef, w_s);
         }
-        {
+        if constexpr (!PREP) {
             // tanh(angle) * pi on the waves other than the coefficient wave.
             const int tl = NTH >= 128 ? (tid < 64 ? tid : tid - 64) : tid;
             const bool tw = NTH < 128 || tid < 64 || tid >= 128;
@@ -1183,7 +1213,9 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 }
             }
         }
-        if constexpr (kEarlyGate) {
+        if constexpr (PREP) {
+            gates();
+        } else if constexpr (kEarlyGate) {
             if (wave == 0) gates();  // wave 1 runs the coefficients and decay weights meanwhile
         }
         __syncthreads();
@@ -1221,7 +1253,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 }
             }
         }
-        if constexpr (kEarlyGate) {
+        if constexpr (kEarlyGate && !PREP) {
             if (wave == 1) gates();  // wave 0 runs the angle sums meanwhile
         }
         __syncthreads();
@@ -1439,9 +1471,14 @@ struct BlockArgs {
     ScanArgs s;         // mixer parameters, B, L, G, H, R and the output y (proj and gate are set in the kernel)
 };
 
-// HELP: the block has DT more waves, which compute half of the in_proj
-// tiles of the one chunk (L <= 32) and then end; S_BARRIER waits on the
-// surviving waves only, so the scan's barriers are unaffected.
+// HELP (one chunk, L <= 32; the dt/A/trap/angle columns one column tile, the
+// last): the block has DT more waves. The DT scan waves compute the other
+// column tiles of their row tile (wave w: rows 16 w .. 16 w + 15); each
+// helper computes the last tile for all 32 rows and, from it, helper 0 the
+// chunk's step coefficients and then its decay weights, helper 1 tanh(angle)
+// * pi, while the scan waves copy their rows, form the norm scales and the
+// gates (scan_head's PREP form). The helpers end after the barrier that ends
+// step b; S_BARRIER then waits on the surviving waves only.
 template <int NT, int DT, int KSI, int GS, int NCT, bool ALL_LIVE, bool HELP>
 __global__ __launch_bounds__(64 * DT * (HELP ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(1)))
 void mamba3_block_scan_kernel(BlockArgs p) {
@@ -1450,6 +1487,8 @@ void mamba3_block_scan_kernel(BlockArgs p) {
     __shared__ __attribute__((aligned(16))) float w_lds[STAGE ? NCT * 16 * 64 : 4];
     static_assert(DT == 2, "one wave per 16-row tile of the 32-token chunk");
     __shared__ ScanLds<C, NT, DT> sh;
+    constexpr int HP = 17;  // helper staging: [32 rows][16 columns], rows HP floats apart
+    __shared__ float hs[HELP ? DT : 1][HELP ? C * HP : 1];
     extern __shared__ __attribute__((aligned(16))) float proj_s[];  // [C, pp]
 
     const int64_t H = p.s.H, L = p.s.L;
@@ -1491,69 +1530,74 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             return 2 * DI + 16 * (j - 2 * DTL);
         }
 
-        // Wave w computes the chunk's 16-row tile w % 2 against the head's
-        // column tiles j = w / 2, w / 2 + NW / 2, ... (NW = DT waves, or 2 DT
-        // with the helper waves). The tiles past the head's count repeat its
-        // last one and are not stored.
-        //
         // STAGE (d_model 64): before the first chunk the block copies the
         // head's weight rows into LDS with direct global-to-LDS loads (each
         // instruction moves four 256-byte rows; no registers, all in flight
         // at once, each row read from L2 once per block instead of once per
         // wave); row r of tile j holds its 16-byte chunk c at slot c ^ r, so
         // the 16 lanes of a fragment read hit 16 different bank groups.
-        // Otherwise every wave loads its weight fragments into registers,
-        // with all loads issued before the first wait.
+        __device__ void stage(int ncol) const {
+            if constexpr (STAGE) {
+                static_assert(KSI == 2 && ALL_LIVE, "staging takes d_model 64 rows: 16 chunks of 16 bytes");
+                constexpr int NW = HELP ? 2 * DT : DT;
+                const int lane = threadIdx.x & 63;
+                const int rq = lane >> 4, slot = lane & 15;
+#pragma unroll 1
+                for (int u = wave; u < 4 * NCT; u += NW) {  // quarter-tile u: tile u / 4, rows 4 (u % 4) ..
+                    const int j = u >> 2, row = 4 * (u & 3) + rq;
+                    const int n = tile_col(j < ncol ? j : ncol - 1) + row;
+                    const float* src = p.in_w + static_cast<int64_t>(n < W ? n : W - 1) * 64 + 4 * (slot ^ row);
+                    __builtin_amdgcn_global_load_lds(
+                        (const __attribute__((address_space(1))) void*)src,
+                        (__attribute__((address_space(3))) void*)(w_lds + u * 256), 16, 0, 0);
+                }
+                __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the LDS copies have landed
+                __syncthreads();
+            }
+        }
+
+        // Column tile j's 16 weight rows as this lane's fragments (lane l = 16 g + i: row i, k = 32 s + 8 g ..).
+        __device__ void weights(int j, int ncol, float (&wv)[KSI][8], bool (&wlive)[KSI]) const {
+            if constexpr (STAGE) {
+                const float* rowp = w_lds + ((j < NCT ? j : NCT - 1) * 16 + li) * 64;
+#pragma unroll
+                for (int s2 = 0; s2 < KSI; ++s2) {
+                    const int cc = 8 * s2 + 2 * grp;
+                    const float4 lo = *reinterpret_cast<const float4*>(rowp + 4 * (cc ^ li));
+                    const float4 hi = *reinterpret_cast<const float4*>(rowp + 4 * ((cc + 1) ^ li));
+                    wv[s2][0] = lo.x; wv[s2][1] = lo.y; wv[s2][2] = lo.z; wv[s2][3] = lo.w;
+                    wv[s2][4] = hi.x; wv[s2][5] = hi.y; wv[s2][6] = hi.z; wv[s2][7] = hi.w;
+                    wlive[s2] = true;
+                }
+            } else {
+                const int n0 = tile_col(j < ncol ? j : ncol - 1);
+                const int wr = n0 + li < W ? n0 + li : W - 1;
+                tile_load8<KSI>(p.in_w + static_cast<int64_t>(wr) * dm, dm, grp, wv, wlive);
+            }
+        }
+
+        // The chunk's in_proj tiles into proj_s, then a barrier. Without
+        // HELP, wave w computes the chunk's 16-row tile w % 2 against the
+        // head's column tiles j = w / 2, w / 2 + NW / 2, ... (NW = DT); with
+        // HELP (scan waves only), row tile w against every tile but the last.
+        // The tiles past the head's count repeat its last one and are not
+        // stored. Every wave normalises its x fragments once; all of its
+        // weight loads are in flight before the first wait.
         __device__ void before(int64_t c0) const {
-            constexpr int NW = HELP ? 2 * DT : DT;
-            constexpr int NTW = (NCT + NW / 2 - 1) / (NW / 2);  // column tiles per wave
+            constexpr int NTW = HELP ? NCT - 1 : (NCT + DT / 2 - 1) / (DT / 2);  // column tiles per wave
             const int ncol = 2 * (D / 16) + (W - 2 * DI + 15) / 16;
-            const int rt = wave & 1, j0 = wave >> 1;
+            const int rt = HELP ? wave : wave & 1, j0 = HELP ? 0 : wave >> 1, jstep = HELP ? 1 : DT / 2;
             float xv[KSI][8], nw[KSI][8];
             bool live[KSI], nlive[KSI];
             const int64_t r = c0 + 16 * rt + li;
             tile_load8<KSI>(xw + (r < L ? r : L - 1) * p.x_ts, dm, grp, xv, live);
             tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
+            if (c0 == 0) stage(ncol);
             float wv[NTW][KSI][8];
             bool wlive[NTW][KSI];
-            if constexpr (STAGE) {
-                static_assert(KSI == 2 && ALL_LIVE, "staging takes d_model 64 rows: 16 chunks of 16 bytes");
-                if (c0 == 0) {
-                    const int lane = threadIdx.x & 63;
-                    const int rq = lane >> 4, slot = lane & 15;
-#pragma unroll 1
-                    for (int u = wave; u < 4 * NCT; u += NW) {  // quarter-tile u: tile u / 4, rows 4 (u % 4) ..
-                        const int j = u >> 2, row = 4 * (u & 3) + rq;
-                        const int n = tile_col(j < ncol ? j : ncol - 1) + row;
-                        const float* src = p.in_w + static_cast<int64_t>(n < W ? n : W - 1) * 64 + 4 * (slot ^ row);
-                        __builtin_amdgcn_global_load_lds(
-                            (const __attribute__((address_space(1))) void*)src,
-                            (__attribute__((address_space(3))) void*)(w_lds + u * 256), 16, 0, 0);
-                    }
-                    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the LDS copies have landed
-                    __syncthreads();
-                }
 #pragma unroll
-                for (int i = 0; i < NTW; ++i) {
-                    const int j = j0 + i * (NW / 2);
-                    const float* rowp = w_lds + ((j < NCT ? j : NCT - 1) * 16 + li) * 64;
-#pragma unroll
-                    for (int s2 = 0; s2 < KSI; ++s2) {
-                        const int cc = 8 * s2 + 2 * grp;
-                        const float4 lo = *reinterpret_cast<const float4*>(rowp + 4 * (cc ^ li));
-                        const float4 hi = *reinterpret_cast<const float4*>(rowp + 4 * ((cc + 1) ^ li));
-                        wv[i][s2][0] = lo.x; wv[i][s2][1] = lo.y; wv[i][s2][2] = lo.z; wv[i][s2][3] = lo.w;
-                        wv[i][s2][4] = hi.x; wv[i][s2][5] = hi.y; wv[i][s2][6] = hi.z; wv[i][s2][7] = hi.w;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < NTW; ++i) {
-                    const int j = j0 + i * (NW / 2);
-                    const int n0 = tile_col(j < ncol ? j : ncol - 1);
-                    const int wr = n0 + li < W ? n0 + li : W - 1;
-                    tile_load8<KSI>(p.in_w + static_cast<int64_t>(wr) * dm, dm, grp, wv[i], wlive[i]);
-                }
+            for (int i = 0; i < NTW; ++i) weights(j0 + i * jstep, ncol, wv[i], wlive[i]);
+            if constexpr (!STAGE) {
                 // Every loaded value is held here, so all the loads are in
                 // flight together and waited on once: left to itself the
                 // compiler issues the later tiles' loads after the first
@@ -1568,7 +1612,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);
 #pragma unroll
             for (int i = 0; i < NTW; ++i) {
-                const int j = j0 + i * (NW / 2);
+                const int j = j0 + i * jstep;
                 tile_f32x4 y = tile_mfma_f32<KSI, ALL_LIVE>(wv[i], xv, live);
                 y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
                 if (j < ncol) *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + tile_col(j) + 4 * grp) = y;
@@ -1578,11 +1622,59 @@ void mamba3_block_scan_kernel(BlockArgs p) {
         __device__ void after(int64_t, bool) const {}
     };
     const Hooks hooks{p, xw, proj_s, w_lds, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h)};
-    if (HELP && wave >= DT) {
-        hooks.before(0);  // the helpers' share of the chunk's in_proj tiles, then they end
-        return;
+    if constexpr (HELP) {
+        if (wave >= DT) {
+            // The last column tile (dt, A, trap logits, angles) for both row tiles into this helper's
+            // staging rows, with the scan waves' arithmetic.
+            const int ncol = 2 * (D / 16) + (W - 2 * DI + 15) / 16;
+            const int j = ncol - 1, hw = wave - DT;
+            float nw[KSI][8], wv[KSI][8];
+            bool nlive[KSI], wlive[KSI];
+            float xv[2][KSI][8];
+            bool live[2][KSI];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int64_t r = 16 * rt + li;
+                tile_load8<KSI>(xw + (r < L ? r : L - 1) * p.x_ts, dm, grp, xv[rt], live[rt]);
+            }
+            tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
+            hooks.stage(ncol);
+            hooks.weights(j, ncol, wv, wlive);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                tile_rms_norm<KSI, GS>(xv[rt], nw, p.norm_eps);
+                tile_f32x4 y = tile_mfma_f32<KSI, ALL_LIVE>(wv, xv[rt], live[rt]);
+                y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
+#pragma unroll
+                for (int v = 0; v < 4; ++v) hs[hw][(16 * rt + li) * HP + 4 * grp + v] = y[v];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // Column offsets inside the tile: dt h, A H + h, trap 2H + h, angle r 3H + r. Tokens past L
+            // hold the last token's values (their x rows are clamped), as the scan's own copy reads them.
+            const int Hi = static_cast<int>(H), Lc = static_cast<int>(L);
+            const float* row = hs[hw];
+            if (hw == 0) {
+                if (lane < C)
+                    token_coefficients<C>(lane, row[lane * HP + h], row[lane * HP + Hi + h], row[lane * HP + 2 * Hi + h],
+                                          p.s.dt_bias[h], p.s.a_floor, Lc, sh.coef);
+            } else {
+                const int R = static_cast<int>(p.s.R);
+                constexpr int RM = ScanLds<C, NT, DT>::RM;
+#pragma unroll 1
+                for (int i = lane; i < C * R; i += 64) {
+                    const int t = i / R, rr = i - t * R;
+                    sh.ang_s[t * RM + rr] = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
+                }
+            }
+            __syncthreads();  // with the end of the scan waves' in_proj: coefficients and angles are in
+            if (hw == 0) decay_walk<C, true>(lane, true, sh.coef, sh.w_s);
+            __syncthreads();  // with the end of the scan waves' step b: the decay weights are in
+            return;
+        }
     }
-    scan_head<C, NT, DT, true, Hooks, false>(a, sh, b, h, 0, hooks);
+    scan_head<C, NT, DT, true, Hooks, false, HELP>(a, sh, b, h, 0, hooks);
 }
 
 // Geometries of the block kernel: (d_state, headdim, the in_proj's 32-wide k
@@ -1599,7 +1691,8 @@ bool launch_block_scan(const BlockArgs& p, int64_t N, int64_t D, int64_t gs, hip
     const int64_t ncol = 2 * (D / 16) + (p.W - 2 * DI + 15) / 16;
 #define MLK_BLOCK(NV, DV, KSIV, GSV, NCTV)                                                                       \
     if (N == NV && D == DV && ksi == KSIV && gs == GSV && ncol <= NCTV) {                                         \
-        const bool all_live = p.dm == 32 * KSIV, help = p.s.L <= 32;                                             \
+        const bool all_live = p.dm == 32 * KSIV,                                                                 \
+                   help = p.s.L <= 32 && p.s.G * NV == 16 && 3 * p.s.H + p.s.R <= 16;                            \
         if (all_live && help) {                                                                                  \
             hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV, true, true>), grid,   \
                                dim3(8 * DV), lds, stream, p);                                                     \
