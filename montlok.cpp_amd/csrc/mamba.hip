@@ -828,6 +828,15 @@ __global__ __launch_bounds__(64) void rec_chunk_kernel(RecArgs a) {
 // prep -> rotate -> rec_chunk_kernel sequence bit for bit; q and k never leave
 // LDS. Blocks are ordered so that the heads of one window run on one XCD and
 // share its L2 copy of the window's B/C rows.
+// sin and cos of a running angle sum, reduced by whole turns in fp32 first.
+__device__ __forceinline__ void rotation_of(float cumulative, float* sine, float* cosine) {
+    const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
+    double sd, cd;
+    sincos_d(static_cast<double>(cumulative - wraps), &sd, &cd);
+    *sine = static_cast<float>(sd);
+    *cosine = static_cast<float>(cd);
+}
+
 // The step coefficients of token ct < C of a chunk (one lane per token):
 // dt = softplus(dt logit + bias), A = -max(heavy_tail(A logit), floor), then
 // (alpha, beta, gamma) by step_coefficients (zero for tokens past Lc) and dt.
@@ -986,6 +995,7 @@ struct ScanLds {
 struct NoChunkHooks {
     __device__ void before(int64_t) const {}
     __device__ void after(int64_t, bool) const {}
+    __device__ const float* rotations() const { return nullptr; }
 };
 
 // The scan of one (window, head) by the DT waves of threads tid_base ..
@@ -999,10 +1009,12 @@ struct NoChunkHooks {
 // heads can share a block. PREP (TILE, one chunk, two waves): other waves of
 // the block have already formed the chunk's coefficients and tanh(angle) * pi
 // (before the barrier that ends hooks.before) and its decay weights (before
-// the barrier that ends step b): step a skips the dt/A/trap and angle columns,
-// steps a and b run without a barrier between them (the norm scales read the
-// B/C rows where hooks.before left them), and both waves form their gates in
-// step b.
+// the barrier that ends step b), and, before the latter, the running angle
+// sums and the sin/cos of each (token, angle) pair at hooks.rotations()
+// ([C][N / 2] pairs): step a skips the dt/A/trap and angle columns, steps a
+// and b run without a barrier between them (the norm scales read the B/C rows
+// where hooks.before left them), both waves form their gates in step b, step
+// c skips the angle sums and step d reads the rotations.
 template <int C, int NT, int DT, bool TILE, class Hooks, bool TILE_OUT = TILE, bool PREP = false>
 __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>& sh, int64_t b, int64_t h,
                                           int tid_base, const Hooks& hooks) {
@@ -1240,7 +1252,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 q_sh[i] = (qv[j] * sqb[j]) * cw + cb;
             }
         }
-        if (tid < R) {
+        if (!PREP && tid < R) {
 #pragma unroll
             for (int t0 = 0; t0 < C; t0 += 16) {
                 float term[16];
@@ -1262,11 +1274,14 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         for (int i = tid; i < C * R; i += NTH) {
             const int t = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - t * R;
             {
-                const float cumulative = cum_s[t * RM + r];
-                const float wraps = __fmul_rn(kTwoPiF, floorf(cumulative / kTwoPiF));
-                double sd, cd;
-                sincos_d(static_cast<double>(cumulative - wraps), &sd, &cd);
-                const float sine = static_cast<float>(sd), cosine = static_cast<float>(cd);
+                float sine, cosine;
+                if constexpr (PREP) {
+                    const float* rot = hooks.rotations() + 2 * (t * RM + r);
+                    sine = rot[0];
+                    cosine = rot[1];
+                } else {
+                    rotation_of(cum_s[t * RM + r], &sine, &cosine);
+                }
                 float* qp = q_sh + t * NP + 2 * r;
                 float* kq = k_sh + t * NP + 2 * r;
                 const float ql = qp[0], qr = qp[1], kl = kq[0], kr = kq[1];
@@ -1620,8 +1635,10 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             __syncthreads();
         }
         __device__ void after(int64_t, bool) const {}
+        __device__ const float* rotations() const { return rot; }
+        const float* rot;
     };
-    const Hooks hooks{p, xw, proj_s, w_lds, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h)};
+    const Hooks hooks{p, xw, proj_s, w_lds, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h), &hs[HELP ? 1 : 0][0]};
     if constexpr (HELP) {
         if (wave >= DT) {
             // The last column tile (dt, A, trap logits, angles) for both row tiles into this helper's
@@ -1669,8 +1686,40 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 }
             }
             __syncthreads();  // with the end of the scan waves' in_proj: coefficients and angles are in
-            if (hw == 0) decay_walk<C, true>(lane, true, sh.coef, sh.w_s);
-            __syncthreads();  // with the end of the scan waves' step b: the decay weights are in
+            if (hw == 0) {
+                decay_walk<C, true>(lane, true, sh.coef, sh.w_s);
+            } else {
+                // The running angle sums of the chunk (one lane per angle, from zero: the first chunk), as
+                // step c forms them, then the sin/cos of every (token, angle) pair, as step d would, into
+                // this helper's staging rows (its tile values are dead).
+                const int R = static_cast<int>(p.s.R);
+                constexpr int RM = ScanLds<C, NT, DT>::RM;
+                if (lane < R) {
+                    double running = 0.0;
+#pragma unroll
+                    for (int t0 = 0; t0 < C; t0 += 16) {
+                        float term[16];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) term[i] = sh.ang_s[(t0 + i) * RM + lane] * sh.coef[3][t0 + i];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            running += static_cast<double>(term[i]);
+                            sh.cum_s[(t0 + i) * RM + lane] = static_cast<float>(running);
+                        }
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                float* rot = hs[1];
+                static_assert(2 * C * RM <= C * HP, "the rotations fit the staging rows");
+#pragma unroll 1
+                for (int i = lane; i < C * R; i += 64) {
+                    const int t = i / R, rr = i - t * R;
+                    rotation_of(sh.cum_s[t * RM + rr], &rot[2 * (t * RM + rr)], &rot[2 * (t * RM + rr) + 1]);
+                }
+            }
+            __syncthreads();  // with the end of the scan waves' step b: decay weights and rotations are in
             return;
         }
     }
