@@ -1083,7 +1083,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
     // scan with no carried state.
     auto chunk = [&](auto last_c, int64_t c0) {
         constexpr bool last = decltype(last_c)::value;
-        const bool first = c0 == 0;
+        const bool first = PREP || c0 == 0;  // PREP runs one chunk: known here, so its first-chunk zeros fold
         // The thread index is made opaque per chunk so that the per-lane index
         // arithmetic of the phases below is recomputed here (a few integer
         // operations) rather than hoisted out of the loop and held in VGPRs.
@@ -1320,7 +1320,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 }
             }
         }
-        if (wave == DT - 1 && lane < C) {
+        if (!first && wave == DT - 1 && lane < C) {  // (read for later chunks only)
             float dot = 0.0f;
 #pragma unroll
             for (int n = 0; n < N; ++n) dot = fmaf(q_sh[lane * NP + n], kp_s[par][n], dot);
@@ -1625,13 +1625,19 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                         for (int i = 0; i < NTW; ++i) asm volatile("" : "+v"(wv[i][s2][k]));
             }
             tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);
-#pragma unroll
-            for (int i = 0; i < NTW; ++i) {
+            auto put = [&](int i, tile_f32x4 y) {
                 const int j = j0 + i * jstep;
-                tile_f32x4 y = tile_mfma_f32<KSI, ALL_LIVE>(wv[i], xv, live);
                 y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
                 if (j < ncol) *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + tile_col(j) + 4 * grp) = y;
+            };
+#pragma unroll
+            for (int i = 0; i + 1 < NTW; i += 2) {  // two tiles' chains interleaved
+                tile_f32x4 ya, yb;
+                tile_mfma_f32_pair<KSI, ALL_LIVE>(wv[i], wv[i + 1], xv, live, ya, yb);
+                put(i, ya);
+                put(i + 1, yb);
             }
+            if constexpr (NTW % 2 == 1) put(NTW - 1, tile_mfma_f32<KSI, ALL_LIVE>(wv[NTW - 1], xv, live));
             __syncthreads();
         }
         __device__ void after(int64_t, bool) const {}

@@ -106,4 +106,27 @@ __device__ __forceinline__ tile_f32x4 tile_mfma_f32(const float (&wv)[KS][8], co
     return acc0 + acc1;
 }
 
+// Two tiles against the same x fragments, their four chains interleaved (each
+// tile's products and sums exactly as tile_mfma_f32 forms them).
+template <int KS, bool ALL_LIVE = false>
+__device__ __forceinline__ void tile_mfma_f32_pair(const float (&wa)[KS][8], const float (&wb)[KS][8],
+                                                   const float (&xv)[KS][8], const bool (&live)[KS], tile_f32x4& ya,
+                                                   tile_f32x4& yb) {
+    tile_f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, b0 = a0, b1 = a0;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const bool on = ALL_LIVE || live[s];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const float x0 = on ? xv[s][j] : 0.0f, x1 = on ? xv[s][j + 1] : 0.0f;
+            a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(on ? wa[s][j] : 0.0f, x0, a0, 0, 0, 0);
+            b0 = __builtin_amdgcn_mfma_f32_16x16x4f32(on ? wb[s][j] : 0.0f, x0, b0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(on ? wa[s][j + 1] : 0.0f, x1, a1, 0, 0, 0);
+            b1 = __builtin_amdgcn_mfma_f32_16x16x4f32(on ? wb[s][j + 1] : 0.0f, x1, b1, 0, 0, 0);
+        }
+    }
+    ya = a0 + a1;
+    yb = b0 + b1;
+}
+
 }  // namespace mlk
