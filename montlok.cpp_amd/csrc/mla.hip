@@ -21,7 +21,11 @@
 // the B-operand layout of O^T = V^T P^T: lane l holds query l%16 and keys
 // 16t + 4(l/16) + v of every 16-key tile t, and those 8 values (two tiles) are
 // exactly the 8 k-slots the next MFMA needs. Only V has to be laid out
-// transposed in LDS. Running max, running sum and rescale are per lane.
+// transposed in LDS. Running max, running sum and rescale are per lane. With
+// a positive scale s (every MLA caller's), a chunk's max is taken over the raw
+// scores and scaled once (RN(max x) s = max RN(x s): rounding is monotone) and
+// each exponent is one fma, exp2(x s - m) rounded once; otherwise the scores
+// are scaled first and exp2(RN(x s) - m) is formed.
 //   BF16: v_mfma_f32_16x16x32_bf16, q/k/v and p rounded to bf16, fp32
 //         accumulation and fp32 softmax (bf16-weight configurations).
 //   FP32: v_mfma_f32_16x16x4_f32, fp32 throughout (fp32 configurations).
@@ -167,7 +171,7 @@ __device__ __forceinline__ float lane_xor32(float x) {
     return __int_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
-template <int HD, bool BF16, bool VEC>
+template <int HD, bool BF16, bool VEC, bool RAWMAX>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p) {
     using E = AttnElem<BF16>;
     using T = typename E::T;
@@ -273,13 +277,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p) {
                 for (int v = 0; v < 4; ++v) {
                     const int64_t key = kbase + 16 * t + 4 * g + v;
                     const bool ok = key < p.kv_length && key <= qpos + p.offset;
-                    const float x = ok ? s[t][v] * p.scale_log2 : -INFINITY;
+                    const float x = ok ? (RAWMAX ? s[t][v] : s[t][v] * p.scale_log2) : -INFINITY;
                     s[t][v] = x;
                     mx = fmaxf(mx, x);
                 }
             }
             mx = xor_max(mx, 16);
             mx = xor_max(mx, 32);
+            if constexpr (RAWMAX) mx *= p.scale_log2;  // the max of the scaled scores (the scale is positive)
             const float m_new = fmaxf(m_run[i], mx);
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
@@ -289,7 +294,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p) {
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const float e = __builtin_amdgcn_exp2f(s[t][v] - m_use);
+                    const float e = __builtin_amdgcn_exp2f(RAWMAX ? fmaf(s[t][v], p.scale_log2, -m_use) : s[t][v] - m_use);
                     s[t][v] = e;
                     psum += e;
                 }
@@ -364,10 +369,15 @@ template <int HD, bool BF16>
 void launch_attn(const AttnArgs& p, bool vec, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(ceil_div(p.q_length, kQueriesPerBlock)), static_cast<unsigned>(p.heads),
                     static_cast<unsigned>(p.batch));
-    if (vec) {
-        hipLaunchKernelGGL((attn_kernel<HD, BF16, true>), grid, dim3(256), 0, stream, p);
+    const bool raw = p.scale_log2 > 0.0f;
+    if (vec && raw) {
+        hipLaunchKernelGGL((attn_kernel<HD, BF16, true, true>), grid, dim3(256), 0, stream, p);
+    } else if (vec) {
+        hipLaunchKernelGGL((attn_kernel<HD, BF16, true, false>), grid, dim3(256), 0, stream, p);
+    } else if (raw) {
+        hipLaunchKernelGGL((attn_kernel<HD, BF16, false, true>), grid, dim3(256), 0, stream, p);
     } else {
-        hipLaunchKernelGGL((attn_kernel<HD, BF16, false>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((attn_kernel<HD, BF16, false, false>), grid, dim3(256), 0, stream, p);
     }
 }
 
@@ -417,7 +427,7 @@ struct MlaAttendArgs {
 // block.
 // LNIN: the latent rows arrive normalised, in bf16 (the in_proj's LayerNorm
 // epilogue, the same arithmetic as below), and the block skips its LayerNorm.
-template <int HD, int NOPE, int KV, int NW, int TPW, bool LNIN>
+template <int HD, int NOPE, int KV, int NW, int TPW, bool LNIN, bool RAWMAX>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 3 : 1)))
 void mla_attend_kernel(MlaAttendArgs p) {
     constexpr int THREADS = 64 * NW;
@@ -736,13 +746,14 @@ void mla_attend_kernel(MlaAttendArgs p) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int key = kbase + 16 * t + 4 * g + v;
-                    const float x = (key < L && key <= qpos) ? sc[t][v] * p.scale_log2 : -INFINITY;
+                    const float x = (key < L && key <= qpos) ? (RAWMAX ? sc[t][v] : sc[t][v] * p.scale_log2) : -INFINITY;
                     sc[t][v] = x;
                     mx = fmaxf(mx, x);
                 }
             }
             mx = xor_max(mx, 16);
             mx = xor_max(mx, 32);
+            if constexpr (RAWMAX) mx *= p.scale_log2;  // the max of the scaled scores (the scale is positive)
             const float m_new = fmaxf(m_run[i], mx);
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             const float corr = __builtin_amdgcn_exp2f(m_run[i] - m_use);
@@ -752,7 +763,7 @@ void mla_attend_kernel(MlaAttendArgs p) {
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
+                    const float e = __builtin_amdgcn_exp2f(RAWMAX ? fmaf(sc[t][v], p.scale_log2, -m_use) : sc[t][v] - m_use);
                     sc[t][v] = e;
                     psum += e;
                 }
@@ -1186,7 +1197,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
                 for (int t = 0; t < NKT; ++t) {
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
-                        float xv = sc[t][v] * p.scale_log2;
+                        float xv = sc[t][v];
                         if (t == DIAG) xv = 4 * g + v <= li ? xv : -INFINITY;  // key 16 t + 4g + v <= query li
                         sc[t][v] = xv;
                         mx = fmaxf(mx, xv);
@@ -1194,6 +1205,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
                 }
                 mx = fmaxf(mx, lane_xor16(mx));
                 mx = fmaxf(mx, lane_xor32(mx));
+                mx *= p.scale_log2;  // the max of the scaled scores (the scale is positive)
                 const float m_new = FIRST ? mx : fmaxf(m_run[I], mx);
                 const float m_use = m_new == -INFINITY ? 0.0f : m_new;
                 float corr = 0.0f;
@@ -1204,7 +1216,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
                 for (int t = 0; t < NKT; ++t) {
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
-                        const float e = __builtin_amdgcn_exp2f(sc[t][v] - m_use);
+                        const float e = __builtin_amdgcn_exp2f(fmaf(sc[t][v], p.scale_log2, -m_use));
                         sc[t][v] = e;
                         psum += e;
                     }
@@ -1414,9 +1426,17 @@ extern "C" mlk_status mlk_mla_attend(const float* projected, int64_t batch, int6
     const dim3 grid(static_cast<unsigned>(batch * heads));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (cfg32) {
-        hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, false>), grid, dim3(256), 0, s, p);
+        if (p.scale_log2 > 0.0f) {
+            hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, false, true>), grid, dim3(256), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, false, false>), grid, dim3(256), 0, s, p);
+        }
     } else {
-        hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, false>), grid, dim3(512), 0, s, p);
+        if (p.scale_log2 > 0.0f) {
+            hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, false, true>), grid, dim3(512), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, false, false>), grid, dim3(512), 0, s, p);
+        }
     }
     return launch_status("mla_attend");
 }
@@ -1450,9 +1470,17 @@ extern "C" mlk_status mlk_mla_attend_normed(const float* projected, int64_t batc
     const dim3 grid(static_cast<unsigned>(batch * heads));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (cfg32) {
-        hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, true>), grid, dim3(256), 0, s, p);
+        if (p.scale_log2 > 0.0f) {
+            hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, true, true>), grid, dim3(256), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((mla_attend_kernel<32, 16, 64, 4, 2, true, false>), grid, dim3(256), 0, s, p);
+        }
     } else {
-        hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, true>), grid, dim3(512), 0, s, p);
+        if (p.scale_log2 > 0.0f) {
+            hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, true, true>), grid, dim3(512), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((mla_attend_kernel<64, 32, 64, 8, 2, true, false>), grid, dim3(512), 0, s, p);
+        }
     }
     return launch_status("mla_attend_normed");
 }
@@ -1469,6 +1497,10 @@ extern "C" mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t len
                        kv_rank == 64 && length <= 128;
     if (!built) {
         set_error("mla_forward: geometry without the per-window kernel (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    if (!(static_cast<float>(scale * 1.4426950408889634) > 0.0f)) {
+        set_error("mla_forward: the per-window kernel takes a positive softmax scale (use the separate operators)");
         return MLK_ERR_UNSUPPORTED;
     }
     if (!aligned16(x) || x_token_stride % 4 != 0 || x_batch_stride % 4 != 0 || !aligned16(cosine) ||
