@@ -944,7 +944,9 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     }
 
     // 2. in_proj: per (tile, row tile) the linear's chain over the 8 k steps, the first half's steps
-    // before the second half is stored.
+    // before the second half is stored. Waves 0..3 run their three tiles over every row tile; waves 4..7
+    // their two q tiles over every row tile and the k_rope tile over the two row tiles whose epilogue they
+    // take (w - 4 and w), into acc[2][0] and acc[2][1].
     f32x4 acc[3][RT];
 #pragma unroll
     for (int t = 0; t < 3; ++t)
@@ -964,15 +966,33 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
             *reinterpret_cast<bf16x8*>(xq_s + sw(row, c8)) = o;
         }
         __syncthreads();
+        auto rows = [&](auto nt_c) {  // the first NT tiles over every row tile
+            constexpr int NT = decltype(nt_c)::value;
 #pragma unroll
-        for (int m = 0; m < RT; ++m) {
+            for (int m = 0; m < RT; ++m) {
 #pragma unroll
-            for (int s = hf * SH; s < (hf + 1) * SH; ++s) {
-                const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * m + li, 32 * s + 8 * g));
+                for (int s = hf * SH; s < (hf + 1) * SH; ++s) {
+                    const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * m + li, 32 * s + 8 * g));
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
-                    acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[t][s]), xf,
-                                                                        acc[t][m], 0, 0, 0);
+                    for (int t = 0; t < NT; ++t)
+                        acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[t][s]), xf,
+                                                                            acc[t][m], 0, 0, 0);
+                }
+            }
+        };
+        if (wave < 4) {
+            rows(std::integral_constant<int, 3>{});
+        } else {
+            rows(std::integral_constant<int, 2>{});
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int m = wave - 4 + 4 * u;
+#pragma unroll
+                for (int s = hf * SH; s < (hf + 1) * SH; ++s) {
+                    const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xq_s + sw(16 * m + li, 32 * s + 8 * g));
+                    acc[2][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[2][s]), xf,
+                                                                        acc[2][u], 0, 0, 0);
+                }
             }
         }
     }
@@ -1011,11 +1031,18 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         *reinterpret_cast<uint2*>(xq_s + sw(row, q0 + 4 * g)) = make_uint2(pack2(yn[0], yn[1]), pack2(yn[2], yn[3]));
         *reinterpret_cast<uint32_t*>(xq_s + sw(row, q0 + NOPE + 2 * g)) = pack2(qr[0], qr[2]);
         *reinterpret_cast<uint32_t*>(xq_s + sw(row, q0 + NOPE + 2 * g + 8)) = pack2(qr[1], qr[3]);
-        if (wave < 4) {
-            *reinterpret_cast<f32x4*>(lat_f + lat_at(row, 4 * wave + g)) = y3;
-        } else if ((m & 3) == wave - 4) {  // uniform per wave: a scalar branch
+        if (wave < 4) *reinterpret_cast<f32x4*>(lat_f + lat_at(row, 4 * wave + g)) = y3;
+    }
+    if (wave >= 4) {  // k_rope of row tiles w - 4 and w
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int row = 16 * (wave - 4 + 4 * u) + li;
+            const double2 ca = *reinterpret_cast<const double2*>(cs_d + cs_at(row, g));
+            const double2 cb = *reinterpret_cast<const double2*>(cs_d + cs_at(row, g + 4));
+            const double2 sa = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, g));
+            const double2 sb = *reinterpret_cast<const double2*>(cs_d + LMAX * ROPE + cs_at(row, g + 4));
             float kr[4];
-            rope4(y3, ca, cb, sa, sb, kr);
+            rope4(acc[2][u], ca, cb, sa, sb, kr);
             *reinterpret_cast<uint32_t*>(kr_s + row * ROPE + 2 * g) = pack2(kr[0], kr[2]);
             *reinterpret_cast<uint32_t*>(kr_s + row * ROPE + 2 * g + 8) = pack2(kr[1], kr[3]);
         }
