@@ -213,7 +213,8 @@ mlk_status mlk_mla_attend_normed(const float* projected, int64_t batch, int64_t 
  * cos/sin [L, rope]; out [B, L, d_model] contiguous. The result equals the
  * separate path (linear, mlk_layer_norm_bf16, mlk_mla_attend_normed, linear)
  * bit for bit. Built for 8 heads of 32 (nope 16, rope 16), kv_rank 64,
- * L <= 128, 16-byte aligned operands; MLK_ERR_UNSUPPORTED otherwise. */
+ * L <= 128, a positive scale, 16-byte aligned operands; MLK_ERR_UNSUPPORTED
+ * otherwise. */
 mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_t d_model, int64_t x_batch_stride,
                            int64_t x_token_stride, const void* in_proj_weight, const float* kv_norm_w,
                            const float* kv_norm_b, double kv_norm_eps, const void* kv_up_weight,
