@@ -316,3 +316,30 @@ def test_window_kernel_vs_oracle(dev, oracle):
     assert _C.mla_forward_launches() == ["mla_forward"]
     expect = _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, L, True, scale, cos, sin)
     assert_close(out, expect, tol=BF16_TOL, name="per-window mla_forward vs oracle")
+
+
+@pytest.mark.parametrize("scale", [-0.17677669529663687, 0.0])
+def test_non_positive_scale_takes_the_scaled_softmax(dev, oracle, scale):
+    """A softmax scale that is not positive: the per-window kernel declines (its max is taken over raw
+    scores), the four-launch path runs the kernels' scaled-scores form, and the result still matches the
+    oracle chain and the separate operators (their attention kernel in the same form) bit for bit."""
+    from montlok import _C
+
+    rng = np.random.default_rng(32)
+    B, L, d, H, hd, nope, kv_rank = 4, 96, 256, 8, 32, 16, 64
+    x = rng.standard_normal((B, L, d)).astype(np.float32)
+    p = _mla_params(rng, d, H, hd, nope, kv_rank, True)
+    cos, sin = rope_tables(L, hd - nope)
+
+    def w(a):
+        return _t(a, dev).to(torch.bfloat16)
+
+    in_w = np.concatenate([p["q"], p["kv_down"], p["k_rope"]])
+    args = (_t(x, dev), w(in_w), torch.empty(0, device=dev), _t(p["ln_w"], dev), _t(p["ln_b"], dev), 1e-5,
+            w(p["kv_up"]), w(p["o"]), _t(cos, dev), _t(sin, dev), H, hd, nope, kv_rank, L, True, scale)
+    out = _C._mla_forward(*args, allow_fused=True)
+    assert _C.mla_forward_launches() == ["linear", "layer_norm_bf16", "mla_attend_normed", "linear"]
+    separate = _C._mla_forward(*args, allow_fused=False)
+    assert_bitwise(out, separate.cpu().numpy(), f"scale {scale}: fused attention vs separate operators")
+    expect = _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, L, True, scale, cos, sin)
+    assert_close(out, expect, tol=BF16_TOL, name=f"scale {scale}: mla_forward vs oracle")
