@@ -153,24 +153,29 @@ def _time_graph(g, replays: int) -> float:
 def _gpu_steps(step_fns, steps: int, warmup: int, budget_s: float = 10.0) -> dict:
     """Times exactly `steps` steps; step i runs step_fns[i % len(step_fns)].
 
-    The `steps` steps are captured, in order, into one HIP graph, and the `warmup` steps before them into
-    another (capture runs nothing; the caller has run every step function once). The warm-up is one replay
-    of the `warmup`-step graph, so the GPU runs the warm-up steps back to back and reaches its working clock,
-    right before the timed region: one replay of the `steps`-step graph between two HIP events, synchronized
-    on both sides, no host work between the steps. ms_per_step is that region's time / steps. Further
+    The `steps` steps are captured, in order, into one HIP graph (capture runs nothing; the caller has run
+    every step function once). The warm-up runs `warmup` steps back to back right before the timed region:
+    as one replay of a graph of warmup % steps steps (those just before the timed graph's first in the
+    rotation of step functions) and warmup // steps replays of the timed graph itself (so the timed replay
+    is not its first launch when warmup >= steps). The timed region is one replay of the `steps`-step graph between two HIP events,
+    synchronized on both sides, no host work between the steps; ms_per_step is its time / steps. Further
     replays of the same graph (30, or as many as fit in `budget_s`, at least 3) give the median and the
-    spread of the per-step time."""
+    spread of the per-step time. With several step functions the timed steps continue the warm-up's
+    rotation only when steps is a multiple of their count (as in every workload here)."""
     import statistics
 
     import torch
 
     n = len(step_fns)
-    g = _graph([step_fns[(warmup + i) % n] for i in range(steps)], prerun=False)
+    g = _graph([step_fns[i % n] for i in range(steps)], prerun=False)
     _upload(g)
-    if warmup > 0:
-        wg = _graph([step_fns[i % n] for i in range(warmup)], prerun=False)
+    full, rest = divmod(warmup, steps)
+    if rest > 0:  # the steps just before the timed graph's first in the rotation
+        wg = _graph([step_fns[(i - rest) % n] for i in range(rest)], prerun=False)
         _upload(wg)
         wg.replay()
+    for _ in range(full):
+        g.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
