@@ -30,7 +30,8 @@ def test_device_math_bounds(dev):
     assert _ulp_err(out["exp"], np.exp(x)).max() <= 4
     # tanh: absolute error (the kernels add it to an O(1) bias).
     assert np.abs(out["tanh"] - np.tanh(x)).max() <= 4e-16
-    assert np.abs(out["sigmoid"] - 1 / (1 + np.exp(-x))).max() <= 4e-16
+    with np.errstate(over="ignore"):  # exp(745) is inf in numpy too: the reference sigmoid is then 0
+        assert np.abs(out["sigmoid"] - 1 / (1 + np.exp(-x))).max() <= 4e-16
     pos = np.abs(x) + 0.5
     r = _C.math_check(torch.from_numpy(pos).to(dev))["recip"].cpu().numpy()
     assert _ulp_err(r, 1.0 / pos).max() <= 1

@@ -81,7 +81,8 @@ def _oracle_tail(oracle, layer, backbone: np.ndarray, depth: int) -> np.ndarray:
     def prepare(hc, norm, streams, n_streams):
         return oracle.mhc_prepare(streams, _np(hc.dyn_norm.weight), hc.dyn_norm.eps,
                                   hc._projection_block().cpu().numpy(), _np(hc.pre_bias), _np(hc.post_bias),
-                                  _np(hc.res_bias), float(hc.pre_alpha), float(hc.post_alpha), float(hc.res_alpha),
+                                  _np(hc.res_bias), float(hc.pre_alpha.detach()), float(hc.post_alpha.detach()),
+                                  float(hc.res_alpha.detach()),
                                   hc.sinkhorn_iters, n_streams, _np(norm.weight), norm.eps)
 
     def ffn(x):
