@@ -1006,20 +1006,24 @@ struct NoChunkHooks {
 // given) likewise for the outputs: a.out [B, L, d_inner], or the current
 // chunk's rows at a.out + (t - c0) d_inner.
 // Every thread of the block runs the same sequence of barriers, so several
-// heads can share a block. PREP (TILE, one chunk, two waves): other waves of
-// the block have already formed the chunk's coefficients and tanh(angle) * pi
-// (before the barrier that ends hooks.before) and its decay weights (before
-// the barrier that ends step b), and, before the latter, the running angle
-// sums and the sin/cos of each (token, angle) pair at hooks.rotations()
-// ([C][N / 2] pairs): step a skips the dt/A/trap and angle columns, steps a
-// and b run without a barrier between them (the norm scales read the B/C rows
-// where hooks.before left them), both waves form their gates in step b, step
-// c skips the angle sums and step d reads the rotations.
+// heads can share a block. PREP (TILE, one chunk, the first and last; two
+// waves): other waves of the block have already formed the chunk's
+// coefficients and tanh(angle) * pi (before the barrier that ends
+// hooks.before); they form its decay weights before the barrier that ends
+// step d, and the running angle sums and the sin/cos of each (token, angle)
+// pair at hooks.rotations() ([C][N / 2] pairs) before hooks.wait_rotations()
+// returns. Step a skips the dt/A/trap and angle columns; steps a to d run
+// without a barrier: each wave forms the norm scales of the rows it scales
+// in step c (read from the B/C rows where hooks.before left them) and its
+// gates, and rotates those rows in step d; step c skips the angle sums. Step
+// e forms every G tile on every wave in registers, and step f reads them
+// there.
 template <int C, int NT, int DT, bool TILE, class Hooks, bool TILE_OUT = TILE, bool PREP = false>
 __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>& sh, int64_t b, int64_t h,
                                           int tid_base, const Hooks& hooks) {
     static_assert(C == 32, "the BCNorm step takes one lane per (token, B|C) pair of a 64-lane wave");
     static_assert(!PREP || (TILE && DT == 2), "PREP: the tiled two-wave scan");
+    static_assert(!PREP || NT == 1, "PREP: step c's rows of a wave are 4 wave + q + 8 j (N = 16, 128 threads)");
     constexpr int N = 16 * NT, D = 16 * DT, NTH = 64 * DT;
     constexpr int CT = C / 16;
     constexpr int NP = N + 4, WP = C + 4;
@@ -1103,9 +1107,12 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         // predicated store of its output (the last chunk's stores are guarded),
         // where the fp64 chains run one after another.
         double gz[CT][4];
+        // PREP: the wave forms the gates of token tile 0 only; those of tile 1 arrive from the other
+        // waves at hooks.late_gates() ([DT][4][64], the lane order of gz[1]) by the end of step d.
+        constexpr int GT = PREP ? 1 : CT;
         auto gates = [&]() {
 #pragma unroll
-            for (int tt = 0; tt < CT; ++tt)
+            for (int tt = 0; tt < GT; ++tt)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const double z = static_cast<double>(zx[tt][v]);
@@ -1113,7 +1120,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                     gz[tt][v] = a.gate_logits ? sz : z;
                 }
 #pragma unroll
-            for (int tt = 0; tt < CT; ++tt)
+            for (int tt = 0; tt < GT; ++tt)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(gz[tt][v]));
         };
@@ -1163,7 +1170,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                     const int t = 16 * st + 4 * g + v;
                     const int tc = t < Lc ? t : Lc - 1;
                     vx[st][v] = xc[static_cast<unsigned>(tc * st32 + col)];
-                    zx[st][v] = zc[static_cast<unsigned>(tc * gst32 + col)];
+                    if (st < GT) zx[st][v] = zc[static_cast<unsigned>(tc * gst32 + col)];
                 }
 #pragma unroll
             for (int j = 0; j < BU; ++j) {
@@ -1188,16 +1195,24 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         }
         if constexpr (!PREP) __syncthreads();
         // b. Norm scales, coefficients, tanh(angle) * pi.
-        if (tid < 2 * C) {
-            const int t = tid % C;
-            const bool isb = tid < C;
-            if constexpr (PREP) {  // the rows as step a copies them (tokens past the end read the last one)
+        if constexpr (PREP) {
+            // Each wave forms the scales of the rows its threads scale in step c (rows 4 wave + q +
+            // 8 j, q, j < 4), from the rows as step a copies them (tokens past the end read the last
+            // one): lanes 0..15 the B rows, 16..31 the C rows. Steps b and c then need no barrier.
+            if (lane < 32) {
+                const int k = lane & 15, t = 4 * wave + (k & 3) + 8 * (k >> 2);
+                const bool isb = lane < 16;
                 const int tc = t < Lc ? t : Lc - 1;
                 sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? brow : crow) + static_cast<int64_t>(tc) * a.st,
                                                              isb ? a.b_eps : a.c_eps);
-            } else {
-                sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? k_sh : q_sh) + t * NP, isb ? a.b_eps : a.c_eps);
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        } else if (tid < 2 * C) {
+            const int t = tid % C;
+            const bool isb = tid < C;
+            sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? k_sh : q_sh) + t * NP, isb ? a.b_eps : a.c_eps);
         }
         // The coefficient wave (wave 1, or wave 0 when the block has one wave)
         // goes on to the decay weights (decay_walk). tanh runs on the other waves.
@@ -1230,7 +1245,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         } else if constexpr (kEarlyGate) {
             if (wave == 0) gates();  // wave 1 runs the coefficients and decay weights meanwhile
         }
-        __syncthreads();
+        if constexpr (!PREP) __syncthreads();
         // c. q and k (all values read before any is written back); the
         //    running angle sums into cum_s; the decay weights.
         {
@@ -1268,38 +1283,59 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         if constexpr (kEarlyGate && !PREP) {
             if (wave == 1) gates();  // wave 0 runs the angle sums meanwhile
         }
-        __syncthreads();
-        // d. Rotation of the (2r, 2r + 1) pairs.
+        // d. Rotation of the (2r, 2r + 1) pairs. PREP: each wave rotates the rows it scaled in step
+        //    c, once the rotations are in (hooks.wait_rotations), with no barrier before.
+        auto rotate = [&](int t, int r, float sine, float cosine) {
+            float* qp = q_sh + t * NP + 2 * r;
+            float* kq = k_sh + t * NP + 2 * r;
+            const float ql = qp[0], qr = qp[1], kl = kq[0], kr = kq[1];
+            qp[0] = fmaf(ql, cosine, -(qr * sine));
+            qp[1] = fmaf(ql, sine, qr * cosine);
+            kq[0] = fmaf(kl, cosine, -(kr * sine));
+            kq[1] = fmaf(kl, sine, kr * cosine);
+        };
+        if constexpr (PREP) {
+            // The pairs were scaled in step c by other lanes of this wave.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            hooks.wait_rotations();
+            const float* rot = hooks.rotations();
 #pragma unroll 1
-        for (int i = tid; i < C * R; i += NTH) {
-            const int t = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - t * R;
-            {
+            for (int i = lane; i < 16 * R; i += 64) {
+                const int k = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - k * R;
+                const int t = 4 * wave + (k & 3) + 8 * (k >> 2);
+                rotate(t, r, rot[2 * (t * RM + r)], rot[2 * (t * RM + r) + 1]);
+            }
+        } else {
+            __syncthreads();
+#pragma unroll 1
+            for (int i = tid; i < C * R; i += NTH) {
+                const int t = static_cast<int>((static_cast<unsigned>(i) * rmagic) >> 16), r = i - t * R;
                 float sine, cosine;
-                if constexpr (PREP) {
-                    const float* rot = hooks.rotations() + 2 * (t * RM + r);
-                    sine = rot[0];
-                    cosine = rot[1];
-                } else {
-                    rotation_of(cum_s[t * RM + r], &sine, &cosine);
-                }
-                float* qp = q_sh + t * NP + 2 * r;
-                float* kq = k_sh + t * NP + 2 * r;
-                const float ql = qp[0], qr = qp[1], kl = kq[0], kr = kq[1];
-                qp[0] = fmaf(ql, cosine, -(qr * sine));
-                qp[1] = fmaf(ql, sine, qr * cosine);
-                kq[0] = fmaf(kl, cosine, -(kr * sine));
-                kq[1] = fmaf(kl, sine, kr * cosine);
+                rotation_of(cum_s[t * RM + r], &sine, &cosine);
+                rotate(t, r, sine, cosine);
             }
         }
         __syncthreads();
-        // e. Masked G^T tiles into LDS (tile pair p on wave p % DT); ck; k_p.
+        if constexpr (PREP) {
+            static_assert(CT == 2, "PREP: two token tiles");
+#pragma unroll
+            for (int v = 0; v < 4; ++v) gz[1][v] = hooks.late_gates()[(wave * 4 + v) * 64 + lane];
+        }
+        // e. Masked G^T tiles into LDS (tile pair p on wave p % DT); ck; k_p. PREP (one chunk, the
+        //    first and last): every wave forms every tile pair into registers (pg), the products and
+        //    rounding of the LDS form, and goes straight on to its outputs.
+        f32x4_t pg[PREP ? NPAIR : 1];
         {
             int p = 0;
 #pragma unroll
             for (int tt = 0; tt < CT; ++tt) {
 #pragma unroll
                 for (int st = 0; st <= tt; ++st, ++p) {
-                    if (p % DT != wave || 16 * tt >= Lc) continue;
+                    // (PREP forms every tile: rows past the end hold the last token's values, and
+                    // the tiles stay one straight block whose product chains interleave.)
+                    if (!PREP && (p % DT != wave || 16 * tt >= Lc)) continue;
                     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int nt = 0; nt < NT; ++nt) {
@@ -1316,21 +1352,67 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
 #pragma unroll
                         for (int v = 0; v < 4; ++v) pv[v] = 4 * g + v <= li ? pv[v] : 0.0f;
                     }
-                    p_s[p * 64 + lane] = pv;
+                    if constexpr (PREP)
+                        pg[p] = pv;
+                    else
+                        p_s[p * 64 + lane] = pv;
                 }
             }
         }
-        if (!first && wave == DT - 1 && lane < C) {  // (read for later chunks only)
-            float dot = 0.0f;
+        if constexpr (!PREP) {
+            if (!first && wave == DT - 1 && lane < C) {  // (read for later chunks only)
+                float dot = 0.0f;
 #pragma unroll
-            for (int n = 0; n < N; ++n) dot = fmaf(q_sh[lane * NP + n], kp_s[par][n], dot);
-            ck_s[lane] = dot * w_s[lane * WP + kWp];
+                for (int n = 0; n < N; ++n) dot = fmaf(q_sh[lane * NP + n], kp_s[par][n], dot);
+                ck_s[lane] = dot * w_s[lane * WP + kWp];
+            }
+            if (tid < N) kp_s[par ^ 1][tid] = k_sh[(C - 1) * NP + tid];
+            __syncthreads();
         }
-        if (tid < N) kp_s[par ^ 1][tid] = k_sh[(C - 1) * NP + tid];
-        __syncthreads();
         // f. This wave's output columns (gates formed above for two-wave
-        //    blocks, here otherwise).
-        {
+        //    blocks, here otherwise). PREP (the first chunk: no carried
+        //    state): every token tile's products first, then the outputs, so
+        //    the predicated stores do not split the product chains.
+        if constexpr (PREP) {
+            f32x4_t Y[CT];
+            int p0 = 0;
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt) {
+                Y[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st <= tt; ++st)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        Y[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pg[p0 + st][v], vx[st][v], Y[tt], 0, 0, 0);
+                p0 += tt + 1;
+            }
+            float o[CT][4];
+#pragma unroll
+            for (int tt = 0; tt < CT; ++tt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float y = fmaf(skip, vx[tt][v], Y[tt][v]);
+                    o[tt][v] = static_cast<float>(static_cast<double>(y) * gz[tt][v]);
+                }
+            // 32-bit row offsets from this lane's column (C rows of d_inner floats); a whole chunk
+            // stores without per-lane predication.
+            float* ocol = orow + col;
+            const int di = static_cast<int>(d_inner);
+            if (Lc == C) {
+#pragma unroll
+                for (int tt = 0; tt < CT; ++tt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) ocol[static_cast<unsigned>((16 * tt + 4 * g + v) * di)] = o[tt][v];
+            } else {
+#pragma unroll
+                for (int tt = 0; tt < CT; ++tt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int t = 16 * tt + 4 * g + v;
+                        if (t < Lc) ocol[static_cast<unsigned>(t * di)] = o[tt][v];
+                    }
+            }
+        } else {
             if constexpr (!kEarlyGate) gates();
             int p0 = 0;  // index of pair (tt, 0)
 #pragma unroll
@@ -1493,7 +1575,7 @@ struct BlockArgs {
 // chunk's step coefficients and then its decay weights, helper 1 tanh(angle)
 // * pi, while the scan waves copy their rows, form the norm scales and the
 // gates (scan_head's PREP form). The helpers end after the barrier that ends
-// step b; S_BARRIER then waits on the surviving waves only.
+// step d; S_BARRIER then waits on the surviving waves only.
 template <int NT, int DT, int KSI, int GS, int NCT, bool ALL_LIVE, bool HELP>
 __global__ __launch_bounds__(64 * DT * (HELP ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(1)))
 void mamba3_block_scan_kernel(BlockArgs p) {
@@ -1504,6 +1586,8 @@ void mamba3_block_scan_kernel(BlockArgs p) {
     __shared__ ScanLds<C, NT, DT> sh;
     constexpr int HP = 17;  // helper staging: [32 rows][16 columns], rows HP floats apart
     __shared__ float hs[HELP ? DT : 1][HELP ? C * HP : 1];
+    __shared__ int rot_ready;  // HELP: set by helper 1 once the rotations are in hs[1]
+    __shared__ double lg[HELP ? DT * 4 * 64 : 1];  // HELP: the gates of token tile 1, [scan wave][v][lane]
     extern __shared__ __attribute__((aligned(16))) float proj_s[];  // [C, pp]
 
     const int64_t H = p.s.H, L = p.s.L;
@@ -1642,9 +1726,20 @@ void mamba3_block_scan_kernel(BlockArgs p) {
         }
         __device__ void after(int64_t, bool) const {}
         __device__ const float* rotations() const { return rot; }
+        // The scan waves' wait for helper 1's rotations: it sets the flag after writing them, with
+        // nothing in between that waits on the scan waves, so the wait ends.
+        __device__ void wait_rotations() const {
+            while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+                __builtin_amdgcn_s_sleep(1);
+        }
+        __device__ const double* late_gates() const { return late; }
         const float* rot;
+        int* ready;
+        const double* late;
     };
-    const Hooks hooks{p, xw, proj_s, w_lds, L, li, grp, wave, dm, W, DI, pp, static_cast<int>(h), &hs[HELP ? 1 : 0][0]};
+    if (threadIdx.x == 0) rot_ready = 0;  // read after the in_proj barrier, set after it
+    const Hooks hooks{p,  xw, proj_s, w_lds, L,  li, grp, wave, dm, W, DI, pp, static_cast<int>(h), &hs[HELP ? 1 : 0][0],
+                      &rot_ready, lg};
     if constexpr (HELP) {
         if (wave >= DT) {
             // The last column tile (dt, A, trap logits, angles) for both row tiles into this helper's
@@ -1724,8 +1819,18 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                     const int t = i / R, rr = i - t * R;
                     rotation_of(sh.cum_s[t * RM + rr], &rot[2 * (t * RM + rr)], &rot[2 * (t * RM + rr) + 1]);
                 }
+                __hip_atomic_store(&rot_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
-            __syncthreads();  // with the end of the scan waves' step b: decay weights and rotations are in
+            // Helper hw forms the gates of token tile 1 for scan wave hw's lanes (tokens 16 + 4 grp +
+            // v, head column 16 hw + li), as scan_head forms them from z (the head's first columns of
+            // the rows; tokens past the end read the last one).
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int t = 16 + 4 * grp + v, tc = t < Lc ? t : Lc - 1;
+                const double z = static_cast<double>(proj_s[tc * pp + static_cast<int>(h) * D + 16 * hw + li]);
+                lg[(hw * 4 + v) * 64 + lane] = z / (1.0 + exp_d(-z));
+            }
+            __syncthreads();  // with the end of the scan waves' step d: the decay weights and gates are in
             return;
         }
     }
