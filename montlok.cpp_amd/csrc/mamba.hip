@@ -992,6 +992,11 @@ struct ScanLds {
 };
 
 // Called by every thread of the block around each chunk of the scan.
+// PREP's split of the output gates: a scan wave forms those of token tile 0
+// and of v < kPrepOwnV in tile 1 (token 16 + 4 g + v); the rest arrive at
+// hooks.late_gates(), [DT][4 - kPrepOwnV][64] in lane order.
+constexpr int kPrepOwnV = 2;
+
 struct NoChunkHooks {
     __device__ void before(int64_t) const {}
     __device__ void after(int64_t, bool) const {}
@@ -1007,7 +1012,7 @@ struct NoChunkHooks {
 // chunk's rows at a.out + (t - c0) d_inner.
 // Every thread of the block runs the same sequence of barriers, so several
 // heads can share a block. PREP (TILE, one chunk, the first and last; two
-// waves): other waves of the block have already formed the chunk's
+// waves; the gate columns in the projection rows, a.gst = a.st): other waves of the block have already formed the chunk's
 // coefficients and tanh(angle) * pi (before the barrier that ends
 // hooks.before); they form its decay weights before the barrier that ends
 // step d, and the running angle sums and the sin/cos of each (token, angle)
@@ -1107,28 +1112,34 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         // predicated store of its output (the last chunk's stores are guarded),
         // where the fp64 chains run one after another.
         double gz[CT][4];
-        // PREP: the wave forms the gates of token tile 0 only; those of tile 1 arrive from the other
-        // waves at hooks.late_gates() ([DT][4][64], the lane order of gz[1]) by the end of step d.
-        constexpr int GT = PREP ? 1 : CT;
+        // PREP: the wave forms the gates of (token tile, v) pairs own(tt, v); the others arrive from
+        // the other waves at hooks.late_gates() by the end of step d.
+        auto own = [](int tt, int v) { return !PREP || tt == 0 || v < kPrepOwnV; };
         auto gates = [&]() {
 #pragma unroll
-            for (int tt = 0; tt < GT; ++tt)
+            for (int tt = 0; tt < CT; ++tt)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
+                    if (!own(tt, v)) continue;
                     const double z = static_cast<double>(zx[tt][v]);
                     const double sz = z / (1.0 + exp_d(-z));
                     gz[tt][v] = a.gate_logits ? sz : z;
                 }
 #pragma unroll
-            for (int tt = 0; tt < GT; ++tt)
+            for (int tt = 0; tt < CT; ++tt)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(gz[tt][v]));
+                for (int v = 0; v < 4; ++v)
+                    if (own(tt, v)) asm volatile("" : "+v"(gz[tt][v]));
         };
         // a. Every global load of the chunk issued before the first wait
         //    (tokens past the end read the last token; they carry no weight).
         //    Offsets are 32-bit from the chunk's first row (checked at launch).
+        //    PREP reads the tile's rows unclamped: its rows past the end hold
+        //    the last token's values already (hooks.before clamps its x rows),
+        //    and keeps this thread's B/C values in bx/cx for step c.
+        constexpr int BU = C * N / NTH;
+        float bx[BU], cx[BU];
         {
-            constexpr int BU = C * N / NTH;
             constexpr int MU = (3 * C + NTH - 1) / NTH;
             constexpr int AU = (C * RM + NTH - 1) / NTH;
             const int st32 = static_cast<int>(a.st), gst32 = static_cast<int>(a.gst);
@@ -1139,11 +1150,16 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
             const float* ac = arow + cr;
             const float* xc = xrow + cr;
             const float* zc = zrow + cg;
-            float bx[BU], cx[BU], mx[MU], ax[AU];
+            float mx[MU], ax[AU];
+            // PREP offsets: a per-lane base plus a multiple of the row stride that is the same for
+            // every lane, so no per-lane multiply per load.
+            const unsigned pb0 = static_cast<unsigned>((tid / N) * st32 + n_own);
+            const unsigned px0 = static_cast<unsigned>(4 * g * st32 + col);
 #pragma unroll
             for (int j = 0; j < BU; ++j) {
                 const int t = (tid + NTH * j) / N;
-                const unsigned off = static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + n_own);
+                const unsigned off = PREP ? pb0 + static_cast<unsigned>(j * (NTH / N) * st32)
+                                          : static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + n_own);
                 bx[j] = bc[off];
                 cx[j] = cc[off];
             }
@@ -1169,11 +1185,18 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 for (int v = 0; v < 4; ++v) {
                     const int t = 16 * st + 4 * g + v;
                     const int tc = t < Lc ? t : Lc - 1;
-                    vx[st][v] = xc[static_cast<unsigned>(tc * st32 + col)];
-                    if (st < GT) zx[st][v] = zc[static_cast<unsigned>(tc * gst32 + col)];
+                    if constexpr (PREP) {  // (the gate rows are the projection rows: gate = proj)
+                        const unsigned off = px0 + static_cast<unsigned>((16 * st + v) * st32);
+                        vx[st][v] = xc[off];
+                        if (own(st, v)) zx[st][v] = zc[off];
+                    } else {
+                        vx[st][v] = xc[static_cast<unsigned>(tc * st32 + col)];
+                        zx[st][v] = zc[static_cast<unsigned>(tc * gst32 + col)];
+                    }
                 }
 #pragma unroll
             for (int j = 0; j < BU; ++j) {
+                if constexpr (PREP) break;
                 const int t = (tid + NTH * j) / N;
                 k_sh[t * NP + n_own] = bx[j];
                 q_sh[t * NP + n_own] = cx[j];
@@ -1197,13 +1220,12 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         // b. Norm scales, coefficients, tanh(angle) * pi.
         if constexpr (PREP) {
             // Each wave forms the scales of the rows its threads scale in step c (rows 4 wave + q +
-            // 8 j, q, j < 4), from the rows as step a copies them (tokens past the end read the last
-            // one): lanes 0..15 the B rows, 16..31 the C rows. Steps b and c then need no barrier.
+            // 8 j, q, j < 4), from the rows step a reads: lanes 0..15 the B rows, 16..31 the C rows.
+            // Steps b and c then need no barrier.
             if (lane < 32) {
                 const int k = lane & 15, t = 4 * wave + (k & 3) + 8 * (k >> 2);
                 const bool isb = lane < 16;
-                const int tc = t < Lc ? t : Lc - 1;
-                sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? brow : crow) + static_cast<int64_t>(tc) * a.st,
+                sc_s[isb ? 0 : 1][t] = bc_norm_scale_rows<N>((isb ? brow : crow) + t * static_cast<int>(a.st),
                                                              isb ? a.b_eps : a.c_eps);
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1254,8 +1276,8 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
 #pragma unroll
             for (int j = 0; j < QU; ++j) {
                 const int t = (tid + NTH * j) / N, i = t * NP + n_own;
-                kv[j] = k_sh[i];
-                qv[j] = q_sh[i];
+                kv[j] = PREP ? bx[j] : k_sh[i];
+                qv[j] = PREP ? cx[j] : q_sh[i];
                 skb[j] = sc_s[0][t];
                 sqb[j] = sc_s[1][t];
             }
@@ -1321,7 +1343,8 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         if constexpr (PREP) {
             static_assert(CT == 2, "PREP: two token tiles");
 #pragma unroll
-            for (int v = 0; v < 4; ++v) gz[1][v] = hooks.late_gates()[(wave * 4 + v) * 64 + lane];
+            for (int v = kPrepOwnV; v < 4; ++v)
+                gz[1][v] = hooks.late_gates()[(wave * (4 - kPrepOwnV) + v - kPrepOwnV) * 64 + lane];
         }
         // e. Masked G^T tiles into LDS (tile pair p on wave p % DT); ck; k_p. PREP (one chunk, the
         //    first and last): every wave forms every tile pair into registers (pg), the products and
@@ -1587,7 +1610,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
     constexpr int HP = 17;  // helper staging: [32 rows][16 columns], rows HP floats apart
     __shared__ float hs[HELP ? DT : 1][HELP ? C * HP : 1];
     __shared__ int rot_ready;  // HELP: set by helper 1 once the rotations are in hs[1]
-    __shared__ double lg[HELP ? DT * 4 * 64 : 1];  // HELP: the gates of token tile 1, [scan wave][v][lane]
+    __shared__ double lg[HELP ? DT * (4 - kPrepOwnV) * 64 : 1];  // HELP: the scan waves' late gates
     extern __shared__ __attribute__((aligned(16))) float proj_s[];  // [C, pp]
 
     const int64_t H = p.s.H, L = p.s.L;
@@ -1821,14 +1844,13 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 }
                 __hip_atomic_store(&rot_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
-            // Helper hw forms the gates of token tile 1 for scan wave hw's lanes (tokens 16 + 4 grp +
-            // v, head column 16 hw + li), as scan_head forms them from z (the head's first columns of
-            // the rows; tokens past the end read the last one).
+            // Helper hw forms the late gates of scan wave hw's lanes (token tile 1, v >= kPrepOwnV:
+            // tokens 16 + 4 grp + v, head column 16 hw + li), as scan_head forms them from z (the
+            // head's first columns of the rows; the tile's rows past the end hold the last token's).
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int t = 16 + 4 * grp + v, tc = t < Lc ? t : Lc - 1;
-                const double z = static_cast<double>(proj_s[tc * pp + static_cast<int>(h) * D + 16 * hw + li]);
-                lg[(hw * 4 + v) * 64 + lane] = z / (1.0 + exp_d(-z));
+            for (int v = kPrepOwnV; v < 4; ++v) {
+                const double z = static_cast<double>(proj_s[(16 + 4 * grp + v) * pp + static_cast<int>(h) * D + 16 * hw + li]);
+                lg[(hw * (4 - kPrepOwnV) + v - kPrepOwnV) * 64 + lane] = z / (1.0 + exp_d(-z));
             }
             __syncthreads();  // with the end of the scan waves' step d: the decay weights and gates are in
             return;
