@@ -1658,14 +1658,19 @@ void mamba3_block_scan_kernel(BlockArgs p) {
         // at once, each row read from L2 once per block instead of once per
         // wave); row r of tile j holds its 16-byte chunk c at slot c ^ r, so
         // the 16 lanes of a fragment read hit 16 different bank groups.
-        __device__ void stage(int ncol) const {
+        // stage_issue puts the copies in flight (a compile-time count per wave, so the waits the
+        // compiler places for the x fragments leave them outstanding: the norm of x runs while they
+        // land); stage_wait waits for them and for the other waves'.
+        __device__ void stage_issue(int ncol) const {
             if constexpr (STAGE) {
                 static_assert(KSI == 2 && ALL_LIVE, "staging takes d_model 64 rows: 16 chunks of 16 bytes");
                 constexpr int NW = HELP ? 2 * DT : DT;
+                static_assert((4 * NCT) % NW == 0, "every wave issues the same number of quarter tiles");
                 const int lane = threadIdx.x & 63;
                 const int rq = lane >> 4, slot = lane & 15;
-#pragma unroll 1
-                for (int u = wave; u < 4 * NCT; u += NW) {  // quarter-tile u: tile u / 4, rows 4 (u % 4) ..
+#pragma unroll
+                for (int k = 0; k < 4 * NCT / NW; ++k) {  // quarter-tile u: tile u / 4, rows 4 (u % 4) ..
+                    const int u = wave + k * NW;
                     const int j = u >> 2, row = 4 * (u & 3) + rq;
                     const int n = tile_col(j < ncol ? j : ncol - 1) + row;
                     const float* src = p.in_w + static_cast<int64_t>(n < W ? n : W - 1) * 64 + 4 * (slot ^ row);
@@ -1673,6 +1678,10 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                         (const __attribute__((address_space(1))) void*)src,
                         (__attribute__((address_space(3))) void*)(w_lds + u * 256), 16, 0, 0);
                 }
+            }
+        }
+        __device__ void stage_wait() const {
+            if constexpr (STAGE) {
                 __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the LDS copies have landed
                 __syncthreads();
             }
@@ -1714,7 +1723,13 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             const int64_t r = c0 + 16 * rt + li;
             tile_load8<KSI>(xw + (r < L ? r : L - 1) * p.x_ts, dm, grp, xv, live);
             tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
-            if (c0 == 0) stage(ncol);
+            // (HELP runs one chunk, c0 = 0: no branch, so the compiler's wait for x leaves the
+            // copies outstanding.)
+            if (HELP || c0 == 0) stage_issue(ncol);
+            if constexpr (STAGE) {
+                tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);  // while the weight rows land
+                if (HELP || c0 == 0) stage_wait();
+            }
             float wv[NTW][KSI][8];
             bool wlive[NTW][KSI];
 #pragma unroll
@@ -1730,8 +1745,8 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                     for (int k = 0; k < 8; ++k)
 #pragma unroll
                         for (int i = 0; i < NTW; ++i) asm volatile("" : "+v"(wv[i][s2][k]));
+                tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);
             }
-            tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);
             auto put = [&](int i, tile_f32x4 y) {
                 const int j = j0 + i * jstep;
                 y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
@@ -1779,11 +1794,13 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 tile_load8<KSI>(xw + (r < L ? r : L - 1) * p.x_ts, dm, grp, xv[rt], live[rt]);
             }
             tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
-            hooks.stage(ncol);
+            hooks.stage_issue(ncol);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) tile_rms_norm<KSI, GS>(xv[rt], nw, p.norm_eps);
+            hooks.stage_wait();
             hooks.weights(j, ncol, wv, wlive);
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
-                tile_rms_norm<KSI, GS>(xv[rt], nw, p.norm_eps);
                 tile_f32x4 y = tile_mfma_f32<KSI, ALL_LIVE>(wv, xv[rt], live[rt]);
                 y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
 #pragma unroll
