@@ -1593,12 +1593,14 @@ struct BlockArgs {
 
 // HELP (one chunk, L <= 32; the dt/A/trap/angle columns one column tile, the
 // last): the block has DT more waves. The DT scan waves compute the other
-// column tiles of their row tile (wave w: rows 16 w .. 16 w + 15); each
-// helper computes the last tile for all 32 rows and, from it, helper 0 the
-// chunk's step coefficients and then its decay weights, helper 1 tanh(angle)
-// * pi, while the scan waves copy their rows, form the norm scales and the
-// gates (scan_head's PREP form). The helpers end after the barrier that ends
-// step d; S_BARRIER then waits on the surviving waves only.
+// column tiles of their row tile (wave w: rows 16 w .. 16 w + 15) but the
+// last two; each helper computes the last tile for all 32 rows (helper 1 the
+// second-to-last beside it) and, from it, helper 0 the chunk's step
+// coefficients and then its decay weights, helper 1 tanh(angle) * pi, then
+// the running angle sums and rotations, and both some of the gates, while the
+// scan waves copy their rows, form the norm scales and the other gates
+// (scan_head's PREP form). The helpers end after the barrier that ends step
+// d; S_BARRIER then waits on the surviving waves only.
 template <int NT, int DT, int KSI, int GS, int NCT, bool ALL_LIVE, bool HELP>
 __global__ __launch_bounds__(64 * DT * (HELP ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(1)))
 void mamba3_block_scan_kernel(BlockArgs p) {
@@ -1680,6 +1682,14 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 }
             }
         }
+        // The normalised fragments are pinned before the barrier: left to itself the compiler
+        // schedules part of the norm after it, where it delays the first products.
+        __device__ static void hold(float (&v)[KSI][8]) {
+#pragma unroll
+            for (int s2 = 0; s2 < KSI; ++s2)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(v[s2][k]));
+        }
         __device__ void stage_wait() const {
             if constexpr (STAGE) {
                 __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the LDS copies have landed
@@ -1710,12 +1720,12 @@ void mamba3_block_scan_kernel(BlockArgs p) {
         // The chunk's in_proj tiles into proj_s, then a barrier. Without
         // HELP, wave w computes the chunk's 16-row tile w % 2 against the
         // head's column tiles j = w / 2, w / 2 + NW / 2, ... (NW = DT); with
-        // HELP (scan waves only), row tile w against every tile but the last.
+        // HELP (scan waves only), row tile w against every tile but the last two.
         // The tiles past the head's count repeat its last one and are not
         // stored. Every wave normalises its x fragments once; all of its
         // weight loads are in flight before the first wait.
         __device__ void before(int64_t c0) const {
-            constexpr int NTW = HELP ? NCT - 1 : (NCT + DT / 2 - 1) / (DT / 2);  // column tiles per wave
+            constexpr int NTW = HELP ? NCT - 2 : (NCT + DT / 2 - 1) / (DT / 2);  // column tiles per wave
             const int ncol = 2 * (D / 16) + (W - 2 * DI + 15) / 16;
             const int rt = HELP ? wave : wave & 1, j0 = HELP ? 0 : wave >> 1, jstep = HELP ? 1 : DT / 2;
             float xv[KSI][8], nw[KSI][8];
@@ -1728,6 +1738,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             if (HELP || c0 == 0) stage_issue(ncol);
             if constexpr (STAGE) {
                 tile_rms_norm<KSI, GS>(xv, nw, p.norm_eps);  // while the weight rows land
+                hold(xv);
                 if (HELP || c0 == 0) stage_wait();
             }
             float wv[NTW][KSI][8];
@@ -1796,12 +1807,28 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             tile_load8<KSI>(p.norm_w, dm, grp, nw, nlive);
             hooks.stage_issue(ncol);
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) tile_rms_norm<KSI, GS>(xv[rt], nw, p.norm_eps);
+            for (int rt = 0; rt < 2; ++rt) {
+                tile_rms_norm<KSI, GS>(xv[rt], nw, p.norm_eps);
+                hooks.hold(xv[rt]);
+            }
             hooks.stage_wait();
             hooks.weights(j, ncol, wv, wlive);
+            // Helper 1 also computes the second-to-last tile (the C rows) for both row tiles, its
+            // chains interleaved with the last tile's; the scan waves skip it.
+            float wc[KSI][8];
+            bool wclive[KSI];
+            if (hw == 1) hooks.weights(j - 1, ncol, wc, wclive);
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
-                tile_f32x4 y = tile_mfma_f32<KSI, ALL_LIVE>(wv, xv[rt], live[rt]);
+                tile_f32x4 y;
+                if (hw == 1) {
+                    tile_f32x4 yc;
+                    tile_mfma_f32_pair<KSI, ALL_LIVE>(wv, wc, xv[rt], live[rt], y, yc);
+                    yc += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
+                    *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + hooks.tile_col(j - 1) + 4 * grp) = yc;
+                } else {
+                    y = tile_mfma_f32<KSI, ALL_LIVE>(wv, xv[rt], live[rt]);
+                }
                 y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
 #pragma unroll
                 for (int v = 0; v < 4; ++v) hs[hw][(16 * rt + li) * HP + 4 * grp + v] = y[v];
@@ -1891,7 +1918,7 @@ bool launch_block_scan(const BlockArgs& p, int64_t N, int64_t D, int64_t gs, hip
 #define MLK_BLOCK(NV, DV, KSIV, GSV, NCTV)                                                                       \
     if (N == NV && D == DV && ksi == KSIV && gs == GSV && ncol <= NCTV) {                                         \
         const bool all_live = p.dm == 32 * KSIV,                                                                 \
-                   help = p.s.L <= 32 && p.s.G * NV == 16 && 3 * p.s.H + p.s.R <= 16;                            \
+                   help = p.s.L <= 32 && p.s.G * NV == 16 && 3 * p.s.H + p.s.R <= 16 && ncol == NCTV;            \
         if (all_live && help) {                                                                                  \
             hipLaunchKernelGGL((mamba3_block_scan_kernel<NV / 16, DV / 16, KSIV, GSV, NCTV, true, true>), grid,   \
                                dim3(8 * DV), lds, stream, p);                                                     \
