@@ -222,6 +222,27 @@ mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_
                            int64_t head_dim, int64_t nope_dim, int64_t kv_rank, int32_t weight_dtype, double scale,
                            float* out, mlk_stream_t stream);
 
+/* The three bf16 weights of mlk_mla_forward re-laid in its kernel's fragment
+ * order, for mlk_mla_forward_packed (no counterpart in the reference: a copy a
+ * caller makes once per weight update and keeps). In the row-major layout each
+ * fragment load of the kernel reads 16 rows' 64-byte pieces; every block reads
+ * all three weights, and those loads bounded the kernel's start and its last
+ * head round. mlk_mla_packed_elems: bf16 elements of the packed copy for the
+ * geometry, 0 where the per-window kernel is not built for it.
+ * mlk_mla_pack_weights writes it (16-byte aligned buffers; MLK_ERR_UNSUPPORTED
+ * for other geometries or dtypes). mlk_mla_forward_packed is mlk_mla_forward
+ * with the packed copy in place of the three weights: same conditions, the
+ * same result bit for bit. */
+int64_t mlk_mla_packed_elems(int64_t d_model, int64_t heads, int64_t head_dim, int64_t nope_dim, int64_t kv_rank);
+mlk_status mlk_mla_pack_weights(const void* in_proj_weight, const void* kv_up_weight, const void* out_weight,
+                                int64_t d_model, int64_t heads, int64_t head_dim, int64_t nope_dim, int64_t kv_rank,
+                                int32_t weight_dtype, void* packed, mlk_stream_t stream);
+mlk_status mlk_mla_forward_packed(const float* x, int64_t batch, int64_t length, int64_t d_model,
+                                  int64_t x_batch_stride, int64_t x_token_stride, const void* packed_weights,
+                                  const float* kv_norm_w, const float* kv_norm_b, double kv_norm_eps,
+                                  const float* cosine, const float* sine, int64_t heads, int64_t head_dim,
+                                  int64_t nope_dim, int64_t kv_rank, double scale, float* out, mlk_stream_t stream);
+
 /* ----------------------------------------------------------------- mHC -- */
 
 /* mhc_prepare(streams, norm_w, eps, proj_w, pre_bias, post_bias, res_bias,

@@ -30,6 +30,8 @@
 //         accumulation and fp32 softmax (bf16-weight configurations).
 //   FP32: v_mfma_f32_16x16x4_f32, fp32 throughout (fp32 configurations).
 
+#include <initializer_list>
+
 #include "mlk_common.h"
 
 namespace mlk {
@@ -837,6 +839,36 @@ void mla_attend_kernel(MlaAttendArgs p) {
 // The x / q / attention tile is [128 rows x 256] bf16 with 16-byte units
 // XOR-swizzled by the row (unit u of row r at u ^ (r mod 8)), so the MFMA
 // fragment reads (16 rows, one unit each per lane group) are conflict-free.
+//
+// PACKED: the three weights come re-laid in the kernel's fragment order
+// (mla_pack_kernel), so that a wave's fragment load is one contiguous 1 KB
+// read: in the row-major layout it touches 16 rows' 64-byte pieces, and with
+// every block fetching the whole of each weight from L2 those loads bounded
+// the kernel's start (in_proj fragments) and its last head round (o_proj
+// fragments).
+// Row order of the rope tiles: column 4g + v of a tile is rope dim 2g, 2g + 8,
+// 2g + 1, 2g + 9 for v = 0..3, so a lane holds each dim with its
+// rotate_half partner (dim +- 8).
+__device__ __forceinline__ int mla_rope_order(int c) { return 2 * (c >> 2) + ((c >> 1) & 1) + 8 * (c & 1); }
+
+// The packed weights of mla_window_kernel<H, true>, in 16-byte units (8 bf16):
+// in_proj unit (tile * D / 32 + s) * 64 + lane holds W_in row 16 tile + r,
+// k = 32 s + 8 (lane / 16) .. + 7, with r = lane % 16, or mla_rope_order of
+// it for the rope tiles (each head's q rope tile 2h + 1 and the k_rope tile
+// 2H + 4); then the kv_up rows, unit ((head * CT + ct) * KV / 32 + ks) * 64 +
+// lane = row head * UPW + 16 ct + r, k = 32 ks + 8 (lane / 16); then the
+// out_proj rows, unit (tile * D / 32 + s) * 64 + lane = row 16 tile + r.
+template <int H>
+struct MlaPack {
+    static constexpr int HD = 32, NOPE = 16, ROPE = 16, KV = 64, D = H * HD, UPW = NOPE + HD, CT = UPW / 16;
+    static constexpr int IN_TILES = (D + KV + ROPE) / 16;
+    static constexpr int IN_UNITS = IN_TILES * (D / 32) * 64;
+    static constexpr int UP_UNITS = H * CT * (KV / 32) * 64;
+    static constexpr int OUT_UNITS = (D / 16) * (D / 32) * 64;
+    static constexpr int UNITS = IN_UNITS + UP_UNITS + OUT_UNITS;
+    __device__ static bool rope_tile(int tile) { return (tile < 2 * H && (tile & 1) != 0) || tile == 2 * H + KV / 16; }
+};
+
 struct MlaWindowArgs {
     const float* x;  // [B, L, D], tokens x_ts apart, windows x_bs apart
     int64_t x_bs, x_ts;
@@ -853,7 +885,7 @@ struct MlaWindowArgs {
     float scale_log2;
 };
 
-template <int H>
+template <int H, bool PACKED>
 __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     constexpr int HD = 32, NOPE = 16, ROPE = 16, KV = 64;  // rope pairs (i, i + 8)
     constexpr int D = H * HD;
@@ -863,6 +895,9 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     constexpr int SLOT = 2 * LMAX * HD;  // one head's k [keys, HD] and v^T [HD, keys], bf16, swizzled
     constexpr int HG = 4;                // heads at a time, two waves each
     static_assert(H == 8, "the wave -> column tile map assumes 8 heads on 8 waves");
+    static_assert(MlaPack<H>::HD == HD && MlaPack<H>::NOPE == NOPE && MlaPack<H>::ROPE == ROPE &&
+                      MlaPack<H>::KV == KV && MlaPack<H>::UPW == UPW,
+                  "the packed layout's geometry");
     __shared__ __attribute__((aligned(16))) u16 xq_s[LMAX * D];
     __shared__ __attribute__((aligned(16))) u16 lat_s[LMAX * LP];
     __shared__ __attribute__((aligned(16))) u16 kr_s[LMAX * ROPE];
@@ -886,7 +921,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     // the tile is rope dim 2g, 2g + 8, 2g + 1, 2g + 9 for v = 0..3, so the lane that holds a dim also
     // holds its rotate_half partner (dim +- 8). Each output element still comes from its own W row and x
     // row by the same chain of products, so the values are the linear's.
-    auto rp = [](int c) { return 2 * (c >> 2) + ((c >> 1) & 1) + 8 * (c & 1); };
+    auto rp = [](int c) { return mla_rope_order(c); };
     auto pack2 = [](float a, float b) -> uint32_t {  // two bf16 (round to nearest even) in one word
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
     };
@@ -921,7 +956,9 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         for (int t = 0; t < 3; ++t)
 #pragma unroll
             for (int s = hf * SH; s < (hf + 1) * SH; ++s)
-                wf[t][s] = *reinterpret_cast<const uint4*>(p.w_in + (16 * tiles[t] + wrow[t]) * D + 32 * s + 8 * g);
+                wf[t][s] = *reinterpret_cast<const uint4*>(
+                    PACKED ? p.w_in + ((tiles[t] * (D / 32) + s) * 64 + lane) * 8
+                           : p.w_in + (16 * tiles[t] + wrow[t]) * D + 32 * s + 8 * g);
     }
     // cos/sin of every row into LDS as doubles, converted once for all heads (the upper half of the head
     // slots, free until the heads run; the fp32 latent takes the lower half): thread t takes 4 values of
@@ -1073,7 +1110,9 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int ks = 0; ks < KV / 32; ++ks)
-            wu[ct][ks] = *reinterpret_cast<const uint4*>(p.w_up + (grp * UPW + 16 * ct + li) * KV + 32 * ks + 8 * g);
+            wu[ct][ks] = *reinterpret_cast<const uint4*>(
+                PACKED ? p.w_up + (((grp * CT + ct) * (KV / 32) + ks) * 64 + lane) * 8
+                       : p.w_up + (grp * UPW + 16 * ct + li) * KV + 32 * ks + 8 * g);
 
     // 4. kv_norm: LayerNorm of the latent rows into bf16 with mla_attend_kernel's arithmetic: per group of
     // four columns (a + b) + (c + d) in fp64, the row's 16 groups combined by the butterfly xor 8, 4, 2, 1
@@ -1172,8 +1211,9 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
             for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
                 for (int ks = 0; ks < KV / 32; ++ks)
-                    wu[ct][ks] = *reinterpret_cast<const uint4*>(p.w_up + ((h + HG) * UPW + 16 * ct + li) * KV +
-                                                                 32 * ks + 8 * g);
+                    wu[ct][ks] = *reinterpret_cast<const uint4*>(
+                        PACKED ? p.w_up + ((((h + HG) * CT + ct) * (KV / 32) + ks) * 64 + lane) * 8
+                               : p.w_up + ((h + HG) * UPW + 16 * ct + li) * KV + 32 * ks + 8 * g);
         }
         __syncthreads();
         if (r + 1 == H / HG) {
@@ -1181,7 +1221,9 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int s = 0; s < D / 32; ++s)
-                    wo[t][s] = *reinterpret_cast<const uint4*>(p.w_out + (16 * (2 * wave + t) + li) * D + 32 * s + 8 * g);
+                    wo[t][s] = *reinterpret_cast<const uint4*>(
+                        PACKED ? p.w_out + (((2 * wave + t) * (D / 32) + s) * 64 + lane) * 8
+                               : p.w_out + (16 * (2 * wave + t) + li) * D + 32 * s + 8 * g);
         }
         // Causal attention (top-left) of head h: query tiles (wg, 7 - wg, wg + 2, 5 - wg), 16 rows each,
         // against key chunk 0 (keys 0..63) and, for the tiles past row 63 when L > 64, chunk 1 (keys
@@ -1350,6 +1392,32 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     }
 }
 
+
+// The weights of mla_window_kernel<H, true> into the MlaPack layout, one 16-byte
+// unit per thread (a copy: every unit is one unit of the row-major weight).
+template <int H>
+__global__ __launch_bounds__(256) void mla_pack_kernel(const u16* w_in, const u16* w_up, const u16* w_out, u16* packed) {
+    using P = MlaPack<H>;
+    const int u = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    if (u >= P::UNITS) return;
+    const int lane = u % 64, r = lane % 16, g = lane / 16;
+    constexpr int KS = P::D / 32, US = P::KV / 32;
+    const u16* src;
+    if (u < P::IN_UNITS) {
+        const int tile = u / (KS * 64), s = (u / 64) % KS;
+        src = w_in + (16 * tile + (P::rope_tile(tile) ? mla_rope_order(r) : r)) * P::D + 32 * s + 8 * g;
+    } else if (u < P::IN_UNITS + P::UP_UNITS) {
+        const int v = u - P::IN_UNITS;
+        const int head = v / (P::CT * US * 64), ct = (v / (US * 64)) % P::CT, ks = (v / 64) % US;
+        src = w_up + (head * P::UPW + 16 * ct + r) * P::KV + 32 * ks + 8 * g;
+    } else {
+        const int v = u - P::IN_UNITS - P::UP_UNITS;
+        const int tile = v / (KS * 64), s = (v / 64) % KS;
+        src = w_out + (16 * tile + r) * P::D + 32 * s + 8 * g;
+    }
+    reinterpret_cast<uint4*>(packed)[u] = *reinterpret_cast<const uint4*>(src);
+}
+
 }  // namespace
 }  // namespace mlk
 
@@ -1512,16 +1580,17 @@ extern "C" mlk_status mlk_mla_attend_normed(const float* projected, int64_t batc
     return launch_status("mla_attend_normed");
 }
 
-extern "C" mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_t d_model,
-                                      int64_t x_batch_stride, int64_t x_token_stride, const void* in_proj_weight,
-                                      const float* kv_norm_w, const float* kv_norm_b, double kv_norm_eps,
-                                      const void* kv_up_weight, const void* out_weight, const float* cosine,
-                                      const float* sine, int64_t heads, int64_t head_dim, int64_t nope_dim,
-                                      int64_t kv_rank, int32_t weight_dtype, double scale, float* out,
-                                      mlk_stream_t stream) {
-    MLK_CHECK(batch >= 0 && length >= 1 && heads > 0 && d_model == heads * head_dim, "invalid MLA geometry");
-    const bool built = weight_dtype == MLK_DTYPE_BF16 && heads == 8 && head_dim == 32 && nope_dim == 16 &&
-                       kv_rank == 64 && length <= 128;
+namespace {
+
+// The geometry mla_window_kernel is built for, and its operand checks; MLK_OK when the kernel takes the
+// call, MLK_ERR_UNSUPPORTED (with the reason) when the separate operators must run it.
+mlk_status mla_window_supported(const float* x, int64_t length, int64_t d_model, int64_t x_batch_stride,
+                                int64_t x_token_stride, const float* kv_norm_w, const float* kv_norm_b,
+                                const float* cosine, const float* sine, int64_t heads, int64_t head_dim,
+                                int64_t nope_dim, int64_t kv_rank, double scale, const float* out,
+                                std::initializer_list<const void*> weights) {
+    const bool built = heads == 8 && head_dim == 32 && nope_dim == 16 && kv_rank == 64 && length <= 128 &&
+                       d_model == heads * head_dim;
     if (!built) {
         set_error("mla_forward: geometry without the per-window kernel (use the separate operators)");
         return MLK_ERR_UNSUPPORTED;
@@ -1530,23 +1599,100 @@ extern "C" mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t len
         set_error("mla_forward: the per-window kernel takes a positive softmax scale (use the separate operators)");
         return MLK_ERR_UNSUPPORTED;
     }
-    if (!aligned16(x) || x_token_stride % 4 != 0 || x_batch_stride % 4 != 0 || !aligned16(cosine) ||
-        !aligned16(sine) || !aligned16(kv_norm_w) || (kv_norm_b != nullptr && !aligned16(kv_norm_b)) ||
-        !aligned16(in_proj_weight) || !aligned16(kv_up_weight) || !aligned16(out_weight) || !aligned16(out)) {
+    bool aligned = aligned16(x) && x_token_stride % 4 == 0 && x_batch_stride % 4 == 0 && aligned16(cosine) &&
+                   aligned16(sine) && aligned16(kv_norm_w) && (kv_norm_b == nullptr || aligned16(kv_norm_b)) &&
+                   aligned16(out);
+    for (const void* w : weights) aligned = aligned && aligned16(w);
+    if (!aligned) {
         set_error("mla_forward: operands must be 16-byte aligned for the per-window kernel (use the separate operators)");
         return MLK_ERR_UNSUPPORTED;
     }
+    return MLK_OK;
+}
+
+mlk_status mla_window_launch(const float* x, int64_t batch, int64_t length, int64_t d_model, int64_t x_batch_stride,
+                             int64_t x_token_stride, const void* w_in, const float* kv_norm_w, const float* kv_norm_b,
+                             double kv_norm_eps, const void* w_up, const void* w_out, const float* cosine,
+                             const float* sine, double scale, float* out, bool packed, mlk_stream_t stream) {
     MLK_CHECK(x_token_stride >= d_model && (length == 1 || x_batch_stride >= length * x_token_stride),
               "x strides must cover the rows");
     if (batch == 0) return MLK_OK;
-    MLK_CHECK(x && in_proj_weight && kv_norm_w && kv_up_weight && out_weight && cosine && sine && out,
-              "null tensor pointer");
+    MLK_CHECK(x && w_in && kv_norm_w && w_up && w_out && cosine && sine && out, "null tensor pointer");
     MLK_CHECK(batch <= 0x7fffffff, "too many windows for one launch");
-    MlaWindowArgs p{x, x_batch_stride, x_token_stride, static_cast<const u16*>(in_proj_weight), kv_norm_w, kv_norm_b,
-                    static_cast<double>(static_cast<float>(kv_norm_eps)), static_cast<const u16*>(kv_up_weight),
-                    static_cast<const u16*>(out_weight), cosine, sine, out, length,
+    MlaWindowArgs p{x, x_batch_stride, x_token_stride, static_cast<const u16*>(w_in), kv_norm_w, kv_norm_b,
+                    static_cast<double>(static_cast<float>(kv_norm_eps)), static_cast<const u16*>(w_up),
+                    static_cast<const u16*>(w_out), cosine, sine, out, length,
                     static_cast<float>(scale * 1.4426950408889634)};
-    hipLaunchKernelGGL((mla_window_kernel<8>), dim3(static_cast<unsigned>(batch)), dim3(512), 0,
-                       reinterpret_cast<hipStream_t>(stream), p);
+    const dim3 grid(static_cast<unsigned>(batch));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (packed) {
+        hipLaunchKernelGGL((mla_window_kernel<8, true>), grid, dim3(512), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((mla_window_kernel<8, false>), grid, dim3(512), 0, s, p);
+    }
     return launch_status("mla_forward");
+}
+
+}  // namespace
+
+extern "C" mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_t d_model,
+                                      int64_t x_batch_stride, int64_t x_token_stride, const void* in_proj_weight,
+                                      const float* kv_norm_w, const float* kv_norm_b, double kv_norm_eps,
+                                      const void* kv_up_weight, const void* out_weight, const float* cosine,
+                                      const float* sine, int64_t heads, int64_t head_dim, int64_t nope_dim,
+                                      int64_t kv_rank, int32_t weight_dtype, double scale, float* out,
+                                      mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 1 && heads > 0 && d_model == heads * head_dim, "invalid MLA geometry");
+    if (weight_dtype != MLK_DTYPE_BF16) {
+        set_error("mla_forward: the per-window kernel takes bf16 weights (use the separate operators)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    const mlk_status ok = mla_window_supported(x, length, d_model, x_batch_stride, x_token_stride, kv_norm_w, kv_norm_b,
+                                               cosine, sine, heads, head_dim, nope_dim, kv_rank, scale, out,
+                                               {in_proj_weight, kv_up_weight, out_weight});
+    if (ok != MLK_OK) return ok;
+    return mla_window_launch(x, batch, length, d_model, x_batch_stride, x_token_stride, in_proj_weight, kv_norm_w,
+                             kv_norm_b, kv_norm_eps, kv_up_weight, out_weight, cosine, sine, scale, out, false, stream);
+}
+
+extern "C" int64_t mlk_mla_packed_elems(int64_t d_model, int64_t heads, int64_t head_dim, int64_t nope_dim,
+                                        int64_t kv_rank) {
+    const bool built = heads == 8 && head_dim == 32 && nope_dim == 16 && kv_rank == 64 && d_model == heads * head_dim;
+    return built ? static_cast<int64_t>(MlaPack<8>::UNITS) * 8 : 0;
+}
+
+extern "C" mlk_status mlk_mla_pack_weights(const void* in_proj_weight, const void* kv_up_weight, const void* out_weight,
+                                           int64_t d_model, int64_t heads, int64_t head_dim, int64_t nope_dim,
+                                           int64_t kv_rank, int32_t weight_dtype, void* packed, mlk_stream_t stream) {
+    if (weight_dtype != MLK_DTYPE_BF16 || mlk_mla_packed_elems(d_model, heads, head_dim, nope_dim, kv_rank) == 0) {
+        set_error("mla_pack_weights: geometry without the per-window kernel (bf16, 8 heads of 32, rope 16, kv rank 64)");
+        return MLK_ERR_UNSUPPORTED;
+    }
+    MLK_CHECK(in_proj_weight && kv_up_weight && out_weight && packed, "null tensor pointer");
+    MLK_CHECK(aligned16(in_proj_weight) && aligned16(kv_up_weight) && aligned16(out_weight) && aligned16(packed),
+              "mla_pack_weights: operands must be 16-byte aligned");
+    constexpr int kUnits = MlaPack<8>::UNITS;
+    hipLaunchKernelGGL((mla_pack_kernel<8>), dim3((kUnits + 255) / 256), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), static_cast<const u16*>(in_proj_weight),
+                       static_cast<const u16*>(kv_up_weight), static_cast<const u16*>(out_weight),
+                       static_cast<u16*>(packed));
+    return launch_status("mla_pack_weights");
+}
+
+extern "C" mlk_status mlk_mla_forward_packed(const float* x, int64_t batch, int64_t length, int64_t d_model,
+                                             int64_t x_batch_stride, int64_t x_token_stride, const void* packed_weights,
+                                             const float* kv_norm_w, const float* kv_norm_b, double kv_norm_eps,
+                                             const float* cosine, const float* sine, int64_t heads, int64_t head_dim,
+                                             int64_t nope_dim, int64_t kv_rank, double scale, float* out,
+                                             mlk_stream_t stream) {
+    MLK_CHECK(batch >= 0 && length >= 1 && heads > 0 && d_model == heads * head_dim, "invalid MLA geometry");
+    const mlk_status ok = mla_window_supported(x, length, d_model, x_batch_stride, x_token_stride, kv_norm_w, kv_norm_b,
+                                               cosine, sine, heads, head_dim, nope_dim, kv_rank, scale, out,
+                                               {packed_weights});
+    if (ok != MLK_OK) return ok;
+    const u16* w = static_cast<const u16*>(packed_weights);
+    return mla_window_launch(x, batch, length, d_model, x_batch_stride, x_token_stride, w, kv_norm_w, kv_norm_b,
+                             kv_norm_eps, w + 8 * MlaPack<8>::IN_UNITS,
+                             w + 8 * (MlaPack<8>::IN_UNITS + MlaPack<8>::UP_UNITS), cosine, sine, scale, out, true,
+                             stream);
 }

@@ -51,6 +51,9 @@ def _load():
         "mlk_mla_rope_qk": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
         "mlk_mla_forward": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _dbl, _vp, _vp, _vp, _vp, _i64, _i64,
                             _i64, _i64, C.c_int32, _dbl, _vp, _vp],
+        "mlk_mla_pack_weights": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, C.c_int32, _vp, _vp],
+        "mlk_mla_forward_packed": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _dbl, _vp, _vp, _i64, _i64, _i64,
+                                   _i64, _dbl, _vp, _vp],
         "mlk_mla_attend": [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _dbl, _vp, _vp,
                            _vp, _dbl, _vp, _vp],
         "mlk_attention": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, C.c_int32,
@@ -76,6 +79,8 @@ def _load():
         fn.restype = C.c_int
     lib.mlk_mamba3_workspace_bytes.argtypes = [_i64] * 5
     lib.mlk_mamba3_workspace_bytes.restype = C.c_size_t
+    lib.mlk_mla_packed_elems.argtypes = [_i64] * 5
+    lib.mlk_mla_packed_elems.restype = C.c_int64
     _lib = lib
     return lib
 
@@ -873,6 +878,46 @@ def mla_forward_launches() -> list[str] | None:
     return _MLA_PATH["last"]
 
 
+# Packed copies of the per-window kernel's weights (mlk_mla_pack_weights), one per (in_proj, kv_up, out)
+# weight triple: the entry keeps the three tensors, so their storage stays theirs while it is cached, and
+# is used only while each tensor is the same object at the same version (an in-place update makes a new
+# copy). A few entries at most, oldest dropped first.
+_MLA_PACKS: list = []
+_MLA_PACKS_MAX = 4
+
+
+def _mla_packed(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nope_dim, kv_lora_rank):
+    """The packed weights of mlk_mla_forward_packed, from the cache or made now; None where the geometry
+    has no packed form."""
+    ws = (in_proj_weight, kv_up_weight, out_weight)
+    versions = tuple(w._version for w in ws)
+    for entry in _MLA_PACKS:
+        if all(a is b for a, b in zip(entry[0], ws)) and entry[1] == versions:
+            return entry[2]
+    packed = mla_pack_weights(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nope_dim, kv_lora_rank)
+    if packed is None:
+        return None
+    _MLA_PACKS.insert(0, (ws, versions, packed))
+    del _MLA_PACKS[_MLA_PACKS_MAX:]
+    return packed
+
+
+def mla_pack_weights(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nope_dim, kv_lora_rank):
+    """The three bf16 weights of the per-window MLA kernel in its fragment order (mlk_mla_pack_weights), or
+    None where that kernel is not built for the geometry."""
+    for name, w in (("in_proj_weight", in_proj_weight), ("kv_up_weight", kv_up_weight), ("out_weight", out_weight)):
+        _check(w.is_cuda and w.dtype == torch.bfloat16 and w.is_contiguous(), f"{name} must be contiguous bf16 on GPU")
+    d_model = n_heads * head_dim
+    lib = _load()
+    elems = lib.mlk_mla_packed_elems(d_model, n_heads, head_dim, nope_dim, kv_lora_rank)
+    if elems <= 0:
+        return None
+    packed = torch.empty(elems, dtype=torch.bfloat16, device=in_proj_weight.device)
+    _call("mlk_mla_pack_weights", _ptr(in_proj_weight), _ptr(kv_up_weight), _ptr(out_weight), d_model, n_heads,
+          head_dim, nope_dim, kv_lora_rank, _WEIGHT_DTYPES[torch.bfloat16], _ptr(packed), _stream())
+    return packed
+
+
 def _mla_window(x, in_proj_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight, cosine,
                 sine, n_heads, head_dim, nope_dim, kv_lora_rank, scale):
     """The whole forward for every causal query, one block per window (bf16 weights, 8 heads of 32, rope 16,
@@ -895,10 +940,16 @@ def _mla_window(x, in_proj_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv
                                                                                        "kv_norm.bias")
     out = torch.empty((batch, length, d_model), dtype=torch.float32, device=x.device)
     lib = _load()
-    status = lib.mlk_mla_forward(_ptr(x), batch, length, d_model, x.stride(0), x.stride(1), _ptr(in_proj_weight),
-                                 _ptr(w), _ptr(b), float(kv_norm_eps), _ptr(kv_up_weight), _ptr(out_weight),
-                                 _ptr(cosine), _ptr(sine), n_heads, head_dim, nope_dim, kv_lora_rank,
-                                 _WEIGHT_DTYPES[torch.bfloat16], float(scale), _ptr(out), _stream())
+    packed = _mla_packed(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nope_dim, kv_lora_rank)
+    if packed is not None:
+        status = lib.mlk_mla_forward_packed(_ptr(x), batch, length, d_model, x.stride(0), x.stride(1), _ptr(packed),
+                                            _ptr(w), _ptr(b), float(kv_norm_eps), _ptr(cosine), _ptr(sine), n_heads,
+                                            head_dim, nope_dim, kv_lora_rank, float(scale), _ptr(out), _stream())
+    else:
+        status = lib.mlk_mla_forward(_ptr(x), batch, length, d_model, x.stride(0), x.stride(1),
+                                     _ptr(in_proj_weight), _ptr(w), _ptr(b), float(kv_norm_eps), _ptr(kv_up_weight),
+                                     _ptr(out_weight), _ptr(cosine), _ptr(sine), n_heads, head_dim, nope_dim,
+                                     kv_lora_rank, _WEIGHT_DTYPES[torch.bfloat16], float(scale), _ptr(out), _stream())
     if status == 3:  # MLK_ERR_UNSUPPORTED
         return None
     if status != 0:
@@ -1023,7 +1074,7 @@ def exported_symbols() -> list[str]:
             "mlk_mamba3_siso_recurrent_noalloc", "mlk_mamba3_siso_forward", "mlk_rms_norm_mamba3_forward",
             "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear",
             "mlk_layer_norm_bf16", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend", "mlk_mla_attend_normed",
-            "mlk_mla_forward"]
+            "mlk_mla_forward", "mlk_mla_packed_elems", "mlk_mla_pack_weights", "mlk_mla_forward_packed"]
 
 
 def math_check(x: torch.Tensor) -> dict:

@@ -295,6 +295,50 @@ def test_window_kernel_equals_separate_path(dev, B, L, bias, strided):
     assert_bitwise(one, four.cpu().numpy(), f"per-window MLA {B}x{L} vs four launches")
 
 
+def test_packed_weights_equal_row_major(dev):
+    """_C.mla_forward runs the per-window kernel on its weights re-laid in the kernel's fragment order
+    (mlk_mla_pack_weights, cached per weight triple): the result equals mlk_mla_forward on the row-major
+    weights bit for bit, and the packed copy follows an in-place update of a weight."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(7)
+    B, L, H, hd, nope, kvr = 6, 100, 8, 32, 16, 64
+    d, rope = H * hd, hd - nope
+    bf = torch.bfloat16
+    x = torch.randn(B, L, d, generator=g).to(dev)
+    in_w = (torch.randn(d + kvr + rope, d, generator=g) * 0.05).to(dev, bf)
+    up_w = (torch.randn(H * (nope + hd), kvr, generator=g) * 0.1).to(dev, bf)
+    o_w = (torch.randn(d, d, generator=g) * 0.05).to(dev, bf)
+    ln_w = (1 + 0.1 * torch.randn(kvr, generator=g)).to(dev)
+    ln_b = (0.1 * torch.randn(kvr, generator=g)).to(dev)
+    cos, sin = (t.to(dev) for t in rope_tables_t(L, rope))
+    scale = hd ** -0.5
+    lib = _C.library()
+
+    def row_major():
+        out = torch.empty(B, L, d, device=dev)
+        status = lib.mlk_mla_forward(x.data_ptr(), B, L, d, x.stride(0), x.stride(1), in_w.data_ptr(),
+                                     ln_w.data_ptr(), ln_b.data_ptr(), 1e-5, up_w.data_ptr(), o_w.data_ptr(),
+                                     cos.data_ptr(), sin.data_ptr(), H, hd, nope, kvr, 1, scale, out.data_ptr(),
+                                     _C._stream())
+        assert status == 0, lib.mlk_last_error().decode()
+        return out
+
+    args = (x, in_w, x.new_empty(0), ln_w, ln_b, 1e-5, up_w, o_w, cos, sin, H, hd, nope, kvr, L, True, scale)
+    packed = _C.mla_forward(*args)
+    assert _C.mla_forward_launches() == ["mla_forward"]
+    assert_bitwise(packed, row_major().cpu().numpy(), "packed vs row-major weights")
+    with torch.no_grad():
+        o_w.mul_(0.5)
+        up_w.mul_(1.25)
+    again = _C.mla_forward(*args)
+    assert not torch.equal(again, packed), "the weight update must reach the kernel"
+    assert_bitwise(again, row_major().cpu().numpy(), "packed vs row-major weights after an in-place update")
+    assert lib.mlk_mla_packed_elems(d, H, hd, nope, kvr) == _C.mla_pack_weights(in_w, up_w, o_w, H, hd, nope,
+                                                                                 kvr).numel()
+    assert lib.mlk_mla_packed_elems(d, H, hd, nope, 32) == 0, "no packed form without the per-window kernel"
+
+
 def test_window_kernel_vs_oracle(dev, oracle):
     """The per-window kernel against the oracle chain at the MLA block geometry (bf16 weights: 2e-2)."""
     from montlok import _C
