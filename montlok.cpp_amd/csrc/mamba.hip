@@ -1761,16 +1761,35 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             auto put = [&](int i, tile_f32x4 y) {
                 const int j = j0 + i * jstep;
                 y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
-                if (j < ncol) *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + tile_col(j) + 4 * grp) = y;
+                // (HELP: every tile of the scan waves lies below ncol = NCT, checked at launch, so the
+                // store needs no branch and stays in one block with the products.)
+                if (HELP || j < ncol) *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + tile_col(j) + 4 * grp) = y;
             };
+            // Two tiles' chains interleaved per pair; a pair's results are summed and stored after the
+            // next pair's products are issued, so the accumulator reads do not drain the matrix core.
+            tile_f32x4 pa, pb;
 #pragma unroll
-            for (int i = 0; i + 1 < NTW; i += 2) {  // two tiles' chains interleaved
+            for (int i = 0; i + 1 < NTW; i += 2) {
                 tile_f32x4 ya, yb;
                 tile_mfma_f32_pair<KSI, ALL_LIVE>(wv[i], wv[i + 1], xv, live, ya, yb);
-                put(i, ya);
-                put(i + 1, yb);
+                if (i > 0) {
+                    put(i - 2, pa);
+                    put(i - 1, pb);
+                }
+                pa = ya;
+                pb = yb;
             }
-            if constexpr (NTW % 2 == 1) put(NTW - 1, tile_mfma_f32<KSI, ALL_LIVE>(wv[NTW - 1], xv, live));
+            if constexpr (NTW % 2 == 1) {
+                const tile_f32x4 y = tile_mfma_f32<KSI, ALL_LIVE>(wv[NTW - 1], xv, live);
+                if constexpr (NTW > 1) {
+                    put(NTW - 3, pa);
+                    put(NTW - 2, pb);
+                }
+                put(NTW - 1, y);
+            } else {
+                put(NTW - 2, pa);
+                put(NTW - 1, pb);
+            }
             __syncthreads();
         }
         __device__ void after(int64_t, bool) const {}
@@ -1818,20 +1837,27 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             float wc[KSI][8];
             bool wclive[KSI];
             if (hw == 1) hooks.weights(j - 1, ncol, wc, wclive);
+            // Both row tiles' products first, then the stores (in one block, the row tiles' chains
+            // interleave and the accumulator reads do not drain the matrix core between them).
+            tile_f32x4 y[2];
+            if (hw == 1) {
+                tile_f32x4 yc[2];
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) tile_mfma_f32_pair<KSI, ALL_LIVE>(wv, wc, xv[rt], live[rt], y[rt], yc[rt]);
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    yc[rt] += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
+                    *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + hooks.tile_col(j - 1) + 4 * grp) = yc[rt];
+                }
+            } else {
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) y[rt] = tile_mfma_f32<KSI, ALL_LIVE>(wv, xv[rt], live[rt]);
+            }
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
-                tile_f32x4 y;
-                if (hw == 1) {
-                    tile_f32x4 yc;
-                    tile_mfma_f32_pair<KSI, ALL_LIVE>(wv, wc, xv[rt], live[rt], y, yc);
-                    yc += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
-                    *reinterpret_cast<tile_f32x4*>(proj_s + (16 * rt + li) * pp + hooks.tile_col(j - 1) + 4 * grp) = yc;
-                } else {
-                    y = tile_mfma_f32<KSI, ALL_LIVE>(wv, xv[rt], live[rt]);
-                }
-                y += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
+                y[rt] += tile_f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // the linear's (zero) bias add
 #pragma unroll
-                for (int v = 0; v < 4; ++v) hs[hw][(16 * rt + li) * HP + 4 * grp + v] = y[v];
+                for (int v = 0; v < 4; ++v) hs[hw][(16 * rt + li) * HP + 4 * grp + v] = y[rt][v];
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -1844,24 +1870,32 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 if (lane < C)
                     token_coefficients<C>(lane, row[lane * HP + h], row[lane * HP + Hi + h], row[lane * HP + 2 * Hi + h],
                                           p.s.dt_bias[h], p.s.a_floor, Lc, sh.coef);
-            } else {
+            } else if (lane < C * static_cast<int>(p.s.R)) {
+                // tanh(angle) * pi of the first 64 (token, angle) items; the rest after the barrier, where
+                // this helper has slack and the scan waves do not wait for it.
                 const int R = static_cast<int>(p.s.R);
                 constexpr int RM = ScanLds<C, NT, DT>::RM;
-#pragma unroll 1
-                for (int i = lane; i < C * R; i += 64) {
-                    const int t = i / R, rr = i - t * R;
-                    sh.ang_s[t * RM + rr] = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
-                }
+                const int t = lane / R, rr = lane - t * R;
+                sh.ang_s[t * RM + rr] = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
             }
-            __syncthreads();  // with the end of the scan waves' in_proj: coefficients and angles are in
+            __syncthreads();  // with the end of the scan waves' in_proj: the coefficients are in
             if (hw == 0) {
                 decay_walk<C, true>(lane, true, sh.coef, sh.w_s);
             } else {
-                // The running angle sums of the chunk (one lane per angle, from zero: the first chunk), as
-                // step c forms them, then the sin/cos of every (token, angle) pair, as step d would, into
-                // this helper's staging rows (its tile values are dead).
+                // The remaining tanh(angle) * pi items, then the running angle sums of the chunk (one lane
+                // per angle, from zero: the first chunk), as step c forms them, then the sin/cos of every
+                // (token, angle) pair, as step d would, into this helper's staging rows (its tile values
+                // are dead by then).
                 const int R = static_cast<int>(p.s.R);
                 constexpr int RM = ScanLds<C, NT, DT>::RM;
+#pragma unroll 1
+                for (int i = lane + 64; i < C * R; i += 64) {
+                    const int t = i / R, rr = i - t * R;
+                    sh.ang_s[t * RM + rr] = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 if (lane < R) {
                     double running = 0.0;
 #pragma unroll
@@ -1888,13 +1922,19 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 }
                 __hip_atomic_store(&rot_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
-            // Helper hw forms the late gates of scan wave hw's lanes (token tile 1, v >= kPrepOwnV:
-            // tokens 16 + 4 grp + v, head column 16 hw + li), as scan_head forms them from z (the
-            // head's first columns of the rows; the tile's rows past the end hold the last token's).
+            // Helper 0 (done with its decay weights well before helper 1's rotations) forms the late
+            // gates of both scan waves (token tile 1, v >= kPrepOwnV: tokens 16 + 4 grp + v, head column
+            // 16 sw + li), as scan_head forms them from z (the head's first columns of the rows; the
+            // tile's rows past the end hold the last token's).
+            if (hw == 0) {
 #pragma unroll
-            for (int v = kPrepOwnV; v < 4; ++v) {
-                const double z = static_cast<double>(proj_s[(16 + 4 * grp + v) * pp + static_cast<int>(h) * D + 16 * hw + li]);
-                lg[(hw * (4 - kPrepOwnV) + v - kPrepOwnV) * 64 + lane] = z / (1.0 + exp_d(-z));
+                for (int sw = 0; sw < DT; ++sw)
+#pragma unroll
+                    for (int v = kPrepOwnV; v < 4; ++v) {
+                        const double z = static_cast<double>(
+                            proj_s[(16 + 4 * grp + v) * pp + static_cast<int>(h) * D + 16 * sw + li]);
+                        lg[(sw * (4 - kPrepOwnV) + v - kPrepOwnV) * 64 + lane] = z / (1.0 + exp_d(-z));
+                    }
             }
             __syncthreads();  // with the end of the scan waves' step d: the decay weights and gates are in
             return;
