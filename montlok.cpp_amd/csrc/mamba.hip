@@ -1601,6 +1601,10 @@ struct BlockArgs {
 // scan waves copy their rows, form the norm scales and the other gates
 // (scan_head's PREP form). The helpers end after the barrier that ends step
 // d; S_BARRIER then waits on the surviving waves only.
+// i / R as (i * hmagic(R)) >> 16, exact for i < 2^10 and 0 < R <= 32 (the helpers' (token, angle) item
+// indices, i < C * R <= 256): a multiply and a shift instead of the integer division's VALU sequence.
+__device__ __forceinline__ unsigned hmagic(int R) { return (65536u + static_cast<unsigned>(R) - 1u) / static_cast<unsigned>(R); }
+
 template <int NT, int DT, int KSI, int GS, int NCT, bool ALL_LIVE, bool HELP>
 __global__ __launch_bounds__(64 * DT * (HELP ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(1)))
 void mamba3_block_scan_kernel(BlockArgs p) {
@@ -1875,7 +1879,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 // this helper has slack and the scan waves do not wait for it.
                 const int R = static_cast<int>(p.s.R);
                 constexpr int RM = ScanLds<C, NT, DT>::RM;
-                const int t = lane / R, rr = lane - t * R;
+                const int t = static_cast<int>((static_cast<unsigned>(lane) * hmagic(R)) >> 16), rr = lane - t * R;
                 sh.ang_s[t * RM + rr] = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
             }
             __syncthreads();  // with the end of the scan waves' in_proj: the coefficients are in
@@ -1890,7 +1894,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 constexpr int RM = ScanLds<C, NT, DT>::RM;
 #pragma unroll 1
                 for (int i = lane + 64; i < C * R; i += 64) {
-                    const int t = i / R, rr = i - t * R;
+                    const int t = static_cast<int>((static_cast<unsigned>(i) * hmagic(R)) >> 16), rr = i - t * R;
                     sh.ang_s[t * RM + rr] = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1917,7 +1921,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 static_assert(2 * C * RM <= C * HP, "the rotations fit the staging rows");
 #pragma unroll 1
                 for (int i = lane; i < C * R; i += 64) {
-                    const int t = i / R, rr = i - t * R;
+                    const int t = static_cast<int>((static_cast<unsigned>(i) * hmagic(R)) >> 16), rr = i - t * R;
                     rotation_of(sh.cum_s[t * RM + rr], &rot[2 * (t * RM + rr)], &rot[2 * (t * RM + rr) + 1]);
                 }
                 __hip_atomic_store(&rot_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
