@@ -902,6 +902,7 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     __shared__ __attribute__((aligned(16))) u16 lat_s[LMAX * LP];
     __shared__ __attribute__((aligned(16))) u16 kr_s[LMAX * ROPE];
     __shared__ __attribute__((aligned(16))) u16 head_s[HG * SLOT];
+    __shared__ __attribute__((aligned(16))) float lnp_s[2 * KV];  // the LayerNorm's weight, then its bias (+0.0 if none)
     // [LMAX, KV] fp32 until the LayerNorm has run; 16-byte chunk c of row r at slot c ^ (r % 16), so the
     // epilogue's stores (16 rows, one chunk) and the LayerNorm's reads (one row, 16 chunks) are conflict-free.
     float* lat_f = reinterpret_cast<float*>(head_s);
@@ -972,6 +973,19 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     const int crow = tid >> 2, ccol = 4 * (tid & 3), crc = crow < L ? crow : L - 1;
     const float4 cv = *reinterpret_cast<const float4*>(p.cosine + crc * ROPE + ccol);
     const float4 sv = *reinterpret_cast<const float4*>(p.sine + crc * ROPE + ccol);
+    // The LayerNorm's weight and bias into LDS with the tables (read there after the epilogue instead of
+    // from L2 then): threads 0 .. 2 KV / 4 - 1 take one float4 each. A missing bias reads the weight and
+    // masks it to +0.0 bit-wise (a select here would become a branch around the load, and the branch a
+    // wait for every load in flight).
+    static_assert(2 * KV / 4 <= 512, "one float4 of the LayerNorm parameters per thread");
+    const bool ln_part = tid < 2 * KV / 4, ln_bias = tid >= KV / 4;
+    const uint32_t bmask = p.ln_b != nullptr || !ln_bias ? 0xffffffffu : 0u;
+    const float* ln_src = ln_bias && p.ln_b != nullptr ? p.ln_b : p.ln_w;
+    const float4 lnv = *reinterpret_cast<const float4*>(ln_src + 4 * ((ln_part ? tid : 0) % (KV / 4)));
+    if (ln_part)
+        *reinterpret_cast<float4*>(lnp_s + 4 * tid) =
+            make_float4(__uint_as_float(__float_as_uint(lnv.x) & bmask), __uint_as_float(__float_as_uint(lnv.y) & bmask),
+                        __uint_as_float(__float_as_uint(lnv.z) & bmask), __uint_as_float(__float_as_uint(lnv.w) & bmask));
     {
         const int p0 = ccol / 2;  // pairs p0, p0 + 1 of the row
         *reinterpret_cast<double2*>(cs_d + cs_at(crow, p0)) = make_double2(cv.x, cv.y);
@@ -1088,17 +1102,11 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     // LayerNorm operands: four lanes per row, lane q = lane % 4 holding the row's four-column groups q,
     // q + 4, q + 8, q + 12; wave w takes rows 16 w .. 16 w + 15.
     const int lq = lane & 3, lrow = 16 * wave + (lane >> 2);
-    // A missing bias reads the weight and masks it to +0.0 bit-wise: a select here would become a branch
-    // around the load, and the branch a wait for every load in flight.
-    const bool has_b = p.ln_b != nullptr;
-    const uint32_t bmask = has_b ? 0xffffffffu : 0u;
     float4 lnw[4], lnb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        lnw[i] = *reinterpret_cast<const float4*>(p.ln_w + 4 * (lq + 4 * i));
-        const float4 r = *reinterpret_cast<const float4*>((has_b ? p.ln_b : p.ln_w) + 4 * (lq + 4 * i));
-        lnb[i] = make_float4(__uint_as_float(__float_as_uint(r.x) & bmask), __uint_as_float(__float_as_uint(r.y) & bmask),
-                             __uint_as_float(__float_as_uint(r.z) & bmask), __uint_as_float(__float_as_uint(r.w) & bmask));
+        lnw[i] = *reinterpret_cast<const float4*>(lnp_s + 4 * (lq + 4 * i));
+        lnb[i] = *reinterpret_cast<const float4*>(lnp_s + KV + 4 * (lq + 4 * i));
     }
     const int grp = wave >> 1;  // head group: heads grp, grp + HG
     const int wg = wave & 1;
