@@ -1614,7 +1614,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
     static_assert(DT == 2, "one wave per 16-row tile of the 32-token chunk");
     __shared__ ScanLds<C, NT, DT> sh;
     constexpr int HP = 17;  // helper staging: [32 rows][16 columns], rows HP floats apart
-    __shared__ float hs[HELP ? DT : 1][HELP ? C * HP : 1];
+    __shared__ __attribute__((aligned(16))) float hs[HELP ? DT : 1][HELP ? C * HP : 1];
     __shared__ int rot_ready;  // HELP: set by helper 1 once the rotations are in hs[1]
     __shared__ double lg[HELP ? DT * (4 - kPrepOwnV) * 64 : 1];  // HELP: the scan waves' late gates
     extern __shared__ __attribute__((aligned(16))) float proj_s[];  // [C, pp]
@@ -1887,31 +1887,38 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 decay_walk<C, true>(lane, true, sh.coef, sh.w_s);
             } else {
                 // The remaining tanh(angle) * pi items, then the running angle sums of the chunk (one lane
-                // per angle, from zero: the first chunk), as step c forms them, then the sin/cos of every
-                // (token, angle) pair, as step d would, into this helper's staging rows (its tile values
-                // are dead by then).
+                // per angle, from zero: the first chunk) as step c forms them: each term tanh(angle) * pi
+                // * dt in fp32, widened, added in token order in fp64, the sum rounded to fp32 where it is
+                // used. The terms are formed for every item at once, in helper 0's staging rows (dead after
+                // the barrier), so the lanes that walk the sums only add and store; then the sin/cos of
+                // every (token, angle) pair, as step d would, into this helper's staging rows (its tile
+                // values are dead by then).
                 const int R = static_cast<int>(p.s.R);
                 constexpr int RM = ScanLds<C, NT, DT>::RM;
+                static_assert(sizeof(double) * C * RM <= sizeof(float) * C * HP, "the sums fit the staging rows");
+                double* cum_d = reinterpret_cast<double*>(&hs[0][0]);
+                if (lane < C * R) {  // items 0 .. 63: tanh formed before the barrier
+                    const int t = static_cast<int>((static_cast<unsigned>(lane) * hmagic(R)) >> 16), rr = lane - t * R;
+                    cum_d[t * RM + rr] = static_cast<double>(sh.ang_s[t * RM + rr] * sh.coef[3][t]);
+                }
 #pragma unroll 1
                 for (int i = lane + 64; i < C * R; i += 64) {
                     const int t = static_cast<int>((static_cast<unsigned>(i) * hmagic(R)) >> 16), rr = i - t * R;
-                    sh.ang_s[t * RM + rr] = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
+                    const float a = tanhf_cr(row[t * HP + 3 * Hi + rr]) * kPiF;
+                    cum_d[t * RM + rr] = static_cast<double>(a * sh.coef[3][t]);
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 if (lane < R) {
+                    double term[C];
+#pragma unroll
+                    for (int t = 0; t < C; ++t) term[t] = cum_d[t * RM + lane];
                     double running = 0.0;
 #pragma unroll
-                    for (int t0 = 0; t0 < C; t0 += 16) {
-                        float term[16];
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) term[i] = sh.ang_s[(t0 + i) * RM + lane] * sh.coef[3][t0 + i];
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            running += static_cast<double>(term[i]);
-                            sh.cum_s[(t0 + i) * RM + lane] = static_cast<float>(running);
-                        }
+                    for (int t = 0; t < C; ++t) {
+                        running += term[t];
+                        cum_d[t * RM + lane] = running;
                     }
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1922,7 +1929,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
 #pragma unroll 1
                 for (int i = lane; i < C * R; i += 64) {
                     const int t = static_cast<int>((static_cast<unsigned>(i) * hmagic(R)) >> 16), rr = i - t * R;
-                    rotation_of(sh.cum_s[t * RM + rr], &rot[2 * (t * RM + rr)], &rot[2 * (t * RM + rr) + 1]);
+                    rotation_of(static_cast<float>(cum_d[t * RM + rr]), &rot[2 * (t * RM + rr)], &rot[2 * (t * RM + rr) + 1]);
                 }
                 __hip_atomic_store(&rot_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
