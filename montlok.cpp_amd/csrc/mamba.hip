@@ -992,9 +992,10 @@ struct ScanLds {
 };
 
 // Called by every thread of the block around each chunk of the scan.
-// PREP's split of the output gates: a scan wave forms those of token tile 0
-// and of v < kPrepOwnV in tile 1 (token 16 + 4 g + v); the rest arrive at
-// hooks.late_gates(), [DT][4 - kPrepOwnV][64] in lane order.
+// PREP's split of the outputs: a scan wave forms token tile 0's outputs of its
+// columns; the block's other waves form tile 1's. The scan wave also forms the
+// tile-1 gates of v < kPrepOwnV (token 16 + 4 g + v) and hands them over at
+// hooks.share_gate(v, gate) before the barrier that ends step d.
 constexpr int kPrepOwnV = 2;
 
 struct NoChunkHooks {
@@ -1020,9 +1021,9 @@ struct NoChunkHooks {
 // returns. Step a skips the dt/A/trap and angle columns; steps a to d run
 // without a barrier: each wave forms the norm scales of the rows it scales
 // in step c (read from the B/C rows where hooks.before left them) and its
-// gates, and rotates those rows in step d; step c skips the angle sums. Step
-// e forms every G tile on every wave in registers, and step f reads them
-// there.
+// gates, and rotates those rows in step d; step c skips the angle sums. Steps
+// e and f form token tile 0's G tile, products and outputs in registers (tile
+// 1's are the other waves' after the barrier that ends step d).
 template <int C, int NT, int DT, bool TILE, class Hooks, bool TILE_OUT = TILE, bool PREP = false>
 __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>& sh, int64_t b, int64_t h,
                                           int tid_base, const Hooks& hooks) {
@@ -1033,6 +1034,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
     constexpr int CT = C / 16;
     constexpr int NP = N + 4, WP = C + 4;
     constexpr int NPAIR = CT * (CT + 1) / 2;
+    constexpr int CTE = PREP ? 1 : CT;  // token tiles whose outputs this scan forms
     constexpr int RM = N / 2;  // rotary angles at most
     constexpr bool kEarlyGate = DT == 2;
     static_assert(NTH % N == 0, "a thread keeps one q/k column across the chunk");
@@ -1264,6 +1266,8 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         }
         if constexpr (PREP) {
             gates();
+#pragma unroll
+            for (int v = 0; v < kPrepOwnV; ++v) hooks.share_gate(v, gz[1][v]);
         } else if constexpr (kEarlyGate) {
             if (wave == 0) gates();  // wave 1 runs the coefficients and decay weights meanwhile
         }
@@ -1340,20 +1344,15 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
             }
         }
         __syncthreads();
-        if constexpr (PREP) {
-            static_assert(CT == 2, "PREP: two token tiles");
-#pragma unroll
-            for (int v = kPrepOwnV; v < 4; ++v)
-                gz[1][v] = hooks.late_gates()[(wave * (4 - kPrepOwnV) + v - kPrepOwnV) * 64 + lane];
-        }
+        static_assert(!PREP || CT == 2, "PREP: two token tiles");
         // e. Masked G^T tiles into LDS (tile pair p on wave p % DT); ck; k_p. PREP (one chunk, the
-        //    first and last): every wave forms every tile pair into registers (pg), the products and
-        //    rounding of the LDS form, and goes straight on to its outputs.
+        //    first and last): every wave forms token tile 0's pair into registers (pg), the products
+        //    and rounding of the LDS form, and goes straight on to its outputs.
         f32x4_t pg[PREP ? NPAIR : 1];
         {
             int p = 0;
 #pragma unroll
-            for (int tt = 0; tt < CT; ++tt) {
+            for (int tt = 0; tt < CTE; ++tt) {
 #pragma unroll
                 for (int st = 0; st <= tt; ++st, ++p) {
                     // (PREP forms every tile: rows past the end hold the last token's values, and
@@ -1394,13 +1393,13 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         }
         // f. This wave's output columns (gates formed above for two-wave
         //    blocks, here otherwise). PREP (the first chunk: no carried
-        //    state): every token tile's products first, then the outputs, so
+        //    state): token tile 0's products first, then its outputs, so
         //    the predicated stores do not split the product chains.
         if constexpr (PREP) {
-            f32x4_t Y[CT];
+            f32x4_t Y[CTE];
             int p0 = 0;
 #pragma unroll
-            for (int tt = 0; tt < CT; ++tt) {
+            for (int tt = 0; tt < CTE; ++tt) {
                 Y[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st <= tt; ++st)
@@ -1409,9 +1408,9 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                         Y[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pg[p0 + st][v], vx[st][v], Y[tt], 0, 0, 0);
                 p0 += tt + 1;
             }
-            float o[CT][4];
+            float o[CTE][4];
 #pragma unroll
-            for (int tt = 0; tt < CT; ++tt)
+            for (int tt = 0; tt < CTE; ++tt)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const float y = fmaf(skip, vx[tt][v], Y[tt][v]);
@@ -1423,12 +1422,12 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
             const int di = static_cast<int>(d_inner);
             if (Lc == C) {
 #pragma unroll
-                for (int tt = 0; tt < CT; ++tt)
+                for (int tt = 0; tt < CTE; ++tt)
 #pragma unroll
                     for (int v = 0; v < 4; ++v) ocol[static_cast<unsigned>((16 * tt + 4 * g + v) * di)] = o[tt][v];
             } else {
 #pragma unroll
-                for (int tt = 0; tt < CT; ++tt)
+                for (int tt = 0; tt < CTE; ++tt)
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int t = 16 * tt + 4 * g + v;
@@ -1597,10 +1596,11 @@ struct BlockArgs {
 // last two; each helper computes the last tile for all 32 rows (helper 1 the
 // second-to-last beside it) and, from it, helper 0 the chunk's step
 // coefficients and then its decay weights, helper 1 tanh(angle) * pi, then
-// the running angle sums and rotations, and both some of the gates, while the
+// the running angle sums and rotations, and helper 0 some of the gates, while the
 // scan waves copy their rows, form the norm scales and the other gates
-// (scan_head's PREP form). The helpers end after the barrier that ends step
-// d; S_BARRIER then waits on the surviving waves only.
+// (scan_head's PREP form). After the barrier that ends step d each helper
+// forms token tile 1's outputs of one head column tile while the scan waves
+// form tile 0's, and ends.
 // i / R as (i * hmagic(R)) >> 16, exact for i < 2^10 and 0 < R <= 32 (the helpers' (token, angle) item
 // indices, i < C * R <= 256): a multiply and a shift instead of the integer division's VALU sequence.
 __device__ __forceinline__ unsigned hmagic(int R) { return (65536u + static_cast<unsigned>(R) - 1u) / static_cast<unsigned>(R); }
@@ -1616,7 +1616,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
     constexpr int HP = 17;  // helper staging: [32 rows][16 columns], rows HP floats apart
     __shared__ __attribute__((aligned(16))) float hs[HELP ? DT : 1][HELP ? C * HP : 1];
     __shared__ int rot_ready;  // HELP: set by helper 1 once the rotations are in hs[1]
-    __shared__ double lg[HELP ? DT * (4 - kPrepOwnV) * 64 : 1];  // HELP: the scan waves' late gates
+    __shared__ double lg[HELP ? DT * 4 * 64 : 1];  // HELP: token tile 1's gates, [scan wave][v][lane]
     extern __shared__ __attribute__((aligned(16))) float proj_s[];  // [C, pp]
 
     const int64_t H = p.s.H, L = p.s.L;
@@ -1804,10 +1804,11 @@ void mamba3_block_scan_kernel(BlockArgs p) {
             while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
                 __builtin_amdgcn_s_sleep(1);
         }
-        __device__ const double* late_gates() const { return late; }
+        // A scan wave's tile-1 gate v (< kPrepOwnV) of this lane, for the helper that forms the outputs.
+        __device__ void share_gate(int v, double gate) const { gates[(wave * 4 + v) * 64 + (threadIdx.x & 63)] = gate; }
         const float* rot;
         int* ready;
-        const double* late;
+        double* gates;
     };
     if (threadIdx.x == 0) rot_ready = 0;  // read after the in_proj barrier, set after it
     const Hooks hooks{p,  xw, proj_s, w_lds, L,  li, grp, wave, dm, W, DI, pp, static_cast<int>(h), &hs[HELP ? 1 : 0][0],
@@ -1933,8 +1934,8 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 }
                 __hip_atomic_store(&rot_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
-            // Helper 0 (done with its decay weights well before helper 1's rotations) forms the late
-            // gates of both scan waves (token tile 1, v >= kPrepOwnV: tokens 16 + 4 grp + v, head column
+            // Helper 0 (done with its decay weights well before helper 1's rotations) forms the other
+            // token tile 1 gates of both column tiles (v >= kPrepOwnV: tokens 16 + 4 grp + v, head column
             // 16 sw + li), as scan_head forms them from z (the head's first columns of the rows; the
             // tile's rows past the end hold the last token's).
             if (hw == 0) {
@@ -1944,10 +1945,65 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                     for (int v = kPrepOwnV; v < 4; ++v) {
                         const double z = static_cast<double>(
                             proj_s[(16 + 4 * grp + v) * pp + static_cast<int>(h) * D + 16 * sw + li]);
-                        lg[(sw * (4 - kPrepOwnV) + v - kPrepOwnV) * 64 + lane] = z / (1.0 + exp_d(-z));
+                        lg[(sw * 4 + v) * 64 + lane] = z / (1.0 + exp_d(-z));
                     }
             }
-            __syncthreads();  // with the end of the scan waves' step d: the decay weights and gates are in
+            __syncthreads();  // with the end of the scan waves' step d: decay weights, gates, q and k are in
+            // Token tile 1's outputs of head column tile hw (tokens 16 + 4 grp + v, column 16 hw + li), as
+            // scan_head's steps e and f form them: the masked G^T tiles (1, 0) and (1, 1) from the scaled and
+            // rotated q/k rows and the decay weights, their products with x in the same order, the skip term
+            // and the gate (the scan waves take tile 0).
+            {
+                using SL = ScanLds<C, NT, DT>;
+                f32x4_t pg[2];
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const float4 k4 = *reinterpret_cast<const float4*>(sh.k_sh + (16 * st + li) * SL::NP + 16 * nt + 4 * grp);
+                        const float4 q4 = *reinterpret_cast<const float4*>(sh.q_sh + (16 + li) * SL::NP + 16 * nt + 4 * grp);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, q4.x, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, q4.y, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, q4.z, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, q4.w, acc, 0, 0, 0);
+                    }
+                    const float4 w4 = *reinterpret_cast<const float4*>(sh.w_s + (16 + li) * SL::WP + 16 * st + 4 * grp);
+                    f32x4_t pv = f32x4_t{w4.x * acc[0], w4.y * acc[1], w4.z * acc[2], w4.w * acc[3]};
+                    if (st == 1) {  // W[t][s] is defined for s <= t only
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) pv[v] = 4 * grp + v <= li ? pv[v] : 0.0f;
+                    }
+                    pg[st] = pv;
+                }
+                const int xcol = DI + static_cast<int>(h) * D + 16 * hw + li;
+                float vx[2][4];
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) vx[st][v] = proj_s[(16 * st + 4 * grp + v) * pp + xcol];
+                f32x4_t Y = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(pg[st][v], vx[st][v], Y, 0, 0, 0);
+                const float skip = p.s.skip[h];
+                float o[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float y = fmaf(skip, vx[1][v], Y[v]);
+                    o[v] = static_cast<float>(static_cast<double>(y) * lg[(hw * 4 + v) * 64 + lane]);
+                }
+                float* ocol = p.s.out + b * L * DI + h * D + 16 * hw + li;
+                if (L == C) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) ocol[static_cast<unsigned>((16 + 4 * grp + v) * DI)] = o[v];
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (16 + 4 * grp + v < L) ocol[static_cast<unsigned>((16 + 4 * grp + v) * DI)] = o[v];
+                }
+            }
             return;
         }
     }
