@@ -59,6 +59,8 @@ def _oracle_block(oracle, block, x):
 @pytest.mark.parametrize("dm,H,groups,B,L", [(64, 4, 8, 64, 32),   # the block workload
                                               (64, 4, 8, 3, 45),    # two chunks, the second partial
                                               (64, 4, 8, 1, 1),
+                                              (64, 4, 8, 6, 27),    # one chunk, token tile 1 partial
+                                              (64, 4, 8, 4, 12),    # one chunk, token tile 1 past the end
                                               (64, 4, 8, 5, 96),    # three full chunks
                                               (32, 2, 4, 7, 33)])   # d_model 32 in 4 groups of 8, 2 heads
 def test_block_vs_oracle_and_separate_ops(dev, oracle, dm, H, groups, B, L):
