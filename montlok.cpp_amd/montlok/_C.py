@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes as C
 import json
 import os
+import weakref
 from pathlib import Path
 
 import torch
@@ -879,25 +880,37 @@ def mla_forward_launches() -> list[str] | None:
 
 
 # Packed copies of the per-window kernel's weights (mlk_mla_pack_weights), one per (in_proj, kv_up, out)
-# weight triple: the entry keeps the three tensors, so their storage stays theirs while it is cached, and
-# is used only while each tensor is the same object at the same version (an in-place update makes a new
-# copy). A few entries at most, oldest dropped first.
+# weight triple. An entry holds the three tensors only through weak references (a deleted model's weights
+# and its entry go together) and is used only while each weight is the same live object with the same
+# data_ptr() and _version, the key the reference's own weight caches use; an in-place update through the
+# tensor or a `.data = new` swap makes a new copy. Like the reference's caches it cannot see an in-place
+# change made through `w.data` (that leaves both data_ptr and _version as they were). A pack made while a
+# stream is being captured is used for that call and not cached (its pack kernel runs only at replay).
+# A few entries at most, oldest dropped first.
 _MLA_PACKS: list = []
 _MLA_PACKS_MAX = 4
+
+
+def _weight_key(w):
+    return (w.data_ptr(), w._version)
 
 
 def _mla_packed(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nope_dim, kv_lora_rank):
     """The packed weights of mlk_mla_forward_packed, from the cache or made now; None where the geometry
     has no packed form."""
     ws = (in_proj_weight, kv_up_weight, out_weight)
-    versions = tuple(w._version for w in ws)
-    for entry in _MLA_PACKS:
-        if all(a is b for a, b in zip(entry[0], ws)) and entry[1] == versions:
-            return entry[2]
+    keys = tuple(_weight_key(w) for w in ws)
+    stream = torch.cuda.current_stream(in_proj_weight.device)
+    _MLA_PACKS[:] = [e for e in _MLA_PACKS if all(r() is not None for r in e[0])]
+    for refs, ekeys, packed, made_on in _MLA_PACKS:
+        if all(r() is w for r, w in zip(refs, ws)) and ekeys == keys:
+            if stream != made_on:
+                packed.record_stream(stream)
+            return packed
     packed = mla_pack_weights(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nope_dim, kv_lora_rank)
-    if packed is None:
-        return None
-    _MLA_PACKS.insert(0, (ws, versions, packed))
+    if packed is None or torch.cuda.is_current_stream_capturing():
+        return packed
+    _MLA_PACKS.insert(0, (tuple(weakref.ref(w) for w in ws), keys, packed, stream))
     del _MLA_PACKS[_MLA_PACKS_MAX:]
     return packed
 

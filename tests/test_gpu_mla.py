@@ -334,6 +334,20 @@ def test_packed_weights_equal_row_major(dev):
     again = _C.mla_forward(*args)
     assert not torch.equal(again, packed), "the weight update must reach the kernel"
     assert_bitwise(again, row_major().cpu().numpy(), "packed vs row-major weights after an in-place update")
+    # A `.data = new` swap keeps the object and its _version but moves data_ptr: the cache must see it.
+    version = o_w._version
+    o_w.data = (torch.randn(d, d, generator=g) * 0.05).to(dev, bf)
+    assert o_w._version == version
+    swapped = _C.mla_forward(*args)
+    assert not torch.equal(swapped, again), "the swapped weight must reach the kernel"
+    assert_bitwise(swapped, row_major().cpu().numpy(), "packed vs row-major weights after a .data swap")
+    # On another stream the cached pack is reused (recorded on that stream) and gives the same bits.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        on_side = _C.mla_forward(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(on_side, swapped)
     assert lib.mlk_mla_packed_elems(d, H, hd, nope, kvr) == _C.mla_pack_weights(in_w, up_w, o_w, H, hd, nope,
                                                                                  kvr).numel()
     assert lib.mlk_mla_packed_elems(d, H, hd, nope, 32) == 0, "no packed form without the per-window kernel"

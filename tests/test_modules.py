@@ -241,3 +241,40 @@ def test_block_and_decode_stack_contract():
     assert s.head.weight.shape == (1, 128) and len(s.layers) == 2
     with pytest.raises(ValueError, match="expects"):
         b(torch.zeros(2, 3, 32))
+
+
+def test_mla_pack_cache_holds_weights_weakly(monkeypatch):
+    """The packed-weight cache keys on (object, data_ptr, _version) and holds its weights only weakly:
+    a `.data` swap misses the cache, and deleting the weights drops their entry (CPU tensors and a stub
+    packer stand in for the device)."""
+    import gc
+
+    from montlok import _C
+
+    made = []
+
+    def fake_pack(a, b, c, *rest):
+        made.append((a.data_ptr(), b.data_ptr(), c.data_ptr()))
+        return torch.zeros(1)
+
+    class _Stream:
+        def __eq__(self, other):
+            return True
+
+    monkeypatch.setattr(_C, "mla_pack_weights", fake_pack)
+    monkeypatch.setattr(_C.torch.cuda, "current_stream", lambda device=None: _Stream())
+    monkeypatch.setattr(_C.torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setattr(_C, "_MLA_PACKS", [])
+    ws = [torch.zeros(4), torch.zeros(5), torch.zeros(6)]
+    first = _C._mla_packed(*ws, 8, 32, 16, 64)
+    assert _C._mla_packed(*ws, 8, 32, 16, 64) is first and len(made) == 1
+    ws[1].add_(1.0)  # in-place through the tensor: _version moves
+    assert _C._mla_packed(*ws, 8, 32, 16, 64) is not first and len(made) == 2
+    ws[2].data = torch.ones(6)  # data swap: same object and _version, new data_ptr
+    _C._mla_packed(*ws, 8, 32, 16, 64)
+    assert len(made) == 3
+    assert len(_C._MLA_PACKS) == 3
+    del ws
+    gc.collect()
+    _C._mla_packed(torch.zeros(4), torch.zeros(5), torch.zeros(6), 8, 32, 16, 64)
+    assert len(_C._MLA_PACKS) == 1, "entries of deleted weights must be dropped"
