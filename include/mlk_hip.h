@@ -314,8 +314,14 @@ mlk_status mlk_mamba3_siso_recurrent(const float* q, const int64_t* q_strides, c
  * library load to process end, so batch * length * heads may be at most
  * MLK_NOALLOC_SCRATCH_BYTES / 12 (699,050); larger calls fail with
  * MLK_ERR_INVALID_ARGUMENT. The entry point calls no allocating routine.
- * All calls on one GPU share its array: calls that overlap on one GPU (other
- * streams, other host threads) race and must be serialised by the caller. */
+ * All calls on one GPU share its array, and the library orders them: each
+ * call's stream first waits on an event that the previous call recorded on
+ * its own stream after using the array (a mutex orders the enqueues of host
+ * threads). Under HIP graph capture no event is waited on or recorded (a
+ * capture cannot wait on work outside it): a captured call is ordered only by
+ * its graph, so a graph holding it must not be replayed while another call on
+ * that GPU may run. The first call on each device (which looks the array's
+ * address up and creates its event) must happen outside capture. */
 #define MLK_NOALLOC_SCRATCH_BYTES (8u << 20)
 mlk_status mlk_mamba3_siso_recurrent_noalloc(const float* q, const int64_t* q_strides, const float* k,
                                              const int64_t* k_strides, const float* v, const int64_t* v_strides,

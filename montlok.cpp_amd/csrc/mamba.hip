@@ -2352,10 +2352,19 @@ constexpr size_t kNoallocScratchBytes = MLK_NOALLOC_SCRATCH_BYTES;
 __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
 constexpr int kMaxDevices = 64;
+// g_scratch_mutex guards the per-device table and is held across each call's
+// enqueue (wait, launches, record), so the calls' order on the array is the
+// order in which they took the lock, whatever host thread or stream made them.
+// g_scratch_done[device] is recorded on the calling stream after each use of
+// that device's array, and the next call's stream waits on it first.
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
+hipEvent_t g_scratch_done[kMaxDevices] = {};
+bool g_scratch_recorded[kMaxDevices] = {};
 
-mlk_status scratch_for_current_device(void** ptr) {
+// Looks the array's device address up (once per device, with that device
+// current) and creates the device's event. The caller holds g_scratch_mutex.
+mlk_status scratch_for_current_device(int* device_out) {
     int device = -1;
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) {
@@ -2366,7 +2375,6 @@ mlk_status scratch_for_current_device(void** ptr) {
         set_error("mamba3_siso_recurrent_noalloc: device index beyond the library's table");
         return MLK_ERR_UNSUPPORTED;
     }
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (g_scratch_ptr[device] == nullptr) {
         void* found = nullptr;
         err = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
@@ -2374,9 +2382,17 @@ mlk_status scratch_for_current_device(void** ptr) {
             set_error(std::string("mamba3_siso_recurrent_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(err));
             return MLK_ERR_RUNTIME;
         }
+        hipEvent_t done = nullptr;
+        err = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+        if (err != hipSuccess) {
+            set_error(std::string("mamba3_siso_recurrent_noalloc: hipEventCreateWithFlags: ") +
+                      hipGetErrorString(err));
+            return MLK_ERR_RUNTIME;
+        }
+        g_scratch_done[device] = done;
         g_scratch_ptr[device] = found;
     }
-    *ptr = g_scratch_ptr[device];
+    *device_out = device;
     return MLK_OK;
 }
 
@@ -2424,12 +2440,44 @@ mlk_status mlk_mamba3_siso_recurrent_noalloc(const float* q, const int64_t* q_st
     MLK_CHECK(q && k && v && gate && adt && dt && trap_logit && skip && out, "null tensor pointer");
     MLK_CHECK(q_strides && k_strides && v_strides && gate_strides && adt_strides && dt_strides && trap_strides,
               "null stride array");
-    void* coef = nullptr;
-    const mlk_status st = scratch_for_current_device(&coef);
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // Outside capture the call's stream waits for the previous use of the array
+    // on any stream and marks its own use. Under capture the graph's own order
+    // holds: an event recorded outside a capture cannot be waited on inside it.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hipError_t err = hipStreamIsCapturing(s, &capture);
+    if (err != hipSuccess) {
+        set_error(std::string("mamba3_siso_recurrent_noalloc: hipStreamIsCapturing: ") + hipGetErrorString(err));
+        return MLK_ERR_RUNTIME;
+    }
+    const bool eager = capture == hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    int device = -1;
+    if (hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices && !eager &&
+        g_scratch_ptr[device] == nullptr) {
+        set_error("mamba3_siso_recurrent_noalloc: the first call on a device must be made outside graph capture");
+        return MLK_ERR_INVALID_ARGUMENT;
+    }
+    const mlk_status st = scratch_for_current_device(&device);
     if (st != MLK_OK) return st;
-    return siso_recurrent(q, q_strides, k, k_strides, v, v_strides, gate, gate_strides, adt, adt_strides, dt,
-                          dt_strides, trap_logit, trap_strides, skip, batch, length, heads, d_state, headdim, out,
-                          static_cast<float*>(coef), reinterpret_cast<hipStream_t>(stream));
+    if (eager && g_scratch_recorded[device]) {
+        err = hipStreamWaitEvent(s, g_scratch_done[device], 0);
+        if (err != hipSuccess) {
+            set_error(std::string("mamba3_siso_recurrent_noalloc: hipStreamWaitEvent: ") + hipGetErrorString(err));
+            return MLK_ERR_RUNTIME;
+        }
+    }
+    const mlk_status run = siso_recurrent(q, q_strides, k, k_strides, v, v_strides, gate, gate_strides, adt,
+                                          adt_strides, dt, dt_strides, trap_logit, trap_strides, skip, batch, length,
+                                          heads, d_state, headdim, out, static_cast<float*>(g_scratch_ptr[device]), s);
+    if (run != MLK_OK || !eager) return run;
+    err = hipEventRecord(g_scratch_done[device], s);
+    if (err != hipSuccess) {
+        set_error(std::string("mamba3_siso_recurrent_noalloc: hipEventRecord: ") + hipGetErrorString(err));
+        return MLK_ERR_RUNTIME;
+    }
+    g_scratch_recorded[device] = true;
+    return MLK_OK;
 }
 
 mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_t length, int64_t width,

@@ -424,8 +424,9 @@ def mamba3_siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip):
 
 def mamba3_siso_recurrent_noalloc(q, k, v, gate, adt, dt, trap_logit, skip):
     """mamba3_siso_recurrent through the entry point that allocates no device memory: the coefficients live
-    in the library's static per-GPU scratch (B * L * H at most 699,050). Same result bit for bit; calls that
-    overlap on one GPU race. No counterpart in the reference."""
+    in the library's static per-GPU scratch (B * L * H at most 699,050). Same result bit for bit. The library
+    orders the calls that share a GPU's scratch across streams with an event; under graph capture only the
+    graph orders them, and the first call on a device must be eager. No counterpart in the reference."""
     return _siso_recurrent(q, k, v, gate, adt, dt, trap_logit, skip, noalloc=True)
 
 

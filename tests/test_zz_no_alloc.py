@@ -2,7 +2,8 @@
 no counterpart in the reference) against mlk_mamba3_siso_recurrent, which takes
 a caller workspace: bit for bit, on two calls in a row (the second smaller, so
 it runs over what the first left in the static scratch), with strided views,
-and a size beyond the static scratch rejected before any launch."""
+a size beyond the static scratch rejected before any launch, calls on two
+streams ordered by the library, and the call captured in a HIP graph."""
 
 from __future__ import annotations
 
@@ -52,3 +53,57 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(dev):
     c = torch.zeros(B, L, H, device=dev)
     with pytest.raises(RuntimeError, match="exceeds the static scratch"):
         _C.mamba3_siso_recurrent_noalloc(q, q, v, v, c, c, c, torch.zeros(H, device=dev))
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    """A long call on one stream, then at once a shorter one on another: the second call's coefficients
+    would overwrite the first's while the first still reads them, unless the library orders the two."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(41)
+    big = _inputs(g, 16, 2048, 16, 16, 32, dev)  # B * L * H = 524,288 of the scratch's 699,050
+    small = _inputs(g, 8, 512, 4, 16, 32, dev)
+    expect_big = _C.mamba3_siso_recurrent(*big)
+    expect_small = _C.mamba3_siso_recurrent(*small)
+    torch.cuda.synchronize()
+    for trial in range(3):
+        sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+        sa.wait_stream(torch.cuda.current_stream())
+        sb.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(sa):
+            got_big = _C.mamba3_siso_recurrent_noalloc(*big)
+        with torch.cuda.stream(sb):
+            got_small = _C.mamba3_siso_recurrent_noalloc(*small)
+        torch.cuda.synchronize()
+        assert_bitwise(got_big, expect_big.cpu().numpy(), f"first call, stream A, trial {trial}")
+        assert_bitwise(got_small, expect_small.cpu().numpy(), f"second call, stream B, trial {trial}")
+
+
+def test_noalloc_under_graph_capture(dev):
+    """One eager call (the per-device set-up), then the call captured in a graph: every replay, with other
+    eager noalloc calls between them that overwrite the scratch, equals the workspace form bit for bit."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(43)
+    args = _inputs(g, 8, 96, 4, 16, 32, dev)
+    other = _inputs(g, 4, 200, 2, 32, 64, dev)
+    expect = _C.mamba3_siso_recurrent(*args).cpu().numpy()
+    expect_other = _C.mamba3_siso_recurrent(*other).cpu().numpy()
+    _C.mamba3_siso_recurrent_noalloc(*args)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _C.mamba3_siso_recurrent_noalloc(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = _C.mamba3_siso_recurrent_noalloc(*args)
+    for replay in range(4):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bitwise(out, expect, f"graph replay {replay}")
+        eager = _C.mamba3_siso_recurrent_noalloc(*other)
+        torch.cuda.synchronize()
+        assert_bitwise(eager, expect_other, f"eager call after replay {replay}")
