@@ -698,7 +698,7 @@ def bench_mla(steps: int, warmup: int, cpu: bool) -> dict:
         ops = separate_ops
     table = _kernel_table(ops, _op_times(ops, max(4, steps // 8)), "bf16")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
-    line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms, "bf16 weights, f32 activations/accumulate",
+    line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms, "bf16 weights and contraction operands, fp32 accumulate",
                       "synthetic (seeded N(0,1) inputs, N(0,0.02) bf16 weights)",
                       {"workload": "mla_causal_fwd", "windows": B, "seq_len": L, "d_model": d, "heads": H,
                        "head_dim": hd, "rope_dim": r, "kv_rank": kvr, "rope_theta": cfg["theta"],
@@ -1059,7 +1059,7 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
                                                                    ops["mamba_out_proj"]["flops"]) + \
         2 * ops["mla_forward"]["flops"]
     line = _base_line(B / (ms * 1e-3), "windows/s", steps, warmup, ms,
-                      "bf16 weights, f32 activations/state/accumulate",
+                      "bf16 weights and contraction operands, fp32 accumulate and state",
                       "synthetic (seeded N(0,1) features clipped to [-8,8], N(0,0.02) bf16 weights)",
                       {"workload": "rdt4quant_stack_4_layers", "windows": B, "seq_len": L, "features": cfg["features"],
                        "d_model": d, "layers": cfg["layers"], "n_streams": n, "sinkhorn_iters": cfg["iters"],

@@ -204,3 +204,41 @@ def test_mhc_errors(dev):
     with pytest.raises(RuntimeError, match="res must be contiguous"):
         _C.mhc_combine(s, torch.zeros(1, 4, 4, 4, device=dev).transpose(2, 3), torch.zeros(1, 4, 4, device=dev),
                        torch.zeros(1, 4, 8, device=dev))
+
+
+def test_mhc_combine_prepare_plain_store_branch(dev, oracle):
+    """Above 65,536 tokens the fused combine+prepare stores its outputs with plain (not non-temporal)
+    stores. At 70,000 tokens x d 256 x n 4 it equals combine then prepare bit for bit, and a 1,024-token
+    slice matches the oracle (montlok_selftest.cpp:606-677)."""
+    from montlok import _C
+
+    rng = np.random.default_rng(70000)
+    n, d, B, L = 4, 256, 70, 1000
+    s, nw, pw, pb, qb, rb = _random_mhc(rng, B, L, n, d)
+    alphas = (0.7, 0.6, 0.8)
+    p = (_t(nw, dev), 1e-5, _t(pw, dev), _t(pb, dev), _t(qb, dev), _t(rb, dev),
+         *(torch.tensor(a, device=dev) for a in alphas), 20)
+    ts = _t(s, dev)
+    agg, pre, post, res = _C.mhc_prepare(ts, *p)
+    out = torch.tanh(agg)
+    fused = _C.mhc_combine_prepare(ts, res, post, out, *p)
+    sep_streams = _C.mhc_combine(ts, res, post, out)
+    sep = _C.mhc_prepare(sep_streams, *p)
+    assert fused[0].shape == (B, L, n, d)
+    assert_bitwise(fused[0], sep_streams.cpu().numpy(), "streams, 70,000 tokens")
+    for name, a, b in zip(("agg", "pre", "post", "res"), fused[1:], sep):
+        assert_bitwise(a, b.cpu().numpy(), f"{name}, 70,000 tokens")
+    # The oracle on a 1,024-token slice: the first 1,024 tokens of windows 37 and 38.
+    w0 = 37
+    s_sl = s[w0:w0 + 2]
+    res_sl, post_sl, out_sl = (t[w0:w0 + 2].cpu().numpy() for t in (res, post, out))
+    e_new = oracle.mhc_combine(s_sl, res_sl, post_sl, out_sl)
+    e_prep = oracle.mhc_prepare(e_new, nw, 1e-5, pw, pb, qb, rb, *alphas, 20)
+    flat = lambda a: a.reshape(2 * L, *a.shape[2:])[:1024]  # noqa: E731
+    assert_bitwise(flat(fused[0][w0:w0 + 2].cpu().numpy()), flat(e_new), "streams vs oracle, 1,024 tokens")
+    mism = 0
+    for name, a, e in zip(("agg", "pre", "post", "res"), fused[1:], e_prep):
+        a_sl = flat(a[w0:w0 + 2].cpu().numpy())
+        assert_close(a_sl, flat(np.asarray(e)), name=f"{name} vs oracle")
+        mism += bit_mismatches(a_sl, flat(np.asarray(e)))
+    assert mism <= max(4, 1024 * n // 1000), mism

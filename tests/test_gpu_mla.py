@@ -17,7 +17,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import BF16_TOL, assert_bitwise, assert_close
+import bf16_emu as emu
+from helpers import BF16_TOL, assert_bitwise, assert_close, assert_emulated, rel_err, row_errors
 
 pytestmark = pytest.mark.gpu
 
@@ -401,3 +402,56 @@ def test_non_positive_scale_takes_the_scaled_softmax(dev, oracle, scale):
     assert_bitwise(out, separate.cpu().numpy(), f"scale {scale}: fused attention vs separate operators")
     expect = _oracle_mla(oracle, x, p, H, hd, nope, kv_rank, L, True, scale, cos, sin)
     assert_close(out, expect, tol=BF16_TOL, name=f"scale {scale}: mla_forward vs oracle")
+
+
+@pytest.mark.parametrize("geometry", sorted(MLA_GEOMETRIES))
+def test_bf16_mla_vs_emulation(dev, oracle, geometry):
+    """The bf16 MLA forms (the one-launch kernel where built, the four-launch path, the separate operators)
+    against the float64 restatement of their roundings (tests/bf16_emu.py: normwise EMU_TOL, median row
+    EMU_ROW_MEDIAN_TOL), and against the fp32 oracle chain within the 2e-2 contract; both printed."""
+    from montlok import _C
+
+    rng = np.random.default_rng(77)
+    B, L, d, H, hd, nope, kvr = MLA_GEOMETRIES[geometry]
+    x = rng.standard_normal((B, L, d)).astype(np.float32)
+    p = _mla_params(rng, d, H, hd, nope, kvr, True)
+    cos, sin = rope_tables(L, hd - nope)
+    scale = 1.0 / math.sqrt(hd)
+    bw = lambda a: _t(a, dev).to(torch.bfloat16)  # noqa: E731
+    in_w = np.concatenate([p["q"], p["kv_down"], p["k_rope"]])
+    args = (_t(x, dev), bw(in_w), torch.empty(0, device=dev), _t(p["ln_w"], dev), _t(p["ln_b"], dev), 1e-5,
+            bw(p["kv_up"]), bw(p["o"]), _t(cos, dev), _t(sin, dev), H, hd, nope, kvr, L, True, scale)
+    emulated = emu.mla_forward(x, p["q"], p["kv_down"], p["k_rope"], p["ln_w"], p["ln_b"], 1e-5, p["kv_up"], p["o"],
+                               cos, sin, H, hd, nope, scale)
+    fp32 = _oracle_mla(oracle, x, p, H, hd, nope, kvr, L, True, scale, cos, sin)
+    paths = {"four launches": _C._mla_forward(*args, allow_fused=True, allow_window=False),
+             "separate operators": _C._mla_forward(*args, allow_fused=False)}
+    if geometry == "block":
+        paths["one launch"] = _C._mla_forward(*args, allow_fused=True)
+        assert _C.mla_forward_launches() == ["mla_forward"]
+    for name, out in paths.items():
+        e_orc = assert_close(out, fp32, tol=BF16_TOL, name=f"{geometry} {name} vs the fp32 oracle")
+        m_orc = float(np.median(row_errors(out, fp32)))
+        e_emu, m_emu = assert_emulated(out, emulated, name=f"{geometry} {name} vs the bf16 emulation")
+        print(f"MLA {geometry} {name}: vs the bf16 emulation {e_emu:.2e} (median row {m_emu:.1e}), "
+              f"vs the fp32 oracle {e_orc:.2e} (median row {m_orc:.1e})")
+
+
+@pytest.mark.parametrize("B,Lq,Lk,H,hd,mask", ATTN_CASES)
+def test_bf16_attention_vs_emulation(dev, oracle, B, Lq, Lk, H, hd, mask):
+    """_C.attention in bf16 against the float64 restatement of its roundings (normwise EMU_TOL, median row
+    EMU_ROW_MEDIAN_TOL); the fp32 oracle's distance printed beside it."""
+    from montlok import _C
+
+    rng = np.random.default_rng(B + Lq + Lk + hd + mask)
+    q = rng.standard_normal((B, Lq, H, hd)).astype(np.float32)
+    k = rng.standard_normal((B, Lk, H, hd)).astype(np.float32)
+    v = rng.standard_normal((B, Lk, H, hd)).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    out = _C.attention(_t(q, dev), _t(k, dev), _t(v, dev), mask, scale, torch.bfloat16)
+    emulated = emu.attention(q, k, v, mask, scale)
+    fp32 = oracle.sdpa(q, k, v, mask, scale)
+    e_orc, m_orc = rel_err(out, fp32), float(np.median(row_errors(out, fp32)))
+    e_emu, m_emu = assert_emulated(out, emulated, name="bf16 attention vs the emulation")
+    print(f"bf16 attention {B}x{Lq}x{Lk} h{H} hd{hd} mask {mask}: vs the bf16 emulation {e_emu:.2e} "
+          f"(median row {m_emu:.1e}), vs the fp32 oracle {e_orc:.2e} (median row {m_orc:.1e})")
