@@ -19,6 +19,11 @@ time / K. Further replays of the same graph (30, or as many as fit in 10 s)
 give the median and spread of the per-step time. Inputs are resident in HBM
 before timing.
 
+With no --workload, the line is the block's and, under "configs", the other
+four workloads' figures from the same run (value, ms per step, median, the
+dominant kernel's roofline and counter traffic, the CPU baseline); --configs
+none measures the named workload alone.
+
 Prints one JSON line: whole-job throughput, the roofline of the dominant
 kernel (per-launch average from HIP events over graph replays of that kernel
 on the stream it runs on) and the CPU baseline: the reference's CPU kernels
@@ -198,6 +203,17 @@ def _gpu_steps(step_fns, steps: int, warmup: int, budget_s: float = 10.0) -> dic
     return {"steps": steps, "ms_per_step": total_ms / steps, "timed_region_ms": total_ms,
             "median_ms_per_step": statistics.median(per), "p10_ms_per_step": per[int(0.1 * (reps - 1))],
             "p90_ms_per_step": per[int(0.9 * (reps - 1))], "median_replays": reps}
+
+
+def _floor_ms(shapes, steps: int) -> float:
+    """Milliseconds per step of a HIP graph holding `steps` steps of empty kernels in the given launch shapes
+    (blocks, threads, dynamic LDS bytes): the floor a step of launches in those shapes pays before any work."""
+    from montlok import _C
+
+    g = _graph([lambda s=s: _C.empty_kernel(*s) for _ in range(steps) for s in shapes])
+    _upload(g)
+    g.replay()
+    return _time_graph(g, 10) / steps
 
 
 def _timing_fields(t: dict) -> dict:
@@ -541,6 +557,16 @@ def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
         }
     table = _kernel_table(ops, _op_times(ops, max(8, steps)), "f32")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
+    floor = None
+    if launches == ["rms_norm_mamba3_forward", "linear_residual"]:
+        # The graph-node floor of the step: empty kernels in the two launches' shapes (the mixer: a block of
+        # 8 waves per (window, head) with its dynamic LDS; the out_proj: a wave per 16 x 16 output tile).
+        mixer = (B * H, 256, 4 * 32 * ((W + 15) // 16 * 16 + 4))
+        out_proj = (-(-T // 16) * -(-d // 16), 64, 0)
+        floor = {name: _floor_ms([shape], steps) for name, shape in (("mixer", mixer), ("out_proj", out_proj))}
+        floor["step"] = _floor_ms([mixer, out_proj], steps)
+        floor["ms_per_step_over_floor"] = ms / floor["step"]
+        floor["shapes"] = {"mixer": list(mixer), "out_proj": list(out_proj)}
     line = _base_line(B / (ms * 1e-3), "windows/s", t["steps"], warmup, ms, "f32",
                       "synthetic (seeded N(0,1) inputs, Kaiming-uniform weights, dt bias per mamba3.py:128-130)",
                       {"workload": "rmsnorm_mamba3_block", "windows": B, "seq_len": L, "d_model": d, "heads": H,
@@ -556,6 +582,8 @@ def bench_block(steps: int, warmup: int, cpu: bool) -> dict:
     line["step_hbm_frac"] = total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
     line["step_fp32_frac"] = total_flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFS["f32"]
     line["tokens_per_s"] = T / (ms * 1e-3)
+    if floor is not None:
+        line["graph_node_floor_ms"] = floor
     if cpu:
         line["cpu_baseline"] = cpu_baseline_block(cfg, x_cpu, norm_w, wts, geo)
         line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
@@ -1111,6 +1139,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="block", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--configs", choices=("all", "none"), default="all",
+                    help="also measure the other workloads, each summarised under \"configs\" (default: all)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -1118,13 +1148,49 @@ def main() -> int:
               f"shard by independent windows, tokens and streams, one share per GPU, with no exchange between "
               f"GPUs inside a step.", file=sys.stderr)
         return 2
+    import torch
+
+    t0 = time.perf_counter()
     line = WORKLOADS[args.workload](args.steps, args.warmup, cpu=not args.no_cpu)
+    print(f"bench: {args.workload} done in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    copy = copy_bandwidth()
     if line["roofline"]["bound"] == "hbm":
-        copy = copy_bandwidth()
         line["roofline"]["copy_GBs"] = copy
         line["roofline"]["frac_of_copy"] = line["roofline"]["achieved"] / copy
+    if args.configs == "all":
+        line["configs"] = {args.workload: "this line"}
+        for name, fn in WORKLOADS.items():
+            if name == args.workload:
+                continue
+            t1 = time.perf_counter()
+            sub = fn(args.steps, args.warmup, cpu=not args.no_cpu)
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            line["configs"][name] = _config_summary(sub, copy)
+            print(f"bench: {name} done in {time.perf_counter() - t1:.1f} s", file=sys.stderr, flush=True)
     print(json.dumps(line))
     return 0
+
+
+def _config_summary(sub: dict, copy_gbs: float) -> dict:
+    """The fields of another workload's line that the default line carries for it."""
+    roof = {k: sub["roofline"][k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac", "traffic",
+                                            "launch_ms")}
+    if roof["bound"] == "hbm":
+        roof["copy_GBs"] = copy_gbs
+        roof["frac_of_copy"] = roof["achieved"] / copy_gbs
+    out = {"value": sub["value"], "unit": sub["unit"], "steps": sub["steps"],
+           "warmup": sub["warmup"], "ms_per_step": sub["ms_per_step"],
+           "median_ms_per_step": sub["median_ms_per_step"], "dtype": sub["dtype"], "config": sub["config"],
+           "roofline": roof, "kernels": sub.get("kernels")}
+    for k in ("step_hbm_frac", "step_roofline_frac", "step_mfma_frac", "step_fp32_frac"):
+        if k in sub:
+            out[k] = sub[k]
+    if "cpu_baseline" in sub:
+        cb = sub["cpu_baseline"]
+        out["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample", "one_thread_value",
+                                                 "gpu_over_cpu") if k in cb}
+    return out
 
 
 if __name__ == "__main__":

@@ -68,6 +68,12 @@ int mlk_abi_version(void);
  * Writes at most `capacity` bytes including the terminating NUL. */
 mlk_status mlk_build_info(char* buffer, size_t capacity);
 
+/* Launches a kernel that does nothing, with `blocks` x `threads` and the
+ * given dynamic LDS: a diagnostic with no counterpart in the reference. HIP
+ * graph nodes of it, in a kernel's launch shape, time the floor that launch
+ * pays before any of its work (the measurement reports it beside the step). */
+mlk_status mlk_empty_kernel(int64_t blocks, int64_t threads, size_t dynamic_lds_bytes, mlk_stream_t stream);
+
 /* ---------------------------------------------------------------- norms -- */
 
 /* rms_norm(x, weight, eps, groups) -- montlok.cpp:915-938, kernel

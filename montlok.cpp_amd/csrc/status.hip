@@ -23,9 +23,22 @@ mlk_status launch_status(const char* what) {
     return MLK_OK;
 }
 
+// A kernel that does nothing: graph nodes of it with a kernel's launch shape
+// time the floor that launch pays before any of its work.
+__global__ void empty_kernel() {}
+
 }  // namespace mlk
 
 extern "C" {
+
+mlk_status mlk_empty_kernel(int64_t blocks, int64_t threads, size_t dynamic_lds_bytes, mlk_stream_t stream) {
+    MLK_CHECK(blocks > 0 && blocks <= (int64_t{1} << 31) - 1, "blocks must be in [1, 2^31)");
+    MLK_CHECK(threads > 0 && threads <= 1024, "threads must be in [1, 1024]");
+    MLK_CHECK(dynamic_lds_bytes <= 160 * 1024, "dynamic LDS must be at most 160 KiB");
+    hipLaunchKernelGGL(mlk::empty_kernel, dim3(static_cast<unsigned>(blocks)), dim3(static_cast<unsigned>(threads)),
+                       dynamic_lds_bytes, reinterpret_cast<hipStream_t>(stream));
+    return mlk::launch_status("empty_kernel");
+}
 
 const char* mlk_last_error(void) { return mlk::g_last_error.c_str(); }
 

@@ -38,6 +38,8 @@ def _load():
     lib.mlk_last_error.restype = C.c_char_p
     lib.mlk_abi_version.restype = C.c_int
     lib.mlk_build_info.argtypes = [C.c_char_p, C.c_size_t]
+    lib.mlk_empty_kernel.argtypes = [_i64, _i64, C.c_size_t, _vp]
+    lib.mlk_empty_kernel.restype = C.c_int
     sigs = {
         "mlk_rms_norm": [_vp, _i64, _i64, _i64, _vp, _dbl, _i64, _vp, _vp],
         "mlk_add_rms_norm": [_vp, _vp, _i64, _i64, _vp, _dbl, _i64, _vp, _vp, _vp],
@@ -1082,13 +1084,19 @@ def set_isa(name: str, force: bool = False) -> str:
 
 def exported_symbols() -> list[str]:
     """Names of the C ABI entry points this module binds."""
-    return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_rms_norm", "mlk_add_rms_norm",
+    return ["mlk_last_error", "mlk_abi_version", "mlk_build_info", "mlk_empty_kernel", "mlk_rms_norm", "mlk_add_rms_norm",
             "mlk_layer_norm", "mlk_swiglu", "mlk_mhc_prepare", "mlk_mhc_combine", "mlk_mhc_combine_prepare",
             "mlk_math_check", "mlk_mamba3_workspace_bytes", "mlk_mamba3_siso_recurrent",
             "mlk_mamba3_siso_recurrent_noalloc", "mlk_mamba3_siso_forward", "mlk_rms_norm_mamba3_forward",
             "mlk_mamba3_siso_step", "mlk_linear", "mlk_linear_residual", "mlk_rms_norm_linear",
             "mlk_layer_norm_bf16", "mlk_mla_rope_qk", "mlk_attention", "mlk_mla_attend", "mlk_mla_attend_normed",
             "mlk_mla_forward", "mlk_mla_packed_elems", "mlk_mla_pack_weights", "mlk_mla_forward_packed"]
+
+
+def empty_kernel(blocks: int, threads: int, dynamic_lds_bytes: int = 0) -> None:
+    """One launch of a kernel that does nothing, in the given launch shape, on the current stream (graph
+    nodes of it time a launch's floor). No counterpart in the reference."""
+    _call("mlk_empty_kernel", blocks, threads, dynamic_lds_bytes, _stream())
 
 
 def math_check(x: torch.Tensor) -> dict:
