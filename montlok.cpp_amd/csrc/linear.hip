@@ -34,6 +34,10 @@
 // groups inside the MFMA); for fp32 weights the result differs from a
 // sequential fp32 dot product by rounding only.
 
+#include <cstdlib>
+#include <type_traits>
+#include <cstring>
+
 #include "mlk_common.h"
 #include "tile_f32.h"
 
@@ -654,11 +658,176 @@ __global__ __launch_bounds__(kThreads) void linear_t32_kernel(LinearArgs p) {
     }
 }
 
+// bf16 weights, K = 256 and a wide output, streaming form: the weights stay in
+// registers and x streams through LDS. Each wave owns 32 columns of W (its A
+// fragments for all of K: 16 k steps x 16 bytes per lane), a block of 8 waves
+// a group of 256 columns. Blocks are persistent, one per CU: block (row part,
+// column group) walks its row part's 32-row tiles; each x tile is loaded from
+// HBM into registers a tile ahead, rounded to bf16 and written to one of two
+// LDS buffers (one barrier per tile). The column groups of a row part run on
+// one XCD (round-robin dispatch puts block i on XCD i % 8), so x comes from
+// HBM once and from that XCD's L2 for the other groups (without that
+// placement: 643 instead of 455 us). Per 32 x 32 tile the chain over k is
+// linear_t32_kernel's (32 x 32 x 16 MFMA, W as A, x as B, k steps in order),
+// so the two kernels give the same bits; the W fragments are read once per
+// block instead of from LDS once per 64 columns and 256 rows. Accumulator lane
+// (h, l): row l, columns 8j + 4h .. + 3 (j = 0..3), stored as 16-byte pieces.
+//   262144 x 256 -> 1192: 455 us against 508-528 us for linear_t32_kernel.
+//   Measured and not kept: two 32-row chains per wave (515 us), the output
+//   rows staged through LDS so each store writes whole 128-byte pieces (482
+//   us; non-temporal, 639 us), x two tiles ahead (485 us), every B fragment
+//   read from LDS before the chain (no change). Without its stores the kernel
+//   takes 372 us; a plain fill writes the 1.25 GB output in 187 us.
+constexpr int kStreamWaves = 8;
+constexpr int kStreamCols = 32 * kStreamWaves;  // columns per block
+constexpr int kStreamRT = 1;                    // 32-row tiles per step
+constexpr int kStreamRows = 32 * kStreamRT;     // rows per step
+constexpr int kStreamK = 256;                   // the form takes K = 256 exactly (16-byte aligned operands)
+
+__global__ __launch_bounds__(64 * kStreamWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
+    using T = u16;
+    constexpr int kSteps = kStreamK / 16;
+    constexpr int kPitch = kStreamK + 8;      // LDS row pitch in bf16 (+16 bytes)
+    constexpr int kThr = 64 * kStreamWaves;
+    constexpr int kTPR = kThr / kStreamRows;  // threads per x row
+    constexpr int kXPer = kStreamK / kTPR;    // x floats per thread per tile
+    static_assert(kXPer % 8 == 0, "whole 16-byte bf16 units per thread");
+    __shared__ __attribute__((aligned(16))) T x_lds[2][kStreamRows * kPitch];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    // Block -> (XCD, local index) -> (row part, column group): the groups of a row part share an XCD.
+    const int xcd = blockIdx.x % 8;
+    const int local = blockIdx.x / 8;
+    const int cg = local % col_groups;
+    const int rpl = local / col_groups;
+    const int rp = rpl * 8 + xcd;
+    if (rp >= row_parts) return;
+    const int64_t tiles = (p.rows + kStreamRows - 1) / kStreamRows;
+    const int64_t t_begin = tiles * rp / row_parts, t_end = tiles * (rp + 1) / row_parts;
+    if (t_begin >= t_end) return;
+    const int64_t n_wave = static_cast<int64_t>(cg) * kStreamCols + 32 * wave;  // this wave's first column
+    const bool wave_live = n_wave < p.N;
+    const bool vec_out = (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 &&
+                         (p.residual == nullptr ||
+                          ((reinterpret_cast<uintptr_t>(p.residual) & 15) == 0 && p.res_stride % 4 == 0));
+
+    // W fragments: step s holds column n_wave + r32, k = 16 s + 8 h .. + 7 (zero past N).
+    uint4 wf[kSteps];
+    {
+        const T* w = static_cast<const T*>(p.w);
+        const int64_t n = n_wave + r32;
+        const T* wrow = w + (n < p.N ? n : p.N - 1) * kStreamK + 8 * h;
+        const uint32_t keep = n < p.N ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const uint4 v = *reinterpret_cast<const uint4*>(wrow + 16 * s);
+            wf[s] = uint4{v.x & keep, v.y & keep, v.z & keep, v.w & keep};
+        }
+    }
+    // x tile loads: thread t takes row t / kTPR, columns kXPer (t % kTPR) .. (rows past the end read the
+    // last row and are zeroed where they are converted).
+    const int xr = threadIdx.x / kTPR, xc = kXPer * (threadIdx.x % kTPR);
+    float4 xv[kXPer / 4];
+    auto load_tile = [&](int64_t t) {
+        const int64_t row = t * kStreamRows + xr;
+        const float* src = p.x + (row < p.rows ? row : p.rows - 1) * p.x_stride + xc;
+#pragma unroll
+        for (int q = 0; q < kXPer / 4; ++q) xv[q] = *reinterpret_cast<const float4*>(src + 4 * q);
+    };
+    auto store_tile = [&](int64_t t, T* buf) {
+        const bool live = t * kStreamRows + xr < p.rows;
+#pragma unroll
+        for (int u = 0; u < kXPer / 8; ++u) {
+            const float4 a = xv[2 * u], b = xv[2 * u + 1];
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            bf16x8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = static_cast<__bf16>(live ? v[j] : 0.0f);
+            *reinterpret_cast<bf16x8*>(buf + xr * kPitch + xc + 8 * u) = o;
+        }
+    };
+
+    load_tile(t_begin);
+    store_tile(t_begin, x_lds[0]);
+    __syncthreads();
+    auto iteration = [&](int64_t t, auto par_c) {
+        constexpr int PAR = decltype(par_c)::value;  // (t - t_begin) % 2: the LDS buffer of tile t
+        const bool more = t + 1 < t_end;
+        if (more) load_tile(t + 1);
+        const T* buf = x_lds[PAR];
+        if (wave_live) {
+            f32x16 acc[kStreamRT];
+#pragma unroll
+            for (int m = 0; m < kStreamRT; ++m)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[m][v] = 0.0f;
+            uint4 xb[kStreamRT][kSteps];
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s)
+#pragma unroll
+                for (int m = 0; m < kStreamRT; ++m)
+                    xb[m][s] = *reinterpret_cast<const uint4*>(buf + (32 * m + r32) * kPitch + 16 * s + 8 * h);
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+#pragma unroll
+                for (int m = 0; m < kStreamRT; ++m) {
+                    acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[s]),
+                                                                     __builtin_bit_cast(bf16x8, xb[m][s]), acc[m], 0,
+                                                                     0, 0);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < kStreamRT; ++m) {
+                const int64_t row = t * kStreamRows + 32 * m + r32;
+                if (row < p.rows) {
+                    float* orow = p.out + row * p.out_stride;
+                    const float* rrow = p.residual != nullptr ? p.residual + row * p.res_stride : nullptr;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int64_t col = n_wave + 8 * j + 4 * h;
+                        f32x4 y = {acc[m][4 * j], acc[m][4 * j + 1], acc[m][4 * j + 2], acc[m][4 * j + 3]};
+                        if (p.bias != nullptr) {
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) y[u] += p.bias[col + u < p.N ? col + u : p.N - 1];
+                        }
+                        if (col + 4 <= p.N && vec_out) {
+                            if (rrow != nullptr) y = *reinterpret_cast<const f32x4*>(rrow + col) + y;
+                            *reinterpret_cast<f32x4*>(orow + col) = y;
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                if (col + u < p.N) orow[col + u] = rrow != nullptr ? rrow[col + u] + y[u] : y[u];
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        if (more) store_tile(t + 1, x_lds[PAR ^ 1]);
+        __syncthreads();
+    };
+    for (int64_t t = t_begin; t < t_end; t += 2) {
+        iteration(t, std::integral_constant<int, 0>{});
+        if (t + 1 < t_end) iteration(t + 1, std::integral_constant<int, 1>{});
+    }
+}
+
 // Shapes too small to give the 128-row blocks one per CU (256 CUs), with K
 // held in at most eight 32-wide steps.
 bool small_shape(int64_t rows, int64_t K, int64_t N) {
     return K % 8 == 0 && K <= 256 && ceil_div(rows, kRowsPerBlock) * ceil_div(N, kColsPerChunk) < 256 &&
            ceil_div(rows, 16) * ceil_div(N, 16) <= 0x7fffffff;
+}
+
+// MLK_LINEAR_FORM=t32 keeps linear_t32_kernel for the shapes the streaming form takes (read at each
+// call, so a caller can compare the two forms).
+bool stream_form() {
+    const char* v = std::getenv("MLK_LINEAR_FORM");
+    return !(v != nullptr && std::strcmp(v, "t32") == 0);
 }
 
 template <bool BF16W, bool VEC>
@@ -684,6 +853,17 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
     // form, whose smaller blocks give more parallelism (32768 x 256 -> 336:
     // 28 us against 42 us; 262144 x 40 -> 256: 90 against 129 us).
     if constexpr (BF16W) {
+        if (VEC && p.K == kStreamK && p.x_stride % 4 == 0 && n_chunks >= 12 && stream_form()) {
+            const int col_groups = static_cast<int>(ceil_div(p.N, kStreamCols));
+            // One block per CU (256 CUs): per XCD 32 block slots, whole row parts of col_groups blocks each.
+            const int parts_per_xcd = 32 / col_groups;
+            if (parts_per_xcd >= 1) {
+                const int row_parts = 8 * parts_per_xcd;
+                hipLaunchKernelGGL(linear_stream_kernel, dim3(static_cast<unsigned>(8 * parts_per_xcd * col_groups)),
+                                   dim3(64 * kStreamWaves), 0, stream, p, col_groups, row_parts);
+                return;
+            }
+        }
         if (p.K <= KC && n_chunks >= 12) {
             const int64_t row_blocks32 = ceil_div(rows, 2 * kRowsPerBlock);
             int64_t gy32 = 1;

@@ -815,6 +815,18 @@ void mla_attend_kernel(MlaAttendArgs p) {
 
 // ------------------------------------------------- whole MLA forward per window
 
+// x of a window goes in MLK_MLA_XPARTS parts of K, MLK_MLA_XDEPTH of them in
+// flight: one part at a time (its successor issued once it has landed) took
+// the 256 x 128 workload from 30.6 to 29.5 us per step (median), because every
+// block's part 0 then lands early instead of with the whole burst; four parts
+// spill registers (37.5 us).
+#ifndef MLK_MLA_XPARTS
+#define MLK_MLA_XPARTS 2
+#endif
+#ifndef MLK_MLA_XDEPTH
+#define MLK_MLA_XDEPTH 1
+#endif
+
 // mla_forward (montlok.cpp:1159-1211) for every causal query, one block of 8
 // waves per window, so that neither the in_proj output nor the attention
 // output goes through HBM: x is read once and the o_proj result written once.
@@ -930,33 +942,44 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
     // 1. Loads: x rows (rows past L read row L - 1 and are zeroed) and the W
     // fragments of this wave's in_proj tiles; everything else waits until
     // the W fragments are dead, so the registers hold.
-    // x goes in two halves of K (k < D / 2, then the rest), each followed by the W fragments of its k
-    // steps, so the first half's products start while the second half is still arriving.
-    constexpr int XU = LMAX * (D / 8) / 512;  // 8-float units per thread, XU / 2 per half
-    constexpr int SH = D / 64;                // k steps per half
-    float4 xa[XU], xb[XU];
-    auto xunit = [&](int j, int& row, int& c8) {  // unit j: half j / (XU / 2), 16 rows of 16 units per pass
-        const int hf = j / (XU / 2), u = tid + 512 * (j % (XU / 2));
-        row = u / (D / 16);
-        c8 = hf * (D / 2) + (u % (D / 16)) * 8;
+    // x goes in XP parts of K (part q: k in [q D / XP, (q + 1) D / XP)), each followed by the W fragments of
+    // its k steps. The first XDEPTH parts are issued here; part q + XDEPTH is issued once part q has landed
+    // (after its barrier below), so that, with every block loading at once, the first parts land early and
+    // their products run while the later parts arrive.
+    constexpr int XP = MLK_MLA_XPARTS, XDEPTH = MLK_MLA_XDEPTH;
+    static_assert(XP == 2 || XP == 4, "x in two or four parts of K");
+    static_assert(XDEPTH >= 1 && XDEPTH <= XP, "parts in flight");
+    constexpr int XU = LMAX * (D / 8) / 512;  // 8-float units per thread, XU / XP per part
+    constexpr int SH = D / 32 / XP;           // k steps per part
+    constexpr int PW = D / XP / 8;            // 8-float units of a row in one part
+    constexpr int RU = XDEPTH * (XU / XP);    // registers hold the parts in flight: part q in slot q % XDEPTH
+    float4 xa[RU], xb[RU];
+    auto xunit = [&](int j, int& row, int& c8) {  // unit j: part j / (XU / XP), PW units per row
+        const int q = j / (XU / XP), u = tid + 512 * (j % (XU / XP));
+        row = u / PW;
+        c8 = q * (D / XP) + (u % PW) * 8;
+    };
+    auto slot = [](int j) { return (j / (XU / XP)) % XDEPTH * (XU / XP) + j % (XU / XP); };
+    auto load_x = [&](int q) {
+#pragma unroll
+        for (int j = q * (XU / XP); j < (q + 1) * (XU / XP); ++j) {
+            int row, c8;
+            xunit(j, row, c8);
+            const float* src = xw + (row < L ? row : L - 1) * p.x_ts + c8;
+            xa[slot(j)] = *reinterpret_cast<const float4*>(src);
+            xb[slot(j)] = *reinterpret_cast<const float4*>(src + 4);
+        }
     };
     const int tiles[3] = {2 * wave, 2 * wave + 1, 2 * H + (wave < 5 ? wave : 4)};
     const int wrow[3] = {li, rp(li), wave < 4 ? li : rp(li)};  // W row of lane li in each tile
     uint4 wf[3][D / 32];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-        for (int j = hf * (XU / 2); j < (hf + 1) * (XU / 2); ++j) {
-            int row, c8;
-            xunit(j, row, c8);
-            const float* src = xw + (row < L ? row : L - 1) * p.x_ts + c8;
-            xa[j] = *reinterpret_cast<const float4*>(src);
-            xb[j] = *reinterpret_cast<const float4*>(src + 4);
-        }
+    for (int q = 0; q < XP; ++q) {
+        if (q < XDEPTH) load_x(q);
 #pragma unroll
         for (int t = 0; t < 3; ++t)
 #pragma unroll
-            for (int s = hf * SH; s < (hf + 1) * SH; ++s)
+            for (int s = q * SH; s < (q + 1) * SH; ++s)
                 wf[t][s] = *reinterpret_cast<const uint4*>(
                     PACKED ? p.w_in + ((tiles[t] * (D / 32) + s) * 64 + lane) * 8
                            : p.w_in + (16 * tiles[t] + wrow[t]) * D + 32 * s + 8 * g);
@@ -994,29 +1017,31 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
         *reinterpret_cast<double2*>(cs_d + LMAX * ROPE + cs_at(crow, p0 + 1)) = make_double2(sv.z, sv.w);
     }
 
-    // 2. in_proj: per (tile, row tile) the linear's chain over the 8 k steps, the first half's steps
-    // before the second half is stored. Waves 0..3 run their three tiles over every row tile; waves 4..7
-    // their two q tiles over every row tile and the k_rope tile over the two row tiles whose epilogue they
-    // take (w - 4 and w), into acc[2][0] and acc[2][1].
+    // 2. in_proj: per (tile, row tile) the linear's chain over the 8 k steps, part by part of K. Waves 0..3
+    // run their three tiles over every row tile; waves 4..7 their two q tiles over every row tile and the
+    // k_rope tile over the two row tiles whose epilogue they take (w - 4 and w), into acc[2][0] and
+    // acc[2][1].
     f32x4 acc[3][RT];
 #pragma unroll
     for (int t = 0; t < 3; ++t)
 #pragma unroll
         for (int m = 0; m < RT; ++m) acc[t][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+    for (int hf = 0; hf < XP; ++hf) {
 #pragma unroll
-        for (int j = hf * (XU / 2); j < (hf + 1) * (XU / 2); ++j) {
+        for (int j = hf * (XU / XP); j < (hf + 1) * (XU / XP); ++j) {
             int row, c8;
             xunit(j, row, c8);
             const bool live = row < L;
-            const float v[8] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w};
+            const float4 a = xa[slot(j)], b4 = xb[slot(j)];
+            const float v[8] = {a.x, a.y, a.z, a.w, b4.x, b4.y, b4.z, b4.w};
             bf16x8 o;
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = static_cast<__bf16>(live ? v[e] : 0.0f);
             *reinterpret_cast<bf16x8*>(xq_s + sw(row, c8)) = o;
         }
         __syncthreads();
+        if (hf + XDEPTH < XP) load_x(hf + XDEPTH);
         auto rows = [&](auto nt_c) {  // the first NT tiles over every row tile
             constexpr int NT = decltype(nt_c)::value;
 #pragma unroll

@@ -258,3 +258,27 @@ def test_rms_norm_linear_beyond_the_fused_form(dev):
         assert status == 3
         fused = _C.rms_norm_linear(x, nw, 1e-5, groups, w)
         assert torch.equal(fused, _C.linear(_C.rms_norm(x, nw, 1e-5, groups), w))
+
+
+@pytest.mark.parametrize("M,N,bias,strided", [(9000, 1192, True, False), (70000, 1192, False, True), (31, 768, True, False),
+                                              (4096, 2000, False, False)])
+def test_streaming_form_equals_t32_form(dev, oracle, M, N, bias, strided, monkeypatch):
+    """bf16 weights, K = 256, 12 or more 64-column chunks: the streaming form (weights in registers, x
+    tiles through LDS) gives linear_t32_kernel's result bit for bit (MLK_LINEAR_FORM=t32 selects that
+    form), and both match the product of bf16-rounded inputs."""
+    from montlok import _C
+
+    rng = np.random.default_rng(M + N)
+    K = 256
+    xw = rng.standard_normal((M, K + (16 if strided else 0))).astype(np.float32)
+    x = _t(xw, dev)[:, 8:8 + K] if strided else _t(xw, dev)
+    w = _bf16_round(rng.standard_normal((N, K)) * 0.02)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    args = (x, _t(w, dev).bfloat16(), None if b is None else _t(b, dev))
+    streaming = _C.linear(*args)
+    monkeypatch.setenv("MLK_LINEAR_FORM", "t32")
+    t32 = _C.linear(*args)
+    monkeypatch.delenv("MLK_LINEAR_FORM")
+    assert torch.equal(streaming, t32), "streaming form vs linear_t32_kernel"
+    x_np = xw[:, 8:8 + K] if strided else xw
+    assert_close(streaming, oracle.linear(_bf16_round(x_np), w, b), tol=1e-6, name="bf16-input product")
