@@ -674,10 +674,10 @@ __global__ __launch_bounds__(kThreads) void linear_t32_kernel(LinearArgs p) {
 // (h, l): row l, columns 8j + 4h .. + 3 (j = 0..3), stored as 16-byte pieces.
 //   262144 x 256 -> 1192: 455 us against 508-528 us for linear_t32_kernel.
 //   Measured and not kept: two 32-row chains per wave (515 us), the output
-//   rows staged through LDS so each store writes whole 128-byte pieces (482
-//   us; non-temporal, 639 us), x two tiles ahead (485 us), every B fragment
-//   read from LDS before the chain (no change). Without its stores the kernel
-//   takes 372 us; a plain fill writes the 1.25 GB output in 187 us.
+//   rows staged through LDS so each store writes whole 128-byte pieces (459
+//   us), non-temporal stores (1.5 ms), x two tiles ahead (469 us). Without
+//   its stores the kernel takes 261 us, and a plain fill writes the 1.25 GB
+//   output in 187 us: the stores add their whole time to the rest.
 constexpr int kStreamWaves = 8;
 constexpr int kStreamCols = 32 * kStreamWaves;  // columns per block
 constexpr int kStreamRT = 1;                    // 32-row tiles per step
