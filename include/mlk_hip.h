@@ -272,14 +272,21 @@ mlk_status mlk_mhc_prepare(const float* streams, int64_t tokens, int64_t n, int6
 /* mhc_combine(streams, res, post, out) -- montlok.cpp:726-739, and
  * mhc_combine_collapse -- montlok.cpp:743-758 (kernel montlok_mhc.h:336-438).
  * new_streams: [tokens, n, d] contiguous or NULL; collapsed: [tokens, d] or
- * NULL (mean over the rounded new streams). At least one must be given. */
+ * NULL (mean over the rounded new streams). At least one must be given.
+ * new_streams may be `streams` itself (in place, as montlok_mhc.h:440-497
+ * does) when the streams are contiguous [tokens, n, d] and n <= 8; any other
+ * overlap between them is not supported. */
 mlk_status mlk_mhc_combine(const float* streams, int64_t tokens, int64_t n, int64_t d, int64_t stream_stride,
                            int64_t token_stride, const float* res, const float* post, const float* out,
                            float* new_streams, float* collapsed, mlk_stream_t stream);
 
 /* mhc_combine_prepare(streams, res, post, out, <next hc args>) --
  * montlok.cpp:763-802, kernel montlok_mhc.h:511-522. Writes new_streams
- * [tokens, n, d] and the next residual's agg/pre/post/res. */
+ * [tokens, n, d] and the next residual's agg/pre/post/res. The buffers of the
+ * reference's stage-2 variants (montlok.cpp:807-912) are allowed: new_streams
+ * may be `streams` itself when the streams are contiguous [tokens, n, d] and
+ * n <= 8, post_out and res_out may be `post` and `res`, and agg_out may be
+ * `out`; the values are those of distinct buffers. */
 mlk_status mlk_mhc_combine_prepare(const float* streams, int64_t tokens, int64_t n, int64_t d,
                                    int64_t stream_stride, int64_t token_stride, const float* res, const float* post,
                                    const float* out, const float* norm_w, double eps, const double* proj_w,

@@ -594,12 +594,14 @@ __global__ __launch_bounds__(kWave) void mhc_prepare_generic_kernel(GenericArgs 
 // token's coefficients fetched once for twice the work and twice the loads in
 // flight; 8.3 -> 7.85 us at 8192 tokens, d = 128).
 template <int N, typename I, int CPT = 1>
-__global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __restrict__ streams, int64_t tokens,
+// streams and new_streams may be one buffer (in place): a thread writes exactly
+// the stream elements it has read, and every new value depends on all of them.
+__global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* streams, int64_t tokens,
                                                                  int64_t d, int64_t sd, int64_t ts,
                                                                  const float* __restrict__ res,
                                                                  const float* __restrict__ post,
                                                                  const float* __restrict__ out,
-                                                                 float* __restrict__ new_streams,
+                                                                 float* new_streams,
                                                                  float* __restrict__ collapsed) {
     const I chunks = static_cast<I>(d / 4 / CPT);
     const I idx = static_cast<I>(blockIdx.x) * kBlock + threadIdx.x;
@@ -680,14 +682,16 @@ __global__ __launch_bounds__(kBlock) void mhc_combine_vec_kernel(const float* __
     }
 }
 
-// Any n, d, stride and alignment: one thread per (token, k).
+// Any n, d, stride and alignment: one thread per (token, k). The token's n
+// old stream values at k are read before any new one is stored (n <= 8 in
+// registers), so streams and new_streams may be one buffer.
 template <typename I>
-__global__ __launch_bounds__(kBlock) void mhc_combine_scalar_kernel(const float* __restrict__ streams,
+__global__ __launch_bounds__(kBlock) void mhc_combine_scalar_kernel(const float* streams,
                                                                     int64_t tokens, int n, int64_t d, int64_t sd,
                                                                     int64_t ts, const float* __restrict__ res,
                                                                     const float* __restrict__ post,
                                                                     const float* __restrict__ out,
-                                                                    float* __restrict__ new_streams,
+                                                                    float* new_streams,
                                                                     float* __restrict__ collapsed) {
     const I idx = static_cast<I>(blockIdx.x) * kBlock + threadIdx.x;
     if (static_cast<int64_t>(idx) >= tokens * d) return;
@@ -696,11 +700,23 @@ __global__ __launch_bounds__(kBlock) void mhc_combine_scalar_kernel(const float*
     const int64_t k = idx - token_i * static_cast<I>(d);
     const double o = static_cast<double>(out[token * d + k]);
     const float* s = streams + token * ts + k;
+    constexpr int kMax = 8;
+    double old[kMax];
+    const bool held = n <= kMax;
+#pragma unroll
+    for (int j = 0; j < kMax; ++j) old[j] = held && j < n ? static_cast<double>(s[j * sd]) : 0.0;
     double mean = 0.0;
     for (int i = 0; i < n; ++i) {
         double acc = static_cast<double>(post[token * n + i]) * o;
-        for (int j = 0; j < n; ++j) {
-            acc = fma(static_cast<double>(res[(token * n + i) * n + j]), static_cast<double>(s[j * sd]), acc);
+        if (held) {
+#pragma unroll
+            for (int j = 0; j < kMax; ++j) {
+                if (j < n) acc = fma(static_cast<double>(res[(token * n + i) * n + j]), old[j], acc);
+            }
+        } else {
+            for (int j = 0; j < n; ++j) {
+                acc = fma(static_cast<double>(res[(token * n + i) * n + j]), static_cast<double>(s[j * sd]), acc);
+            }
         }
         const float nv = static_cast<float>(acc);
         if (new_streams != nullptr) new_streams[(token * n + i) * d + k] = nv;
@@ -760,6 +776,13 @@ mlk_status launch_combine(const float* streams, int64_t tokens, int64_t n, int64
     }
     return launch_status("mhc_combine");
 }
+
+// The streams may be overwritten in place (new_streams == streams) when they
+// are contiguous [tokens, n, d] and n <= 8 (the combine kernels then hold a
+// token's old values at each k before storing the new ones; the fused combine
+// + prepare kernel reads everything a token needs before its first barrier
+// and stores after it).
+bool in_place_ok(int64_t n, int64_t d, int64_t sd, int64_t ts) { return n <= 8 && sd == d && ts == n * d; }
 
 bool prepare_fast(const PrepareArgs& a, int64_t n, int64_t d) {
     auto al16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -878,6 +901,8 @@ mlk_status mlk_mhc_combine(const float* streams, int64_t tokens, int64_t n, int6
                            float* new_streams, float* collapsed, mlk_stream_t stream) {
     MLK_CHECK(n > 0 && d > 0, "streams must be non-empty");
     MLK_CHECK(new_streams != nullptr || collapsed != nullptr || tokens == 0, "mhc_combine needs an output");
+    MLK_CHECK(new_streams != streams || in_place_ok(n, d, stream_stride, token_stride),
+              "in-place mhc_combine needs contiguous [tokens, n, d] streams and n <= 8");
     if (tokens == 0) return MLK_OK;
     return launch_combine(streams, tokens, n, d, stream_stride, token_stride, res, post, out, new_streams, collapsed,
                           stream);
@@ -892,6 +917,8 @@ mlk_status mlk_mhc_combine_prepare(const float* streams, int64_t tokens, int64_t
                                    float* new_streams, float* agg_out, float* pre_out, float* post_out,
                                    float* res_out, mlk_stream_t stream) {
     MLK_CHECK(new_streams != nullptr || tokens == 0, "new_streams must be given");
+    MLK_CHECK(new_streams != streams || in_place_ok(n, d, stream_stride, token_stride),
+              "in-place mhc_combine_prepare needs contiguous [tokens, n, d] streams and n <= 8");
     mlk_status st = check_prepare(tokens, n, d, proj_w, sinkhorn_iters);
     if (st != MLK_OK) return st;
     if (tokens == 0) return MLK_OK;

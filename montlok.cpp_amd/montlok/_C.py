@@ -385,16 +385,39 @@ def mhc_combine_collapse(streams, res, post, out):
 def mhc_combine_prepare(streams, res, post, out, norm_w, eps, proj_w, pre_bias, post_bias, res_bias, pre_alpha,
                         post_alpha, res_alpha, sinkhorn_iters, agg_norm_w=None, agg_norm_eps=0.0):
     """montlok.cpp:763-802 -> (new_streams, agg, pre, post, res) of the next residual."""
+    return _mhc_combine_prepare(streams, res, post, out, norm_w, eps, proj_w, pre_bias, post_bias, res_bias,
+                                pre_alpha, post_alpha, res_alpha, sinkhorn_iters, agg_norm_w, agg_norm_eps)
+
+
+def _mhc_combine_prepare(streams, res, post, out, norm_w, eps, proj_w, pre_bias, post_bias, res_bias, pre_alpha,
+                         post_alpha, res_alpha, sinkhorn_iters, agg_norm_w=None, agg_norm_eps=0.0, *,
+                         reuse_streams=False, into=None):
+    """mhc_combine_prepare with the buffers of montlok.cpp:807-852, 853-912 (mhc_combine_prepare_inplace,
+    mhc_combine_prepare_reuse): reuse_streams writes the new streams over `streams` (contiguous
+    [B, L, n, d], n <= 8); `into` = (agg, pre, post, res) buffers the next residual's coefficients are
+    written into (they may be the `res` and `post` this call reads). Values are those of the plain call."""
     B, L, n, d, sd, ts = _combine_inputs(streams, res, post, out)
     (nw, pb, qb, rb), (pa, qa, ra), anw = _prepare_params(n, d, norm_w, proj_w, pre_bias, post_bias, res_bias,
                                                           pre_alpha, post_alpha, res_alpha, sinkhorn_iters,
                                                           agg_norm_w)
     dev = streams.device
-    new = torch.empty((B, L, n, d), dtype=torch.float32, device=dev)
-    agg = torch.empty((B, L, d), dtype=torch.float32, device=dev)
-    pre_o = torch.empty((B, L, n), dtype=torch.float32, device=dev)
-    post_o = torch.empty((B, L, n), dtype=torch.float32, device=dev)
-    res_o = torch.empty((B, L, n, n), dtype=torch.float32, device=dev)
+    if reuse_streams:
+        _check(streams.dim() == 4 and sd == d and ts == n * d and n <= 8,
+               "in-place mHC requires contiguous materialised streams with at most eight lanes")
+        new = streams
+    else:
+        new = torch.empty((B, L, n, d), dtype=torch.float32, device=dev)
+    if into is not None:
+        agg, pre_o, post_o, res_o = into
+        for t, shape, name in ((agg, (B, L, d), "agg"), (pre_o, (B, L, n), "pre"), (post_o, (B, L, n), "post"),
+                               (res_o, (B, L, n, n), "res")):
+            _check(t.dtype == torch.float32 and t.is_contiguous() and tuple(t.shape) == shape,
+                   f"{name} workspace must be contiguous float32 {list(shape)}")
+    else:
+        agg = torch.empty((B, L, d), dtype=torch.float32, device=dev)
+        pre_o = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+        post_o = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+        res_o = torch.empty((B, L, n, n), dtype=torch.float32, device=dev)
     _call("mlk_mhc_combine_prepare", _ptr(streams), B * L, n, d, sd, ts, _ptr(res), _ptr(post), _ptr(out), _ptr(nw),
           float(eps), _ptr(proj_w), _ptr(pb), _ptr(qb), _ptr(rb), _ptr(pa), _ptr(qa), _ptr(ra), int(sinkhorn_iters),
           _ptr(anw), float(agg_norm_eps), _ptr(new), _ptr(agg), _ptr(pre_o), _ptr(post_o), _ptr(res_o), _stream())
@@ -655,9 +678,12 @@ def stage2_tail_forward(backbone, depth, n_streams, attn_hc, attn_hc_eps, attn_s
     Packs (as model.py:160-232 builds them): each mHC pack holds dyn-norm weight, fp64 projection block,
     pre/post/res bias and pre/post/res alpha; the MLA pack holds the full and tail in_proj weights, q weight,
     kv-norm weight and bias (empty = none), kv_up weight, o_proj weight, cos and sin; the FFN pack holds the
-    in weight and bias and the out weight and bias (empty = none). MONTLOK_STAGE2_INPLACE and
-    MONTLOK_STAGE2_REUSE_COEFF change only where the reference keeps its buffers, not the values, so they
-    have no counterpart here."""
+    in weight and bias and the out weight and bias (empty = none).
+
+    Buffers, as montlok.cpp:1291-1295 chooses them (values are the same either way): with
+    MONTLOK_STAGE2_INPLACE unset or not "0" and n_streams <= 8, each residual write after the first goes
+    over the materialised streams in place; with MONTLOK_STAGE2_REUSE_COEFF unset or not "0", the next
+    residual's agg/pre/post/res are written over the current ones."""
     _check(depth > 0, "depth must be positive")
     _check(n_streams > 0, "n_streams must be positive")
     _check(len(attn_hc) == 8 and len(ffn_hc) == 8, "each mHC tensor pack must contain dyn/proj/biases/alphas")
@@ -681,9 +707,21 @@ def stage2_tail_forward(backbone, depth, n_streams, attn_hc, attn_hc_eps, attn_s
         return swiglu_mlp(inputs, ffn[0], ffn[1] if ffn[1].numel() else None, ffn[2],
                           ffn[3] if ffn[3].numel() else None)
 
-    agg, _, post, res = prepare(backbone, attn_hc, attn_hc_eps, attn_sinkhorn_iters, n_streams, attn_norm_weight,
-                                attn_norm_eps)
+    agg, pre, post, res = prepare(backbone, attn_hc, attn_hc_eps, attn_sinkhorn_iters, n_streams,
+                                  attn_norm_weight, attn_norm_eps)
     streams = backbone
+    use_inplace = n_streams <= 8 and os.environ.get("MONTLOK_STAGE2_INPLACE") != "0"
+    reuse_coefficients = os.environ.get("MONTLOK_STAGE2_REUSE_COEFF") != "0"
+
+    def combine_prepare_reuse(streams, agg, pre, post, res, out, hc, eps, iters, norm_weight, norm_eps, in_place):
+        return _mhc_combine_prepare(streams, res, post, out, hc[0], eps, hc[1], hc[2], hc[3], hc[4], hc[5], hc[6],
+                                    hc[7], iters, norm_weight, norm_eps, reuse_streams=in_place,
+                                    into=(agg, pre, post, res))
+
+    def combine_prepare_inplace(streams, res, post, out, hc, eps, iters, norm_weight, norm_eps):
+        return _mhc_combine_prepare(streams, res, post, out, hc[0], eps, hc[1], hc[2], hc[3], hc[4], hc[5], hc[6],
+                                    hc[7], iters, norm_weight, norm_eps, reuse_streams=True)
+
     for step in range(depth):
         if step + 1 == depth:
             attn_out = run_mla(agg, 1)
@@ -695,10 +733,29 @@ def stage2_tail_forward(backbone, depth, n_streams, attn_hc, attn_hc_eps, attn_s
                                               ffn_norm_eps)
             return mhc_combine_collapse(written, f_res, f_post, ffn_mlp(f_agg))
         attn_out = run_mla(agg, agg.size(1))
-        streams, f_agg, _, f_post, f_res = combine_prepare(streams, res, post, attn_out, ffn_hc, ffn_hc_eps,
-                                                           ffn_sinkhorn_iters, ffn_norm_weight, ffn_norm_eps)
-        streams, agg, _, post, res = combine_prepare(streams, f_res, f_post, ffn_mlp(f_agg), attn_hc, attn_hc_eps,
-                                                     attn_sinkhorn_iters, attn_norm_weight, attn_norm_eps)
+        if reuse_coefficients:
+            streams = combine_prepare_reuse(streams, agg, pre, post, res, attn_out, ffn_hc, ffn_hc_eps,
+                                            ffn_sinkhorn_iters, ffn_norm_weight, ffn_norm_eps,
+                                            use_inplace and streams.dim() == 4)[0]
+            ffn_out = ffn_mlp(agg)
+            streams = combine_prepare_reuse(streams, agg, pre, post, res, ffn_out, attn_hc, attn_hc_eps,
+                                            attn_sinkhorn_iters, attn_norm_weight, attn_norm_eps, use_inplace)[0]
+            continue
+        if use_inplace and streams.dim() == 4:
+            streams, f_agg, _, f_post, f_res = combine_prepare_inplace(streams, res, post, attn_out, ffn_hc,
+                                                                       ffn_hc_eps, ffn_sinkhorn_iters,
+                                                                       ffn_norm_weight, ffn_norm_eps)
+        else:
+            streams, f_agg, _, f_post, f_res = combine_prepare(streams, res, post, attn_out, ffn_hc, ffn_hc_eps,
+                                                               ffn_sinkhorn_iters, ffn_norm_weight, ffn_norm_eps)
+        ffn_out = ffn_mlp(f_agg)
+        if use_inplace:
+            streams, agg, pre, post, res = combine_prepare_inplace(streams, f_res, f_post, ffn_out, attn_hc,
+                                                                   attn_hc_eps, attn_sinkhorn_iters,
+                                                                   attn_norm_weight, attn_norm_eps)
+        else:
+            streams, agg, pre, post, res = combine_prepare(streams, f_res, f_post, ffn_out, attn_hc, attn_hc_eps,
+                                                           attn_sinkhorn_iters, attn_norm_weight, attn_norm_eps)
     raise AssertionError("unreachable stage-2 loop")
 
 

@@ -242,3 +242,48 @@ def test_mhc_combine_prepare_plain_store_branch(dev, oracle):
         assert_close(a_sl, flat(np.asarray(e)), name=f"{name} vs oracle")
         mism += bit_mismatches(a_sl, flat(np.asarray(e)))
     assert mism <= max(4, 1024 * n // 1000), mism
+
+
+@pytest.mark.parametrize("n,d,B,L", [(4, 128, 3, 50), (4, 256, 2, 33), (4, 512, 2, 9), (3, 64, 2, 21), (8, 32, 1, 17),
+                                     (5, 18, 2, 7)])
+def test_combine_prepare_in_place_and_reused_buffers(dev, n, d, B, L):
+    """The stage-2 buffer variants (montlok.cpp:807-912): new streams written over the old ones and the next
+    residual's coefficients over the current res/post (and agg over out) give the out-of-place values bit for
+    bit, through the fused kernel (n = 4, d <= 256) and through combine then prepare (the other shapes)."""
+    from montlok import _C
+
+    rng = np.random.default_rng(n * d + L)
+    s, nw, pw, pb, qb, rb = _random_mhc(rng, B, L, n, d)
+    p = (_t(nw, dev), 1e-5, _t(pw, dev), _t(pb, dev), _t(qb, dev), _t(rb, dev),
+         *(torch.tensor(a, device=dev) for a in (0.7, 0.6, 0.8)), 20)
+    streams = _t(s, dev)
+    agg, pre, post, res = _C.mhc_prepare(streams, *p)
+    out = torch.tanh(agg)
+    expect = _C.mhc_combine_prepare(streams, res, post, out, *p)
+    work = [streams.clone(), agg.clone(), pre.clone(), post.clone(), res.clone(), out.clone()]
+    got = _C._mhc_combine_prepare(work[0], work[4], work[3], work[5], *p, reuse_streams=True,
+                                  into=(work[5], work[2], work[3], work[4]))
+    assert got[0].data_ptr() == work[0].data_ptr() and got[1].data_ptr() == work[5].data_ptr()
+    for name, a, b in zip(("streams", "agg", "pre", "post", "res"), got, expect):
+        assert_bitwise(a, b.cpu().numpy(), f"in place {name} n{n} d{d}")
+    # mhc_combine in place as well
+    moved = streams.clone()
+    _C._call("mlk_mhc_combine", moved.data_ptr(), B * L, n, d, d, n * d, res.data_ptr(), post.data_ptr(),
+             out.data_ptr(), moved.data_ptr(), None, _C._stream())
+    assert_bitwise(moved, _C.mhc_combine(streams, res, post, out).cpu().numpy(), f"combine in place n{n} d{d}")
+
+
+def test_in_place_rejects_strided_streams(dev):
+    from montlok import _C
+
+    s = torch.zeros(1, 4, 4, 16, device=dev)
+    wide = torch.zeros(1, 4, 4, 24, device=dev)[..., :16]
+    res, post, out = torch.zeros(1, 4, 4, 4, device=dev), torch.zeros(1, 4, 4, device=dev), torch.zeros(1, 4, 16,
+                                                                                                          device=dev)
+    lib = _C.library()
+    st = lib.mlk_mhc_combine(wide.data_ptr(), 4, 4, 16, 24, 96, res.data_ptr(), post.data_ptr(), out.data_ptr(),
+                             wide.data_ptr(), None, _C._stream())
+    assert st == 1 and "in-place mhc_combine needs contiguous" in lib.mlk_last_error().decode()
+    st = lib.mlk_mhc_combine(s.data_ptr(), 4, 4, 16, 16, 64, res.data_ptr(), post.data_ptr(), out.data_ptr(),
+                             s.data_ptr(), None, _C._stream())
+    assert st == 0

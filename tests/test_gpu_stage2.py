@@ -139,3 +139,29 @@ def test_stage2_tail_bf16_weights(dev, oracle):
     with torch.no_grad():
         got = _run(layer, backbone.to(dev), 2, bf16=True)
     assert_close(got, _oracle_tail(oracle, layer, backbone.numpy(), 2), tol=BF16_TOL, name="stage2 bf16")
+
+
+@pytest.mark.parametrize("n_streams", [4, 3])
+def test_stage2_buffer_variants_same_values(dev, monkeypatch, n_streams):
+    """MONTLOK_STAGE2_INPLACE and MONTLOK_STAGE2_REUSE_COEFF (montlok.cpp:1291-1295) change only where the
+    streams and coefficients live: all four combinations give the same bits, and the in-place,
+    coefficient-reusing default holds less device memory at its peak than neither."""
+    layer = _layer(256, 384, n_streams, seed=21)
+    backbone = torch.randn(4, 64, 256, generator=torch.Generator().manual_seed(4)).to(dev)
+    results, peaks = {}, {}
+    for inplace in ("1", "0"):
+        for reuse in ("1", "0"):
+            monkeypatch.setenv("MONTLOK_STAGE2_INPLACE", inplace)
+            monkeypatch.setenv("MONTLOK_STAGE2_REUSE_COEFF", reuse)
+            with torch.no_grad():
+                _run(layer, backbone, 3, bf16=False)  # warm the caches and packs
+                torch.cuda.synchronize()
+                torch.cuda.reset_peak_memory_stats()
+                base = torch.cuda.memory_allocated()
+                results[(inplace, reuse)] = _run(layer, backbone, 3, bf16=False)
+                torch.cuda.synchronize()
+                peaks[(inplace, reuse)] = torch.cuda.max_memory_allocated() - base
+    ref = results[("0", "0")]
+    for key, got in results.items():
+        assert torch.equal(got, ref), f"INPLACE={key[0]} REUSE_COEFF={key[1]}"
+    assert peaks[("1", "1")] < peaks[("0", "0")], peaks
