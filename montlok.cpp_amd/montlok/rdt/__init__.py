@@ -7,8 +7,9 @@ python/montlok/rdt/__init__.py:27).
 Switches (README.md:265-280 of the reference), read on every call:
 
 - ``MONTLOK_CPP=0``, ``MONTLOK_CPP_MHC=0``, ``MONTLOK_CPP_LAYERS=0``: the
-  reference runs the upstream PyTorch modules instead; this package has no
-  such forward, so the affected modules raise ``RuntimeError``.
+  affected modules run the upstream PyTorch forward (``torch_path``) on the
+  input's device instead of their kernels, as the reference does; with the
+  switches on, a module that cannot take its kernels raises.
 - ``MONTLOK_CPP_FUSED=0``: Mamba-3 pre-processing as tensor operations, then
   the recurrence kernel alone (``mamba3.cpp_backend``).
 - ``MONTLOK_CPP_TAIL=0``: the model evaluates every position and takes the

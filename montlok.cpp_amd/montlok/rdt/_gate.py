@@ -2,9 +2,11 @@
 
 The reference enables its CPU kernels with ``MONTLOK_CPP=1`` and per-family
 switches (``MONTLOK_CPP_LAYERS``, ``MONTLOK_CPP_MHC``; python/montlok/rdt/
-layers.py:32-39, mhc.py:62-69, mla.py:86-104) and falls back to the upstream
-PyTorch modules otherwise. This package ships the GPU kernels only: outside the
-conditions below a module raises instead of computing something else.
+layers.py:32-39, mhc.py:62-69, mla.py:86-104) and runs the upstream PyTorch
+modules where a switch turns them off. The modules here do the same for the
+switches (``backend_enabled`` false: the tensor programs of ``torch_path``).
+With the switches on, a module takes its GPU kernels or raises: the conditions
+below are checked, and there is no silent second path.
 """
 
 from __future__ import annotations

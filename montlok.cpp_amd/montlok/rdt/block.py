@@ -18,7 +18,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ._gate import ext, require_gpu_inference
+from ._gate import backend_enabled, ext, require_gpu_inference
+from .linear import cpu_linear
 from .layers import GroupedRMSNormHIP, RMSNormHIP
 from .mamba3 import Mamba3HIP
 
@@ -38,6 +39,8 @@ class Mamba3BlockHIP(nn.Module):
     def forward(self, x: torch.Tensor, **_: object) -> torch.Tensor:
         if x.ndim != 3 or x.shape[-1] != self.mamba.d_model:
             raise ValueError("Mamba3BlockHIP expects [batch, length, d_model]")
+        if not backend_enabled():
+            return x + self.mamba(self.norm(x))  # each module's upstream PyTorch forward
         require_gpu_inference(type(self).__name__, x)
         return ext().mamba3_block(x, *self._args())
 
@@ -71,7 +74,7 @@ class DecodeStackHIP(nn.Module):
         """Every bar of ``x [B, L, d_model]`` -> ``[B, L, n_outputs]``."""
         for layer in self.layers:
             x = layer(x)
-        return ext().linear(self.final_norm(x), self.head.weight, self.head.bias)
+        return cpu_linear(self.final_norm(x), self.head.weight, self.head.bias)
 
     def step(self, x: torch.Tensor, states: list[dict]) -> torch.Tensor:
         """One bar ``x [S, d_model]`` per stream -> ``[S, n_outputs]``; ``states`` advance in place."""

@@ -5,7 +5,8 @@ the reference subclasses (reference/Model/layers/rmsnorm.py:9-60,
 swiglu.py:10-35, torch.nn.LayerNorm), so state dicts load unchanged; each
 forward is one GPU op from ``montlok._C`` (python/montlok/rdt/layers.py:48-92).
 ``install_cpu_layers(model)`` re-classes matching instances of a built model
-(layers.py:95-115). ``MONTLOK_CPP_LAYERS=0`` switches these layers off.
+(layers.py:95-115). ``MONTLOK_CPP_LAYERS=0`` (or ``MONTLOK_CPP=0``) runs the
+upstream PyTorch forward instead (``torch_path``), as the reference does.
 """
 
 from __future__ import annotations
@@ -13,7 +14,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ._gate import ext, require_gpu_inference
+from . import torch_path
+from ._gate import backend_enabled, ext, require_gpu_inference
 
 _FAMILY = "MONTLOK_CPP_LAYERS"
 
@@ -32,6 +34,8 @@ class RMSNormHIP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.shape[-1] != self.dim:
             raise ValueError(f"expected last dim {self.dim}, got {x.shape[-1]}")
+        if not backend_enabled(_FAMILY):
+            return torch_path.rms_norm(x, self.weight, self.eps)
         require_gpu_inference(type(self).__name__, x, _FAMILY)
         return ext().rms_norm(x, self.weight, self.eps, 1)
 
@@ -56,6 +60,8 @@ class GroupedRMSNormHIP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.shape[-1] != self.dim:
             raise ValueError(f"expected last dim {self.dim}, got {x.shape[-1]}")
+        if not backend_enabled(_FAMILY):
+            return torch_path.rms_norm(x, self.weight, self.eps, self.num_groups)
         require_gpu_inference(type(self).__name__, x, _FAMILY)
         return ext().rms_norm(x, self.weight, self.eps, self.num_groups)
 
@@ -68,6 +74,8 @@ class LayerNormHIP(nn.LayerNorm):
             raise RuntimeError("LayerNormHIP: needs one normalized dimension and an affine weight")
         if x.shape[-1] != self.normalized_shape[0]:
             raise ValueError(f"expected last dim {self.normalized_shape[0]}, got {x.shape[-1]}")
+        if not backend_enabled(_FAMILY):
+            return super().forward(x)
         require_gpu_inference(type(self).__name__, x, _FAMILY)
         return ext().layer_norm(x, self.weight, self.bias, self.eps)
 
@@ -89,6 +97,8 @@ class SwiGLUHIP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.shape[-1] != self.d_model:
             raise ValueError(f"expected last dim {self.d_model}, got {x.shape[-1]}")
+        if not backend_enabled(_FAMILY):
+            return torch_path.swiglu(x, self.w_in, self.w_down)
         require_gpu_inference(type(self).__name__, x, _FAMILY)
         return ext().swiglu_mlp(x, self.w_in.weight, self.w_in.bias, self.w_down.weight, self.w_down.bias)
 

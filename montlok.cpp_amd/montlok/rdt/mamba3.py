@@ -29,7 +29,8 @@ Backends (chosen per call from the environment, as mamba3.py:50-54 does):
     phase by rounding; the reference's own gate for this pair is
     2e-5 (1 + max|y|) (tests/rdt/test_rdt_kernels.py:126-128).
 ``MONTLOK_CPP`` other than ``1``
-    raises: this package has no PyTorch forward of its own.
+    the pure PyTorch quadratic form of the reference's own fallback
+    (mamba3.py:199-256; ``torch_path.mamba3_forward``) on the input's device.
 """
 
 from __future__ import annotations
@@ -41,6 +42,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from . import torch_path
 from ._gate import backend_enabled, ext, require_gpu_inference
 
 
@@ -114,6 +116,8 @@ class Mamba3HIP(nn.Module):
     def forward(self, inputs: torch.Tensor, **_: object) -> torch.Tensor:
         if inputs.ndim != 3 or inputs.shape[-1] != self.d_model:
             raise ValueError("Mamba3HIP expects [batch, length, d_model]")
+        if cpp_backend() is None:
+            return torch_path.mamba3_forward(self, inputs)
         require_gpu_inference(type(self).__name__, inputs)
         c = ext()
         if cpp_backend() == "recurrent":
@@ -162,6 +166,8 @@ class Mamba3HIP(nn.Module):
 
     def forward_projected(self, projected: torch.Tensor) -> torch.Tensor:
         """in_proj output [B, L, W] -> out_proj input [B, L, d_inner] (mamba3.py:175-197)."""
+        if cpp_backend() is None:
+            return torch_path.mamba3_mixer(self, projected)
         require_gpu_inference(type(self).__name__, projected)
         return ext().mamba3_siso_forward(projected, None, *self._mixer_args(), *self._geometry())
 

@@ -17,7 +17,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ._gate import ext, require_gpu_inference
+from . import torch_path
+from ._gate import backend_enabled, ext, require_gpu_inference
 from .layers import RMSNormHIP
 
 _FAMILY = "MONTLOK_CPP_MHC"
@@ -131,6 +132,8 @@ class ManifoldHyperConnectionHIP(nn.Module):
 
     def forward(self, streams: torch.Tensor, fn) -> torch.Tensor:
         self._check_streams(streams)
+        if not backend_enabled(_FAMILY):
+            return torch_path.mhc_forward(self, streams, fn)
         self._require(streams)
         streams, prepared = self._prepare(streams)
         agg = prepared[0]
@@ -146,6 +149,8 @@ class ManifoldHyperConnectionHIP(nn.Module):
         length = streams.shape[1]
         if not 1 <= n_last <= length:
             raise ValueError("n_last must be between 1 and the sequence length")
+        if not backend_enabled(_FAMILY):
+            return torch_path.mhc_forward(self, streams, fn, n_last)
         self._require(streams)
         streams, prepared = self._prepare(streams)
         agg, _pre, post, res = prepared

@@ -21,7 +21,8 @@ import math
 import torch
 from torch import nn
 
-from ._gate import ext, require_gpu_inference
+from . import torch_path
+from ._gate import backend_enabled, ext, require_gpu_inference
 
 _FAMILY = "MONTLOK_CPP_LAYERS"
 
@@ -126,8 +127,16 @@ class MLAHIP(nn.Module):
 
     def forward(self, x: torch.Tensor, word_pos=None, morph_depth=None, attn_mask=None, causal: bool = True,
                 cache=None, pos_offset: int = 0) -> torch.Tensor:
+        if not backend_enabled(_FAMILY) and cache is None and attn_mask is None and word_pos is None and \
+                morph_depth is None:
+            return self._torch_forward(x, x.shape[1], causal, pos_offset)
         self._check(x, word_pos, morph_depth, attn_mask, cache)
         return self._attend(x, x.shape[1], causal, pos_offset)
+
+    def _torch_forward(self, x: torch.Tensor, n_last: int, causal: bool, pos_offset: int) -> torch.Tensor:
+        """``MONTLOK_CPP_LAYERS=0`` / ``MONTLOK_CPP=0``: the upstream PyTorch forward (``torch_path``)."""
+        cos, sin = self._rope_tables(x.shape[1], pos_offset, x.device)
+        return torch_path.mla_forward(self, x, cos, sin, n_last, causal)
 
     def forward_last(self, x: torch.Tensor, n_last: int = 1, pos_offset: int = 0) -> torch.Tensor:
         """Causal attention output ``[B, n_last, d_model]`` of the trailing positions."""
@@ -135,6 +144,8 @@ class MLAHIP(nn.Module):
             raise ValueError("x must have shape [B, L, d_model]")
         if not 1 <= n_last <= x.shape[1]:
             raise ValueError("n_last must be between 1 and the sequence length")
+        if not backend_enabled(_FAMILY):
+            return self._torch_forward(x, n_last, True, pos_offset)
         self._check(x)
         return self._attend(x, n_last, True, pos_offset)
 

@@ -42,7 +42,8 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from ._gate import ext, require_gpu_inference
+from ._gate import backend_enabled, ext, require_gpu_inference
+from .linear import cpu_linear
 from .layers import GroupedRMSNormHIP, LayerNormHIP, RMSNormHIP, SwiGLUHIP
 from .mamba3 import Mamba3HIP, cpp_backend
 from .mhc import ManifoldHyperConnectionHIP
@@ -354,8 +355,9 @@ class RDT4QuantHIP(nn.Module):
 
     def _embed(self, inputs: torch.Tensor) -> torch.Tensor:
         x = inputs.float()
-        require_gpu_inference(type(self).__name__, x, _FAMILY)
-        return self.input_norm(ext().linear(x, self.projection.weight, self.projection.bias))
+        if backend_enabled():
+            require_gpu_inference(type(self).__name__, x, _FAMILY)
+        return self.input_norm(cpu_linear(x, self.projection.weight, self.projection.bias))
 
     def encode(self, inputs: torch.Tensor, depth: int):
         """Hidden states of every position after ``depth`` stage-2 passes, and the core's info dict."""
@@ -383,7 +385,7 @@ class RDT4QuantHIP(nn.Module):
 
     def _head(self, hidden: torch.Tensor, head: nn.Linear, rows: int) -> torch.Tensor:
         last = self.final_norm(hidden[:, -1].contiguous())
-        return self._quantiles(ext().linear(last, head.weight, head.bias).reshape(-1, rows, 3))
+        return self._quantiles(cpu_linear(last, head.weight, head.bias).reshape(-1, rows, 3))
 
     def _hidden_for_head(self, embedded: torch.Tensor, depth: int) -> torch.Tensor:
         """model.py:366-370: the tail path, or (``MONTLOK_CPP_TAIL=0``) the full recurrence's hidden states."""
@@ -416,10 +418,11 @@ class MultiAssetRDTHIP(RDT4QuantHIP):
         if domain not in self.stock_heads or asset_id is None:
             raise ValueError("typed stock domain and asset identifiers are required")
         x = inputs.float()
-        require_gpu_inference(type(self).__name__, x, _FAMILY)
+        if backend_enabled():
+            require_gpu_inference(type(self).__name__, x, _FAMILY)
         identity = self.asset_embedding(asset_id)
         period = self.period_embedding.weight[0 if domain == "equity_daily" else 1]
-        projected = ext().linear(x, self.stock_projection.weight, self.stock_projection.bias)
+        projected = cpu_linear(x, self.stock_projection.weight, self.stock_projection.bias)
         embedded = self.stock_norm(projected + identity[:, None] + period)
         hidden = self._hidden_for_head(embedded, depth)
         return self._head(hidden, self.stock_heads[domain], 3), hidden.detach().float().square().mean().sqrt()

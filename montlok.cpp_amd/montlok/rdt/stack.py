@@ -21,8 +21,9 @@ from types import SimpleNamespace
 
 import torch
 from torch import nn
+from torch.nn import functional as F
 
-from ._gate import ext, require_gpu_inference
+from ._gate import backend_enabled, ext, require_gpu_inference
 from .layers import RMSNormHIP
 from .mamba3 import Mamba3HIP
 from .mhc import ManifoldHyperConnectionHIP
@@ -58,6 +59,13 @@ class HybridStackHIP(nn.Module):
     def forward(self, features: torch.Tensor) -> torch.Tensor:
         if features.ndim != 3:
             raise ValueError("features must be [B, L, d_features]")
+        if not backend_enabled():
+            # The kernels switched off: the module chain, each module's upstream PyTorch forward.
+            streams = self.hcs[0].expand(F.linear(features, self.feature_proj.weight.to(features.dtype),
+                                                  self.feature_proj.bias.to(features.dtype)))
+            for hc, norm, mixer in zip(self.hcs, self.norms, self.mixers):
+                streams = hc(streams, lambda agg, norm=norm, mixer=mixer: mixer(norm(agg)))
+            return self.hcs[-1].collapse(streams)
         require_gpu_inference(type(self).__name__, features)
         c = ext()
         h = c.linear(features, self.feature_proj.weight, self.feature_proj.bias)

@@ -8,8 +8,9 @@ reference's own tests give that pair.
   2e-5 (1 + max|y|) (tests/rdt/test_rdt_kernels.py:126-128).
 - MONTLOK_CPP_TAIL=0, MONTLOK_CPP_NATIVE_STAGE1=0, MONTLOK_CPP_NATIVE_STAGE2=0:
   the model's quantiles against the default path at 1e-5 normwise.
-- MONTLOK_CPP_MHC=0, MONTLOK_CPP_LAYERS=0, MONTLOK_CPP=0: the reference runs
-  upstream PyTorch there; this package has no such forward and raises.
+- MONTLOK_CPP_MHC=0, MONTLOK_CPP_LAYERS=0, MONTLOK_CPP=0: the upstream
+  PyTorch forward of that family on the device (no kernel called), against the
+  kernel path at 2e-5 (1 + max|y|).
 """
 
 from __future__ import annotations
@@ -92,13 +93,70 @@ def test_model_switches_keep_the_result(dev, clean_env, switch):
     assert_close(other, base, tol=tol, name=f"{switch}=0 vs default")
 
 
-@pytest.mark.parametrize("switch", ["MONTLOK_CPP_MHC", "MONTLOK_CPP_LAYERS"])
-def test_family_switches_raise(dev, clean_env, switch):
-    from montlok.rdt import ManifoldHyperConnectionHIP, RMSNormHIP
+def _no_kernels(monkeypatch, *modules):
+    """Make every kernel call of the given drop-in modules fail, so a result proves the PyTorch path ran."""
 
-    module = ManifoldHyperConnectionHIP(16, n_streams=2).to(dev) if switch == "MONTLOK_CPP_MHC" else \
-        RMSNormHIP(16).to(dev)
-    x = torch.randn(1, 3, 2, 16, device=dev) if switch == "MONTLOK_CPP_MHC" else torch.randn(3, 16, device=dev)
+    def refuse():
+        raise AssertionError("a kernel was called with its family switched off")
+
+    for mod in modules:
+        monkeypatch.setattr(mod, "ext", refuse)
+
+
+@pytest.mark.parametrize("switch", ["MONTLOK_CPP_MHC", "MONTLOK_CPP_LAYERS", "MONTLOK_CPP"])
+def test_family_switches_run_upstream_pytorch(dev, clean_env, switch):
+    """Each family switch runs that family's upstream PyTorch forward on the device (no kernel is called),
+    within the reference's PyTorch-vs-kernel tolerance 2e-5 (1 + max|y|) of the kernel path."""
+    import montlok.rdt.layers as layers_mod
+    import montlok.rdt.mamba3 as mamba_mod
+    import montlok.rdt.mhc as mhc_mod
+    import montlok.rdt.mla as mla_mod
+    from types import SimpleNamespace
+
+    from montlok.rdt import MLAHIP, ManifoldHyperConnectionHIP, Mamba3HIP, RMSNormHIP
+
+    torch.manual_seed(9)
+    hc = ManifoldHyperConnectionHIP(64, n_streams=4).to(dev)
+    with torch.no_grad():
+        for a in (hc.pre_alpha, hc.post_alpha, hc.res_alpha):
+            a.fill_(0.7)
+        hc.res_bias.normal_()
+    norm = RMSNormHIP(64).to(dev)
+    cfg = SimpleNamespace(d_model=64, n_heads=2, head_dim=32, nope_head_dim=16, rope_head_dim=16, kv_lora_rank=32,
+                          q_lora_rank=0, rope_theta=10000.0)
+    mla = MLAHIP(cfg).to(dev).eval()
+    mamba = Mamba3HIP(64, d_state=16, headdim=32).to(dev).eval()
+    streams = torch.randn(2, 20, 4, 64, device=dev)
+
+    def run():
+        with torch.no_grad():
+            return (hc(streams, lambda agg: mla(norm(agg))), mamba(norm(streams[:, :, 0])))
+
+    kernels = run()
     clean_env.setenv(switch, "0")
-    with torch.no_grad(), pytest.raises(RuntimeError, match="switched off"):
-        module(x, lambda a: a) if switch == "MONTLOK_CPP_MHC" else module(x)
+    families = {"MONTLOK_CPP_MHC": (mhc_mod,), "MONTLOK_CPP_LAYERS": (layers_mod, mla_mod),
+                "MONTLOK_CPP": (mhc_mod, layers_mod, mla_mod, mamba_mod)}[switch]
+    _no_kernels(clean_env, *families)
+    upstream = run()
+    for name, a, b in zip(("mHC over RMSNorm -> MLA", "RMSNorm -> Mamba-3"), upstream, kernels):
+        _assert_ref_tol(a, b, 2e-5, f"{switch}=0: {name}")
+
+
+def test_model_with_kernels_off(dev, clean_env):
+    """MONTLOK_CPP=0: the model runs the upstream module chain on the device; its quantiles agree with the
+    kernel path within the reference's tolerance for a PyTorch-vs-kernel pair."""
+    import montlok.rdt.layers as layers_mod
+    import montlok.rdt.mamba3 as mamba_mod
+    import montlok.rdt.mhc as mhc_mod
+    import montlok.rdt.mla as mla_mod
+    import montlok.rdt.model as model_mod
+
+    m = _model(seed=4).to(dev)
+    x = torch.randn(2, 24, 7, generator=torch.Generator().manual_seed(4)).to(dev)
+    with torch.no_grad():
+        base, _ = m(x, 2)
+    clean_env.setenv("MONTLOK_CPP", "0")
+    _no_kernels(clean_env, layers_mod, mamba_mod, mhc_mod, mla_mod, model_mod)
+    with torch.no_grad():
+        other, _ = m(x, 2)
+    _assert_ref_tol(other, base, 2e-5, "MONTLOK_CPP=0 model")

@@ -84,10 +84,12 @@ def test_layers_install_and_contract():
 
 
 def test_modules_refuse_other_paths(monkeypatch):
-    """No CPU or autograd fallback: the modules raise instead of computing something else."""
+    """With the kernels switched on there is no CPU or autograd fallback: the modules raise instead of
+    computing something else. Only an explicit switch selects the upstream PyTorch forward."""
     from montlok.rdt import Mamba3HIP, RMSNormCPU, cpu_linear
+    from montlok.rdt import torch_path
 
-    x = torch.zeros(2, 3, 64)
+    x = torch.randn(2, 3, 64)
     with torch.no_grad(), pytest.raises(RuntimeError, match="must be on the ROCm device"):
         Mamba3HIP(64, d_state=16, headdim=32)(x)
     with torch.no_grad(), pytest.raises(RuntimeError, match="must be on the ROCm device"):
@@ -95,8 +97,11 @@ def test_modules_refuse_other_paths(monkeypatch):
     with pytest.raises(RuntimeError, match="cpu_linear"):
         cpu_linear(x, torch.zeros(4, 64))
     monkeypatch.setenv("MONTLOK_CPP_LAYERS", "0")
-    with torch.no_grad(), pytest.raises(RuntimeError, match="switched off"):
-        RMSNormCPU(64)(x)
+    norm = RMSNormCPU(64)
+    with torch.no_grad():
+        assert torch.equal(norm(x), torch_path.rms_norm(x, norm.weight, norm.eps))
+        with pytest.raises(RuntimeError, match="must be on the ROCm device"):
+            Mamba3HIP(64, d_state=16, headdim=32)(x)  # the Mamba-3 kernels are still on
 
 
 def test_stage2_tail_argument_checks():
