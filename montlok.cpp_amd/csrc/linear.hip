@@ -677,7 +677,8 @@ __global__ __launch_bounds__(kThreads) void linear_t32_kernel(LinearArgs p) {
 //   rows staged through LDS so each store writes whole 128-byte pieces (459
 //   us), non-temporal stores (1.5 ms), x two tiles ahead (469 us). Without
 //   its stores the kernel takes 261 us, and a plain fill writes the 1.25 GB
-//   output in 187 us: the stores add their whole time to the rest.
+//   output in 187 us: the stores add their whole time to the rest, which is
+//   what linear_stream_sw_kernel below (the default) works on: 445 us.
 constexpr int kStreamWaves = 8;
 constexpr int kStreamCols = 32 * kStreamWaves;  // columns per block
 constexpr int kStreamRT = 1;                    // 32-row tiles per step
@@ -816,6 +817,163 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
     }
 }
 
+// The streaming form with its output stores on separate waves: waves 0..7
+// compute as in linear_stream_kernel but leave each 32 x 256 result tile in
+// one of two LDS buffers; waves 8..11 store the tile of the previous step from
+// there (whole 1 KB row pieces per instruction), so the global stores run
+// while the next tile's products are formed. Same products and order as
+// linear_stream_kernel (and linear_t32_kernel), same bits. 12 waves put three
+// on a SIMD: the computing waves load x's fragments half of K at a time and
+// the storing waves unroll by two, which keeps both within 168 registers
+// without spills. 262144 x 256 -> 1192: 445 us against 457 us for
+// linear_stream_kernel (MLK_LINEAR_STORE_WAVES=0 selects that one).
+constexpr int kStoreWaves = 4;
+
+__global__ __launch_bounds__(64 * (kStreamWaves + kStoreWaves))
+void linear_stream_sw_kernel(LinearArgs p, int col_groups, int row_parts) {
+    using T = u16;
+    constexpr int kSteps = kStreamK / 16;
+    constexpr int kPitch = kStreamK + 8;      // x tile row pitch in bf16 (+16 bytes)
+    constexpr int kOPitch = kStreamCols + 4;  // output tile row pitch in floats (+16 bytes)
+    constexpr int kThr = 64 * kStreamWaves;   // the computing waves' threads
+    constexpr int kTPR = kThr / kStreamRows;  // threads per x row
+    constexpr int kXPer = kStreamK / kTPR;    // x floats per thread per tile
+    static_assert(kStreamRT == 1 && kXPer % 8 == 0, "one 32-row tile per step, whole 16-byte bf16 units");
+    __shared__ __attribute__((aligned(16))) T x_lds[2][kStreamRows * kPitch];
+    __shared__ __attribute__((aligned(16))) float o_lds[2][kStreamRows * kOPitch];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool storer = wave >= kStreamWaves;
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    const int xcd = blockIdx.x % 8;
+    const int local = blockIdx.x / 8;
+    const int cg = local % col_groups;
+    const int rpl = local / col_groups;
+    const int rp = rpl * 8 + xcd;
+    if (rp >= row_parts) return;
+    const int64_t tiles = (p.rows + kStreamRows - 1) / kStreamRows;
+    const int64_t t_begin = tiles * rp / row_parts, t_end = tiles * (rp + 1) / row_parts;
+    if (t_begin >= t_end) return;
+    const int64_t n_block = static_cast<int64_t>(cg) * kStreamCols;
+    const int64_t n_wave = n_block + 32 * (storer ? 0 : wave);  // a computing wave's first column
+    const bool wave_live = !storer && n_wave < p.N;
+    const bool vec_out = (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 &&
+                         (p.residual == nullptr ||
+                          ((reinterpret_cast<uintptr_t>(p.residual) & 15) == 0 && p.res_stride % 4 == 0));
+
+    uint4 wf[kSteps];
+    if (!storer) {  // the storing waves hold no weights
+        const T* w = static_cast<const T*>(p.w);
+        const int64_t n = n_wave + r32;
+        const T* wrow = w + (n < p.N ? n : p.N - 1) * kStreamK + 8 * h;
+        const uint32_t keep = n < p.N ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const uint4 v = *reinterpret_cast<const uint4*>(wrow + 16 * s);
+            wf[s] = uint4{v.x & keep, v.y & keep, v.z & keep, v.w & keep};
+        }
+    }
+    const int xr = threadIdx.x / kTPR, xc = kXPer * (threadIdx.x % kTPR);
+    float4 xv[kXPer / 4];
+    auto load_tile = [&](int64_t t) {
+        const int64_t row = t * kStreamRows + xr;
+        const float* src = p.x + (row < p.rows ? row : p.rows - 1) * p.x_stride + xc;
+#pragma unroll
+        for (int q = 0; q < kXPer / 4; ++q) xv[q] = *reinterpret_cast<const float4*>(src + 4 * q);
+    };
+    auto store_tile = [&](int64_t t, T* buf) {
+        const bool live = t * kStreamRows + xr < p.rows;
+#pragma unroll
+        for (int u = 0; u < kXPer / 8; ++u) {
+            const float4 a = xv[2 * u], b = xv[2 * u + 1];
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            bf16x8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = static_cast<__bf16>(live ? v[j] : 0.0f);
+            *reinterpret_cast<bf16x8*>(buf + xr * kPitch + xc + 8 * u) = o;
+        }
+    };
+    // The storing waves: tile t of buffer `buf`, lane u = 64 (wave - 8) + lane takes float4 u + 256 i of the
+    // tile (row (u + 256 i) / 64, columns 4 ((u + 256 i) % 64) ..), so each instruction writes one row's
+    // 1 KB of this column group.
+    auto write_out = [&](int64_t t, const float* buf) __attribute__((always_inline)) {
+        const int u = 64 * (wave - kStreamWaves) + lane;
+#pragma unroll 2
+        for (int i = 0; i < kStreamRows * kStreamCols / 4 / (64 * kStoreWaves); ++i) {
+            const int e = u + 64 * kStoreWaves * i;
+            const int rr = e / (kStreamCols / 4), c4 = 4 * (e % (kStreamCols / 4));
+            const int64_t row = t * kStreamRows + rr;
+            const int64_t col = n_block + c4;
+            if (row >= p.rows || col >= p.N) continue;
+            f32x4 y = *reinterpret_cast<const f32x4*>(buf + rr * kOPitch + c4);
+            float* orow = p.out + row * p.out_stride;
+            const float* rrow = p.residual != nullptr ? p.residual + row * p.res_stride : nullptr;
+            if (p.bias != nullptr) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) y[q] += p.bias[col + q < p.N ? col + q : p.N - 1];
+            }
+            if (col + 4 <= p.N && vec_out) {
+                if (rrow != nullptr) y = *reinterpret_cast<const f32x4*>(rrow + col) + y;
+                *reinterpret_cast<f32x4*>(orow + col) = y;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (col + q < p.N) orow[col + q] = rrow != nullptr ? rrow[col + q] + y[q] : y[q];
+                }
+            }
+        }
+    };
+
+    // Both kinds of wave pass the same barriers: one before the first step and one after each step.
+    if (storer) {
+        __syncthreads();
+        for (int64_t t = t_begin; t < t_end; ++t) {
+            if (t > t_begin) write_out(t - 1, o_lds[(t - 1 - t_begin) & 1]);
+            __syncthreads();
+        }
+        write_out(t_end - 1, o_lds[(t_end - 1 - t_begin) & 1]);
+        return;
+    }
+    load_tile(t_begin);
+    store_tile(t_begin, x_lds[0]);
+    __syncthreads();
+    auto iteration = [&](int64_t t, auto par_c) {
+        constexpr int PAR = decltype(par_c)::value;  // (t - t_begin) % 2: the buffers of tile t
+        const bool more = t + 1 < t_end;
+        if (more) load_tile(t + 1);
+        if (wave_live) {
+            const T* buf = x_lds[PAR];
+            f32x16 acc;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+            // x fragments in two halves of K: within the registers of three waves per SIMD.
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint4 xb[kSteps / 2];
+#pragma unroll
+                for (int s = 0; s < kSteps / 2; ++s)
+                    xb[s] = *reinterpret_cast<const uint4*>(buf + r32 * kPitch + 16 * (s + half * kSteps / 2) + 8 * h);
+#pragma unroll
+                for (int s = 0; s < kSteps / 2; ++s)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[s + half * kSteps / 2]),
+                                                                  __builtin_bit_cast(bf16x8, xb[s]), acc, 0, 0, 0);
+            }
+            float* ob = o_lds[PAR] + r32 * kOPitch + 32 * wave + 4 * h;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<f32x4*>(ob + 8 * j) = f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
+        }
+        if (more) store_tile(t + 1, x_lds[PAR ^ 1]);
+        __syncthreads();
+    };
+    for (int64_t t = t_begin; t < t_end; t += 2) {
+        iteration(t, std::integral_constant<int, 0>{});
+        if (t + 1 < t_end) iteration(t + 1, std::integral_constant<int, 1>{});
+    }
+}
+
 // Shapes too small to give the 128-row blocks one per CU (256 CUs), with K
 // held in at most eight 32-wide steps.
 bool small_shape(int64_t rows, int64_t K, int64_t N) {
@@ -828,6 +986,11 @@ bool small_shape(int64_t rows, int64_t K, int64_t N) {
 bool stream_form() {
     const char* v = std::getenv("MLK_LINEAR_FORM");
     return !(v != nullptr && std::strcmp(v, "t32") == 0);
+}
+
+bool store_waves() {
+    const char* v = std::getenv("MLK_LINEAR_STORE_WAVES");
+    return !(v != nullptr && std::strcmp(v, "0") == 0);
 }
 
 template <bool BF16W, bool VEC>
@@ -859,8 +1022,14 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
             const int parts_per_xcd = 32 / col_groups;
             if (parts_per_xcd >= 1) {
                 const int row_parts = 8 * parts_per_xcd;
-                hipLaunchKernelGGL(linear_stream_kernel, dim3(static_cast<unsigned>(8 * parts_per_xcd * col_groups)),
-                                   dim3(64 * kStreamWaves), 0, stream, p, col_groups, row_parts);
+                const dim3 grid(static_cast<unsigned>(8 * parts_per_xcd * col_groups));
+                if (store_waves()) {
+                    hipLaunchKernelGGL(linear_stream_sw_kernel, grid, dim3(64 * (kStreamWaves + kStoreWaves)), 0,
+                                       stream, p, col_groups, row_parts);
+                } else {
+                    hipLaunchKernelGGL(linear_stream_kernel, grid, dim3(64 * kStreamWaves), 0, stream, p,
+                                       col_groups, row_parts);
+                }
                 return;
             }
         }

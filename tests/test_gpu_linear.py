@@ -264,8 +264,9 @@ def test_rms_norm_linear_beyond_the_fused_form(dev):
                                               (4096, 2000, False, False)])
 def test_streaming_form_equals_t32_form(dev, oracle, M, N, bias, strided, monkeypatch):
     """bf16 weights, K = 256, 12 or more 64-column chunks: the streaming form (weights in registers, x
-    tiles through LDS) gives linear_t32_kernel's result bit for bit (MLK_LINEAR_FORM=t32 selects that
-    form), and both match the product of bf16-rounded inputs."""
+    tiles through LDS; by default with separate storing waves, MLK_LINEAR_STORE_WAVES=0 without) gives
+    linear_t32_kernel's result bit for bit (MLK_LINEAR_FORM=t32 selects that form), also with the residual
+    epilogue, and all match the product of bf16-rounded inputs."""
     from montlok import _C
 
     rng = np.random.default_rng(M + N)
@@ -275,10 +276,21 @@ def test_streaming_form_equals_t32_form(dev, oracle, M, N, bias, strided, monkey
     w = _bf16_round(rng.standard_normal((N, K)) * 0.02)
     b = rng.standard_normal(N).astype(np.float32) if bias else None
     args = (x, _t(w, dev).bfloat16(), None if b is None else _t(b, dev))
-    streaming = _C.linear(*args)
+    res = torch.randn(M, N, generator=torch.Generator().manual_seed(M)).to(dev)
+
+    def both():
+        return _C.linear(*args), _C.linear_residual(*args, res)
+
+    streaming = both()
+    monkeypatch.setenv("MLK_LINEAR_STORE_WAVES", "0")
+    in_wave = both()
     monkeypatch.setenv("MLK_LINEAR_FORM", "t32")
-    t32 = _C.linear(*args)
+    t32 = both()
     monkeypatch.delenv("MLK_LINEAR_FORM")
-    assert torch.equal(streaming, t32), "streaming form vs linear_t32_kernel"
+    monkeypatch.delenv("MLK_LINEAR_STORE_WAVES")
+    for name, a, c in (("streaming", streaming, t32), ("streaming, stores on the computing waves", in_wave, t32)):
+        assert torch.equal(a[0], c[0]), f"{name} vs linear_t32_kernel"
+        assert torch.equal(a[1], c[1]), f"{name} with residual vs linear_t32_kernel"
+    assert torch.equal(streaming[1], res + streaming[0]), "residual epilogue vs the two steps"
     x_np = xw[:, 8:8 + K] if strided else xw
-    assert_close(streaming, oracle.linear(_bf16_round(x_np), w, b), tol=1e-6, name="bf16-input product")
+    assert_close(streaming[0], oracle.linear(_bf16_round(x_np), w, b), tol=1e-6, name="bf16-input product")
