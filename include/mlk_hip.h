@@ -210,16 +210,18 @@ mlk_status mlk_mla_attend_normed(const float* projected, int64_t batch, int64_t 
  * kv_norm_eps, kv_up_weight, out_weight, cos, sin, n_heads, head_dim,
  * nope_dim, kv_lora_rank, n_last = L, causal = true, scale) --
  * montlok.cpp:1159-1211, every causal query: in_proj, kv_norm, kv_up, RoPE,
- * top-left causal attention and the output projection in one launch, one
- * block per window, so neither the projection nor the attention output goes
- * through HBM. x: rows of d_model floats, x_token_stride apart within a
+ * top-left causal attention and the output projection in one launch (one
+ * block per window; for 4 heads of 64 one block per window and 64 query
+ * rows, walking the key rows up to them), so neither the projection nor the
+ * attention output goes through HBM. x: rows of d_model floats, x_token_stride apart within a
  * window and x_batch_stride apart between windows; in_proj_weight [d_model +
  * kv_rank + rope, d_model], kv_up_weight [heads (nope + head_dim), kv_rank]
  * and out_weight [d_model, d_model], all bf16 (weight_dtype MLK_DTYPE_BF16);
  * cos/sin [L, rope]; out [B, L, d_model] contiguous. The result equals the
  * separate path (linear, mlk_layer_norm_bf16, mlk_mla_attend_normed, linear)
  * bit for bit. Built for 8 heads of 32 (nope 16, rope 16), kv_rank 64,
- * L <= 128, a positive scale, 16-byte aligned operands; MLK_ERR_UNSUPPORTED
+ * L <= 128, and for 4 heads of 64 (nope 32, rope 32), kv_rank 64, L <= 256,
+ * with a positive scale and 16-byte aligned operands; MLK_ERR_UNSUPPORTED
  * otherwise. */
 mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_t d_model, int64_t x_batch_stride,
                            int64_t x_token_stride, const void* in_proj_weight, const float* kv_norm_w,

@@ -1426,6 +1426,554 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
 }
 
 
+// ------------------------------------- whole MLA forward per span of 64 queries
+
+// mla_forward (montlok.cpp:1159-1211) for every causal query at d_model 256,
+// 4 heads of 64 (rope 32, nope 32), kv rank 64 and L <= 256: one block of 8
+// waves per (window, span of 64 query rows), so that neither the in_proj
+// output nor the attention output goes through HBM. A window's rows do not
+// fit one block's LDS as keys and queries at once (mla_window_kernel's form),
+// so each block walks the key rows in 64-row tiles up to its own span:
+//   q        x of the span (bf16 in LDS); wave w: head w / 2, its nope
+//            (w even) or rope (w odd) column tiles over the 4 row tiles, the
+//            linear's chain over the 8 k steps; q rounded to bf16, its rope
+//            dims rotated in fp64 first (the two rope tiles of a head sit in
+//            one wave, so a lane holds dim i and its rotate_half partner
+//            i + 16).
+//   key tile t = 0 .. span: x rows of the tile (loaded a phase ahead), the
+//            latent and k_rope columns of the in_proj (the same chains),
+//            k_rope rotated into every head's k rows, the latent's LayerNorm
+//            (mla_window_kernel's four lanes per row: layer_norm_vec_kernel's
+//            sums), kv_up (wave w: head w / 2, two row tiles), and the causal
+//            attention of the span's queries against the tile with the
+//            running max, sum and output carried across tiles: per query row
+//            the chunk sequence of mla_attend_kernel (its 64-key chunks are
+//            these tiles, in the same order), the same products and the same
+//            softmax arithmetic, so the result is the four-launch path's bit
+//            for bit. Wave w: head w / 2, query tiles (0, 3) or (1, 2) (the
+//            diagonal tile's work balanced).
+//   o_proj   the normalised output rounded to bf16 (the o_proj's operand)
+//            in LDS, then wave w's two output column tiles over the 4 row
+//            tiles, the linear's chain again.
+// Blocks of one window run on one XCD (its L2 serves the later spans' reads
+// of the window's x).
+__global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int spans) {
+    constexpr int H = 4, HD = 64, NOPE = 32, ROPE = 32, HALF = ROPE / 2, KV = 64, D = H * HD;
+    constexpr int SPAN = 64, RT = SPAN / 16;  // rows per span and per key tile, 16-row tiles
+    constexpr int UPW = NOPE + HD;            // kv_up rows of one head
+    constexpr int LP = KV + 8;                // normalised latent pitch in bf16 elements (+16 bytes)
+    constexpr int LAT_T = D / 16, KR_T = LAT_T + KV / 16;  // in_proj tiles: q 0 .., latent LAT_T .., k_rope KR_T ..
+    // x of one row tile set, later the attention output: [SPAN, D] bf16, 16-byte unit u of row r at
+    // u ^ (r % 8); q of the span in the same layout.
+    __shared__ __attribute__((aligned(16))) u16 x_s[SPAN * D];
+    __shared__ __attribute__((aligned(16))) u16 q_s[SPAN * D];
+    // Per head: k [key][HD], unit u of key r at u ^ ((r / 2) % 8); v^T [HD][key], unit u of dim d at
+    // u ^ ((d / 2) % 8): the 16 rows a fragment read touches land in distinct banks. The fp32 latent
+    // ([SPAN, KV], 16-byte chunk c of row r at c ^ (r % 16)) lives in the v^T slots until kv_up.
+    __shared__ __attribute__((aligned(16))) u16 k_s[H * SPAN * HD];
+    __shared__ __attribute__((aligned(16))) u16 vt_s[H * HD * SPAN];
+    __shared__ __attribute__((aligned(16))) u16 lat_s[SPAN * LP];
+    __shared__ __attribute__((aligned(16))) float lnp_s[2 * KV];  // the LayerNorm's weight, then its bias
+    __shared__ __attribute__((aligned(16))) float csq_s[2 * SPAN * ROPE];  // cos, then sin, of the span's rows
+    static_assert(SPAN * KV * 4 <= H * HD * SPAN * 2, "the fp32 latent fits the v^T slots");
+    float* lat_f = reinterpret_cast<float*>(vt_s);
+    auto lat_at = [](int row, int chunk) { return row * KV + 4 * (chunk ^ (row & 15)); };
+    auto sw = [](int row, int col) { return row * D + ((((col >> 3) ^ (row & 7))) << 3) + (col & 7); };
+    auto k_at = [](int key, int dim) { return key * HD + ((((dim >> 3) ^ ((key >> 1) & 7))) << 3) + (dim & 7); };
+    auto v_at = [](int dim, int key) { return dim * SPAN + ((((key >> 3) ^ ((dim >> 1) & 7))) << 3) + (key & 7); };
+    auto pack2 = [](float a, float b) -> uint32_t {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+    };
+    // rotate_half as rope_kernel: x1 c1 - x2 s1 on dim i, x2 c2 + x1 s2 on dim i + HALF, fp64 products
+    // and sum, rounded to fp32.
+    auto rope4 = [](const f32x4& x1, const f32x4& x2, const float4& c1, const float4& c2, const float4& s1,
+                    const float4& s2, float (&o1)[4], float (&o2)[4]) {
+        const float c1a[4] = {c1.x, c1.y, c1.z, c1.w}, c2a[4] = {c2.x, c2.y, c2.z, c2.w};
+        const float s1a[4] = {s1.x, s1.y, s1.z, s1.w}, s2a[4] = {s2.x, s2.y, s2.z, s2.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const double a = static_cast<double>(x1[v]), bq = static_cast<double>(x2[v]);
+            o1[v] = static_cast<float>(__dsub_rn(__dmul_rn(a, c1a[v]), __dmul_rn(bq, s1a[v])));
+            o2[v] = static_cast<float>(__dadd_rn(__dmul_rn(bq, c2a[v]), __dmul_rn(a, s2a[v])));
+        }
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int L = static_cast<int>(p.length);
+    const int64_t windows = gridDim.x / spans;
+    int64_t b;
+    int j;
+    {
+        const int64_t id = blockIdx.x;
+        // The spans of a window are adjacent in dispatch order, in an order rotated from window to window:
+        // consecutive blocks go to the shader arrays in turn, so each array gets heavy and light spans alike.
+        int64_t wi, r;
+        if (windows % 8 == 0) {  // XCD x = id % 8 takes windows x, x + 8, ...
+            const int64_t k = id / 8;
+            wi = k / spans;
+            r = k % spans;
+            b = id % 8 + 8 * wi;
+        } else {
+            wi = id / spans;
+            r = id % spans;
+            b = wi;
+        }
+        j = spans - 1 - static_cast<int>((r + wi) % spans);
+    }
+    const float* xw = p.x + b * p.x_bs;
+
+    // x rows 64 t .. 64 t + 63 (rows past L read row L - 1, zeroed when stored): thread t takes 8-float
+    // units t + 512 i, row u / 32.
+    float4 xa[4], xb[4];
+    auto load_x = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int u = tid + 512 * i, row = SPAN * t + u / 32;
+            const float* src = xw + static_cast<int64_t>(row < L ? row : L - 1) * p.x_ts + (u % 32) * 8;
+            xa[i] = *reinterpret_cast<const float4*>(src);
+            xb[i] = *reinterpret_cast<const float4*>(src + 4);
+        }
+    };
+    auto store_x = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int u = tid + 512 * i, r = u / 32;
+            const bool live = SPAN * t + r < L;
+            const float v[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+            bf16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = static_cast<__bf16>(live ? v[e] : 0.0f);
+            *reinterpret_cast<bf16x8*>(x_s + sw(r, (u % 32) * 8)) = o;
+        }
+    };
+    auto w_in_frag = [&](int tile, int s) {  // W_in row 16 tile + li, k = 32 s + 8 g .. + 7
+        return *reinterpret_cast<const uint4*>(p.w_in + (16 * tile + li) * D + 32 * s + 8 * g);
+    };
+
+    // 1. q of the span.
+    const int h = wave >> 1, wg = wave & 1;
+    load_x(j);
+    uint4 wq[2][D / 32];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < D / 32; ++s) wq[t][s] = w_in_frag(4 * h + 2 * wg + t, s);
+    {  // the LayerNorm's weight and bias (+0.0 where there is none), as mla_window_kernel takes them
+        const bool ln_part = tid < 2 * KV / 4, ln_bias = tid >= KV / 4;
+        const uint32_t bmask = p.ln_b != nullptr || !ln_bias ? 0xffffffffu : 0u;
+        const float* ln_src = ln_bias && p.ln_b != nullptr ? p.ln_b : p.ln_w;
+        const float4 lnv = *reinterpret_cast<const float4*>(ln_src + 4 * ((ln_part ? tid : 0) % (KV / 4)));
+        if (ln_part)
+            *reinterpret_cast<float4*>(lnp_s + 4 * tid) =
+                make_float4(__uint_as_float(__float_as_uint(lnv.x) & bmask), __uint_as_float(__float_as_uint(lnv.y) & bmask),
+                            __uint_as_float(__float_as_uint(lnv.z) & bmask), __uint_as_float(__float_as_uint(lnv.w) & bmask));
+    }
+    {  // cos/sin rows of the span for the q rotation: thread t takes float4 t and t + 512 of [2, SPAN, ROPE]
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int f = tid + 512 * k, tab = f / (SPAN * ROPE / 4), rem = f % (SPAN * ROPE / 4);
+            const int row = rem / (ROPE / 4), pos = SPAN * j + row, pc = pos < L ? pos : L - 1;
+            const float* src = (tab == 0 ? p.cosine : p.sine) + pc * ROPE + 4 * (rem % (ROPE / 4));
+            *reinterpret_cast<float4*>(csq_s + 4 * f) = *reinterpret_cast<const float4*>(src);
+        }
+    }
+    store_x(j);
+    __syncthreads();
+    load_x(0);  // key tile 0, stored once the q products are done
+    {
+        f32x4 aq[2][RT];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int m = 0; m < RT; ++m) aq[t][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < RT; ++m)
+#pragma unroll
+            for (int s = 0; s < D / 32; ++s) {
+                const bf16x8 xf = *reinterpret_cast<const bf16x8*>(x_s + sw(16 * m + li, 32 * s + 8 * g));
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    aq[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wq[t][s]), xf, aq[t][m],
+                                                                       0, 0, 0);
+            }
+        // Lane (g, li) of row tile m holds row 16 m + li, columns 4g .. 4g + 3 of each tile.
+        if (wg == 0) {
+#pragma unroll
+            for (int m = 0; m < RT; ++m)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    *reinterpret_cast<uint2*>(q_s + sw(16 * m + li, HD * h + 16 * t + 4 * g)) =
+                        make_uint2(pack2(aq[t][m][0], aq[t][m][1]), pack2(aq[t][m][2], aq[t][m][3]));
+        } else {
+#pragma unroll
+            for (int m = 0; m < RT; ++m) {
+                const float* cr = csq_s + (16 * m + li) * ROPE + 4 * g;
+                const float* sr = cr + SPAN * ROPE;
+                float o1[4], o2[4];
+                rope4(aq[0][m], aq[1][m], *reinterpret_cast<const float4*>(cr), *reinterpret_cast<const float4*>(cr + HALF),
+                      *reinterpret_cast<const float4*>(sr), *reinterpret_cast<const float4*>(sr + HALF), o1, o2);
+                *reinterpret_cast<uint2*>(q_s + sw(16 * m + li, HD * h + NOPE + 4 * g)) =
+                    make_uint2(pack2(o1[0], o1[1]), pack2(o1[2], o1[3]));
+                *reinterpret_cast<uint2*>(q_s + sw(16 * m + li, HD * h + NOPE + HALF + 4 * g)) =
+                    make_uint2(pack2(o2[0], o2[1]), pack2(o2[2], o2[3]));
+            }
+        }
+    }
+    __syncthreads();  // q is in LDS; every wave is done with x
+
+    // Attention state of the wave's two query tiles QT(i) = (wg, 3 - wg)[i] of head h.
+    float m_run[2], l_run[2];
+    f32x4 o[2][HD / 16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int t = 0; t < HD / 16; ++t) o[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // The weights of the key-tile loop, the same for every tile, fetched once and held: waves 0..3 the W_in
+    // rows of latent tile w (run over the 4 row tiles); waves 4..7 one of the two k_rope tiles, RT_K =
+    // (w - 4) / 2, over row tiles 2 ((w - 4) % 2) and the next. The k_rope tiles take their W rows in the
+    // order kr_dim(c): column 4g + v of tile T is rope dim 2g + 8T, + 16, 2g + 1 + 8T, + 16 for v = 0..3,
+    // so a lane holds each dim i < 16 with its rotate_half partner i + 16 (each column still comes from its
+    // own W row and x row by the linear's chain).
+    constexpr int CT = UPW / 16, CTW = CT / 2;
+    const int kt_t = (wave - 4) >> 1, kt_r = 2 * ((wave - 4) & 1);  // k_rope waves: tile, first row tile
+    auto kr_dim = [](int c, int tt) { return 2 * (c >> 2) + ((c >> 1) & 1) + 8 * tt + 16 * (c & 1); };
+    uint4 wl[D / 32];
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s)
+        wl[s] = wave < 4 ? w_in_frag(LAT_T + wave, s)
+                         : *reinterpret_cast<const uint4*>(p.w_in + (D + KV + kr_dim(li, kt_t)) * D + 32 * s + 8 * g);
+
+    for (int t = 0; t <= j; ++t) {
+        // The lane's row and group indices made opaque to the compiler per key tile, so the many LDS
+        // addresses derived from them are formed where used instead of being held across the loop.
+        int lane_t = lane;
+        asm volatile("" : "+v"(lane_t));
+        const int li = lane_t & 15;
+        const int g = lane_t >> 4;
+        // 2. x of key tile t into LDS (the k_rope waves' cos/sin in flight meanwhile: dims 2g + 8T, + 1 and
+        // their partners + 16, of the two rows the lane rotates).
+        float2 kcs[2][4];
+        if (wave >= 4) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int pos = SPAN * t + 16 * (kt_r + u) + li, pc = pos < L ? pos : L - 1;
+                const float* cr = p.cosine + pc * ROPE + 2 * g + 8 * kt_t;
+                const float* sr = p.sine + pc * ROPE + 2 * g + 8 * kt_t;
+                kcs[u][0] = *reinterpret_cast<const float2*>(cr);
+                kcs[u][1] = *reinterpret_cast<const float2*>(cr + HALF);
+                kcs[u][2] = *reinterpret_cast<const float2*>(sr);
+                kcs[u][3] = *reinterpret_cast<const float2*>(sr + HALF);
+            }
+        }
+        store_x(t);
+        __syncthreads();  // x of tile t is in LDS; the previous tile's attention is done
+        if (t < j) load_x(t + 1);  // the next tile's x, in flight until the next step 2
+        // 3. Latent and k_rope columns of the tile's rows, each (tile, row tile) the linear's chain.
+        if (wave < 4) {
+            f32x4 al[RT];
+#pragma unroll
+            for (int m = 0; m < RT; ++m) al[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+                for (int m = 0; m < RT; ++m) {
+                    const bf16x8 xf = *reinterpret_cast<const bf16x8*>(x_s + sw(16 * m + li, 32 * s + 8 * g));
+                    al[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wl[s]), xf, al[m], 0, 0, 0);
+                }
+#pragma unroll
+            for (int m = 0; m < RT; ++m) *reinterpret_cast<f32x4*>(lat_f + lat_at(16 * m + li, 4 * wave + g)) = al[m];
+        } else {  // k_rope, rotated, into every head's k rows (dims NOPE ..)
+            f32x4 a[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const bf16x8 xf = *reinterpret_cast<const bf16x8*>(x_s + sw(16 * (kt_r + u) + li, 32 * s + 8 * g));
+                    a[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wl[s]), xf, a[u], 0, 0, 0);
+                }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int row = 16 * (kt_r + u) + li;
+                // a[u][0], a[u][2]: dims i = 2g + 8T and i + 1; a[u][1], a[u][3]: their partners i + 16, i + 17.
+                const float2 c1 = kcs[u][0], c2 = kcs[u][1], s1 = kcs[u][2], s2 = kcs[u][3];
+                const f32x4 x1 = {a[u][0], a[u][2], 0.f, 0.f}, x2 = {a[u][1], a[u][3], 0.f, 0.f};
+                float o1[4], o2[4];
+                rope4(x1, x2, make_float4(c1.x, c1.y, 0.f, 0.f), make_float4(c2.x, c2.y, 0.f, 0.f),
+                      make_float4(s1.x, s1.y, 0.f, 0.f), make_float4(s2.x, s2.y, 0.f, 0.f), o1, o2);
+                const uint32_t e1 = pack2(o1[0], o1[1]), e2 = pack2(o2[0], o2[1]);
+#pragma unroll
+                for (int hh = 0; hh < H; ++hh) {
+                    *reinterpret_cast<uint32_t*>(k_s + hh * SPAN * HD + k_at(row, NOPE + 2 * g + 8 * kt_t)) = e1;
+                    *reinterpret_cast<uint32_t*>(k_s + hh * SPAN * HD + k_at(row, NOPE + HALF + 2 * g + 8 * kt_t)) = e2;
+                }
+            }
+        }
+        // The kv_up B fragments of head h, column tiles 3 wg .. 3 wg + 2 (lane (g, li): W_up row
+        // h UPW + 16 ct + li, k = 32 ks + 8g ..), in flight during the LayerNorm.
+        uint4 wu[CTW][KV / 32];
+#pragma unroll
+        for (int c = 0; c < CTW; ++c)
+#pragma unroll
+            for (int ks = 0; ks < KV / 32; ++ks)
+                wu[c][ks] = *reinterpret_cast<const uint4*>(p.w_up + (h * UPW + 16 * (CTW * wg + c) + li) * KV + 32 * ks + 8 * g);
+        __syncthreads();  // the fp32 latent and the rotated k_rope are in LDS; x is free
+
+        // 4. kv_norm: waves 0..3, four lanes per row (lane q holds the row's four-column groups q, q + 4,
+        // q + 8, q + 12; the butterfly's xor-8 and xor-4 levels inside the lane, xor 2 and xor 1 across the
+        // quad): every sum formed as the 16-lane form of layer_norm_vec_kernel forms it.
+        if (wave < 4) {
+            const int lq = lane & 3, lrow = 16 * wave + (lane >> 2);
+            const double inv_dim = 1.0 / static_cast<double>(KV);
+            float4 xv[4], lnw[4], lnb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xv[i] = *reinterpret_cast<const float4*>(lat_f + lat_at(lrow, lq + 4 * i));
+                lnw[i] = *reinterpret_cast<const float4*>(lnp_s + 4 * (lq + 4 * i));
+                lnb[i] = *reinterpret_cast<const float4*>(lnp_s + KV + 4 * (lq + 4 * i));
+            }
+            auto row_sum = [](const double (&sg)[4]) {
+                double u = (sg[0] + sg[2]) + (sg[1] + sg[3]);
+                u += xor_row_d<2>(u);
+                u += xor_row_d<1>(u);
+                return u;
+            };
+            double sg[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                sg[i] = (static_cast<double>(xv[i].x) + static_cast<double>(xv[i].y)) +
+                        (static_cast<double>(xv[i].z) + static_cast<double>(xv[i].w));
+            const double mean = row_sum(sg) * inv_dim;
+            double ac[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ac[i][0] = static_cast<double>(xv[i].x) - mean;
+                ac[i][1] = static_cast<double>(xv[i].y) - mean;
+                ac[i][2] = static_cast<double>(xv[i].z) - mean;
+                ac[i][3] = static_cast<double>(xv[i].w) - mean;
+                sg[i] = (ac[i][0] * ac[i][0] + ac[i][1] * ac[i][1]) + (ac[i][2] * ac[i][2] + ac[i][3] * ac[i][3]);
+            }
+            const double rstd = 1.0 / sqrt(fma(row_sum(sg), inv_dim, p.ln_eps));
+            const uint32_t live = SPAN * t + lrow < L ? 0xffffffffu : 0u;  // keys past L: zero, as the LNIN form reads them
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float o0 = static_cast<float>((ac[i][0] * rstd) * lnw[i].x + static_cast<double>(lnb[i].x));
+                const float o1 = static_cast<float>((ac[i][1] * rstd) * lnw[i].y + static_cast<double>(lnb[i].y));
+                const float o2 = static_cast<float>((ac[i][2] * rstd) * lnw[i].z + static_cast<double>(lnb[i].z));
+                const float o3 = static_cast<float>((ac[i][3] * rstd) * lnw[i].w + static_cast<double>(lnb[i].w));
+                *reinterpret_cast<uint2*>(lat_s + lrow * LP + 4 * (lq + 4 * i)) =
+                    make_uint2(pack2(o0, o1) & live, pack2(o2, o3) & live);
+            }
+        }
+        __syncthreads();  // the normalised latent is in LDS; the fp32 latent is dead
+
+        // 5. kv_up of head h, column tiles 3 wg .. 3 wg + 2 over the 4 row tiles: k_nope formed transposed
+        // (W_up rows as the A operand: four consecutive dims of one key per lane), v as keys x dims (four
+        // consecutive keys of one dim): one 8-byte store per lane either way, the same products in the same
+        // order.
+        auto kv_up = [&](auto wg_c) {
+            constexpr int WG = decltype(wg_c)::value;
+            u16* kh = k_s + h * SPAN * HD;
+            u16* vh = vt_s + h * HD * SPAN;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                bf16x8 la[KV / 32];
+#pragma unroll
+                for (int ks = 0; ks < KV / 32; ++ks)
+                    la[ks] = *reinterpret_cast<const bf16x8*>(lat_s + (16 * rt + li) * LP + 32 * ks + 8 * g);
+#pragma unroll
+                for (int c = 0; c < CTW; ++c) {
+                    constexpr int CT0 = CTW * WG;
+                    const int ct = CT0 + c;
+                    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < KV / 32; ++ks)
+                        a = ct < NOPE / 16
+                                ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wu[c][ks]), la[ks], a, 0, 0, 0)
+                                : __builtin_amdgcn_mfma_f32_16x16x32_bf16(la[ks], __builtin_bit_cast(bf16x8, wu[c][ks]), a, 0, 0, 0);
+                    const uint2 e = make_uint2(pack2(a[0], a[1]), pack2(a[2], a[3]));
+                    if (ct < NOPE / 16) {
+                        *reinterpret_cast<uint2*>(kh + k_at(16 * rt + li, 16 * ct + 4 * g)) = e;
+                    } else {
+                        *reinterpret_cast<uint2*>(vh + v_at(16 * (ct - NOPE / 16) + li, 16 * rt + 4 * g)) = e;
+                    }
+                }
+            }
+        };
+        if (wg == 0) {
+            kv_up(std::integral_constant<int, 0>{});
+        } else {
+            kv_up(std::integral_constant<int, 1>{});
+        }
+        __syncthreads();  // k and v^T of the tile are in LDS
+
+        // 6. The span's queries against key tile t (mla_attend_kernel's chunk t): all four 16-key tiles
+        // below the diagonal tile (t < j); for t == j only the tiles at or below each query tile's
+        // diagonal, the mask on the diagonal tile alone (a tile above it is all -inf in mla_attend_kernel:
+        // it adds nothing to the max, +0 to the sum and zero weights to P). Keys past L lie past every
+        // stored query's diagonal. The first tile starts from m = -inf, l = 0, o = 0.
+        auto attend = [&](auto wg_c, auto first_c, auto diag_c) {
+            constexpr int WG = decltype(wg_c)::value;
+            constexpr bool FIRST = decltype(first_c)::value, DIAG = decltype(diag_c)::value;
+            constexpr int QT[2] = {WG, 3 - WG};
+            const u16* kh = k_s + h * SPAN * HD;
+            const u16* vh = vt_s + h * HD * SPAN;
+            auto unit = [&](auto i_c) {
+                constexpr int I = decltype(i_c)::value;
+                constexpr int NKT = DIAG ? QT[I] + 1 : 4;
+                bf16x8 qb[HD / 32];
+#pragma unroll
+                for (int c = 0; c < HD / 32; ++c)
+                    qb[c] = *reinterpret_cast<const bf16x8*>(q_s + sw(16 * QT[I] + li, HD * h + 32 * c + 8 * g));
+                f32x4 sc[NKT];
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) {
+                    sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < HD / 32; ++c) {
+                        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kh + k_at(16 * kt + li, 32 * c + 8 * g));
+                        sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[c], sc[kt], 0, 0, 0);
+                    }
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        float xv = sc[kt][v];
+                        if (DIAG && kt == QT[I]) xv = 4 * g + v <= li ? xv : -INFINITY;
+                        sc[kt][v] = xv;
+                        mx = fmaxf(mx, xv);
+                    }
+                }
+                mx = fmaxf(mx, lane_xor16(mx));
+                mx = fmaxf(mx, lane_xor32(mx));
+                mx *= p.scale_log2;  // the max of the scaled scores (the scale is positive)
+                const float m_new = FIRST ? mx : fmaxf(m_run[I], mx);
+                const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+                float corr = 0.0f;
+                if constexpr (!FIRST) corr = __builtin_amdgcn_exp2f(m_run[I] - m_use);
+                m_run[I] = m_new;
+                float psum = 0.0f;
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float e = __builtin_amdgcn_exp2f(fmaf(sc[kt][v], p.scale_log2, -m_use));
+                        sc[kt][v] = e;
+                        psum += e;
+                    }
+                }
+                if constexpr (FIRST) {
+                    l_run[I] = psum;
+                } else {
+                    l_run[I] = l_run[I] * corr + psum;
+#pragma unroll
+                    for (int ot = 0; ot < HD / 16; ++ot)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) o[I][ot][v] *= corr;
+                }
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    if (2 * half >= NKT) continue;  // P is zero over both key tiles (known at compile time)
+                    const int ta = 2 * half, tb = 2 * half + 1 < NKT ? 2 * half + 1 : ta;
+                    const uint2 pa = make_uint2(pack2(sc[ta][0], sc[ta][1]), pack2(sc[ta][2], sc[ta][3]));
+                    const uint2 pz = 2 * half + 1 < NKT ? make_uint2(pack2(sc[tb][0], sc[tb][1]), pack2(sc[tb][2], sc[tb][3]))
+                                                        : make_uint2(0u, 0u);
+                    const bf16x8 pb = __builtin_bit_cast(bf16x8, uint4{pa.x, pa.y, pz.x, pz.y});
+#pragma unroll
+                    for (int ot = 0; ot < HD / 16; ++ot) {
+                        const int dim = 16 * ot + li, key0 = 32 * half + 4 * g;
+                        const uint2 lo = *reinterpret_cast<const uint2*>(vh + v_at(dim, key0));
+                        const uint2 hi = *reinterpret_cast<const uint2*>(vh + v_at(dim, key0 + 16));
+                        const uint4 raw = {lo.x, lo.y, hi.x, hi.y};
+                        o[I][ot] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, raw), pb, o[I][ot],
+                                                                            0, 0, 0);
+                    }
+                }
+            };
+            unit(std::integral_constant<int, 0>{});
+            __builtin_amdgcn_sched_barrier(0);  // one unit's operands in registers at a time
+            unit(std::integral_constant<int, 1>{});
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        auto attend_wg = [&](auto first_c, auto diag_c) {
+            if (wg == 0) {
+                attend(std::integral_constant<int, 0>{}, first_c, diag_c);
+            } else {
+                attend(std::integral_constant<int, 1>{}, first_c, diag_c);
+            }
+        };
+        if (t == 0) {
+            if (t == j) attend_wg(T_{}, T_{}); else attend_wg(T_{}, F_{});
+        } else {
+            if (t == j) attend_wg(F_{}, T_{}); else attend_wg(F_{}, F_{});
+        }
+    }
+
+    // 7. Normalised output, rounded to bf16 as the o_proj takes it, into x's place (rows past L are not
+    // stored by the o_proj and are left as they are); the o_proj fragments in flight meanwhile.
+    uint4 wo[2][D / 32];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s = 0; s < D / 32; ++s)
+            wo[c][s] = *reinterpret_cast<const uint4*>(p.w_out + (16 * (2 * wave + c) + li) * D + 32 * s + 8 * g);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 16 * (i == 0 ? wg : 3 - wg) + li;
+        float l = l_run[i] + lane_xor16(l_run[i]);
+        l = l + lane_xor32(l);
+        if (SPAN * j + r >= L) continue;
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int ot = 0; ot < HD / 16; ++ot)
+            *reinterpret_cast<uint2*>(x_s + sw(r, HD * h + 16 * ot + 4 * g)) =
+                make_uint2(pack2(o[i][ot][0] * inv, o[i][ot][1] * inv), pack2(o[i][ot][2] * inv, o[i][ot][3] * inv));
+    }
+    __syncthreads();
+
+    // 8. o_proj: wave w computes output columns 32 w .. 32 w + 31 of the span's rows, two row tiles at a
+    // time (four chains, each the linear's chain over the 8 k steps).
+    float* orow0 = p.out + (b * L + SPAN * j) * static_cast<int64_t>(D);
+#pragma unroll
+    for (int m = 0; m < RT; m += 2) {
+        bf16x8 af[2][D / 32];
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+            for (int s = 0; s < D / 32; ++s)
+                af[mm][s] = *reinterpret_cast<const bf16x8*>(x_s + sw(16 * (m + mm) + li, 32 * s + 8 * g));
+        f32x4 y[2][2];
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) y[mm][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+                    y[mm][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wo[c][s]), af[mm][s],
+                                                                       y[mm][c], 0, 0, 0);
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+            const int row = 16 * (m + mm) + li;
+            if (SPAN * j + row < L) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+                    *reinterpret_cast<f32x4*>(orow0 + row * D + 32 * wave + 16 * c + 4 * g) = y[mm][c] + f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+}
+
 // The weights of mla_window_kernel<H, true> into the MlaPack layout, one 16-byte
 // unit per thread (a copy: every unit is one unit of the row-major weight).
 template <int H>
@@ -1615,17 +2163,18 @@ extern "C" mlk_status mlk_mla_attend_normed(const float* projected, int64_t batc
 
 namespace {
 
-// The geometry mla_window_kernel is built for, and its operand checks; MLK_OK when the kernel takes the
+// The geometries the one-launch kernels are built for (mla_window_kernel: 8 heads of 32, L <= 128;
+// mla_span_kernel: 4 heads of 64, L <= 256), and their operand checks; MLK_OK when a kernel takes the
 // call, MLK_ERR_UNSUPPORTED (with the reason) when the separate operators must run it.
 mlk_status mla_window_supported(const float* x, int64_t length, int64_t d_model, int64_t x_batch_stride,
                                 int64_t x_token_stride, const float* kv_norm_w, const float* kv_norm_b,
                                 const float* cosine, const float* sine, int64_t heads, int64_t head_dim,
                                 int64_t nope_dim, int64_t kv_rank, double scale, const float* out,
                                 std::initializer_list<const void*> weights) {
-    const bool built = heads == 8 && head_dim == 32 && nope_dim == 16 && kv_rank == 64 && length <= 128 &&
-                       d_model == heads * head_dim;
-    if (!built) {
-        set_error("mla_forward: geometry without the per-window kernel (use the separate operators)");
+    const bool window = heads == 8 && head_dim == 32 && nope_dim == 16 && kv_rank == 64 && length <= 128;
+    const bool span = heads == 4 && head_dim == 64 && nope_dim == 32 && kv_rank == 64 && length <= 256;
+    if (!(window || span) || d_model != heads * head_dim) {
+        set_error("mla_forward: geometry without a one-launch kernel (use the separate operators)");
         return MLK_ERR_UNSUPPORTED;
     }
     if (!(static_cast<float>(scale * 1.4426950408889634) > 0.0f)) {
@@ -1646,7 +2195,8 @@ mlk_status mla_window_supported(const float* x, int64_t length, int64_t d_model,
 mlk_status mla_window_launch(const float* x, int64_t batch, int64_t length, int64_t d_model, int64_t x_batch_stride,
                              int64_t x_token_stride, const void* w_in, const float* kv_norm_w, const float* kv_norm_b,
                              double kv_norm_eps, const void* w_up, const void* w_out, const float* cosine,
-                             const float* sine, double scale, float* out, bool packed, mlk_stream_t stream) {
+                             const float* sine, double scale, float* out, int64_t heads, bool packed,
+                             mlk_stream_t stream) {
     MLK_CHECK(x_token_stride >= d_model && (length == 1 || x_batch_stride >= length * x_token_stride),
               "x strides must cover the rows");
     if (batch == 0) return MLK_OK;
@@ -1656,8 +2206,16 @@ mlk_status mla_window_launch(const float* x, int64_t batch, int64_t length, int6
                     static_cast<double>(static_cast<float>(kv_norm_eps)), static_cast<const u16*>(w_up),
                     static_cast<const u16*>(w_out), cosine, sine, out, length,
                     static_cast<float>(scale * 1.4426950408889634)};
-    const dim3 grid(static_cast<unsigned>(batch));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (heads == 4) {  // mla_span_kernel: one block per (window, 64 query rows), row-major weights
+        MLK_CHECK(!packed, "mla_forward: the 4-head kernel takes row-major weights");
+        const int64_t spans = (length + 63) / 64;
+        MLK_CHECK(batch * spans <= 0x7fffffff, "too many windows for one launch");
+        hipLaunchKernelGGL(mla_span_kernel, dim3(static_cast<unsigned>(batch * spans)), dim3(512), 0, s, p,
+                           static_cast<int>(spans));
+        return launch_status("mla_forward");
+    }
+    const dim3 grid(static_cast<unsigned>(batch));
     if (packed) {
         hipLaunchKernelGGL((mla_window_kernel<8, true>), grid, dim3(512), 0, s, p);
     } else {
@@ -1685,7 +2243,8 @@ extern "C" mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t len
                                                {in_proj_weight, kv_up_weight, out_weight});
     if (ok != MLK_OK) return ok;
     return mla_window_launch(x, batch, length, d_model, x_batch_stride, x_token_stride, in_proj_weight, kv_norm_w,
-                             kv_norm_b, kv_norm_eps, kv_up_weight, out_weight, cosine, sine, scale, out, false, stream);
+                             kv_norm_b, kv_norm_eps, kv_up_weight, out_weight, cosine, sine, scale, out, heads, false,
+                             stream);
 }
 
 extern "C" int64_t mlk_mla_packed_elems(int64_t d_model, int64_t heads, int64_t head_dim, int64_t nope_dim,
@@ -1719,6 +2278,10 @@ extern "C" mlk_status mlk_mla_forward_packed(const float* x, int64_t batch, int6
                                              int64_t nope_dim, int64_t kv_rank, double scale, float* out,
                                              mlk_stream_t stream) {
     MLK_CHECK(batch >= 0 && length >= 1 && heads > 0 && d_model == heads * head_dim, "invalid MLA geometry");
+    if (mlk_mla_packed_elems(d_model, heads, head_dim, nope_dim, kv_rank) == 0) {
+        set_error("mla_forward_packed: geometry without packed weights (bf16, 8 heads of 32, rope 16, kv rank 64)");
+        return MLK_ERR_UNSUPPORTED;
+    }
     const mlk_status ok = mla_window_supported(x, length, d_model, x_batch_stride, x_token_stride, kv_norm_w, kv_norm_b,
                                                cosine, sine, heads, head_dim, nope_dim, kv_rank, scale, out,
                                                {packed_weights});
@@ -1726,6 +2289,6 @@ extern "C" mlk_status mlk_mla_forward_packed(const float* x, int64_t batch, int6
     const u16* w = static_cast<const u16*>(packed_weights);
     return mla_window_launch(x, batch, length, d_model, x_batch_stride, x_token_stride, w, kv_norm_w, kv_norm_b,
                              kv_norm_eps, w + 8 * MlaPack<8>::IN_UNITS,
-                             w + 8 * (MlaPack<8>::IN_UNITS + MlaPack<8>::UP_UNITS), cosine, sine, scale, out, true,
-                             stream);
+                             w + 8 * (MlaPack<8>::IN_UNITS + MlaPack<8>::UP_UNITS), cosine, sine, scale, out, heads,
+                             true, stream);
 }

@@ -993,8 +993,10 @@ def mla_pack_weights(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim
 
 def _mla_window(x, in_proj_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight, cosine,
                 sine, n_heads, head_dim, nope_dim, kv_lora_rank, scale):
-    """The whole forward for every causal query, one block per window (bf16 weights, 8 heads of 32, rope 16,
-    kv rank 64, L <= 128, a positive scale); None where that kernel is not built for the call."""
+    """The whole forward for every causal query in one launch (bf16 weights, kv rank 64, a positive scale;
+    8 heads of 32 with rope 16 and L <= 128: one block per window, on packed weights; 4 heads of 64 with rope
+    32 and L <= 256: one block per window and 64 query rows); None where no such kernel is built for the
+    call."""
     batch, length, d_model = x.shape
     ws = [in_proj_weight, kv_up_weight, out_weight]
     if any(w.dtype != torch.bfloat16 or not w.is_contiguous() for w in ws) or x.stride(-1) != 1:

@@ -296,6 +296,39 @@ def test_window_kernel_equals_separate_path(dev, B, L, bias, strided):
     assert_bitwise(one, four.cpu().numpy(), f"per-window MLA {B}x{L} vs four launches")
 
 
+@pytest.mark.parametrize("B,L,bias,strided", [(8, 256, True, False),   # full-stack MLA geometry
+                                              (3, 77, True, False), (2, 1, False, False), (5, 64, False, True),
+                                              (1, 255, True, True), (16, 200, True, False), (9, 130, False, False),
+                                              (4, 65, True, False)])
+def test_span_kernel_equals_separate_path(dev, B, L, bias, strided):
+    """With bf16 weights, 4 heads of 64 (rope 32) and L <= 256 the whole mla_forward is one launch, one
+    block per (window, 64 query rows) walking the key rows up to them: the result equals the four-launch
+    path bit for bit, for ragged lengths (one to four spans, partial last spans), windows not a multiple
+    of 8, no kv_norm bias and token-strided x."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(B * 1000 + L + 5)
+    H, hd, nope, kvr = 4, 64, 32, 64
+    d, rope = H * hd, hd - nope
+    bf = torch.bfloat16
+    wide = torch.randn(B, L, d + 64 if strided else d, generator=g).to(dev)
+    x = wide[..., 32:32 + d] if strided else wide
+    in_w = (torch.randn(d + kvr + rope, d, generator=g) * 0.05).to(dev, bf)
+    up_w = (torch.randn(H * (nope + hd), kvr, generator=g) * 0.1).to(dev, bf)
+    o_w = (torch.randn(d, d, generator=g) * 0.05).to(dev, bf)
+    ln_w = (1 + 0.1 * torch.randn(kvr, generator=g)).to(dev)
+    ln_b = (0.1 * torch.randn(kvr, generator=g)).to(dev) if bias else None
+    cos, sin = (t.to(dev) for t in rope_tables_t(L, rope))
+    args = (x, in_w, x.new_empty(0), ln_w, ln_b, 1e-5, up_w, o_w, cos, sin, H, hd, nope, kvr, L, True, hd ** -0.5)
+    print(f"span kernel case B={B} L={L} bias={bias} strided={strided}", flush=True)
+    one = _C._mla_forward(*args, allow_fused=True)
+    assert _C.mla_forward_launches() == ["mla_forward"], "the geometry has the per-span kernel"
+    four = _C._mla_forward(*args, allow_fused=True, allow_window=False)
+    assert _C.mla_forward_launches() == ["linear", "layer_norm_bf16", "mla_attend_normed", "linear"]
+    assert one.shape == (B, L, d)
+    assert_bitwise(one, four.cpu().numpy(), f"per-span MLA {B}x{L} vs four launches")
+
+
 def test_packed_weights_equal_row_major(dev):
     """_C.mla_forward runs the per-window kernel on its weights re-laid in the kernel's fragment order
     (mlk_mla_pack_weights, cached per weight triple): the result equals mlk_mla_forward on the row-major
