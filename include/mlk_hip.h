@@ -236,7 +236,8 @@ mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t length, int64_
  * fragment load of the kernel reads 16 rows' 64-byte pieces; every block reads
  * all three weights, and those loads bounded the kernel's start and its last
  * head round. mlk_mla_packed_elems: bf16 elements of the packed copy for the
- * geometry, 0 where the per-window kernel is not built for it.
+ * geometry (each of the two one-launch geometries has its own layout), 0 where
+ * no one-launch kernel is built for it.
  * mlk_mla_pack_weights writes it (16-byte aligned buffers; MLK_ERR_UNSUPPORTED
  * for other geometries or dtypes). mlk_mla_forward_packed is mlk_mla_forward
  * with the packed copy in place of the three weights: same conditions, the

@@ -879,6 +879,8 @@ struct MlaPack {
     static constexpr int OUT_UNITS = (D / 16) * (D / 32) * 64;
     static constexpr int UNITS = IN_UNITS + UP_UNITS + OUT_UNITS;
     __device__ static bool rope_tile(int tile) { return (tile < 2 * H && (tile & 1) != 0) || tile == 2 * H + KV / 16; }
+    // The W_in row that lane row r of in_proj tile `tile` holds.
+    __device__ static int in_row(int tile, int r) { return 16 * tile + (rope_tile(tile) ? mla_rope_order(r) : r); }
 };
 
 struct MlaWindowArgs {
@@ -1428,6 +1430,28 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
 
 // ------------------------------------- whole MLA forward per span of 64 queries
 
+// The k_rope tiles of mla_span_kernel take their W rows in this order: column c
+// of tile tt (0, 1) is rope dim 2 (c / 4) + (c / 2) % 2 + 8 tt, plus 16 for odd
+// c, so the lane holding dim i < 16 also holds its rotate_half partner i + 16.
+__device__ __forceinline__ int mla_span_kr_dim(int c, int tt) { return 2 * (c >> 2) + ((c >> 1) & 1) + 8 * tt + 16 * (c & 1); }
+
+// The packed weights of mla_span_kernel<true>, in 16-byte units (8 bf16), the
+// order its waves load them: in_proj unit (tile * D / 32 + s) * 64 + lane holds
+// W_in row in_row(tile, lane % 16), k = 32 s + 8 (lane / 16) .. + 7 (tiles: q
+// 0..15, latent 16..19, k_rope 20, 21); then the kv_up rows, unit ((head * CT +
+// ct) * KV / 32 + ks) * 64 + lane = row head * UPW + 16 ct + lane % 16; then the
+// out_proj rows like the in_proj's.
+struct MlaSpanPack {
+    static constexpr int H = 4, HD = 64, NOPE = 32, ROPE = 32, KV = 64, D = H * HD, UPW = NOPE + HD, CT = UPW / 16;
+    static constexpr int KR_T = (D + KV) / 16;
+    static constexpr int IN_TILES = (D + KV + ROPE) / 16;
+    static constexpr int IN_UNITS = IN_TILES * (D / 32) * 64;
+    static constexpr int UP_UNITS = H * CT * (KV / 32) * 64;
+    static constexpr int OUT_UNITS = (D / 16) * (D / 32) * 64;
+    static constexpr int UNITS = IN_UNITS + UP_UNITS + OUT_UNITS;
+    __device__ static int in_row(int tile, int r) { return tile >= KR_T ? D + KV + mla_span_kr_dim(r, tile - KR_T) : 16 * tile + r; }
+};
+
 // mla_forward (montlok.cpp:1159-1211) for every causal query at d_model 256,
 // 4 heads of 64 (rope 32, nope 32), kv rank 64 and L <= 256: one block of 8
 // waves per (window, span of 64 query rows), so that neither the in_proj
@@ -1456,8 +1480,11 @@ __global__ __launch_bounds__(512) void mla_window_kernel(MlaWindowArgs p) {
 //            in LDS, then wave w's two output column tiles over the 4 row
 //            tiles, the linear's chain again.
 // Blocks of one window run on one XCD (its L2 serves the later spans' reads
-// of the window's x).
+// of the window's x). PACKED: the three weights in MlaSpanPack's order, each
+// wave's fragment load one contiguous 1 KB.
+template <bool PACKED>
 __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int spans) {
+    using PK = MlaSpanPack;
     constexpr int H = 4, HD = 64, NOPE = 32, ROPE = 32, HALF = ROPE / 2, KV = 64, D = H * HD;
     constexpr int SPAN = 64, RT = SPAN / 16;  // rows per span and per key tile, 16-row tiles
     constexpr int UPW = NOPE + HD;            // kv_up rows of one head
@@ -1550,8 +1577,9 @@ __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int span
             *reinterpret_cast<bf16x8*>(x_s + sw(r, (u % 32) * 8)) = o;
         }
     };
-    auto w_in_frag = [&](int tile, int s) {  // W_in row 16 tile + li, k = 32 s + 8 g .. + 7
-        return *reinterpret_cast<const uint4*>(p.w_in + (16 * tile + li) * D + 32 * s + 8 * g);
+    auto w_in_frag = [&](int tile, int s) {  // W_in row PK::in_row(tile, li), k = 32 s + 8 g .. + 7
+        return *reinterpret_cast<const uint4*>(PACKED ? p.w_in + ((tile * (D / 32) + s) * 64 + lane) * 8
+                                                      : p.w_in + PK::in_row(tile, li) * D + 32 * s + 8 * g);
     };
 
     // 1. q of the span.
@@ -1584,6 +1612,19 @@ __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int span
     store_x(j);
     __syncthreads();
     load_x(0);  // key tile 0, stored once the q products are done
+    // The weights of the key-tile loop, the same for every tile, fetched once and held: waves 0..3 the W_in
+    // rows of latent tile w (run over the 4 row tiles); waves 4..7 one of the two k_rope tiles, RT_K =
+    // (w - 4) / 2, over row tiles 2 ((w - 4) % 2) and the next. The k_rope tiles take their W rows in the
+    // order mla_span_kr_dim(c): column 4g + v of tile T is rope dim 2g + 8T, + 16, 2g + 1 + 8T, + 16 for v = 0..3,
+    // so a lane holds each dim i < 16 with its rotate_half partner i + 16 (each column still comes from its
+    // own W row and x row by the linear's chain).
+    constexpr int CT = UPW / 16, CTW = CT / 2;
+    const int kt_t = (wave - 4) >> 1, kt_r = 2 * ((wave - 4) & 1);  // k_rope waves: tile, first row tile
+    static_assert(PK::KR_T == KR_T && PK::D == D && PK::KV == KV && PK::UPW == UPW, "the packed layout's geometry");
+    uint4 wl[D / 32];
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) wl[s] = w_in_frag(wave < 4 ? LAT_T + wave : KR_T + kt_t, s);
+
     {
         f32x4 aq[2][RT];
 #pragma unroll
@@ -1633,21 +1674,6 @@ __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int span
 #pragma unroll
         for (int t = 0; t < HD / 16; ++t) o[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // The weights of the key-tile loop, the same for every tile, fetched once and held: waves 0..3 the W_in
-    // rows of latent tile w (run over the 4 row tiles); waves 4..7 one of the two k_rope tiles, RT_K =
-    // (w - 4) / 2, over row tiles 2 ((w - 4) % 2) and the next. The k_rope tiles take their W rows in the
-    // order kr_dim(c): column 4g + v of tile T is rope dim 2g + 8T, + 16, 2g + 1 + 8T, + 16 for v = 0..3,
-    // so a lane holds each dim i < 16 with its rotate_half partner i + 16 (each column still comes from its
-    // own W row and x row by the linear's chain).
-    constexpr int CT = UPW / 16, CTW = CT / 2;
-    const int kt_t = (wave - 4) >> 1, kt_r = 2 * ((wave - 4) & 1);  // k_rope waves: tile, first row tile
-    auto kr_dim = [](int c, int tt) { return 2 * (c >> 2) + ((c >> 1) & 1) + 8 * tt + 16 * (c & 1); };
-    uint4 wl[D / 32];
-#pragma unroll
-    for (int s = 0; s < D / 32; ++s)
-        wl[s] = wave < 4 ? w_in_frag(LAT_T + wave, s)
-                         : *reinterpret_cast<const uint4*>(p.w_in + (D + KV + kr_dim(li, kt_t)) * D + 32 * s + 8 * g);
-
     for (int t = 0; t <= j; ++t) {
         // The lane's row and group indices made opaque to the compiler per key tile, so the many LDS
         // addresses derived from them are formed where used instead of being held across the loop.
@@ -1670,6 +1696,16 @@ __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int span
                 kcs[u][3] = *reinterpret_cast<const float2*>(sr + HALF);
             }
         }
+        // The kv_up B fragments of head h, column tiles 3 wg .. 3 wg + 2 (lane (g, li): W_up row
+        // h UPW + 16 ct + li, k = 32 ks + 8g ..), in flight until step 5.
+        uint4 wu[CTW][KV / 32];
+#pragma unroll
+        for (int c = 0; c < CTW; ++c)
+#pragma unroll
+            for (int ks = 0; ks < KV / 32; ++ks)
+                wu[c][ks] = *reinterpret_cast<const uint4*>(
+                    PACKED ? p.w_up + (((h * CT + CTW * wg + c) * (KV / 32) + ks) * 64 + lane) * 8
+                           : p.w_up + (h * UPW + 16 * (CTW * wg + c) + li) * KV + 32 * ks + 8 * g);
         store_x(t);
         __syncthreads();  // x of tile t is in LDS; the previous tile's attention is done
         if (t < j) load_x(t + 1);  // the next tile's x, in flight until the next step 2
@@ -1713,14 +1749,6 @@ __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int span
                 }
             }
         }
-        // The kv_up B fragments of head h, column tiles 3 wg .. 3 wg + 2 (lane (g, li): W_up row
-        // h UPW + 16 ct + li, k = 32 ks + 8g ..), in flight during the LayerNorm.
-        uint4 wu[CTW][KV / 32];
-#pragma unroll
-        for (int c = 0; c < CTW; ++c)
-#pragma unroll
-            for (int ks = 0; ks < KV / 32; ++ks)
-                wu[c][ks] = *reinterpret_cast<const uint4*>(p.w_up + (h * UPW + 16 * (CTW * wg + c) + li) * KV + 32 * ks + 8 * g);
         __syncthreads();  // the fp32 latent and the rotated k_rope are in LDS; x is free
 
         // 4. kv_norm: waves 0..3, four lanes per row (lane q holds the row's four-column groups q, q + 4,
@@ -1923,7 +1951,8 @@ __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int span
     for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int s = 0; s < D / 32; ++s)
-            wo[c][s] = *reinterpret_cast<const uint4*>(p.w_out + (16 * (2 * wave + c) + li) * D + 32 * s + 8 * g);
+            wo[c][s] = *reinterpret_cast<const uint4*>(PACKED ? p.w_out + (((2 * wave + c) * (D / 32) + s) * 64 + lane) * 8
+                                                              : p.w_out + (16 * (2 * wave + c) + li) * D + 32 * s + 8 * g);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int r = 16 * (i == 0 ? wg : 3 - wg) + li;
@@ -1974,11 +2003,12 @@ __global__ __launch_bounds__(512) void mla_span_kernel(MlaWindowArgs p, int span
     }
 }
 
-// The weights of mla_window_kernel<H, true> into the MlaPack layout, one 16-byte
-// unit per thread (a copy: every unit is one unit of the row-major weight).
-template <int H>
+// The weights of the one-launch kernels into their packed layouts (MlaPack<8>
+// for mla_window_kernel<8, true>, MlaSpanPack for mla_span_kernel<true>), one
+// 16-byte unit per thread (a copy: every unit is one unit of the row-major
+// weight).
+template <typename P>
 __global__ __launch_bounds__(256) void mla_pack_kernel(const u16* w_in, const u16* w_up, const u16* w_out, u16* packed) {
-    using P = MlaPack<H>;
     const int u = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
     if (u >= P::UNITS) return;
     const int lane = u % 64, r = lane % 16, g = lane / 16;
@@ -1986,7 +2016,7 @@ __global__ __launch_bounds__(256) void mla_pack_kernel(const u16* w_in, const u1
     const u16* src;
     if (u < P::IN_UNITS) {
         const int tile = u / (KS * 64), s = (u / 64) % KS;
-        src = w_in + (16 * tile + (P::rope_tile(tile) ? mla_rope_order(r) : r)) * P::D + 32 * s + 8 * g;
+        src = w_in + P::in_row(tile, r) * P::D + 32 * s + 8 * g;
     } else if (u < P::IN_UNITS + P::UP_UNITS) {
         const int v = u - P::IN_UNITS;
         const int head = v / (P::CT * US * 64), ct = (v / (US * 64)) % P::CT, ks = (v / 64) % US;
@@ -2207,12 +2237,15 @@ mlk_status mla_window_launch(const float* x, int64_t batch, int64_t length, int6
                     static_cast<const u16*>(w_out), cosine, sine, out, length,
                     static_cast<float>(scale * 1.4426950408889634)};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (heads == 4) {  // mla_span_kernel: one block per (window, 64 query rows), row-major weights
-        MLK_CHECK(!packed, "mla_forward: the 4-head kernel takes row-major weights");
+    if (heads == 4) {  // mla_span_kernel: one block per (window, 64 query rows)
         const int64_t spans = (length + 63) / 64;
         MLK_CHECK(batch * spans <= 0x7fffffff, "too many windows for one launch");
-        hipLaunchKernelGGL(mla_span_kernel, dim3(static_cast<unsigned>(batch * spans)), dim3(512), 0, s, p,
-                           static_cast<int>(spans));
+        const dim3 grid(static_cast<unsigned>(batch * spans));
+        if (packed) {
+            hipLaunchKernelGGL((mla_span_kernel<true>), grid, dim3(512), 0, s, p, static_cast<int>(spans));
+        } else {
+            hipLaunchKernelGGL((mla_span_kernel<false>), grid, dim3(512), 0, s, p, static_cast<int>(spans));
+        }
         return launch_status("mla_forward");
     }
     const dim3 grid(static_cast<unsigned>(batch));
@@ -2249,25 +2282,35 @@ extern "C" mlk_status mlk_mla_forward(const float* x, int64_t batch, int64_t len
 
 extern "C" int64_t mlk_mla_packed_elems(int64_t d_model, int64_t heads, int64_t head_dim, int64_t nope_dim,
                                         int64_t kv_rank) {
-    const bool built = heads == 8 && head_dim == 32 && nope_dim == 16 && kv_rank == 64 && d_model == heads * head_dim;
-    return built ? static_cast<int64_t>(MlaPack<8>::UNITS) * 8 : 0;
+    if (d_model != heads * head_dim || kv_rank != 64) return 0;
+    if (heads == 8 && head_dim == 32 && nope_dim == 16) return static_cast<int64_t>(MlaPack<8>::UNITS) * 8;
+    if (heads == 4 && head_dim == 64 && nope_dim == 32) return static_cast<int64_t>(MlaSpanPack::UNITS) * 8;
+    return 0;
 }
 
 extern "C" mlk_status mlk_mla_pack_weights(const void* in_proj_weight, const void* kv_up_weight, const void* out_weight,
                                            int64_t d_model, int64_t heads, int64_t head_dim, int64_t nope_dim,
                                            int64_t kv_rank, int32_t weight_dtype, void* packed, mlk_stream_t stream) {
     if (weight_dtype != MLK_DTYPE_BF16 || mlk_mla_packed_elems(d_model, heads, head_dim, nope_dim, kv_rank) == 0) {
-        set_error("mla_pack_weights: geometry without the per-window kernel (bf16, 8 heads of 32, rope 16, kv rank 64)");
+        set_error("mla_pack_weights: geometry without a one-launch kernel (bf16; 8 heads of 32, rope 16, or 4 heads of 64, "
+                  "rope 32; kv rank 64)");
         return MLK_ERR_UNSUPPORTED;
     }
     MLK_CHECK(in_proj_weight && kv_up_weight && out_weight && packed, "null tensor pointer");
     MLK_CHECK(aligned16(in_proj_weight) && aligned16(kv_up_weight) && aligned16(out_weight) && aligned16(packed),
               "mla_pack_weights: operands must be 16-byte aligned");
-    constexpr int kUnits = MlaPack<8>::UNITS;
-    hipLaunchKernelGGL((mla_pack_kernel<8>), dim3((kUnits + 255) / 256), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), static_cast<const u16*>(in_proj_weight),
-                       static_cast<const u16*>(kv_up_weight), static_cast<const u16*>(out_weight),
-                       static_cast<u16*>(packed));
+    const bool span = heads == 4;
+    const int units = span ? MlaSpanPack::UNITS : MlaPack<8>::UNITS;
+    const dim3 grid(static_cast<unsigned>((units + 255) / 256));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const u16* wi = static_cast<const u16*>(in_proj_weight);
+    const u16* wu = static_cast<const u16*>(kv_up_weight);
+    const u16* wo = static_cast<const u16*>(out_weight);
+    if (span) {
+        hipLaunchKernelGGL((mla_pack_kernel<MlaSpanPack>), grid, dim3(256), 0, s, wi, wu, wo, static_cast<u16*>(packed));
+    } else {
+        hipLaunchKernelGGL((mla_pack_kernel<MlaPack<8>>), grid, dim3(256), 0, s, wi, wu, wo, static_cast<u16*>(packed));
+    }
     return launch_status("mla_pack_weights");
 }
 
@@ -2279,7 +2322,8 @@ extern "C" mlk_status mlk_mla_forward_packed(const float* x, int64_t batch, int6
                                              mlk_stream_t stream) {
     MLK_CHECK(batch >= 0 && length >= 1 && heads > 0 && d_model == heads * head_dim, "invalid MLA geometry");
     if (mlk_mla_packed_elems(d_model, heads, head_dim, nope_dim, kv_rank) == 0) {
-        set_error("mla_forward_packed: geometry without packed weights (bf16, 8 heads of 32, rope 16, kv rank 64)");
+        set_error("mla_forward_packed: geometry without packed weights (8 heads of 32, rope 16, or 4 heads of 64, rope 32; "
+                  "kv rank 64)");
         return MLK_ERR_UNSUPPORTED;
     }
     const mlk_status ok = mla_window_supported(x, length, d_model, x_batch_stride, x_token_stride, kv_norm_w, kv_norm_b,
@@ -2287,8 +2331,9 @@ extern "C" mlk_status mlk_mla_forward_packed(const float* x, int64_t batch, int6
                                                {packed_weights});
     if (ok != MLK_OK) return ok;
     const u16* w = static_cast<const u16*>(packed_weights);
+    const int64_t in_units = heads == 4 ? MlaSpanPack::IN_UNITS : MlaPack<8>::IN_UNITS;
+    const int64_t up_units = heads == 4 ? MlaSpanPack::UP_UNITS : MlaPack<8>::UP_UNITS;
     return mla_window_launch(x, batch, length, d_model, x_batch_stride, x_token_stride, w, kv_norm_w, kv_norm_b,
-                             kv_norm_eps, w + 8 * MlaPack<8>::IN_UNITS,
-                             w + 8 * (MlaPack<8>::IN_UNITS + MlaPack<8>::UP_UNITS), cosine, sine, scale, out, heads,
-                             true, stream);
+                             kv_norm_eps, w + 8 * in_units, w + 8 * (in_units + up_units), cosine, sine, scale, out,
+                             heads, true, stream);
 }

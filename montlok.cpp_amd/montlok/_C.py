@@ -976,8 +976,8 @@ def _mla_packed(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nop
 
 
 def mla_pack_weights(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim, nope_dim, kv_lora_rank):
-    """The three bf16 weights of the per-window MLA kernel in its fragment order (mlk_mla_pack_weights), or
-    None where that kernel is not built for the geometry."""
+    """The three bf16 weights of the one-launch MLA kernel in its fragment order (mlk_mla_pack_weights), or
+    None where no such kernel is built for the geometry."""
     for name, w in (("in_proj_weight", in_proj_weight), ("kv_up_weight", kv_up_weight), ("out_weight", out_weight)):
         _check(w.is_cuda and w.dtype == torch.bfloat16 and w.is_contiguous(), f"{name} must be contiguous bf16 on GPU")
     d_model = n_heads * head_dim
@@ -993,10 +993,10 @@ def mla_pack_weights(in_proj_weight, kv_up_weight, out_weight, n_heads, head_dim
 
 def _mla_window(x, in_proj_weight, kv_norm_weight, kv_norm_bias, kv_norm_eps, kv_up_weight, out_weight, cosine,
                 sine, n_heads, head_dim, nope_dim, kv_lora_rank, scale):
-    """The whole forward for every causal query in one launch (bf16 weights, kv rank 64, a positive scale;
-    8 heads of 32 with rope 16 and L <= 128: one block per window, on packed weights; 4 heads of 64 with rope
-    32 and L <= 256: one block per window and 64 query rows); None where no such kernel is built for the
-    call."""
+    """The whole forward for every causal query in one launch, on the weights packed in the kernel's fragment
+    order (bf16 weights, kv rank 64, a positive scale; 8 heads of 32 with rope 16 and L <= 128: one block per
+    window; 4 heads of 64 with rope 32 and L <= 256: one block per window and 64 query rows); None where no
+    such kernel is built for the call."""
     batch, length, d_model = x.shape
     ws = [in_proj_weight, kv_up_weight, out_weight]
     if any(w.dtype != torch.bfloat16 or not w.is_contiguous() for w in ws) or x.stride(-1) != 1:

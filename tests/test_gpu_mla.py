@@ -329,14 +329,15 @@ def test_span_kernel_equals_separate_path(dev, B, L, bias, strided):
     assert_bitwise(one, four.cpu().numpy(), f"per-span MLA {B}x{L} vs four launches")
 
 
-def test_packed_weights_equal_row_major(dev):
-    """_C.mla_forward runs the per-window kernel on its weights re-laid in the kernel's fragment order
+@pytest.mark.parametrize("B,L,H,hd,nope", [(6, 100, 8, 32, 16), (5, 200, 4, 64, 32)])
+def test_packed_weights_equal_row_major(dev, B, L, H, hd, nope):
+    """_C.mla_forward runs the one-launch kernel on its weights re-laid in the kernel's fragment order
     (mlk_mla_pack_weights, cached per weight triple): the result equals mlk_mla_forward on the row-major
     weights bit for bit, and the packed copy follows an in-place update of a weight."""
     from montlok import _C
 
-    g = torch.Generator().manual_seed(7)
-    B, L, H, hd, nope, kvr = 6, 100, 8, 32, 16, 64
+    g = torch.Generator().manual_seed(7 + H)
+    kvr = 64
     d, rope = H * hd, hd - nope
     bf = torch.bfloat16
     x = torch.randn(B, L, d, generator=g).to(dev)
