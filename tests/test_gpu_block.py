@@ -88,6 +88,40 @@ def test_block_vs_oracle_and_separate_ops(dev, oracle, dm, H, groups, B, L):
     assert_bitwise(out, separate.cpu().numpy(), f"block {B}x{L} vs separate operators")
 
 
+@pytest.mark.parametrize("dm,expand,groups,rope_fraction,B,L", [
+    (32, 2, 4, 0.5, 5, 32),     # d_model 32, one chunk: helper waves, weights masked past d_model
+    (32, 2, 4, 0.5, 3, 20),     # the same, token tile 1 partial
+    (64, 2, 8, 0.0, 4, 32),     # no rotary angles (R = 0), one chunk
+    (64, 2, 8, 0.0, 3, 40),     # R = 0, two chunks
+    (16, 2, 2, 0.5, 6, 30),     # one head (d_model 16)
+    (32, 5, 4, 0.125, 4, 32),   # five heads, one angle: 3H + R = 16, the tile full
+    (32, 5, 4, 0.0, 2, 50)])    # five heads, R = 0, two chunks
+def test_block_kernel_forms(dev, oracle, dm, expand, groups, rope_fraction, B, L):
+    """The mixer kernel's other forms and geometries (d_model below 64 with one-chunk windows, no rotary
+    angles, one and five heads): the one-launch block against the oracle chain at 1e-5 and the separate
+    operators bit for bit."""
+    from montlok import _C
+    from montlok.rdt import Mamba3BlockHIP
+
+    g = torch.Generator().manual_seed(B * 1000 + L * 10 + dm + expand)
+    block = Mamba3BlockHIP(dm, d_state=16, expand=expand, headdim=32, num_groups=groups,
+                           rope_fraction=rope_fraction).eval()
+    m = block.mamba
+    print(f"block form dm={dm} H={m.nheads} R={m.num_rope_angles} B={B} L={L}", flush=True)
+    _init(block, g)
+    x = torch.randn(B, L, dm, generator=g)
+    expect = _oracle_block(oracle, block, x.numpy())
+    block = block.to(dev)
+    xd = x.to(dev)
+    with torch.no_grad():
+        out = block(xd)
+        assert _C.mamba3_block_launches() == ["rms_norm_mamba3_forward", "linear_residual"], "the geometry has the one-launch kernel"
+        separate = xd + _C.mamba3_siso_layer(_C.rms_norm(xd, block.norm.weight, 1e-5, groups), m.in_proj.weight,
+                                             m.out_proj.weight, *m._mixer_args(), *m._geometry())
+    assert_close(out, expect, name=f"block form {dm}/{m.nheads}/{m.num_rope_angles} {B}x{L} vs oracle")
+    assert_bitwise(out, separate.cpu().numpy(), f"block form {dm}/{m.nheads}/{m.num_rope_angles} {B}x{L} vs separate operators")
+
+
 def test_block_many_windows_vs_oracle(dev, oracle):
     """300 windows x 70 tokens: 1200 (window, head) blocks of the fused mixer kernel (the separate in_proj
     takes its tiled form here, so only the oracle gate applies)."""
