@@ -491,7 +491,7 @@ __global__ __launch_bounds__(64) void rec_kernel(int64_t L, int64_t H, int64_t D
             float o;
             if (gate_logits) {
                 const double z = static_cast<double>(g_cur);
-                o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
+                o = static_cast<float>(static_cast<double>(y) * silu_d(z));
             } else {
                 o = y * g_cur;
             }
@@ -753,7 +753,7 @@ __global__ __launch_bounds__(64) void rec_chunk_kernel(RecArgs a) {
                     float o;
                     if (a.gate_logits) {
                         const double z = static_cast<double>(gt);
-                        o = static_cast<float>(static_cast<double>(y) * (z / (1.0 + exp_d(-z))));
+                        o = static_cast<float>(static_cast<double>(y) * silu_d(z));
                     } else {
                         o = y * gt;
                     }
@@ -1124,7 +1124,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 for (int v = 0; v < 4; ++v) {
                     if (!own(tt, v)) continue;
                     const double z = static_cast<double>(zx[tt][v]);
-                    const double sz = z / (1.0 + exp_d(-z));
+                    const double sz = silu_d(z);
                     gz[tt][v] = a.gate_logits ? sz : z;
                 }
 #pragma unroll
@@ -1945,7 +1945,7 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                     for (int v = kPrepOwnV; v < 4; ++v) {
                         const double z = static_cast<double>(
                             proj_s[(16 + 4 * grp + v) * pp + static_cast<int>(h) * D + 16 * sw + li]);
-                        lg[(sw * 4 + v) * 64 + lane] = z / (1.0 + exp_d(-z));
+                        lg[(sw * 4 + v) * 64 + lane] = silu_d(z);
                     }
             }
             __syncthreads();  // with the end of the scan waves' step d: decay weights, gates, q and k are in
@@ -2274,7 +2274,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(StepArgs p) {
         }
         const float y = fmaf(p.skip[h], v_cur, VEC ? acc0 + acc1 : acc0);
         const double zz = static_cast<double>(z[d]);
-        p.out[s_idx * d_inner + h * D + d] = static_cast<float>(static_cast<double>(y) * (zz / (1.0 + exp_d(-zz))));
+        p.out[s_idx * d_inner + h * D + d] = static_cast<float>(static_cast<double>(y) * silu_d(zz));
         vps[d] = v_cur;
         float* kps = p.k_prev + (s_idx * H + h) * N;
         for (int64_t n = d; n < N; n += D) kps[n] = kh[n];
