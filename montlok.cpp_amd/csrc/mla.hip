@@ -1468,7 +1468,8 @@ struct MlaSpanPack {
 //            latent and k_rope columns of the in_proj (the same chains),
 //            k_rope rotated into every head's k rows, the latent's LayerNorm
 //            (mla_window_kernel's four lanes per row: layer_norm_vec_kernel's
-//            sums), kv_up (wave w: head w / 2, two row tiles), and the causal
+//            sums), kv_up (wave w: head w / 2, three of its six column
+//            tiles over the 4 row tiles), and the causal
 //            attention of the span's queries against the tile with the
 //            running max, sum and output carried across tiles: per query row
 //            the chunk sequence of mla_attend_kernel (its 64-key chunks are
