@@ -685,14 +685,19 @@ constexpr int kStreamRT = 1;                    // 32-row tiles per step
 constexpr int kStreamRows = 32 * kStreamRT;     // rows per step
 constexpr int kStreamK = 256;                   // the form takes K = 256 exactly (16-byte aligned operands)
 
+template <int K>
 __global__ __launch_bounds__(64 * kStreamWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
     using T = u16;
-    constexpr int kSteps = kStreamK / 16;
-    constexpr int kPitch = kStreamK + 8;      // LDS row pitch in bf16 (+16 bytes)
+    constexpr int kSteps = K / 16;
+    constexpr int kPitch = K + 8;             // LDS row pitch in bf16 (+16 bytes)
     constexpr int kThr = 64 * kStreamWaves;
     constexpr int kTPR = kThr / kStreamRows;  // threads per x row
-    constexpr int kXPer = kStreamK / kTPR;    // x floats per thread per tile
+    constexpr int kXPer = K / kTPR;           // x floats per thread per tile
+    // x fragments read from LDS a part of K at a time (K = 512: a quarter, so that the W fragments, 128
+    // registers, the next tile's x and the part fit two waves per SIMD); the products keep the order of k.
+    constexpr int kXParts = K / 128;
+    static_assert(kSteps % kXParts == 0, "whole parts of K");
     static_assert(kXPer % 8 == 0, "whole 16-byte bf16 units per thread");
     __shared__ __attribute__((aligned(16))) T x_lds[2][kStreamRows * kPitch];
 
@@ -721,7 +726,7 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
     {
         const T* w = static_cast<const T*>(p.w);
         const int64_t n = n_wave + r32;
-        const T* wrow = w + (n < p.N ? n : p.N - 1) * kStreamK + 8 * h;
+        const T* wrow = w + (n < p.N ? n : p.N - 1) * K + 8 * h;
         const uint32_t keep = n < p.N ? 0xffffffffu : 0u;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
@@ -766,19 +771,23 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
             for (int m = 0; m < kStreamRT; ++m)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[m][v] = 0.0f;
-            uint4 xb[kStreamRT][kSteps];
 #pragma unroll
-            for (int s = 0; s < kSteps; ++s)
+            for (int part = 0; part < kXParts; ++part) {
+                constexpr int kPS = kSteps / kXParts;
+                uint4 xb[kStreamRT][kPS];
 #pragma unroll
-                for (int m = 0; m < kStreamRT; ++m)
-                    xb[m][s] = *reinterpret_cast<const uint4*>(buf + (32 * m + r32) * kPitch + 16 * s + 8 * h);
+                for (int s = 0; s < kPS; ++s)
 #pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
+                    for (int m = 0; m < kStreamRT; ++m)
+                        xb[m][s] = *reinterpret_cast<const uint4*>(buf + (32 * m + r32) * kPitch + 16 * (part * kPS + s) + 8 * h);
 #pragma unroll
-                for (int m = 0; m < kStreamRT; ++m) {
-                    acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[s]),
-                                                                     __builtin_bit_cast(bf16x8, xb[m][s]), acc[m], 0,
-                                                                     0, 0);
+                for (int s = 0; s < kPS; ++s) {
+#pragma unroll
+                    for (int m = 0; m < kStreamRT; ++m) {
+                        acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[part * kPS + s]),
+                                                                         __builtin_bit_cast(bf16x8, xb[m][s]), acc[m], 0,
+                                                                         0, 0);
+                    }
                 }
             }
 #pragma unroll
@@ -1027,9 +1036,22 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
                     hipLaunchKernelGGL(linear_stream_sw_kernel, grid, dim3(64 * (kStreamWaves + kStoreWaves)), 0,
                                        stream, p, col_groups, row_parts);
                 } else {
-                    hipLaunchKernelGGL(linear_stream_kernel, grid, dim3(64 * kStreamWaves), 0, stream, p,
+                    hipLaunchKernelGGL(linear_stream_kernel<kStreamK>, grid, dim3(64 * kStreamWaves), 0, stream, p,
                                        col_groups, row_parts);
                 }
+                return;
+            }
+        }
+        // K = 512 (the stack's Mamba out_proj, 262144 x 512 -> 256): the streaming form with 128 registers of
+        // W fragments per wave, two waves per SIMD (no storing waves: they would leave 168 registers);
+        // 288 -> 190 us against the tiled 16 x 16 x 32 form.
+        if (VEC && p.K == 512 && p.x_stride % 4 == 0 && p.N >= 128 && rows >= 32768 && stream_form()) {
+            const int col_groups = static_cast<int>(ceil_div(p.N, kStreamCols));
+            const int parts_per_xcd = 32 / col_groups;
+            if (parts_per_xcd >= 1) {
+                const int row_parts = 8 * parts_per_xcd;
+                hipLaunchKernelGGL(linear_stream_kernel<512>, dim3(static_cast<unsigned>(8 * parts_per_xcd * col_groups)),
+                                   dim3(64 * kStreamWaves), 0, stream, p, col_groups, row_parts);
                 return;
             }
         }

@@ -260,6 +260,34 @@ def test_rms_norm_linear_beyond_the_fused_form(dev):
         assert torch.equal(fused, _C.linear(_C.rms_norm(x, nw, 1e-5, groups), w))
 
 
+@pytest.mark.parametrize("M,N,bias,strided", [(40000, 256, False, False), (33000, 192, True, True), (35000, 320, True, False)])
+def test_streaming_form_k512(dev, oracle, M, N, bias, strided, monkeypatch):
+    """bf16 weights, K = 512, 128 or more output columns, 32768 or more rows: the streaming form with the W
+    fragments of all of K in registers (ragged column groups, strided x, bias, the residual epilogue)
+    matches the exact product of bf16-rounded inputs at 1e-6, and the tiled 16 x 16 x 32 form
+    (MLK_LINEAR_FORM=t32) to the same bound (their k blockings differ, so not bit for bit)."""
+    from montlok import _C
+
+    rng = np.random.default_rng(M + N + 512)
+    K = 512
+    xw = rng.standard_normal((M, K + (16 if strided else 0))).astype(np.float32)
+    x = _t(xw, dev)[:, 8:8 + K] if strided else _t(xw, dev)
+    w = _bf16_round(rng.standard_normal((N, K)) * 0.02)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    args = (x, _t(w, dev).bfloat16(), None if b is None else _t(b, dev))
+    res = torch.randn(M, N, generator=torch.Generator().manual_seed(M)).to(dev)
+    streaming = _C.linear(*args)
+    with_res = _C.linear_residual(*args, res)
+    monkeypatch.setenv("MLK_LINEAR_FORM", "t32")
+    tiled = _C.linear(*args)
+    monkeypatch.delenv("MLK_LINEAR_FORM")
+    assert torch.equal(with_res, res + streaming), "residual epilogue vs the two steps"
+    x_np = xw[:, 8:8 + K] if strided else xw
+    expect = oracle.linear(_bf16_round(x_np), w, b)
+    assert_close(streaming, expect, tol=1e-6, name="K=512 streaming vs bf16-input product")
+    assert_close(tiled, expect, tol=1e-6, name="K=512 tiled vs bf16-input product")
+
+
 @pytest.mark.parametrize("M,N,bias,strided", [(9000, 1192, True, False), (70000, 1192, False, True), (31, 768, True, False),
                                               (4096, 2000, False, False)])
 def test_streaming_form_equals_t32_form(dev, oracle, M, N, bias, strided, monkeypatch):
