@@ -23,66 +23,95 @@ namespace mlk {
 namespace {
 
 constexpr int kBlock = 256;
+#ifndef MLK_NORM_RPW
+#define MLK_NORM_RPW 4
+#endif
+constexpr int kNormRpw = MLK_NORM_RPW;  // rows per lane group in large launches
 
-template <int LPG, int CPL, bool ADD>
+// RPW groups per lane group, one after the other in the arithmetic but with
+// all their loads issued first: a wave then has RPW times the bytes in flight
+// and a block RPW times the work (262144 rows of 256: one row per wave left the
+// kernel at 46% of HBM, its waves each waiting on one 16-byte load per lane).
+// Group r of block b's lane group k is (b RPW + r) (256 / LPG) + k, so each
+// load instruction still reads the block's groups side by side. Per group the
+// arithmetic is unchanged.
+template <int LPG, int CPL, bool ADD, int RPW = 1>
 __global__ __launch_bounds__(kBlock) void rms_norm_vec_kernel(const float* __restrict__ x,
                                                               const float* __restrict__ right,
                                                               const float* __restrict__ w, int64_t total_groups,
                                                               int64_t groups, int64_t gs, int64_t dim,
                                                               int64_t row_stride, double eps,
                                                               float* __restrict__ residual, float* __restrict__ out) {
-    const int64_t gid = static_cast<int64_t>(blockIdx.x) * (kBlock / LPG) + threadIdx.x / LPG;
     const int li = threadIdx.x % LPG;
-    const bool active = gid < total_groups;
-    const int64_t row = active ? gid / groups : 0;
-    const int64_t g = active ? gid % groups : 0;
-    const float* xg = x + row * row_stride + g * gs;
-    const float* wg = w + g * gs;
+    int64_t gid[RPW], row[RPW], g[RPW];
+    bool active[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        gid[r] = (static_cast<int64_t>(blockIdx.x) * RPW + r) * (kBlock / LPG) + threadIdx.x / LPG;
+        active[r] = gid[r] < total_groups;
+        row[r] = active[r] ? gid[r] / groups : 0;
+        g[r] = active[r] ? gid[r] % groups : 0;
+    }
     // Every load is issued before the first use, without a branch around it:
     // lanes past the last group read group 0 (in bounds); all LPG lanes of a
     // group share `active`, so those sums never meet a live group's.
-    float4 v[CPL], wv[CPL];
+    float4 v[RPW][CPL], wv[RPW][CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) v[c] = *reinterpret_cast<const float4*>(xg + static_cast<int64_t>(c * LPG + li) * 4);
+    for (int r = 0; r < RPW; ++r) {
+        const float* xg = x + row[r] * row_stride + g[r] * gs;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) v[r][c] = *reinterpret_cast<const float4*>(xg + static_cast<int64_t>(c * LPG + li) * 4);
+    }
     if constexpr (ADD) {
-        float4 r[CPL];
+        float4 rv[RPW][CPL];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            r[c] = *reinterpret_cast<const float4*>(right + row * row_stride + g * gs + static_cast<int64_t>(c * LPG + li) * 4);
-        }
+        for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            v[c].x += r[c].x;
-            v[c].y += r[c].y;
-            v[c].z += r[c].z;
-            v[c].w += r[c].w;
-            if (active) {
-                *reinterpret_cast<float4*>(residual + row * dim + g * gs + static_cast<int64_t>(c * LPG + li) * 4) = v[c];
+            for (int c = 0; c < CPL; ++c)
+                rv[r][c] = *reinterpret_cast<const float4*>(right + row[r] * row_stride + g[r] * gs +
+                                                            static_cast<int64_t>(c * LPG + li) * 4);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                v[r][c].x += rv[r][c].x;
+                v[r][c].y += rv[r][c].y;
+                v[r][c].z += rv[r][c].z;
+                v[r][c].w += rv[r][c].w;
+                if (active[r]) {
+                    *reinterpret_cast<float4*>(residual + row[r] * dim + g[r] * gs + static_cast<int64_t>(c * LPG + li) * 4) =
+                        v[r][c];
+                }
             }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+            wv[r][c] = *reinterpret_cast<const float4*>(w + g[r] * gs + static_cast<int64_t>(c * LPG + li) * 4);
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        double sumsq = 0.0;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const double a = v[r][c].x, b = v[r][c].y, cc = v[r][c].z, d = v[r][c].w;
+            sumsq += (a * a + b * b) + (cc * cc + d * d);
         }
-    }
+        sumsq = group_sum_d<LPG>(sumsq);
+        if (!active[r]) continue;
+        const double scale = 1.0 / sqrt(sumsq / static_cast<double>(gs) + eps);
+        float* og = out + row[r] * dim + g[r] * gs;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) wv[c] = *reinterpret_cast<const float4*>(wg + static_cast<int64_t>(c * LPG + li) * 4);
-    double sumsq = 0.0;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const double a = v[c].x, b = v[c].y, cc = v[c].z, d = v[c].w;
-        sumsq += (a * a + b * b) + (cc * cc + d * d);
-    }
-    sumsq = group_sum_d<LPG>(sumsq);
-    if (!active) return;
-    const double scale = 1.0 / sqrt(sumsq / static_cast<double>(gs) + eps);
-    float* og = out + row * dim + g * gs;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const int64_t off = static_cast<int64_t>(c * LPG + li) * 4;
-        const float4 wv_c = wv[c];
-        float4 o;
-        o.x = static_cast<float>((static_cast<double>(v[c].x) * scale) * static_cast<double>(wv_c.x));
-        o.y = static_cast<float>((static_cast<double>(v[c].y) * scale) * static_cast<double>(wv_c.y));
-        o.z = static_cast<float>((static_cast<double>(v[c].z) * scale) * static_cast<double>(wv_c.z));
-        o.w = static_cast<float>((static_cast<double>(v[c].w) * scale) * static_cast<double>(wv_c.w));
-        *reinterpret_cast<float4*>(og + off) = o;
+        for (int c = 0; c < CPL; ++c) {
+            const int64_t off = static_cast<int64_t>(c * LPG + li) * 4;
+            const float4 wv_c = wv[r][c];
+            float4 o;
+            o.x = static_cast<float>((static_cast<double>(v[r][c].x) * scale) * static_cast<double>(wv_c.x));
+            o.y = static_cast<float>((static_cast<double>(v[r][c].y) * scale) * static_cast<double>(wv_c.y));
+            o.z = static_cast<float>((static_cast<double>(v[r][c].z) * scale) * static_cast<double>(wv_c.z));
+            o.w = static_cast<float>((static_cast<double>(v[r][c].w) * scale) * static_cast<double>(wv_c.w));
+            *reinterpret_cast<float4*>(og + off) = o;
+        }
     }
 }
 
@@ -133,11 +162,17 @@ mlk_status launch_rms(const float* x, const float* right, const float* w, int64_
                          (!ADD || (reinterpret_cast<uintptr_t>(right) % 16 == 0 &&
                                    reinterpret_cast<uintptr_t>(residual) % 16 == 0));
     const int64_t chunks = gs / 4;
+    // Four groups per lane group where one each would take 4096 blocks or more.
 #define MLK_RMS_VEC(LPG, CPL)                                                                                \
     do {                                                                                                     \
         const int64_t blocks = ceil_div(total, kBlock / (LPG));                                              \
-        hipLaunchKernelGGL((rms_norm_vec_kernel<LPG, CPL, ADD>), dim3(blocks), dim3(kBlock), 0, stream, x,   \
-                           right, w, total, groups, gs, dim, row_stride, eps_f, residual, out);              \
+        if (blocks >= 4096) {                                                                                \
+            hipLaunchKernelGGL((rms_norm_vec_kernel<LPG, CPL, ADD, kNormRpw>), dim3(ceil_div(blocks, kNormRpw)), dim3(kBlock), \
+                               0, stream, x, right, w, total, groups, gs, dim, row_stride, eps_f, residual, out); \
+        } else {                                                                                             \
+            hipLaunchKernelGGL((rms_norm_vec_kernel<LPG, CPL, ADD>), dim3(blocks), dim3(kBlock), 0, stream, x, \
+                               right, w, total, groups, gs, dim, row_stride, eps_f, residual, out);          \
+        }                                                                                                    \
         return launch_status("rms_norm");                                                                    \
     } while (0)
     if (aligned) {
@@ -165,23 +200,30 @@ mlk_status launch_rms(const float* x, const float* right, const float* w, int64_
 // when possible (two passes over registers: mean, then centred squares).
 // BF16OUT: the float results rounded once more to bf16 (round to nearest
 // even), written as bf16 rows of dim.
-template <int CPL, bool BF16OUT = false>
+template <int CPL, bool BF16OUT = false, int RPW = 1>
 __global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __restrict__ x,
                                                                 const float* __restrict__ w,
                                                                 const float* __restrict__ bias, int64_t rows,
                                                                 int64_t dim, int64_t row_stride, double eps,
                                                                 void* __restrict__ out) {
-    // LPG lanes per row: dim = 4 * CPL * LPG with LPG = 64 / rows-per-wave.
+    // LPG lanes per row: dim = 4 * CPL * LPG with LPG = 64 / rows-per-wave. RPW rows per lane group, all
+    // their loads issued first (as rms_norm_vec_kernel): row r of block b's lane group k is
+    // (b RPW + r) (256 / LPG) + k.
     const int lpg = static_cast<int>(dim / (4 * CPL));
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / lpg) + threadIdx.x / lpg;
     const int li = threadIdx.x % lpg;
-    const bool active = row < rows;
-    const float* xr = x + (active ? row : 0) * row_stride;
+    int64_t row[RPW];
+    bool active[RPW];
     // Loads first, unconditional (rows past the end read row 0; a row's lanes
     // share `active`), weights and bias with them.
-    float4 v[CPL], wv[CPL], bv[CPL];
+    float4 v[RPW][CPL], wv[CPL], bv[CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) v[c] = *reinterpret_cast<const float4*>(xr + (c * lpg + li) * 4);
+    for (int r = 0; r < RPW; ++r) {
+        row[r] = (static_cast<int64_t>(blockIdx.x) * RPW + r) * (kBlock / lpg) + threadIdx.x / lpg;
+        active[r] = row[r] < rows;
+        const float* xr = x + (active[r] ? row[r] : 0) * row_stride;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) v[r][c] = *reinterpret_cast<const float4*>(xr + (c * lpg + li) * 4);
+    }
     const float* bsrc = bias != nullptr ? bias : w;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -189,39 +231,42 @@ __global__ __launch_bounds__(kBlock) void layer_norm_vec_kernel(const float* __r
         bv[c] = *reinterpret_cast<const float4*>(bsrc + (c * lpg + li) * 4);
         if (bias == nullptr) bv[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    double sum = 0.0;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        sum += (static_cast<double>(v[c].x) + static_cast<double>(v[c].y)) +
-               (static_cast<double>(v[c].z) + static_cast<double>(v[c].w));
-    }
-    for (int mask = lpg / 2; mask > 0; mask >>= 1) sum += shfl_xor_d(sum, mask);
     const double inv_dim = 1.0 / static_cast<double>(dim);
-    const double mean = sum * inv_dim;
-    double sumsq = 0.0;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const double a = static_cast<double>(v[c].x) - mean, b = static_cast<double>(v[c].y) - mean;
-        const double cc = static_cast<double>(v[c].z) - mean, d = static_cast<double>(v[c].w) - mean;
-        sumsq += (a * a + b * b) + (cc * cc + d * d);
-    }
-    for (int mask = lpg / 2; mask > 0; mask >>= 1) sumsq += shfl_xor_d(sumsq, mask);
-    if (!active) return;
-    const double rstd = 1.0 / sqrt(fma(sumsq, inv_dim, eps));
+    for (int r = 0; r < RPW; ++r) {
+        double sum = 0.0;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const int off = (c * lpg + li) * 4;
-        float4 o;
-        o.x = static_cast<float>(((static_cast<double>(v[c].x) - mean) * rstd) * wv[c].x + static_cast<double>(bv[c].x));
-        o.y = static_cast<float>(((static_cast<double>(v[c].y) - mean) * rstd) * wv[c].y + static_cast<double>(bv[c].y));
-        o.z = static_cast<float>(((static_cast<double>(v[c].z) - mean) * rstd) * wv[c].z + static_cast<double>(bv[c].z));
-        o.w = static_cast<float>(((static_cast<double>(v[c].w) - mean) * rstd) * wv[c].w + static_cast<double>(bv[c].w));
-        if constexpr (BF16OUT) {
-            auto h = [](float f) { return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f))); };
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + row * dim + off) =
-                make_uint2(h(o.x) | (h(o.y) << 16), h(o.z) | (h(o.w) << 16));
-        } else {
-            *reinterpret_cast<float4*>(static_cast<float*>(out) + row * dim + off) = o;
+        for (int c = 0; c < CPL; ++c) {
+            sum += (static_cast<double>(v[r][c].x) + static_cast<double>(v[r][c].y)) +
+                   (static_cast<double>(v[r][c].z) + static_cast<double>(v[r][c].w));
+        }
+        for (int mask = lpg / 2; mask > 0; mask >>= 1) sum += shfl_xor_d(sum, mask);
+        const double mean = sum * inv_dim;
+        double sumsq = 0.0;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const double a = static_cast<double>(v[r][c].x) - mean, b = static_cast<double>(v[r][c].y) - mean;
+            const double cc = static_cast<double>(v[r][c].z) - mean, d = static_cast<double>(v[r][c].w) - mean;
+            sumsq += (a * a + b * b) + (cc * cc + d * d);
+        }
+        for (int mask = lpg / 2; mask > 0; mask >>= 1) sumsq += shfl_xor_d(sumsq, mask);
+        if (!active[r]) continue;
+        const double rstd = 1.0 / sqrt(fma(sumsq, inv_dim, eps));
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int off = (c * lpg + li) * 4;
+            float4 o;
+            o.x = static_cast<float>(((static_cast<double>(v[r][c].x) - mean) * rstd) * wv[c].x + static_cast<double>(bv[c].x));
+            o.y = static_cast<float>(((static_cast<double>(v[r][c].y) - mean) * rstd) * wv[c].y + static_cast<double>(bv[c].y));
+            o.z = static_cast<float>(((static_cast<double>(v[r][c].z) - mean) * rstd) * wv[c].z + static_cast<double>(bv[c].z));
+            o.w = static_cast<float>(((static_cast<double>(v[r][c].w) - mean) * rstd) * wv[c].w + static_cast<double>(bv[c].w));
+            if constexpr (BF16OUT) {
+                auto hb = [](float f) { return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f))); };
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + row[r] * dim + off) =
+                    make_uint2(hb(o.x) | (hb(o.y) << 16), hb(o.z) | (hb(o.w) << 16));
+            } else {
+                *reinterpret_cast<float4*>(static_cast<float*>(out) + row[r] * dim + off) = o;
+            }
         }
     }
 }
@@ -313,8 +358,13 @@ mlk_status mlk_layer_norm(const float* x, int64_t rows, int64_t dim, int64_t row
         const int64_t blocks = ceil_div(rows, kBlock / lpg);
         switch (cpl) {
             case 1:
-                hipLaunchKernelGGL(layer_norm_vec_kernel<1>, dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias,
-                                   rows, dim, row_stride, eps_f, out);
+                if (blocks >= 4096) {  // four rows per lane group (as rms_norm)
+                    hipLaunchKernelGGL((layer_norm_vec_kernel<1, false, kNormRpw>), dim3(ceil_div(blocks, kNormRpw)), dim3(kBlock), 0,
+                                       stream, x, weight, bias, rows, dim, row_stride, eps_f, out);
+                } else {
+                    hipLaunchKernelGGL(layer_norm_vec_kernel<1>, dim3(blocks), dim3(kBlock), 0, stream, x, weight,
+                                       bias, rows, dim, row_stride, eps_f, out);
+                }
                 break;
             case 2:
                 hipLaunchKernelGGL(layer_norm_vec_kernel<2>, dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias,
@@ -347,8 +397,14 @@ mlk_status mlk_layer_norm_bf16(const float* x, int64_t rows, int64_t dim, int64_
     if (rows == 0) return MLK_OK;
     MLK_CHECK(x != nullptr && weight != nullptr && out != nullptr, "null tensor pointer");
     const int64_t blocks = ceil_div(rows, kBlock / chunks);
-    hipLaunchKernelGGL((layer_norm_vec_kernel<1, true>), dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias, rows,
-                       dim, row_stride, static_cast<double>(static_cast<float>(eps)), out);
+    const double eps_f = static_cast<double>(static_cast<float>(eps));
+    if (blocks >= 4096) {
+        hipLaunchKernelGGL((layer_norm_vec_kernel<1, true, kNormRpw>), dim3(ceil_div(blocks, kNormRpw)), dim3(kBlock), 0, stream, x,
+                           weight, bias, rows, dim, row_stride, eps_f, out);
+    } else {
+        hipLaunchKernelGGL((layer_norm_vec_kernel<1, true>), dim3(blocks), dim3(kBlock), 0, stream, x, weight, bias,
+                           rows, dim, row_stride, eps_f, out);
+    }
     return launch_status("layer_norm_bf16");
 }
 
