@@ -10,7 +10,8 @@ x + out_proj(mamba3(in_proj(GroupedRMSNorm(x)))) over the 64 windows, and the
 value is windows/s. Other workloads: ``mhc`` (the residual mix alone, 8192
 tokens, tokens/s), ``mla`` (causal MLA, 256 x 128 tokens, windows/s),
 ``decode`` (65536 streams x 2 Mamba-3 blocks + head, stream-steps/s),
-``stack`` (the 4-layer hybrid stack, 1024 x 256 tokens, windows/s).
+``stack`` (the 4-layer hybrid stack, 1024 x 256 tokens, windows/s),
+``norms`` (RMSNorm + add-RMSNorm + LayerNorm over 262144 x 256, rows/s).
 
 Timing: W untimed steps (replays of one-step HIP graphs), then exactly K
 steps as one replay of a HIP graph that holds the K steps in order, between
@@ -20,7 +21,7 @@ give the median and spread of the per-step time. Inputs are resident in HBM
 before timing.
 
 With no --workload, the line is the block's and, under "configs", the other
-four workloads' figures from the same run (value, ms per step, median, the
+workloads' figures from the same run (value, ms per step, median, the
 dominant kernel's roofline and counter traffic, the CPU baseline); --configs
 none measures the named workload alone.
 
@@ -1108,7 +1109,121 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
     return line
 
 
-WORKLOADS = {"mhc": bench_mhc, "block": bench_block, "mla": bench_mla, "decode": bench_decode, "stack": bench_stack}
+# ------------------------------------------------------------ norms
+
+# The reference's row-wise norm operators alone (RMSNorm, residual add + RMSNorm, LayerNorm) at the
+# stack's activation size, 262144 tokens x d_model 256: plain HBM-bound kernels, measured so that their
+# fraction of HBM bandwidth is on record beside the fused ones.
+NORMS = dict(rows=262144, dim=256)
+
+
+def cpu_baseline_norms(cfg: dict, budget_s: float = 12.0, rows: int = 16384) -> dict:
+    """The reference's own norm kernels (oracle/_ref) on a slice of the rows (the oracle port where that
+    library is absent)."""
+    import numpy as np
+
+    from oracle import Oracle, Reference, reference_available
+
+    rng = np.random.default_rng(0)
+    d = cfg["dim"]
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    r = rng.standard_normal((rows, d)).astype(np.float32)
+    w = (rng.random(d) + 0.5).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    ref = reference_available()
+    lib = Reference() if ref else Oracle()
+
+    def make_step(threads):
+        if ref:
+            lib.set_threads(threads)
+
+        def step():
+            lib.rms_norm(x, w, 1e-5)
+            lib.add_rms_norm(x, r, w, 1e-5)
+            lib.layer_norm(x, w, b, 1e-5)
+        return step
+
+    return _cpu_legs(make_step, rows, "rows/s", "reference" if ref else "port",
+                     f"rms_norm + add_rms_norm + layer_norm over {rows} of the {cfg['rows']} rows in the "
+                     f"{'reference ' + lib.variant if ref else 'oracle'} build", budget_s)
+
+
+def bench_norms(steps: int, warmup: int, cpu: bool) -> dict:
+    import torch
+
+    from montlok import _C
+
+    cfg = NORMS
+    R, d = cfg["rows"], cfg["dim"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    sets = 4  # 4 x 2 x 256 MiB of inputs > the 256 MB Infinity Cache
+    xs = [torch.randn(R, d, generator=g).to(dev) for _ in range(sets)]
+    rs = [torch.randn(R, d, generator=g).to(dev) for _ in range(sets)]
+    w = (torch.rand(d, generator=g) + 0.5).to(dev)
+    b = torch.randn(d, generator=g).to(dev)
+    out = {}
+
+    def rms(i):
+        return lambda: out.__setitem__("rms", _C.rms_norm(xs[i], w, 1e-5, 1))
+
+    def add(i):
+        return lambda: out.__setitem__("add", _C.add_rms_norm(xs[i], rs[i], w, 1e-5, 1))
+
+    def ln(i):
+        return lambda: out.__setitem__("ln", _C.layer_norm(xs[i], w, b, 1e-5))
+
+    def step(i):
+        fns = (rms(i), add(i), ln(i))
+
+        def run():
+            for f in fns:
+                f()
+        return run
+
+    def outputs():
+        return {k: torch.cat([u.reshape(-1) for u in (v if isinstance(v, tuple) else (v,))]) for k, v in out.items()}
+
+    eager = []
+    for i in range(sets):
+        step(i)()
+        eager.append({k: v.clone() for k, v in outputs().items()})
+    torch.cuda.synchronize()
+    t = _gpu_steps([step(i) for i in range(sets)], steps, warmup)
+    last = eager[(steps - 1) % sets]  # the timed graph's last step leaves its outputs in `out`
+    for k, v in outputs().items():
+        assert torch.equal(v, last[k]), f"graph replay of {k} differs from the eager step"
+    ms = t["ms_per_step"]
+    replays = max(4, steps // sets)
+    f = 4
+    kernels = {}
+    for name, mk, byts in (("rms_norm", rms, 2 * R * d * f), ("add_rms_norm", add, 4 * R * d * f),
+                           ("layer_norm", ln, 2 * R * d * f)):
+        k_ms = _time_graph(_graph([mk(i) for i in range(sets)]), replays) / sets
+        kernels[name] = {"launch_ms": k_ms, "algorithmic_bytes": byts, "achieved_GBs": byts / (k_ms * 1e-3) / 1e9,
+                         "hbm_frac": byts / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    dom = max(kernels, key=lambda k: kernels[k]["launch_ms"])
+    line = _base_line(R / (ms * 1e-3), "rows/s", t["steps"], warmup, ms, "f32 (f64 accumulate)",
+                      "synthetic (seeded N(0,1) rows)",
+                      {"workload": "norms_262144x256", "rows": R, "dim": d,
+                       "step": "rms_norm + add_rms_norm + layer_norm over the same rows",
+                       "launch": "the K steps in one HIP graph, rotating over 4 independent input sets (cold HBM)",
+                       "parallelism": "single GPU"})
+    k = kernels[dom]
+    line["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": k["achieved_GBs"], "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": k["hbm_frac"], "traffic": _traffic("norms_r262144_d256", dom),
+                        "algorithmic_bytes": k["algorithmic_bytes"], "launch_ms": k["launch_ms"]}
+    line["kernels"] = kernels
+    line.update(_timing_fields(t))
+    line["step_roofline_frac"] = (8 * R * d * f) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+    if cpu:
+        line["cpu_baseline"] = cpu_baseline_norms(cfg)
+        line["cpu_baseline"]["gpu_over_cpu"] = line["value"] / line["cpu_baseline"]["value"]
+    return line
+
+
+WORKLOADS = {"mhc": bench_mhc, "block": bench_block, "mla": bench_mla, "decode": bench_decode, "stack": bench_stack,
+             "norms": bench_norms}
 
 
 def copy_bandwidth(mib: int = 1024, reps: int = 10) -> float:
