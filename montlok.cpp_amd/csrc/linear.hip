@@ -45,6 +45,7 @@ namespace mlk {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16;
@@ -678,7 +679,8 @@ __global__ __launch_bounds__(kThreads) void linear_t32_kernel(LinearArgs p) {
 //   us), non-temporal stores (1.5 ms), x two tiles ahead (469 us). Without
 //   its stores the kernel takes 261 us, and a plain fill writes the 1.25 GB
 //   output in 187 us: the stores add their whole time to the rest, which is
-//   what linear_stream_sw_kernel below (the default) works on: 445 us.
+//   what linear_stream_sw_kernel below works on: 445 us (and then
+//   linear_stream_io_kernel, the default: 361 us).
 constexpr int kStreamWaves = 8;
 constexpr int kStreamCols = 32 * kStreamWaves;  // columns per block
 constexpr int kStreamRT = 1;                    // 32-row tiles per step
@@ -835,7 +837,11 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
 // on a SIMD: the computing waves load x's fragments half of K at a time and
 // the storing waves unroll by two, which keeps both within 168 registers
 // without spills. 262144 x 256 -> 1192: 445 us against 457 us for
-// linear_stream_kernel (MLK_LINEAR_STORE_WAVES=0 selects that one).
+// linear_stream_kernel. Where linear_stream_io_kernel takes the shape it is the
+// default; MLK_LINEAR_STORE_WAVES=sw selects this form, =0 linear_stream_kernel.
+// Its stores sit behind branches (the output edge tests), so the compiler's
+// shared load/store counter makes each step's x load wait for the previous
+// step's stores: the IO-wave form's buffer stores remove that.
 constexpr int kStoreWaves = 4;
 
 __global__ __launch_bounds__(64 * (kStreamWaves + kStoreWaves))
@@ -983,6 +989,197 @@ void linear_stream_sw_kernel(LinearArgs p, int col_groups, int row_parts) {
     }
 }
 
+// The streaming form with its memory traffic on separate waves: waves 0..7
+// compute as in linear_stream_kernel, reading x only from LDS and leaving each
+// 32 x 256 result tile in one of two LDS buffers; waves 8..11 ("IO waves")
+// hold the next two x tiles in registers (loads issued two steps before the
+// tile is needed, each instruction one row's 1 KB), round the next step's
+// tile to bf16 into LDS, and store the previous step's result tile (one row's
+// 1 KB of this column group per instruction). No computing wave waits on
+// global memory. Block (row part rp, column group) takes every row_parts-th
+// tile from rp, so all blocks write within one moving window of the output
+// (361 us against 371 us for consecutive tiles per block). Same products and
+// order as linear_stream_kernel (and linear_t32_kernel), same bits. Taken for
+// outputs without a residual, 16-byte aligned, N % 4 = 0.
+//   262144 x 256 -> 1192: 361 us against 445 us for linear_stream_sw_kernel.
+//   Timing copies: the loads and products alone take 220 us, the stores alone
+//   310-350 us (a probe writing the same pattern with nothing else takes 335 us,
+//   against 230 us for each block writing one contiguous range and 192 us for a
+//   fill): the stores bound it. Measured and not kept: a column-blocked output
+//   layout ([5][rows][256], each block's stores contiguous: 384-405 us), three or
+//   more tiles in flight (the registers spill: 760 us).
+template <int I, int U, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < U) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, U>(f);
+    }
+}
+
+constexpr int kIoWaves = 4;
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 data format fields
+
+__global__ __launch_bounds__(64 * (kStreamWaves + kIoWaves))
+void linear_stream_io_kernel(LinearArgs p, int col_groups, int row_parts) {
+    constexpr int DEPTH = 2;  // x tiles in flight per IO lane (three spill)
+    using T = u16;
+    constexpr int kSteps = kStreamK / 16;
+    constexpr int kPitch = kStreamK + 8;      // x tile row pitch in bf16 (+16 bytes)
+    constexpr int kOPitch = kStreamCols + 4;  // output tile row pitch in floats (+16 bytes)
+    constexpr int kIoThr = 64 * kIoWaves;
+    constexpr int kRowsPerPass = kIoThr / (kStreamK / 4);             // x rows one IO instruction covers (4)
+    constexpr int kXLoads = kStreamRows / kRowsPerPass;               // float4 x loads per IO lane per tile (8)
+    constexpr int kOStores = kStreamRows * kStreamCols / 4 / kIoThr;  // float4 stores per IO lane per tile (8)
+    constexpr int U = 2;                                              // steps per unrolled loop trip
+    static_assert(U % DEPTH == 0, "a trip holds whole rotations of the register sets");
+    static_assert(kStreamRT == 1 && kStreamK / 4 == 64 && kStreamCols / 4 == 64, "one row per IO instruction");
+    __shared__ __attribute__((aligned(16))) T x_lds[2][kStreamRows * kPitch];
+    __shared__ __attribute__((aligned(16))) float o_lds[2][kStreamRows * kOPitch];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool io = wave >= kStreamWaves;
+    const int xcd = blockIdx.x % 8;
+    const int local = blockIdx.x / 8;
+    const int cg = local % col_groups;
+    const int rpl = local / col_groups;
+    const int rp = rpl * 8 + xcd;
+    if (rp >= row_parts) return;
+    // Step k of the block computes tile rp + k * row_parts.
+    const int64_t tiles = (p.rows + kStreamRows - 1) / kStreamRows;
+    const int64_t first = rp, tstride = row_parts;
+    const int count = static_cast<int>((tiles - rp + row_parts - 1) / row_parts);
+    if (count <= 0) return;
+    const int64_t n_block = static_cast<int64_t>(cg) * kStreamCols;
+
+    if (io) {
+        const int u = 64 * (wave - kStreamWaves) + lane;
+        const int ur = u / 64, uc = 4 * (u % 64);  // row within a pass, float column (x and output alike)
+        const int64_t col = n_block + uc;
+        const bool col_live = col < p.N;
+        f32x4 bias4 = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias != nullptr && col_live) bias4 = *reinterpret_cast<const f32x4*>(p.bias + col);
+        // Nothing in flight before the loop: a load still pending at its head would make the compiler
+        // wait for every store of the previous steps where the bias is first used in each step.
+        __builtin_amdgcn_s_waitcnt(0);
+        // x rows and result rows through buffer resources: a load past the range returns zeros (rows past
+        // the end, steps outside the block's) and a store past it is dropped, so no memory operation sits
+        // behind a branch and the compiler counts every wave's loads and stores exactly (they share one
+        // counter: a store behind a branch made the loads wait for the newest ones). Offsets: a per-lane
+        // constant plus a uniform part per step and instruction.
+        const int64_t live_cols = p.N - n_block < kStreamCols ? p.N - n_block : kStreamCols;
+        const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(p.x), 0, static_cast<int>(((p.rows - 1) * p.x_stride + kStreamK) * 4), kBufferWord3);
+        const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            p.out + n_block, 0, static_cast<int>(((p.rows - 1) * p.out_stride + live_cols) * 4), kBufferWord3);
+        const uint32_t x_lane = static_cast<uint32_t>((ur * p.x_stride + uc) * 4);
+        const uint32_t o_lane = static_cast<uint32_t>((ur * p.out_stride + uc) * 4);
+        const uint32_t x_pass = static_cast<uint32_t>(kRowsPerPass * p.x_stride * 4);  // between a lane's rows
+        const uint32_t o_pass = static_cast<uint32_t>(kRowsPerPass * p.out_stride * 4);
+        constexpr uint32_t kOut = 0x80000000u;  // past every range
+        f32x4 xs[DEPTH][kXLoads];
+        auto load = [&](auto set_c, int k) __attribute__((always_inline)) {
+            constexpr int S = decltype(set_c)::value;
+            const int64_t row = (first + k * tstride) * kStreamRows;
+            const uint32_t tile = k >= 0 && k < count ? static_cast<uint32_t>(row * p.x_stride * 4) : kOut;
+#pragma unroll
+            for (int q = 0; q < kXLoads; ++q)
+                xs[S][q] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, tile + x_lane + q * x_pass, 0, 0);
+        };
+        auto put = [&](auto set_c, T* buf) __attribute__((always_inline)) {
+            constexpr int S = decltype(set_c)::value;
+#pragma unroll
+            for (int q = 0; q < kXLoads; ++q) {
+                const f32x4 v = xs[S][q];
+                bf16x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = static_cast<__bf16>(v[j]);
+                *reinterpret_cast<bf16x4*>(buf + (ur + kRowsPerPass * q) * kPitch + uc) = o;
+            }
+        };
+        auto write_out = [&](int k, const float* buf) __attribute__((always_inline)) {
+            const int64_t row = (first + k * tstride) * kStreamRows;
+            const bool k_live = k >= 0 && k < count;
+            const uint32_t tile = static_cast<uint32_t>(row * p.out_stride * 4);
+            const int64_t rows_left = p.rows - row;  // rows of this tile that exist
+#pragma unroll
+            for (int i = 0; i < kOStores; ++i) {
+                const int rr = ur + kRowsPerPass * i;
+                f32x4 y = *reinterpret_cast<const f32x4*>(buf + rr * kOPitch + uc);
+                if (p.bias != nullptr) y += bias4;
+                const bool live = k_live & col_live & (rr < rows_left);
+                __builtin_amdgcn_raw_buffer_store_b128(y, out_rsrc, live ? tile + o_lane + i * o_pass : kOut, 0, 0);
+            }
+        };
+        // Step k's x tile lives in register set k % DEPTH. The loop starts DEPTH + 1 steps early (loads
+        // before the block's steps read past the range, stores before them are dropped, the LDS tiles
+        // they write are never read): the first real step then sees the same operations in flight as
+        // every later one, and the compiler's count at the loop head is the steady state's.
+        auto io_step = [&](auto i_c, int k) __attribute__((always_inline)) {
+            constexpr int I = decltype(i_c)::value;  // k + DEPTH + 1 = I (mod U)
+            constexpr int S = I % DEPTH;             // the set of step k + 1
+            constexpr int B = (I + DEPTH) & 1;       // the LDS buffers of steps k + 1 and k - 1
+            if (k + 1 < count) put(std::integral_constant<int, S>{}, x_lds[B]);
+            __builtin_amdgcn_sched_barrier(0);  // the set is free only after its LDS writes
+            load(std::integral_constant<int, S>{}, k + 1 + DEPTH);
+            __builtin_amdgcn_sched_barrier(0);
+            write_out(k - 1, o_lds[B]);
+            __syncthreads();
+        };
+        // Whole trips of U steps without a branch around their memory operations, then the rest.
+        int k0 = -DEPTH - 1;
+        for (; k0 + U <= count; k0 += U) static_for<0, U>([&](auto i_c) { io_step(i_c, k0 + decltype(i_c)::value); });
+        static_for<0, U>([&](auto i_c) {
+            if (k0 + decltype(i_c)::value < count) io_step(i_c, k0 + decltype(i_c)::value);
+        });
+        write_out(count - 1, o_lds[(count - 1) & 1]);
+        return;
+    }
+
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    const int64_t n_wave = n_block + 32 * wave;
+    const bool wave_live = n_wave < p.N;
+    uint4 wf[kSteps];
+    {
+        const T* w = static_cast<const T*>(p.w);
+        const int64_t n = n_wave + r32;
+        const T* wrow = w + (n < p.N ? n : p.N - 1) * kStreamK + 8 * h;
+        const uint32_t keep = n < p.N ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const uint4 v = *reinterpret_cast<const uint4*>(wrow + 16 * s);
+            wf[s] = uint4{v.x & keep, v.y & keep, v.z & keep, v.w & keep};
+        }
+    }
+    for (int k = 0; k <= DEPTH; ++k) __syncthreads();  // the IO waves' steps before the block's
+    auto step = [&](auto par_c) __attribute__((always_inline)) {
+        constexpr int PAR = decltype(par_c)::value;  // k % 2: the buffers of step k
+        if (wave_live) {
+            const T* buf = x_lds[PAR];
+            f32x16 acc;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+            uint4 xb[kSteps];
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) xb[s] = *reinterpret_cast<const uint4*>(buf + r32 * kPitch + 16 * s + 8 * h);
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wf[s]),
+                                                              __builtin_bit_cast(bf16x8, xb[s]), acc, 0, 0, 0);
+            float* ob = o_lds[PAR] + r32 * kOPitch + 32 * wave + 4 * h;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<f32x4*>(ob + 8 * j) = f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
+        }
+        __syncthreads();
+    };
+    for (int k = 0; k < count; k += 2) {
+        step(std::integral_constant<int, 0>{});
+        if (k + 1 < count) step(std::integral_constant<int, 1>{});
+    }
+}
+
 // Shapes too small to give the 128-row blocks one per CU (256 CUs), with K
 // held in at most eight 32-wide steps.
 bool small_shape(int64_t rows, int64_t K, int64_t N) {
@@ -997,9 +1194,22 @@ bool stream_form() {
     return !(v != nullptr && std::strcmp(v, "t32") == 0);
 }
 
-bool store_waves() {
+// MLK_LINEAR_STORE_WAVES selects the streaming form: unset (or "io") the IO-wave form where the output
+// allows it, "sw" the form with storing waves only, "0" the one without either.
+int store_waves() {
     const char* v = std::getenv("MLK_LINEAR_STORE_WAVES");
-    return !(v != nullptr && std::strcmp(v, "0") == 0);
+    if (v != nullptr && std::strcmp(v, "0") == 0) return 0;
+    if (v != nullptr && std::strcmp(v, "sw") == 0) return 1;
+    return 2;
+}
+
+// The IO-wave form: no residual, 16-byte aligned output rows and bias, N % 4 = 0, and x and the output
+// within the 2 GiB a buffer offset reaches.
+bool io_form_fits(const LinearArgs& p, int64_t rows) {
+    auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const int64_t span = (rows + kStreamRows) * (p.out_stride > p.x_stride ? p.out_stride : p.x_stride) * 4;
+    return p.residual == nullptr && p.N % 4 == 0 && a16(p.out) && p.out_stride % 4 == 0 &&
+           (p.bias == nullptr || a16(p.bias)) && span < (int64_t{1} << 31);
 }
 
 template <bool BF16W, bool VEC>
@@ -1032,7 +1242,11 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
             if (parts_per_xcd >= 1) {
                 const int row_parts = 8 * parts_per_xcd;
                 const dim3 grid(static_cast<unsigned>(8 * parts_per_xcd * col_groups));
-                if (store_waves()) {
+                const int form = store_waves();
+                if (form == 2 && io_form_fits(p, rows)) {
+                    hipLaunchKernelGGL(linear_stream_io_kernel, grid, dim3(64 * (kStreamWaves + kIoWaves)), 0, stream, p,
+                                       col_groups, row_parts);
+                } else if (form >= 1) {
                     hipLaunchKernelGGL(linear_stream_sw_kernel, grid, dim3(64 * (kStreamWaves + kStoreWaves)), 0,
                                        stream, p, col_groups, row_parts);
                 } else {

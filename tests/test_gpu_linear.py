@@ -289,12 +289,16 @@ def test_streaming_form_k512(dev, oracle, M, N, bias, strided, monkeypatch):
 
 
 @pytest.mark.parametrize("M,N,bias,strided", [(9000, 1192, True, False), (70000, 1192, False, True), (31, 768, True, False),
-                                              (4096, 2000, False, False)])
+                                              (4096, 2000, False, False), (50001, 1196, True, True),
+                                              (20000, 1194, False, False), (1500, 1192, False, True)])
 def test_streaming_form_equals_t32_form(dev, oracle, M, N, bias, strided, monkeypatch):
-    """bf16 weights, K = 256, 12 or more 64-column chunks: the streaming form (weights in registers, x
-    tiles through LDS; by default with separate storing waves, MLK_LINEAR_STORE_WAVES=0 without) gives
-    linear_t32_kernel's result bit for bit (MLK_LINEAR_FORM=t32 selects that form), also with the residual
-    epilogue, and all match the product of bf16-rounded inputs."""
+    """bf16 weights, K = 256, 12 or more 64-column chunks: the streaming forms (weights in registers, x
+    tiles through LDS; by default the form with IO waves where the output allows it (no residual,
+    N % 4 = 0; N = 1194 and the residual calls take the next form), MLK_LINEAR_STORE_WAVES=sw the form
+    with storing waves, =0 the one with neither) give linear_t32_kernel's result bit for bit
+    (MLK_LINEAR_FORM=t32 selects that form), also with the residual epilogue, at row counts that leave
+    blocks without a tile (31, 1500 rows) or a ragged last tile, and all match the product of bf16-rounded
+    inputs."""
     from montlok import _C
 
     rng = np.random.default_rng(M + N)
@@ -310,13 +314,16 @@ def test_streaming_form_equals_t32_form(dev, oracle, M, N, bias, strided, monkey
         return _C.linear(*args), _C.linear_residual(*args, res)
 
     streaming = both()
+    monkeypatch.setenv("MLK_LINEAR_STORE_WAVES", "sw")
+    store_waves = both()
     monkeypatch.setenv("MLK_LINEAR_STORE_WAVES", "0")
     in_wave = both()
     monkeypatch.setenv("MLK_LINEAR_FORM", "t32")
     t32 = both()
     monkeypatch.delenv("MLK_LINEAR_FORM")
     monkeypatch.delenv("MLK_LINEAR_STORE_WAVES")
-    for name, a, c in (("streaming", streaming, t32), ("streaming, stores on the computing waves", in_wave, t32)):
+    for name, a, c in (("streaming", streaming, t32), ("streaming, storing waves", store_waves, t32),
+                       ("streaming, stores on the computing waves", in_wave, t32)):
         assert torch.equal(a[0], c[0]), f"{name} vs linear_t32_kernel"
         assert torch.equal(a[1], c[1]), f"{name} with residual vs linear_t32_kernel"
     assert torch.equal(streaming[1], res + streaming[0]), "residual epilogue vs the two steps"
