@@ -686,8 +686,13 @@ constexpr int kStreamCols = 32 * kStreamWaves;  // columns per block
 constexpr int kStreamRT = 1;                    // 32-row tiles per step
 constexpr int kStreamRows = 32 * kStreamRT;     // rows per step
 constexpr int kStreamK = 256;                   // the form takes K = 256 exactly (16-byte aligned operands)
+constexpr int kBufferWord3 = 0x00020000;        // raw buffer resource, gfx9 data format fields
 
-template <int K>
+// BUF: no bias or residual, N % 4 = 0, 16-byte aligned output within 2 GiB: the results go out through a
+// buffer resource, a store past its range dropped, so no store sits behind a branch. With the edge tests'
+// branches the compiler cannot count the stores, and its wait for the next tile's x loads (issued before
+// them on the shared load/store counter) waited for every store of the tile.
+template <int K, bool BUF = false>
 __global__ __launch_bounds__(64 * kStreamWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
     using T = u16;
@@ -767,12 +772,12 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
         const bool more = t + 1 < t_end;
         if (more) load_tile(t + 1);
         const T* buf = x_lds[PAR];
+        f32x16 acc[kStreamRT];
+#pragma unroll
+        for (int m = 0; m < kStreamRT; ++m)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[m][v] = 0.0f;
         if (wave_live) {
-            f32x16 acc[kStreamRT];
-#pragma unroll
-            for (int m = 0; m < kStreamRT; ++m)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[m][v] = 0.0f;
 #pragma unroll
             for (int part = 0; part < kXParts; ++part) {
                 constexpr int kPS = kSteps / kXParts;
@@ -792,6 +797,7 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
                     }
                 }
             }
+            if constexpr (!BUF) {
 #pragma unroll
             for (int m = 0; m < kStreamRT; ++m) {
                 const int64_t row = t * kStreamRows + 32 * m + r32;
@@ -816,6 +822,23 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
                             }
                         }
                     }
+                }
+            }
+            }
+        }
+        if constexpr (BUF) {  // every wave, outside any branch (a wave past N stores nothing)
+            const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+                p.out, 0, static_cast<int>(((p.rows - 1) * p.out_stride + p.N) * 4), kBufferWord3);
+#pragma unroll
+            for (int m = 0; m < kStreamRT; ++m) {
+                const int64_t row = t * kStreamRows + 32 * m + r32;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t col = n_wave + 8 * j + 4 * h;
+                    const f32x4 y = {acc[m][4 * j], acc[m][4 * j + 1], acc[m][4 * j + 2], acc[m][4 * j + 3]};
+                    const bool live = row < p.rows && col < p.N;
+                    const uint32_t off = live ? static_cast<uint32_t>((row * p.out_stride + col) * 4) : 0x80000000u;
+                    __builtin_amdgcn_raw_buffer_store_b128(y, out_rsrc, off, 0, 0);
                 }
             }
         }
@@ -1017,7 +1040,6 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 constexpr int kIoWaves = 4;
-constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 data format fields
 
 __global__ __launch_bounds__(64 * (kStreamWaves + kIoWaves))
 void linear_stream_io_kernel(LinearArgs p, int col_groups, int row_parts) {
@@ -1205,6 +1227,13 @@ int store_waves() {
 
 // The IO-wave form: no residual, 16-byte aligned output rows and bias, N % 4 = 0, and x and the output
 // within the 2 GiB a buffer offset reaches.
+// linear_stream_kernel's buffer-store epilogue: no bias or residual, N % 4 = 0, 16-byte aligned output
+// rows within 2 GiB.
+bool buf_out_fits(const LinearArgs& p, int64_t rows) {
+    return p.residual == nullptr && p.bias == nullptr && p.N % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 &&
+           p.out_stride % 4 == 0 && (rows + 1) * p.out_stride * 4 < (int64_t{1} << 31);
+}
+
 bool io_form_fits(const LinearArgs& p, int64_t rows) {
     auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
     const int64_t span = (rows + kStreamRows) * (p.out_stride > p.x_stride ? p.out_stride : p.x_stride) * 4;
@@ -1264,8 +1293,14 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
             const int parts_per_xcd = 32 / col_groups;
             if (parts_per_xcd >= 1) {
                 const int row_parts = 8 * parts_per_xcd;
-                hipLaunchKernelGGL(linear_stream_kernel<512>, dim3(static_cast<unsigned>(8 * parts_per_xcd * col_groups)),
-                                   dim3(64 * kStreamWaves), 0, stream, p, col_groups, row_parts);
+                const dim3 grid(static_cast<unsigned>(8 * parts_per_xcd * col_groups));
+                if (buf_out_fits(p, rows)) {
+                    hipLaunchKernelGGL((linear_stream_kernel<512, true>), grid, dim3(64 * kStreamWaves), 0, stream, p,
+                                       col_groups, row_parts);
+                } else {
+                    hipLaunchKernelGGL((linear_stream_kernel<512, false>), grid, dim3(64 * kStreamWaves), 0, stream, p,
+                                       col_groups, row_parts);
+                }
                 return;
             }
         }
