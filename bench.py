@@ -1117,9 +1117,10 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
 NORMS = dict(rows=262144, dim=256)
 
 
-def cpu_baseline_norms(cfg: dict, budget_s: float = 12.0, rows: int = 16384) -> dict:
-    """The reference's own norm kernels (oracle/_ref) on a slice of the rows (the oracle port where that
-    library is absent)."""
+def cpu_baseline_norms(cfg: dict, budget_s: float = 12.0, rows: int = 65536) -> dict:
+    """The reference's own norm kernels (oracle/_ref) on a quarter of the rows (the oracle port where that
+    library is absent): its five 64 MB operands and results exceed the host's last-level cache, as the
+    workload's exceed the GPU's, where a 16384-row slice would time the CPU from cache."""
     import numpy as np
 
     from oracle import Oracle, Reference, reference_available
@@ -1144,7 +1145,7 @@ def cpu_baseline_norms(cfg: dict, budget_s: float = 12.0, rows: int = 16384) -> 
         return step
 
     return _cpu_legs(make_step, rows, "rows/s", "reference" if ref else "port",
-                     f"rms_norm + add_rms_norm + layer_norm over {rows} of the {cfg['rows']} rows in the "
+                     f"rms_norm + add_rms_norm + layer_norm over {rows} of the {cfg['rows']} rows (x {cfg['dim']}) in the "
                      f"{'reference ' + lib.variant if ref else 'oracle'} build", budget_s)
 
 
