@@ -879,7 +879,9 @@ def bench_decode(steps: int, warmup: int, cpu: bool) -> dict:
                                   bytes=(S * d_inner + d * d_inner + 2 * S * d) * f, flops=2 * S * d_inner * d,
                                   precision="f32"),
     }
-    table = _kernel_table(ops, _op_times(ops, max(4, steps // 4), reps=2), "f32")
+    # Six launches per graph: with two, each replay's start-up cost (about 0.2 ms at these sizes) lands on
+    # the per-launch time.
+    table = _kernel_table(ops, _op_times(ops, max(4, steps // 4), reps=6), "f32")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
     total_bytes = cfg["layers"] * (2 * state_bytes + (W * d + d * d_inner) * f) + S * d * f + S * f
     line = _base_line(S / (ms * 1e-3), "stream-steps/s", steps, warmup, ms, "f32 (fp64 rotary phase)",
@@ -1081,7 +1083,9 @@ def bench_stack(steps: int, warmup: int, cpu: bool) -> dict:
                                 4 * B * m1.n_heads * (L * (L + 1) // 2) * m1.head_dim + 2 * T * d * d,
                                 precision="bf16"),
         }
-        table = _kernel_table(ops, _op_times(ops, 4, reps=2), "bf16")
+        # Eight launches per graph: with two, each replay's start-up cost (about 0.2 ms at these sizes)
+        # lands on the per-launch time (combine + prepare: 673 against 562 us).
+        table = _kernel_table(ops, _op_times(ops, 4, reps=8), "bf16")
     dom = max(table, key=lambda k: table[k]["launch_ms"])
     flops = sum(ops[k]["flops"] for k in ("feature_proj",)) + 2 * (ops["mamba_in_proj"]["flops"] +
                                                                    ops["mamba3_siso_forward"]["flops"] +
