@@ -62,6 +62,33 @@ def test_rms_norm_vs_oracle(dev, oracle, rows, dim, groups):
     assert bit_mismatches(out, expect) <= max(1, x.size // 10000)
 
 
+@pytest.mark.parametrize("rows,dim,groups", [(262147, 256, 1), (65541, 64, 1), (140003, 64, 8), (20001, 1024, 1)])
+def test_norms_four_rows_per_lane_group(dev, oracle, rows, dim, groups):
+    """Launches of 4096 blocks or more give each lane group four rows (every row's loads issued before
+    the first reduction): rms_norm and add_rms_norm at the stack's 262,144 x 256 (plus a ragged tail of
+    rows), grouped, and wide rows, against the oracle; the residual of add_rms_norm bit for bit (one fp32
+    add), the normalised rows as the single-row kernels are (fp64 sums, one rounding)."""
+    from montlok import _C
+
+    rng = np.random.default_rng(rows + dim + groups)
+    x = (rng.standard_normal((rows, dim)) * 3).astype(np.float32)
+    r = rng.standard_normal((rows, dim)).astype(np.float32)
+    w = (rng.random(dim) + 0.5).astype(np.float32)
+    tx, tw = _t(x, dev), _t(w, dev)
+    out = _C.rms_norm(tx, tw, 1e-5, groups)
+    expect = oracle.rms_norm(x, w, 1e-5, groups)
+    assert_close(out, expect, name="rms_norm")
+    assert bit_mismatches(out, expect) <= max(1, x.size // 10000)
+    res, nrm = _C.add_rms_norm(tx, _t(r, dev), tw, 1e-5, groups)
+    e_res, e_nrm = oracle.add_rms_norm(x, r, w, 1e-5, groups)
+    assert bit_mismatches(res, e_res) == 0, "residual"
+    assert_close(nrm, e_nrm, name="add_rms_norm")
+    assert bit_mismatches(nrm, e_nrm) <= max(1, x.size // 10000)
+    if groups == 1 and dim <= 256:
+        b = rng.standard_normal(dim).astype(np.float32)
+        assert_close(_C.layer_norm(tx, tw, _t(b, dev), 1e-5), oracle.layer_norm(x, w, b, 1e-5), name="layer_norm")
+
+
 def test_rms_norm_strided_rows(dev, oracle):
     from montlok import _C
 

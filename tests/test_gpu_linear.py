@@ -260,6 +260,28 @@ def test_rms_norm_linear_beyond_the_fused_form(dev):
         assert torch.equal(fused, _C.linear(_C.rms_norm(x, nw, 1e-5, groups), w))
 
 
+def test_streaming_forms_full_size(dev, monkeypatch):
+    """The stack's Mamba in_proj at its full size, 262144 x 256 -> 1192 (bf16 weights): the IO-wave form,
+    the storing-wave form, the plain streaming form and linear_t32_kernel give the same bits (a property
+    that holds at any size; the oracle comparisons above run at sizes the CPU finishes quickly)."""
+    from montlok import _C
+
+    g = torch.Generator().manual_seed(1192)
+    x = torch.randn(262144, 256, generator=g).to(dev)
+    w = (torch.randn(1192, 256, generator=g) * 0.02).to(dev).bfloat16()
+    outs = {}
+    for form, env in (("io", {}), ("sw", {"MLK_LINEAR_STORE_WAVES": "sw"}), ("plain", {"MLK_LINEAR_STORE_WAVES": "0"}),
+                      ("t32", {"MLK_LINEAR_FORM": "t32"})):
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        outs[form] = _C.linear(x, w)
+        for k in env:
+            monkeypatch.delenv(k)
+    assert torch.isfinite(outs["io"]).all().item()
+    for form in ("sw", "plain", "t32"):
+        assert torch.equal(outs["io"], outs[form]), f"IO-wave form vs {form}"
+
+
 @pytest.mark.parametrize("M,N,bias,strided", [(40000, 256, False, False), (33000, 192, True, True), (35000, 320, True, False)])
 def test_streaming_form_k512(dev, oracle, M, N, bias, strided, monkeypatch):
     """bf16 weights, K = 512, 128 or more output columns, 32768 or more rows: the streaming form with the W
