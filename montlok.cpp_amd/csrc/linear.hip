@@ -494,6 +494,13 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
             bias[v] = p.bias[col < p.N ? col : p.N - 1];
         }
     }
+    // The 16-byte epilogue's residual values are fetched with the operands (this lane's row, clamped), so
+    // their latency passes behind the products instead of after them.
+    const bool vec_out = (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 && n0 + 16 <= p.N &&
+                         (p.residual == nullptr ||
+                          ((reinterpret_cast<uintptr_t>(p.residual) & 15) == 0 && p.res_stride % 4 == 0));
+    f32x4 resv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (vec_out && p.residual != nullptr) resv = *reinterpret_cast<const f32x4*>(p.residual + xr * p.res_stride + n0 + 4 * group);
     f32x4 y;
     if constexpr (BF16W) {
         const u16* wrow = static_cast<const u16*>(p.w) + wr * p.K;
@@ -524,9 +531,8 @@ __global__ __launch_bounds__(64) void linear_small_kernel(LinearArgs p) {
     if (row < p.rows) {
         float* dst = p.out + row * p.out_stride + n0 + 4 * group;
         const float* res = p.residual != nullptr ? p.residual + row * p.res_stride + n0 + 4 * group : nullptr;
-        if ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && p.out_stride % 4 == 0 && n0 + 16 <= p.N &&
-            (res == nullptr || ((reinterpret_cast<uintptr_t>(p.residual) & 15) == 0 && p.res_stride % 4 == 0))) {
-            if (res != nullptr) y = *reinterpret_cast<const f32x4*>(res) + y;
+        if (vec_out) {
+            if (res != nullptr) y = resv + y;
             *reinterpret_cast<f32x4*>(dst) = y;
         } else {
 #pragma unroll
