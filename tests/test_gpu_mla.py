@@ -268,7 +268,8 @@ def test_latent_layernorm_once_per_row(dev, B, L, H, hd, nope):
 
 @pytest.mark.parametrize("B,L,bias,strided", [(16, 128, True, False),   # MLA block geometry
                                               (3, 37, True, False), (2, 1, False, False), (5, 64, False, True),
-                                              (1, 127, True, True), (64, 128, True, False), (9, 100, False, False)])
+                                              (1, 127, True, True), (64, 128, True, False), (9, 100, False, False),
+                                              (256, 128, True, False)])  # the MLA workload's full 256 windows
 def test_window_kernel_equals_separate_path(dev, B, L, bias, strided):
     """With bf16 weights, 8 heads of 32 and L <= 128 the whole mla_forward is one launch, one block per
     window: the result equals the four-launch path (linear, latent LayerNorm into bf16, fused attention,
@@ -299,7 +300,8 @@ def test_window_kernel_equals_separate_path(dev, B, L, bias, strided):
 @pytest.mark.parametrize("B,L,bias,strided", [(8, 256, True, False),   # full-stack MLA geometry
                                               (3, 77, True, False), (2, 1, False, False), (5, 64, False, True),
                                               (1, 255, True, True), (16, 200, True, False), (9, 130, False, False),
-                                              (4, 65, True, False)])
+                                              (4, 65, True, False),
+                                              (1024, 256, True, False)])  # the stack's full 1024 windows
 def test_span_kernel_equals_separate_path(dev, B, L, bias, strided):
     """With bf16 weights, 4 heads of 64 (rope 32) and L <= 256 the whole mla_forward is one launch, one
     block per (window, 64 query rows) walking the key rows up to them: the result equals the four-launch
