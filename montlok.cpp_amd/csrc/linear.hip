@@ -46,6 +46,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // the buffer builtins' 16-byte data type
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16;
@@ -53,6 +54,7 @@ typedef unsigned short u16;
 constexpr int kThreads = 512;                  // 8 waves
 constexpr int kRowsPerBlock = 16 * (kThreads / 64);
 constexpr int kColsPerChunk = 64;
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 data format fields
 
 // Weight element type, K chunk staged per step, LDS row pitch (+16 bytes so
 // consecutive rows start on different banks).
@@ -160,6 +162,9 @@ struct WStage {
     static constexpr int kUnits = (kColsPerChunk * kUnitsPerRow) / kThreads;
     uint4 reg[kUnits];
 
+    // FULL: the chunk lies wholly inside K (K a multiple of the chunk, aligned rows), so every unit is one
+    // 16-byte load with no branch around it.
+    template <bool FULL = false>
     __device__ __forceinline__ void fetch(const LinearArgs& p, int64_t n0, int64_t k0, int kspan) {
         const T* w = static_cast<const T*>(p.w);
 #pragma unroll
@@ -169,6 +174,10 @@ struct WStage {
             const int c = (unit % kUnitsPerRow) * kPer;
             const int64_t n = n0 + r;
             const int64_t k = k0 + c;
+            if constexpr (FULL) {
+                reg[u] = *reinterpret_cast<const uint4*>(w + (n < p.N ? n : p.N - 1) * p.K + k);
+                continue;
+            }
             if (c >= kspan) continue;
             if (VEC && k + kPer <= p.K) {
                 reg[u] = *reinterpret_cast<const uint4*>(w + (n < p.N ? n : p.N - 1) * p.K + k);
@@ -203,8 +212,12 @@ struct WStage {
 // (groups of GS floats) applied to the loaded fragments first, the arithmetic
 // of rms_norm_vec_kernel (tile_rms_norm), so the result equals rms_norm then
 // this kernel bit for bit.
-template <bool BF16W, bool VEC, bool MULTIK, int GS = 0>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void linear_kernel(LinearArgs p) {
+// BUF (no residual, output within 2 GiB): the results go out through a buffer resource, a store past its
+// range dropped, so no store sits behind a branch: with the edge tests' branches the compiler cannot count
+// the stores, and its wait for the next chunk's W loads (issued before them on the shared load/store
+// counter) waited for every store of the chunk.
+template <bool BF16W, bool VEC, bool MULTIK, int GS = 0, bool BUF = false>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BUF ? 3 : 4, BUF ? 3 : 4))) void linear_kernel(LinearArgs p) {
     using T = typename WTraits<BF16W>::T;
     constexpr int KC = WTraits<BF16W>::kKChunk;
     constexpr int kSteps = KC / 32;
@@ -228,11 +241,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
         const int64_t span = ((rem < KC ? rem : KC) + 31) / 32 * 32;
         return static_cast<int>(span);
     };
-    auto n0_of = [&](int64_t it) { return (blockIdx.y + (it / k_chunks) * gridDim.y) * kColsPerChunk; };
+    // One K chunk (!MULTIK): iteration = column chunk, no 64-bit division per iteration.
+    auto n0_of = [&](int64_t it) { return (blockIdx.y + (MULTIK ? it / k_chunks : it) * gridDim.y) * kColsPerChunk; };
 
     WStage<BF16W, VEC> stage;
     AFrag<BF16W> a_cur;  // reloaded per iteration when K spans several chunks
-    stage.fetch(p, n0_of(0), 0, kspan_of(0));
+    stage.template fetch<(GS > 0)>(p, n0_of(0), 0, kspan_of(0));
     load_a<BF16W, VEC>(p, my_row, 0, group, kspan_of(0) / 32, a_cur);
     if constexpr (GS > 0) {
         static_assert(!BF16W && !MULTIK, "the RMSNorm prologue needs all of K in fp32 fragments");
@@ -246,15 +260,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
 
     f32x4 acc[4];
     for (int64_t it = 0; it < iters; ++it) {
-        const int64_t kc = it % k_chunks;
+        const int64_t kc = MULTIK ? it % k_chunks : 0;
         const int64_t n0 = n0_of(it);
         const int steps = kspan_of(kc) / 32;
         const bool more = it + 1 < iters;
-        const int64_t kc_next = (it + 1) % k_chunks;
+        const int64_t kc_next = MULTIK ? (it + 1) % k_chunks : 0;
         if constexpr (MULTIK) {
             if (it > 0) load_a<BF16W, VEC>(p, my_row, kc * KC, group, steps, a_cur);
         }
-        if (more) stage.fetch(p, n0_of(it + 1), kc_next * KC, kspan_of(kc_next));
+        // The bias before the next chunk's W: waiting for it then leaves the W loads in flight (loads and
+        // stores retire in order on one counter).
         float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // fetched with the chunk, used after its MFMAs
         if (p.bias != nullptr) {
 #pragma unroll
@@ -263,6 +278,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
                 bias[t] = p.bias[col < p.N ? col : p.N - 1];
             }
         }
+        // (FULL: fetched past the last chunk too, clamped rows that are never stored, so that no branch
+        // separates these loads from the counter's view of the stores below.)
+        if ((GS > 0) || more) stage.template fetch<(GS > 0)>(p, n0_of(it + 1), kc_next * KC, kspan_of(kc_next));
         if (kc == 0) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -289,7 +307,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
                 }
             }
         }
-        if (kc == k_chunks - 1) {
+        if constexpr (BUF) {
+            static_assert(!MULTIK, "one K chunk: every iteration ends with its stores");
+            const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+                p.out, 0, static_cast<int>(((p.rows - 1) * p.out_stride + p.N) * 4), kBufferWord3);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int64_t col = n0 + 16 * t + li;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int64_t row = row0 + 4 * group + v;
+                    const float y = acc[t][v] + bias[t];
+                    const bool live = col < p.N && row < p.rows;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), out_rsrc,
+                                                          live ? static_cast<uint32_t>((row * p.out_stride + col) * 4)
+                                                               : 0x80000000u, 0, 0);
+                }
+            }
+        } else if (kc == k_chunks - 1) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int64_t col = n0 + 16 * t + li;
@@ -692,7 +727,6 @@ constexpr int kStreamCols = 32 * kStreamWaves;  // columns per block
 constexpr int kStreamRT = 1;                    // 32-row tiles per step
 constexpr int kStreamRows = 32 * kStreamRT;     // rows per step
 constexpr int kStreamK = 256;                   // the form takes K = 256 exactly (16-byte aligned operands)
-constexpr int kBufferWord3 = 0x00020000;        // raw buffer resource, gfx9 data format fields
 
 // BUF: no bias or residual, N % 4 = 0, 16-byte aligned output within 2 GiB: the results go out through a
 // buffer resource, a store past its range dropped, so no store sits behind a branch. With the edge tests'
@@ -844,7 +878,7 @@ void linear_stream_kernel(LinearArgs p, int col_groups, int row_parts) {
                     const f32x4 y = {acc[m][4 * j], acc[m][4 * j + 1], acc[m][4 * j + 2], acc[m][4 * j + 3]};
                     const bool live = row < p.rows && col < p.N;
                     const uint32_t off = live ? static_cast<uint32_t>((row * p.out_stride + col) * 4) : 0x80000000u;
-                    __builtin_amdgcn_raw_buffer_store_b128(y, out_rsrc, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), out_rsrc, off, 0, 0);
                 }
             }
         }
@@ -1112,7 +1146,7 @@ void linear_stream_io_kernel(LinearArgs p, int col_groups, int row_parts) {
             const uint32_t tile = k >= 0 && k < count ? static_cast<uint32_t>(row * p.x_stride * 4) : kOut;
 #pragma unroll
             for (int q = 0; q < kXLoads; ++q)
-                xs[S][q] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, tile + x_lane + q * x_pass, 0, 0);
+                xs[S][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, tile + x_lane + q * x_pass, 0, 0));
         };
         auto put = [&](auto set_c, T* buf) __attribute__((always_inline)) {
             constexpr int S = decltype(set_c)::value;
@@ -1136,7 +1170,7 @@ void linear_stream_io_kernel(LinearArgs p, int col_groups, int row_parts) {
                 f32x4 y = *reinterpret_cast<const f32x4*>(buf + rr * kOPitch + uc);
                 if (p.bias != nullptr) y += bias4;
                 const bool live = k_live & col_live & (rr < rows_left);
-                __builtin_amdgcn_raw_buffer_store_b128(y, out_rsrc, live ? tile + o_lane + i * o_pass : kOut, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), out_rsrc, live ? tile + o_lane + i * o_pass : kOut, 0, 0);
             }
         };
         // Step k's x tile lives in register set k % DEPTH. The loop starts DEPTH + 1 steps early (loads
@@ -1430,7 +1464,15 @@ extern "C" mlk_status mlk_rms_norm_linear(const float* x, int64_t rows, int64_t 
         int64_t gy = 1;
         while (gy < n_chunks && row_blocks * gy < 512) ++gy;
         const dim3 grid(static_cast<unsigned>(row_blocks), static_cast<unsigned>(gy));
-#define MLK_ROWS_GS(G) hipLaunchKernelGGL((linear_kernel<false, true, false, G>), grid, dim3(kThreads), 0, s, p)
+        const bool buf = (rows + 1) * out_stride * 4 < (int64_t{1} << 31);
+#define MLK_ROWS_GS(G)                                                                                              \
+    do {                                                                                                            \
+        if (buf) {                                                                                                  \
+            hipLaunchKernelGGL((linear_kernel<false, true, false, G, true>), grid, dim3(kThreads), 0, s, p);        \
+        } else {                                                                                                    \
+            hipLaunchKernelGGL((linear_kernel<false, true, false, G>), grid, dim3(kThreads), 0, s, p);              \
+        }                                                                                                           \
+    } while (0)
         switch (gs) {
             case 8: MLK_ROWS_GS(8); break;
             case 16: MLK_ROWS_GS(16); break;
