@@ -162,8 +162,8 @@ struct WStage {
     static constexpr int kUnits = (kColsPerChunk * kUnitsPerRow) / kThreads;
     uint4 reg[kUnits];
 
-    // FULL: the chunk lies wholly inside K (K a multiple of the chunk, aligned rows), so every unit is one
-    // 16-byte load with no branch around it.
+    // FULL (VEC, K a multiple of kPer): every unit is one 16-byte load with no branch around it (units past K
+    // or past the chunk's span read a clamped address and are zeroed).
     template <bool FULL = false>
     __device__ __forceinline__ void fetch(const LinearArgs& p, int64_t n0, int64_t k0, int kspan) {
         const T* w = static_cast<const T*>(p.w);
@@ -175,7 +175,10 @@ struct WStage {
             const int64_t n = n0 + r;
             const int64_t k = k0 + c;
             if constexpr (FULL) {
-                reg[u] = *reinterpret_cast<const uint4*>(w + (n < p.N ? n : p.N - 1) * p.K + k);
+                // Every unit one 16-byte load from a clamped address, zeroed past K (K a multiple of kPer).
+                const bool live = c < kspan && k < p.K;
+                const uint4 v = *reinterpret_cast<const uint4*>(w + (n < p.N ? n : p.N - 1) * p.K + (live ? k : 0));
+                reg[u] = live ? v : uint4{0u, 0u, 0u, 0u};
                 continue;
             }
             if (c >= kspan) continue;
@@ -355,7 +358,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BUF ? 
 // the accumulator of lane (g, l) holds row l, columns 4g .. 4g + 3 of a tile
 // and leaves as one 16-byte store (scalar stores at a ragged N edge or an
 // unaligned output).
-template <bool BF16W, bool VEC, int RT, int KS>
+// BUF > 0 (VEC, K a multiple of the 16-byte unit, N % 4 = 0, 16-byte aligned output and residual within
+// 2 GiB): W fetched without per-unit branches (also past the last chunk, clamped) and the results stored
+// through a buffer resource (a store past its range dropped), so no memory operation sits behind a branch
+// and no wait covers the stores or the next W chunk. BUF = 1: no residual; BUF = 2: the residual fetched
+// with the chunk's bias, before its W.
+template <bool BF16W, bool VEC, int RT, int KS, int BUF = 0>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RT * KS > 1 ? 2 : 4, RT * KS > 1 ? 2 : 4)))
 void linear_tiles_kernel(LinearArgs p) {
     using T = typename WTraits<BF16W>::T;
@@ -386,7 +394,7 @@ void linear_tiles_kernel(LinearArgs p) {
 
     WStage<BF16W, VEC> stage;
     AFrag<BF16W> a[RT][KS];
-    stage.fetch(p, n0_of(0), 0, kspan_of(0));
+    stage.template fetch<(BUF > 0)>(p, n0_of(0), 0, kspan_of(0));
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -408,6 +416,19 @@ void linear_tiles_kernel(LinearArgs p) {
                 bias[t][v] = p.bias != nullptr ? p.bias[col < p.N ? col : p.N - 1] : 0.0f;
             }
         }
+        f32x4 resv[BUF == 2 ? RT : 1][4];  // BUF = 2: the residual of this chunk's outputs (clamped rows, columns)
+        if constexpr (BUF == 2) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int64_t row = row0 + 16 * rt + li;
+                const float* rrow = p.residual + (row < p.rows ? row : p.rows - 1) * p.res_stride;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int64_t col = n0 + 16 * t + 4 * group;
+                    resv[rt][t] = *reinterpret_cast<const f32x4*>(rrow + (col < p.N ? col : p.N - 4));
+                }
+            }
+        }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -417,7 +438,7 @@ void linear_tiles_kernel(LinearArgs p) {
             const int64_t it = c * KS + kc;
             const bool more = it + 1 < iters;
             const int kc_next = (kc + 1) % KS;
-            if (more) stage.fetch(p, n0_of(it + 1), static_cast<int64_t>(kc_next) * KC, kspan_of(kc_next));
+            if (BUF > 0 || more) stage.template fetch<(BUF > 0)>(p, n0_of(it + 1), static_cast<int64_t>(kc_next) * KC, kspan_of(kc_next));
             const int steps = kspan_of(kc) / 32;
             const T* buf = w_lds[it & 1];
 #pragma unroll
@@ -444,7 +465,24 @@ void linear_tiles_kernel(LinearArgs p) {
                     }
                 }
             }
-            if (kc == KS - 1) {
+            if (BUF > 0 && kc == KS - 1) {
+                const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+                    p.out, 0, static_cast<int>(((p.rows - 1) * p.out_stride + p.N) * 4), kBufferWord3);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const int64_t row = row0 + 16 * rt + li;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int64_t col = n0 + 16 * t + 4 * group;
+                        f32x4 y = acc[rt][t] + bias[t];
+                        if constexpr (BUF == 2) y = resv[rt][BUF == 2 ? t : 0] + y;
+                        const bool live = row < p.rows && col < p.N;
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            __builtin_bit_cast(u32x4, y), out_rsrc,
+                            live ? static_cast<uint32_t>((row * p.out_stride + col) * 4) : 0x80000000u, 0, 0);
+                    }
+                }
+            } else if (kc == KS - 1) {
                 const bool full = vec_out && n0 + kColsPerChunk <= p.N;
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
@@ -1244,6 +1282,15 @@ void linear_stream_io_kernel(LinearArgs p, int col_groups, int row_parts) {
 
 // Shapes too small to give the 128-row blocks one per CU (256 CUs), with K
 // held in at most eight 32-wide steps.
+// linear_tiles_kernel's BUF form: K a multiple of the 16-byte unit (kper elements), N % 4 = 0, 16-byte
+// aligned output (and residual) rows, the output within 2 GiB.
+bool tiles_buf_fits(const LinearArgs& p, int64_t rows, int kper) {
+    auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    return p.K % kper == 0 && p.N % 4 == 0 && a16(p.out) && p.out_stride % 4 == 0 &&
+           (p.residual == nullptr || (a16(p.residual) && p.res_stride % 4 == 0)) &&
+           (rows + 1) * p.out_stride * 4 < (int64_t{1} << 31);
+}
+
 bool small_shape(int64_t rows, int64_t K, int64_t N) {
     return K % 8 == 0 && K <= 256 && ceil_div(rows, kRowsPerBlock) * ceil_div(N, kColsPerChunk) < 256 &&
            ceil_div(rows, 16) * ceil_div(N, 16) <= 0x7fffffff;
@@ -1368,9 +1415,20 @@ void launch(const LinearArgs& p, int64_t rows, int64_t n_chunks, hipStream_t str
     if (p.K <= KC && !BF16W) {
         hipLaunchKernelGGL((linear_kernel<BF16W, VEC, false>), grid, dim3(kThreads), 0, stream, p);
     } else if (p.K <= KC) {
-        hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 1>), grid, dim3(kThreads), 0, stream, p);
+        // (KS = 1 keeps four waves per SIMD: the residual's registers would spill, so it takes BUF = 1 only)
+        if (VEC && p.residual == nullptr && tiles_buf_fits(p, rows, 16 / static_cast<int>(sizeof(typename WTraits<BF16W>::T)))) {
+            hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 1, VEC ? 1 : 0>), grid, dim3(kThreads), 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 1>), grid, dim3(kThreads), 0, stream, p);
+        }
     } else if (p.K <= 2 * KC) {
-        hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 2>), grid, dim3(kThreads), 0, stream, p);
+        if (VEC && p.residual == nullptr && tiles_buf_fits(p, rows, 16 / static_cast<int>(sizeof(typename WTraits<BF16W>::T)))) {
+            hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 2, VEC ? 1 : 0>), grid, dim3(kThreads), 0, stream, p);
+        } else if (VEC && tiles_buf_fits(p, rows, 16 / static_cast<int>(sizeof(typename WTraits<BF16W>::T)))) {
+            hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 2, VEC ? 2 : 0>), grid, dim3(kThreads), 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((linear_tiles_kernel<BF16W, VEC, 1, 2>), grid, dim3(kThreads), 0, stream, p);
+        }
     } else {
         hipLaunchKernelGGL((linear_kernel<BF16W, VEC, true>), grid, dim3(kThreads), 0, stream, p);
     }
