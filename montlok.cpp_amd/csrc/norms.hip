@@ -49,8 +49,19 @@ __global__ __launch_bounds__(kBlock) void rms_norm_vec_kernel(const float* __res
     for (int r = 0; r < RPW; ++r) {
         gid[r] = (static_cast<int64_t>(blockIdx.x) * RPW + r) * (kBlock / LPG) + threadIdx.x / LPG;
         active[r] = gid[r] < total_groups;
-        row[r] = active[r] ? gid[r] / groups : 0;
-        g[r] = active[r] ? gid[r] % groups : 0;
+        // One group per row (the plain RMSNorm) skips the 64-bit division, whose slow path sat in front of
+        // every load (262144 x 256: 116 -> 106 us); group counts below 2^31 divide in 32 bits.
+        if (groups == 1) {
+            row[r] = active[r] ? gid[r] : 0;
+            g[r] = 0;
+        } else if (total_groups < (int64_t{1} << 31)) {
+            const unsigned gu = static_cast<unsigned>(active[r] ? gid[r] : 0), gn = static_cast<unsigned>(groups);
+            row[r] = gu / gn;
+            g[r] = gu % gn;
+        } else {
+            row[r] = active[r] ? gid[r] / groups : 0;
+            g[r] = active[r] ? gid[r] % groups : 0;
+        }
     }
     // Every load is issued before the first use, without a branch around it:
     // lanes past the last group read group 0 (in bounds); all LPG lanes of a
