@@ -211,6 +211,31 @@ def test_decode_chain_vs_oracle(dev, oracle):
         np.testing.assert_allclose(st["angle"].cpu().numpy(), e["angle"], rtol=1e-6, atol=1e-6)
 
 
+def test_decode_full_streams_steps_equal_forward(dev):
+    """The decode workload's 65,536 streams (2 blocks, d_model 128, d_state 64, 4 heads of 64): two bars
+    stepped from a zero state equal the forward over those two bars to 1e-6 normwise (the step kernel
+    against the chunked scan and the tiled linears: a size-independent property at the full size; the
+    oracle checks the step chain on 1,024 streams)."""
+    from montlok.rdt import DecodeStackHIP
+
+    g = torch.Generator().manual_seed(23)
+    stack = DecodeStackHIP(d_model=128, n_layers=2, d_state=64, headdim=64).eval()
+    for block in stack.layers:
+        _init(block, g)
+    stack = stack.to(dev)
+    S = 65536
+    gd = torch.Generator(device=dev).manual_seed(23)
+    x = torch.randn(S, 2, 128, generator=gd, device=dev)
+    with torch.no_grad():
+        print("decode 65536 streams: forward", flush=True)
+        full = stack(x)
+        states = stack.new_state(S)
+        print("decode 65536 streams: two steps", flush=True)
+        steps = torch.stack([stack.step(x[:, t].contiguous(), states) for t in range(2)], dim=1)
+    assert torch.isfinite(steps).all()
+    assert_close(steps, full, tol=1e-6, name="decode step x 2 vs forward, 65536 streams")
+
+
 def test_decode_steps_equal_forward(dev):
     """T bars stepped from a zero state give the forward over those T bars, row for row."""
     from montlok.rdt import DecodeStackHIP

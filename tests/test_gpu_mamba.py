@@ -196,6 +196,40 @@ def test_fused_scan_equals_unfused_chunked(dev, monkeypatch, B, L, N, G, H, D):
     assert_bitwise(fused_g, unfused_g.cpu().numpy(), "fused vs unfused, explicit gate")
 
 
+def test_stack_scan_full_size(dev, monkeypatch):
+    """The stack's Mamba-3 scan at its full size (1024 windows x 256 tokens, 8 heads of 64, d_state 64, 16
+    angles): the fused kernel against the time-sequential kernel (the reference's association) to 1e-6
+    normwise and per row; the unfused path (prep -> rotate -> recurrence, which with 8192 window x head
+    pairs takes the time-sequential kernel) equals MLK_MAMBA3_SCAN=sequential bit for bit. The oracle
+    checks the same geometry on 2 windows (test_forward_vs_oracle); these are its size-independent
+    properties."""
+    from montlok import _C
+
+    B, L, N, G, H, D, R = 1024, 256, 64, 1, 8, 64, 16
+    W = 2 * H * D + 2 * G * N + 3 * H + R
+    rng = np.random.default_rng(1024)
+    _, p = _random_layer(rng, 1, 1, N, G, H, D, R)
+    plist = [_t(p[k], dev) for k in ("b_bias", "c_bias", "b_norm_w", "c_norm_w", "dt_bias", "skip")]
+    g = torch.Generator(device=dev).manual_seed(1024)
+    tp = torch.randn(B, L, W, generator=g, device=dev)
+    print("stack scan 1024 x 256: fused", flush=True)
+    fused = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "unfused")
+    print("stack scan 1024 x 256: unfused", flush=True)
+    unfused = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    monkeypatch.setenv("MLK_MAMBA3_SCAN", "sequential")
+    print("stack scan 1024 x 256: sequential", flush=True)
+    seq = _C.mamba3_siso_forward(tp, tp.new_empty(0), *plist, N, G, H, D, R, 1e-5, 1e-5, 1e-4)
+    assert torch.equal(unfused, seq), "unfused vs sequential at 1024 x 256"
+    del unfused
+    assert torch.isfinite(fused).all()
+    err = ((fused - seq).abs().amax() / seq.abs().amax()).item()
+    print(f"stack scan 1024 x 256: fused vs sequential {err:.2e} (normwise)", flush=True)
+    assert err <= 1e-6, f"fused vs sequential at 1024 x 256: {err:.2e}"
+    row = ((fused - seq).abs().amax(-1) / seq.abs().amax()).amax().item()
+    assert row <= 1e-6
+
+
 @pytest.mark.parametrize("B,L,N,G,H,D,R", [(5, 40, 16, 1, 4, 16, 4), (3, 77, 64, 2, 4, 16, 32), (2, 33, 32, 1, 3, 16, 0)])
 def test_fused_scan_headdim16_vs_sequential(dev, oracle, monkeypatch, B, L, N, G, H, D, R):
     """headdim 16 (one wave per head, no unfused chunked counterpart), with grouped B/C, every angle
