@@ -1436,6 +1436,9 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
             }
         } else {
             if constexpr (!kEarlyGate) gates();
+            // 32-bit offsets from the chunk's first output row (C rows of d_inner floats).
+            float* ochunk = orow + (TILE_OUT ? 0 : c0) * d_inner;
+            const int di = static_cast<int>(d_inner);
             int p0 = 0;  // index of pair (tt, 0)
 #pragma unroll
             for (int tt = 0; tt < CT; ++tt) {
@@ -1464,7 +1467,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                         // With an explicit gate gz = z, and the double product of two
                         // floats rounded once is the fp32 product y * gate.
                         const float o = static_cast<float>(static_cast<double>(y) * gz[tt][v]);
-                        if (!last || t < Lc) orow[((TILE_OUT ? 0 : c0) + t) * d_inner + col] = o;
+                        if (!last || t < Lc) ochunk[static_cast<unsigned>(t * di + col)] = o;
                     }
                 }
                 p0 += tt + 1;

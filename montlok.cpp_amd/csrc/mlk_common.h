@@ -82,9 +82,8 @@ __device__ __forceinline__ double shfl_d(double v, int src) { return __shfl(v, s
 // underflow to 0). Agrees with a correctly rounded exp to a couple of double
 // ulp; after rounding to float32 the results agree with it except in rare
 // ties.
-__device__ __forceinline__ double exp_d(double x) {
-    // Outside [-746, 710] the result is 0 or +inf; the comparisons keep NaN.
-    x = x < -746.0 ? -746.0 : (x > 710.0 ? 710.0 : x);
+// exp_d_core takes x in [-746, 710] (NaN passes through as NaN); exp_d clamps first.
+__device__ __forceinline__ double exp_d_core(double x) {
     const double kf = __builtin_rint(x * 1.4426950408889634074);
     const double r = fma(-kf, 1.90821492927058770002e-10, fma(-kf, 6.93147180369123816490e-01, x));
     const double r2 = r * r;
@@ -106,6 +105,11 @@ __device__ __forceinline__ double exp_d(double x) {
     const double poly = fma(s1, r8, s0);
     return __builtin_ldexp(poly, static_cast<int>(kf));
 }
+__device__ __forceinline__ double exp_d(double x) {
+    // Outside [-746, 710] the result is 0 or +inf; the comparisons keep NaN.
+    x = x < -746.0 ? -746.0 : (x > 710.0 ? 710.0 : x);
+    return exp_d_core(x);
+}
 
 // 1 / x for positive normal x (also 1 / inf = 0): the hardware reciprocal
 // (relative error ~5e-8) refined by two Newton steps r += r (1 - x r). Over
@@ -126,7 +130,9 @@ __device__ __forceinline__ double recip_pos(double x) {
 // tanh(x) = sign(x) (1 - t) / (1 + t), t = exp(-2 |x|) in (0, 1]: absolute
 // error a few 1e-16 (the consumers add it to an O(1) bias).
 __device__ __forceinline__ double tanh_d(double x) {
-    const double t = exp_d(-2.0 * __builtin_fabs(x));
+    // (the exponent is never positive: only exp_d's lower clamp can bind, and a NaN passes through it)
+    const double m = -2.0 * __builtin_fabs(x);
+    const double t = exp_d_core(m < -746.0 ? -746.0 : m);
     const double y = (1.0 - t) * recip_pos(1.0 + t);
     return __builtin_copysign(y, x);
 }
@@ -138,7 +144,13 @@ __device__ __forceinline__ double sigmoid_fast(double x) { return recip_pos(1.0 
 // (recip_pos: within a double ulp of the quotient, 1 / inf = 0): the IEEE division's scaling and fix-up
 // steps cost the stack's scan 3.5% of its time, and the product differs from the quotient by at most an
 // ulp of a double, far below the float32 rounding the gated output takes next.
-__device__ __forceinline__ double silu_d(double z) { return z * recip_pos(1.0 + exp_d(-z)); }
+// exp(-z)'s argument is clamped to [-746, 710] by min/max, two instructions where exp_d's NaN-keeping
+// selects take six: a NaN z then takes exp(710) = inf instead of exp(NaN), and the gate is z * 0 = NaN
+// either way, so the result equals the select form's for every z.
+__device__ __forceinline__ double silu_d(double z) {
+    const double x = __builtin_fmax(__builtin_fmin(-z, 710.0), -746.0);
+    return z * recip_pos(1.0 + exp_d_core(x));
+}
 
 // sin and cos of x in double for |x| below a few multiples of pi (the Mamba
 // rotary phases are wrapped to [0, 2pi) before this call). Cody-Waite
