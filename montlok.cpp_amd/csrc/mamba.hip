@@ -60,6 +60,15 @@ __device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(ex
 __device__ __forceinline__ float log1pf_cr(float x) { return static_cast<float>(log1p(static_cast<double>(x))); }
 __device__ __forceinline__ float tanhf_cr(float x) { return static_cast<float>(tanh_d(static_cast<double>(x))); }
 
+// base[elem_off] with the byte offset formed in 32 bits: the load can then take a scalar base and a 32-bit
+// vector offset, with no 64-bit address add per load (elem_off * 4 < 2^32 at every call).
+__device__ __forceinline__ float load_off32(const float* base, unsigned elem_off) {
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + (elem_off << 2));
+}
+__device__ __forceinline__ void store_off32(float* base, unsigned elem_off, float v) {
+    *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + (elem_off << 2)) = v;
+}
+
 // torch softplus (beta 1, threshold 20) as montlok_types.h:58-60 evaluates it.
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf_cr(expf_cr(x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf_cr(-x)); }
@@ -1162,15 +1171,15 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                 const int t = (tid + NTH * j) / N;
                 const unsigned off = PREP ? pb0 + static_cast<unsigned>(j * (NTH / N) * st32)
                                           : static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + n_own);
-                bx[j] = bc[off];
-                cx[j] = cc[off];
+                bx[j] = load_off32(bc, off);
+                cx[j] = load_off32(cc, off);
             }
 #pragma unroll
             for (int j = 0; j < MU; ++j) {
                 if constexpr (PREP) break;
                 const int u = tid + NTH * j;
                 const int which = u < 3 * C ? u / C : 0, t = u % C;
-                mx[j] = mc[static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + which * static_cast<int>(H))];
+                mx[j] = load_off32(mc, static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + which * static_cast<int>(H)));
             }
             if (!PREP && R > 0) {
 #pragma unroll
@@ -1178,7 +1187,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                     const unsigned u = static_cast<unsigned>(tid + NTH * j);
                     const unsigned uc = u < static_cast<unsigned>(C * R) ? u : static_cast<unsigned>(C * R - 1);
                     const int t = static_cast<int>((uc * rmagic) >> 16), r = static_cast<int>(uc) - t * R;
-                    ax[j] = ac[static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + r)];
+                    ax[j] = load_off32(ac, static_cast<unsigned>((t < Lc ? t : Lc - 1) * st32 + r));
                 }
             }
 #pragma unroll
@@ -1192,8 +1201,8 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                         vx[st][v] = xc[off];
                         if (own(st, v)) zx[st][v] = zc[off];
                     } else {
-                        vx[st][v] = xc[static_cast<unsigned>(tc * st32 + col)];
-                        zx[st][v] = zc[static_cast<unsigned>(tc * gst32 + col)];
+                        vx[st][v] = load_off32(xc, static_cast<unsigned>(tc * st32 + col));
+                        zx[st][v] = load_off32(zc, static_cast<unsigned>(tc * gst32 + col));
                     }
                 }
 #pragma unroll
@@ -1424,14 +1433,14 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
 #pragma unroll
                 for (int tt = 0; tt < CTE; ++tt)
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) ocol[static_cast<unsigned>((16 * tt + 4 * g + v) * di)] = o[tt][v];
+                    for (int v = 0; v < 4; ++v) store_off32(ocol, static_cast<unsigned>((16 * tt + 4 * g + v) * di), o[tt][v]);
             } else {
 #pragma unroll
                 for (int tt = 0; tt < CTE; ++tt)
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int t = 16 * tt + 4 * g + v;
-                        if (t < Lc) ocol[static_cast<unsigned>(t * di)] = o[tt][v];
+                        if (t < Lc) store_off32(ocol, static_cast<unsigned>(t * di), o[tt][v]);
                     }
             }
         } else {
@@ -1467,7 +1476,7 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
                         // With an explicit gate gz = z, and the double product of two
                         // floats rounded once is the fp32 product y * gate.
                         const float o = static_cast<float>(static_cast<double>(y) * gz[tt][v]);
-                        if (!last || t < Lc) ochunk[static_cast<unsigned>(t * di + col)] = o;
+                        if (!last || t < Lc) store_off32(ochunk, static_cast<unsigned>(t * di + col), o);
                     }
                 }
                 p0 += tt + 1;
@@ -1682,7 +1691,8 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                     const int u = wave + k * NW;
                     const int j = u >> 2, row = 4 * (u & 3) + rq;
                     const int n = tile_col(j < ncol ? j : ncol - 1) + row;
-                    const float* src = p.in_w + static_cast<int64_t>(n < W ? n : W - 1) * 64 + 4 * (slot ^ row);
+                    const unsigned off = static_cast<unsigned>((n < W ? n : W - 1) * 64 + 4 * (slot ^ row)) << 2;
+                    const float* src = reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.in_w) + off);
                     __builtin_amdgcn_global_load_lds(
                         (const __attribute__((address_space(1))) void*)src,
                         (__attribute__((address_space(3))) void*)(w_lds + u * 256), 16, 0, 0);
@@ -2000,11 +2010,11 @@ void mamba3_block_scan_kernel(BlockArgs p) {
                 float* ocol = p.s.out + b * L * DI + h * D + 16 * hw + li;
                 if (L == C) {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) ocol[static_cast<unsigned>((16 + 4 * grp + v) * DI)] = o[v];
+                    for (int v = 0; v < 4; ++v) store_off32(ocol, static_cast<unsigned>((16 + 4 * grp + v) * DI), o[v]);
                 } else {
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
-                        if (16 + 4 * grp + v < L) ocol[static_cast<unsigned>((16 + 4 * grp + v) * DI)] = o[v];
+                        if (16 + 4 * grp + v < L) store_off32(ocol, static_cast<unsigned>((16 + 4 * grp + v) * DI), o[v]);
                 }
             }
             return;
