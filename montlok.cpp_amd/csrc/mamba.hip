@@ -1144,7 +1144,8 @@ __device__ __forceinline__ void scan_head(const ScanArgs& a, ScanLds<C, NT, DT>&
         };
         // a. Every global load of the chunk issued before the first wait
         //    (tokens past the end read the last token; they carry no weight).
-        //    Offsets are 32-bit from the chunk's first row (checked at launch).
+        //    Offsets are 32-bit from the chunk's first row (row strides below 2^25 floats, checked at
+        //    launch).
         //    PREP reads the tile's rows unclamped: its rows past the end hold
         //    the last token's values already (hooks.before clamps its x rows),
         //    and keeps this thread's B/C values in bx/cx for step c.
@@ -2517,8 +2518,12 @@ mlk_status mlk_mamba3_siso_forward(const float* projected, int64_t batch, int64_
     if (blh == 0) return MLK_OK;
     MLK_CHECK(projected && b_bias && c_bias && b_norm_w && c_norm_w && dt_bias && skip && out && workspace,
               "null tensor pointer");
+    // The fused kernel addresses a chunk's 32 rows by 32-bit byte offsets from its first row (row strides
+    // below 2^25 floats); other strides take the separate kernels.
+    const bool narrow_rows = proj_token_stride < (int64_t{1} << 25) &&
+                             (gate == nullptr || gate_token_stride < (int64_t{1} << 25));
     if (scan_mode() == ScanMode::kFused && (d_state == 16 || d_state == 32 || d_state == 64) &&
-        (headdim == 16 || headdim == 32 || headdim == 64) && batch * nheads < (int64_t{1} << 31)) {
+        (headdim == 16 || headdim == 32 || headdim == 64) && batch * nheads < (int64_t{1} << 31) && narrow_rows) {
         ScanArgs s{};
         s.proj = projected;
         s.sb = proj_batch_stride;
